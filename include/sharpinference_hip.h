@@ -1,0 +1,163 @@
+/*
+ * libsharpinference_hip — C ABI of the MI355X (gfx950) backend for
+ * SharpInference's quantized matrix-vector hot path.
+ *
+ * The managed side of SharpInference binds these entry points by P/Invoke
+ * from a HIP executor that mirrors SharpInference.Backends.D3D12Vm's
+ * D3D12VmExecutor; the binding stubs are listed in INTEGRATION.md.  The
+ * reference has no native layer, so every entry point below names the
+ * managed member whose job it takes over.
+ *
+ * Conventions
+ *   - Every function returns an si_hip_status (0 = success).  On failure the
+ *     context's message is set and si_hip_last_error(ctx) returns it; nothing
+ *     falls back to another path (doc/vm-execution-program.md:16,57 of the
+ *     reference: execution failures never trigger a silent retry).
+ *   - Device pointers are plain `void*` from si_hip_alloc (or any device
+ *     allocation of the same GPU).  Sizes are bytes unless named otherwise.
+ *   - All work is ordered on the context's single HIP stream (default
+ *     priority).  A context is locked internally: calls on one context from
+ *     several threads serialise, like D3D12VmExecutor's `gate`
+ *     (D3D12VmExecutor.cs:153,285,307).
+ *   - Matrices are GGUF tensors [rows, cols] with `cols` contiguous
+ *     (GGUF ne0 = cols, ne1 = rows), kept in their native block layout.
+ */
+#ifndef SHARPINFERENCE_HIP_H
+#define SHARPINFERENCE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SI_HIP_ABI_VERSION 1
+
+typedef struct si_hip_context si_hip_context;
+typedef struct si_hip_plan si_hip_plan;
+
+typedef enum si_hip_status {
+    SI_HIP_OK = 0,
+    SI_HIP_ERR_ARGUMENT = 1,      /* ArgumentException / ArgumentOutOfRangeException */
+    SI_HIP_ERR_UNSUPPORTED = 2,   /* NotSupportedException (e.g. unknown tensor type) */
+    SI_HIP_ERR_ADAPTATION = 3,    /* InstructionAdaptationException (shape/signature) */
+    SI_HIP_ERR_DEVICE = 4,        /* HIP runtime failure */
+    SI_HIP_ERR_OUT_OF_MEMORY = 5,
+    SI_HIP_ERR_STATE = 6,         /* call not valid in the context's current state */
+} si_hip_status;
+
+/* GGUF tensor type ids, as GgufModelTensorType (GgufModelFile.cs:24-46). */
+typedef enum si_hip_format {
+    SI_HIP_F32 = 0,
+    SI_HIP_F16 = 1,
+    SI_HIP_Q4_0 = 2,
+    SI_HIP_Q8_0 = 8,
+    SI_HIP_Q4_K = 12,
+    SI_HIP_BF16 = 30,
+} si_hip_format;
+
+/* ---- library and device --------------------------------------------------- */
+
+/* SI_HIP_ABI_VERSION of the loaded library. */
+int si_hip_abi_version(void);
+
+/* Number of visible HIP devices (no context needed). */
+int si_hip_device_count(int* count);
+
+/* Selects `device` and creates a context with its own stream.
+ * Replaces: D3D12VmDeviceFactory adapter selection + the executor's queue and
+ * fence creation (D3D12VmExecutor.cs:80-86). */
+int si_hip_init(int device, si_hip_context** out);
+
+/* Destroys the context (waits for its stream first).  NULL is accepted.
+ * Replaces: D3D12VmExecutor.Dispose. */
+int si_hip_destroy(si_hip_context* ctx);
+
+/* Message of the last failed call on `ctx` (or of the calling thread when
+ * ctx is NULL).  Valid until the next call on the same context/thread. */
+const char* si_hip_last_error(const si_hip_context* ctx);
+
+/* ---- memory ----------------------------------------------------------------- */
+
+/* Bytes of a [rows, cols] tensor of `format`; fails (ARGUMENT) when cols is
+ * not a whole number of blocks.  Replaces: GgufModelFile.GetByteLength
+ * (GgufModelFile.cs:301-331), extended with Q4_K (144 bytes / 256). */
+int si_hip_tensor_bytes(int format, int64_t rows, int64_t cols, uint64_t* bytes);
+
+/* Device buffer of `bytes` (256-byte aligned).  Replaces: the executor's
+ * one committed resource per slot (D3D12VmExecutor.cs:93-97). */
+int si_hip_alloc(si_hip_context* ctx, uint64_t bytes, void** device_ptr);
+int si_hip_free(si_hip_context* ctx, void* device_ptr);
+
+/* Synchronous host -> device copy of raw bytes (GGUF blocks are uploaded
+ * as-is, never repacked).  Replaces: D3D12VmExecutor.Upload
+ * (D3D12VmExecutor.cs:595-625). */
+int si_hip_upload(si_hip_context* ctx, void* device_dst, const void* host_src, uint64_t bytes);
+
+/* Synchronous device -> host copy.  Replaces: D3D12VmExecutor.Readback
+ * (D3D12VmExecutor.cs:682-696). */
+int si_hip_readback(si_hip_context* ctx, void* host_dst, const void* device_src, uint64_t bytes);
+
+/* Device -> device copy, ordered on the context stream. */
+int si_hip_copy(si_hip_context* ctx, void* device_dst, const void* device_src, uint64_t bytes);
+
+/* Fills `count` 32-bit words with `value` by a kernel (no memset nodes, so
+ * it may be recorded into a plan). */
+int si_hip_fill_u32(si_hip_context* ctx, void* device_dst, uint32_t value, uint64_t count);
+
+/* Waits for all work queued on the context.  Replaces: the executor's fence
+ * wait after a submission (Submit / WaitForCompletion, D3D12VmExecutor.cs:875-890). */
+int si_hip_sync(si_hip_context* ctx);
+
+/* ---- hot path ---------------------------------------------------------------- */
+
+/* y[rows] = W[rows, cols] . x[cols] (+ residual[rows] when residual != NULL),
+ * W in GGUF Q8_0 / Q4_0 / Q4_K block layout, x, y, residual FP32.  FP32
+ * arithmetic and accumulation.  `path` (optional) receives 1 for the tiled
+ * gfx950 kernel and 2 for the any-shape kernel.
+ * Replaces: the core.mat-vec instruction (cooperative form
+ * GpuTierZeroInstruction.cs:44-89 on D3D12, CpuInstructionNumerics.MatVec
+ * CpuInstructionNumerics.cs:16-23 on CpuVm) for block-quantized weights,
+ * which the reference rejects (TierZeroOperationContracts.cs:161). */
+int si_hip_gemv(si_hip_context* ctx, int format, const void* w, const float* x, float* y,
+                int64_t rows, int64_t cols, const float* residual, int* path);
+
+/* out[rows, cols] = exact FP32 values of the blocks of W.  Test and
+ * inspection entry point for the block decoder used by the products.
+ * Replaces: the FP16 -> FP32 row conversion step of the CPU matvec
+ * (CpuHalfMatrixOperators.cs:34-36), for quantized blocks. */
+int si_hip_dequant(si_hip_context* ctx, int format, const void* w, float* out, int64_t rows, int64_t cols);
+
+/* ---- recorded entries and timing -------------------------------------------- */
+
+/* Starts recording: until si_hip_plan_end, launches on `ctx` are recorded
+ * instead of executed (uploads, readbacks, allocations and syncs are
+ * rejected with SI_HIP_ERR_STATE).  A plan is the HIP form of a recorded VM
+ * entry (D3D12VmSchedule.Create, D3D12VmSchedule.cs:48-111): one graph,
+ * replayed with one submission. */
+int si_hip_plan_begin(si_hip_context* ctx);
+int si_hip_plan_end(si_hip_context* ctx, si_hip_plan** out);
+int si_hip_plan_destroy(si_hip_plan* plan);
+
+/* Replays the plan on the context stream (asynchronous).
+ * Replaces: D3D12VmExecutor.Execute(entry) (D3D12VmExecutor.cs:283-292). */
+int si_hip_plan_launch(si_hip_plan* plan);
+
+/* Launches plans[i % nplans] for i in [0, steps) back to back (asynchronous). */
+int si_hip_plan_launch_sequence(si_hip_plan* const* plans, int nplans, int64_t steps);
+
+/* GPU microseconds per replay over `repetitions` back-to-back replays,
+ * measured with events on the context stream; repetitions outside 1..1024
+ * is ARGUMENT.  Replaces: D3D12VmExecutor.MeasureGpuMicroseconds
+ * (D3D12VmExecutor.cs:452-478). */
+int si_hip_plan_measure_us(si_hip_plan* plan, int repetitions, double* microseconds);
+
+/* Event pair on the context stream: begin records the start event, end
+ * records the stop event, waits for it and returns the elapsed ms. */
+int si_hip_timer_begin(si_hip_context* ctx);
+int si_hip_timer_end(si_hip_context* ctx, double* milliseconds);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,200 @@
+"""CPU oracle for the quantized matrix-vector hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+the CPU-baseline leg of ``bench.py`` import this package, and only as the
+checker or as the timed CPU baseline.  The product package
+``sharpinference_amd`` never imports it.
+
+The numerics live in ``oracle.c`` (built into ``liboracle.so`` by
+``oracle/Makefile``); this module is a thin ctypes + numpy face on it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K = 0, 1, 2, 8, 12
+BLOCK_ELEMS = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144}
+NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so from oracle.c (gcc, via the Makefile)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(l: ctypes.CDLL) -> None:
+    i64, u64, i32, dbl = ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_double
+    vp = ctypes.c_void_p
+    l.orc_half_to_float.argtypes = [ctypes.c_uint16]
+    l.orc_half_to_float.restype = ctypes.c_float
+    l.orc_float_to_half.argtypes = [ctypes.c_float]
+    l.orc_float_to_half.restype = ctypes.c_uint16
+    l.orc_float_to_bf16.argtypes = [ctypes.c_float]
+    l.orc_float_to_bf16.restype = ctypes.c_uint16
+    l.orc_tensor_bytes.argtypes = [i32, i64, i64]
+    l.orc_tensor_bytes.restype = i64
+    l.orc_row_bytes.argtypes = [i32, i64]
+    l.orc_row_bytes.restype = i64
+    for name in ("orc_gen_q8_0", "orc_gen_q4_0", "orc_gen_q4_k"):
+        getattr(l, name).argtypes = [u64, i64, i64, dbl, vp]
+        getattr(l, name).restype = None
+    l.orc_gen_quant.argtypes = [i32, u64, i64, i64, dbl, vp]
+    l.orc_gen_quant.restype = None
+    for name in ("orc_gen_normal_f32", "orc_gen_normal_f16", "orc_gen_normal_bf16"):
+        getattr(l, name).argtypes = [u64, i64, dbl, dbl, vp]
+        getattr(l, name).restype = None
+    l.orc_dequant.argtypes = [i32, vp, i64, i64, vp]
+    l.orc_dequant.restype = i32
+    l.orc_q4_k_scale_min.argtypes = [i32, vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+    l.orc_q4_k_scale_min.restype = None
+    l.orc_gemv_cpuvm.argtypes = [i32, vp, vp, vp, i64, i64, i32]
+    l.orc_gemv_cpuvm.restype = i32
+    l.orc_gemv_f64.argtypes = [i32, vp, vp, vp, i64, i64]
+    l.orc_gemv_f64.restype = i32
+    l.orc_dot_f32.argtypes = [vp, vp, i64]
+    l.orc_dot_f32.restype = ctypes.c_float
+    l.orc_gemm_prefill_cpuvm.argtypes = [i32, vp, vp, vp, i64, i64, i64, i32]
+    l.orc_gemm_prefill_cpuvm.restype = i32
+    l.orc_gemm_prefill_f64.argtypes = [i32, vp, vp, vp, i64, i64, i64]
+    l.orc_gemm_prefill_f64.restype = i32
+    l.orc_now_seconds.restype = dbl
+    l.orc_max_threads.restype = i32
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous
+    return a.ctypes.data
+
+
+def tensor_bytes(fmt: int, rows: int, cols: int) -> int:
+    return int(lib().orc_tensor_bytes(fmt, rows, cols))
+
+
+def row_bytes(fmt: int, cols: int) -> int:
+    return int(lib().orc_row_bytes(fmt, cols))
+
+
+def gen_quant(fmt: int, seed: int, rows: int, cols: int, sigma: float = 0.02) -> np.ndarray:
+    n = tensor_bytes(fmt, rows, cols)
+    if n < 0:
+        raise ValueError(f"bad shape {rows}x{cols} for format {fmt}")
+    out = np.empty(n, dtype=np.uint8)
+    lib().orc_gen_quant(fmt, seed, rows, cols, sigma, _ptr(out))
+    return out
+
+
+def gen_normal_f32(seed: int, n: int, mean: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_gen_normal_f32(seed, n, mean, sigma, _ptr(out))
+    return out
+
+
+def gen_normal_f16(seed: int, n: int, mean: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    lib().orc_gen_normal_f16(seed, n, mean, sigma, _ptr(out))
+    return out
+
+
+def gen_normal_bf16(seed: int, n: int, mean: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    lib().orc_gen_normal_bf16(seed, n, mean, sigma, _ptr(out))
+    return out
+
+
+def dequant(fmt: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    out = np.empty((rows, cols), dtype=np.float32)
+    rc = lib().orc_dequant(fmt, _ptr(np.ascontiguousarray(w)), rows, cols, _ptr(out))
+    if rc != 0:
+        raise ValueError("dequant: bad shape")
+    return out
+
+
+def q4_k_scale_min(j: int, scales: bytes) -> tuple[int, int]:
+    buf = np.frombuffer(bytes(scales), dtype=np.uint8).copy()
+    sc, m = ctypes.c_int(), ctypes.c_int()
+    lib().orc_q4_k_scale_min(j, _ptr(buf), ctypes.byref(sc), ctypes.byref(m))
+    return sc.value, m.value
+
+
+def gemv_cpuvm(fmt: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int,
+               threads: int = 0) -> np.ndarray:
+    y = np.empty(rows, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rc = lib().orc_gemv_cpuvm(fmt, _ptr(np.ascontiguousarray(w)), _ptr(x), _ptr(y), rows, cols, threads)
+    if rc != 0:
+        raise ValueError("gemv: bad shape")
+    return y
+
+
+def gemv_f64(fmt: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    y = np.empty(rows, dtype=np.float64)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rc = lib().orc_gemv_f64(fmt, _ptr(np.ascontiguousarray(w)), _ptr(x), _ptr(y), rows, cols)
+    if rc != 0:
+        raise ValueError("gemv: bad shape")
+    return y
+
+
+def dot_f32(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return float(lib().orc_dot_f32(_ptr(a), _ptr(b), a.size))
+
+
+def gemm_prefill_cpuvm(fmt: int, w: np.ndarray, x_bf16: np.ndarray, m: int, rows: int, cols: int,
+                       threads: int = 0) -> np.ndarray:
+    y = np.empty((m, rows), dtype=np.float32)
+    rc = lib().orc_gemm_prefill_cpuvm(fmt, _ptr(np.ascontiguousarray(w)), _ptr(np.ascontiguousarray(x_bf16)),
+                                      _ptr(y), m, rows, cols, threads)
+    if rc != 0:
+        raise ValueError("prefill: bad shape")
+    return y
+
+
+def gemm_prefill_f64(fmt: int, w: np.ndarray, x_bf16: np.ndarray, m: int, rows: int, cols: int) -> np.ndarray:
+    y = np.empty((m, rows), dtype=np.float64)
+    rc = lib().orc_gemm_prefill_f64(fmt, _ptr(np.ascontiguousarray(w)), _ptr(np.ascontiguousarray(x_bf16)),
+                                    _ptr(y), m, rows, cols)
+    if rc != 0:
+        raise ValueError("prefill: bad shape")
+    return y
+
+
+def now() -> float:
+    return float(lib().orc_now_seconds())
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().orc_float_to_half(float(x)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().orc_half_to_float(int(h)))

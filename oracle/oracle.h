@@ -1,0 +1,108 @@
+/*
+ * CPU oracle for the quantized matrix-vector hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
+ * calls this code; only tests/, the smoke check and the CPU-baseline leg of
+ * bench.py use it, and only as the checker / the timed CPU baseline.
+ *
+ * What it restates:
+ *   - GGUF tensor byte sizes: SharpInference.Gguf/GgufModelFile.cs:301-331
+ *     (Q4_0 = 18 B / 32, Q8_0 = 34 B / 32).  Q4_K (144 B / 256) is rejected
+ *     by the reference (GgufModelFile.cs:320); its size comes from the GGUF v3
+ *     block definition.
+ *   - Block decoding (dequantisation) of Q8_0, Q4_0, Q4_K: the reference has
+ *     no decoder (it only mirrors the type ids, GgufModelFile.cs:24-46).  The
+ *     algorithm is the public GGML block format of GGUF version 3 (the only
+ *     version the reference reader accepts, GgufModelFile.cs:51,85), as
+ *     implemented by ggml's dequantize_row_q8_0 / _q4_0 / _q4_K.  ggml is not
+ *     a dependency of the reference and is absent from this image.
+ *   - The CpuVm matrix-vector product with FP16 weights:
+ *     SharpInference.Backends.Cpu/CpuHalfMatrixOperators.cs:11-43,123-137
+ *     (dequantised row -> FP32 scratch -> FP32 dot), emitted for core.mat-vec
+ *     by SharpInference.Instructions.Cpu/CpuTierZeroInstruction.cs:47-55.
+ *   - An fp64 recomputation from the exactly dequantised FP32 weights, the
+ *     same kind of truth the reference tests use
+ *     (SharpInference.Tests/GpuMatVecTests.cs:33-34).
+ */
+#ifndef SI_ORACLE_H
+#define SI_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor type ids (GgufModelFile.cs:24-46). */
+enum {
+    ORC_F32 = 0,
+    ORC_F16 = 1,
+    ORC_Q4_0 = 2,
+    ORC_Q8_0 = 8,
+    ORC_Q4_K = 12,
+};
+
+/* ---- scalar conversions ---------------------------------------------- */
+float orc_half_to_float(uint16_t h);
+uint16_t orc_float_to_half(float f);      /* round to nearest even */
+float orc_bf16_to_float(uint16_t b);
+uint16_t orc_float_to_bf16(float f);      /* round to nearest even */
+
+/* ---- sizes ------------------------------------------------------------ */
+/* Bytes of a [rows, cols] tensor of `format`; -1 if cols is not a multiple of
+ * the block size or the format is unknown. */
+int64_t orc_tensor_bytes(int format, int64_t rows, int64_t cols);
+int64_t orc_row_bytes(int format, int64_t cols);
+int orc_block_elems(int format);
+int orc_block_bytes(int format);
+
+/* ---- seeded synthetic generators -------------------------------------- */
+/* Q8_0: q ~ U{-127..127}, d = fp16(|N(0, sigma)| / 127). */
+void orc_gen_q8_0(uint64_t seed, int64_t rows, int64_t cols, double sigma, uint8_t* out);
+/* Q4_0: nibble ~ U{0..15}, d = fp16(|N(0, sigma)| / 8). */
+void orc_gen_q4_0(uint64_t seed, int64_t rows, int64_t cols, double sigma, uint8_t* out);
+/* Q4_K: q ~ U{0..15}, 6-bit sc/m ~ U{0..63},
+ * d = fp16(|N(0, sigma)| / 504), dmin = fp16(|N(0, sigma)| / 63). */
+void orc_gen_q4_k(uint64_t seed, int64_t rows, int64_t cols, double sigma, uint8_t* out);
+void orc_gen_quant(int format, uint64_t seed, int64_t rows, int64_t cols, double sigma, uint8_t* out);
+/* n values ~ N(mean, sigma) as fp32 / fp16 / bf16 bit patterns. */
+void orc_gen_normal_f32(uint64_t seed, int64_t n, double mean, double sigma, float* out);
+void orc_gen_normal_f16(uint64_t seed, int64_t n, double mean, double sigma, uint16_t* out);
+void orc_gen_normal_bf16(uint64_t seed, int64_t n, double mean, double sigma, uint16_t* out);
+
+/* ---- block decoding ----------------------------------------------------- */
+void orc_dequant_row(int format, const uint8_t* row, int64_t cols, float* out);
+int orc_dequant(int format, const uint8_t* w, int64_t rows, int64_t cols, float* out);
+/* Q4_K 6-bit (scale, min) of sub-block j (0..7) from the 12 packed bytes. */
+void orc_q4_k_scale_min(int j, const uint8_t* scales, int* sc, int* m);
+
+/* ---- matrix-vector products -------------------------------------------- */
+/* CpuVm order: per row, dequantise into an FP32 scratch and take the FP32
+ * dot with x; small problems run serially over 1024-element chunks, large
+ * ones run rows in parallel on `threads` threads (<=0: all cores). */
+int orc_gemv_cpuvm(int format, const uint8_t* w, const float* x, float* y,
+                   int64_t rows, int64_t cols, int threads);
+/* fp64 truth over the exactly dequantised weights. */
+int orc_gemv_f64(int format, const uint8_t* w, const float* x, double* y,
+                 int64_t rows, int64_t cols);
+/* FP32 dot in the oracle's fixed order: 8 interleaved fused multiply-add lane accumulators
+ * (element i feeds lane i % 8), then ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)). */
+float orc_dot_f32(const float* a, const float* b, int64_t n);
+
+/* ---- batched prefill product ------------------------------------------- */
+/* Y[m, r] = sum_c X[m, c] * W[r, c] with X bf16, following the
+ * transpose_right branch of CpuInstructionNumerics.MatrixMultiply
+ * (CpuInstructionNumerics.cs:66-77): one CpuVm matvec per token row. */
+int orc_gemm_prefill_cpuvm(int format, const uint8_t* w, const uint16_t* x_bf16, float* y,
+                           int64_t m, int64_t rows, int64_t cols, int threads);
+int orc_gemm_prefill_f64(int format, const uint8_t* w, const uint16_t* x_bf16, double* y,
+                         int64_t m, int64_t rows, int64_t cols);
+
+/* ---- timing helper for the CPU baseline -------------------------------- */
+double orc_now_seconds(void);
+int orc_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,579 @@
+// Quantized matrix-vector product y = W . x for GGUF Q8_0 / Q4_0 / Q4_K
+// weights kept in their native block layout, plus the bit-exact block
+// decoder used to check that layout.
+//
+// Semantics follow the core.mat-vec contract
+// (SharpInference.Graphs/TierZeroOperationContracts.cs:113-115,152,161):
+// W is [rows, cols] row-major (GGUF ne0 = cols contiguous), x is FP32 [cols],
+// y is FP32 [rows], FP32 arithmetic and accumulation.  The reference's CPU
+// form dequantises a row into FP32 and takes an FP32 dot
+// (SharpInference.Backends.Cpu/CpuHalfMatrixOperators.cs:24-41); this kernel
+// computes the same sum factored per block, d * sum(q * x), in FP32.
+//
+// Fast path layout (one "unit" = 64 columns of one row):
+//   Q8_0  two 34-byte blocks, 68 bytes = 17 dwords, dword aligned
+//   Q4_0  two 18-byte blocks, 36 bytes =  9 dwords, dword aligned
+//   Q4_K  one 32-byte quant chunk of a 144-byte super-block plus the
+//         super-block's 16-byte header (d, dmin, 12 scale bytes)
+// A wave holds 64 / LK row slots of LK lanes; lane k of a slot takes units
+// k, k + LK, ... of RL consecutive rows, so every unit's x values are read
+// from LDS once and reused for RL rows.  All weight loads of a lane are
+// issued before x is staged into LDS, so HBM latency overlaps the staging.
+#include "si_internal.hpp"
+
+#include <hip/hip_fp16.h>
+
+namespace si {
+namespace {
+
+constexpr int WG = 256;          // threads per workgroup (4 waves)
+constexpr int XS_UNIT = 68;      // LDS floats per unit: 64 values + 4 pad (bank spread)
+
+struct __attribute__((aligned(4))) u32x4 {
+    uint32_t x, y, z, w;
+};
+
+__device__ __forceinline__ u32x4 ld4(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ uint32_t ld1(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+__device__ __forceinline__ float half_lo(uint32_t v)
+{
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(v & 0xffffu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t v)
+{
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(v >> 16)));
+}
+
+// 4 signed bytes of q times 4 floats, accumulated.
+__device__ __forceinline__ float dot4_i8(uint32_t q, const float4& x, float a)
+{
+    a = fmaf(static_cast<float>(static_cast<int8_t>(q)), x.x, a);
+    a = fmaf(static_cast<float>(static_cast<int8_t>(q >> 8)), x.y, a);
+    a = fmaf(static_cast<float>(static_cast<int8_t>(q >> 16)), x.z, a);
+    a = fmaf(static_cast<float>(static_cast<int8_t>(q >> 24)), x.w, a);
+    return a;
+}
+
+// Hides the known-zero bits of a masked value from the optimiser, so the
+// byte conversions below select one v_cvt_f32_ubyteN each instead of a
+// bit-field extract plus a conversion.
+__device__ __forceinline__ uint32_t opaque(uint32_t v)
+{
+    asm("" : "+v"(v));
+    return v;
+}
+
+// 4 unsigned bytes (each < 256) of q times 4 floats, accumulated.
+__device__ __forceinline__ float dot4_u8(uint32_t q, const float4& x, float a)
+{
+    a = fmaf(static_cast<float>(q & 0xffu), x.x, a);
+    a = fmaf(static_cast<float>((q >> 8) & 0xffu), x.y, a);
+    a = fmaf(static_cast<float>((q >> 16) & 0xffu), x.z, a);
+    a = fmaf(static_cast<float>(q >> 24), x.w, a);
+    return a;
+}
+
+template <int FMT>
+struct QUnit;
+
+// Two Q8_0 blocks {fp16 d; int8 q[32]} back to back.
+template <>
+struct QUnit<FMT_Q8_0> {
+    static constexpr int UNIT_BYTES = 68;
+    uint32_t v[17];
+
+    __device__ __forceinline__ void load(const uint8_t* row, int u)
+    {
+        const uint8_t* p = row + u * UNIT_BYTES;
+        const u32x4 a = ld4(p), b = ld4(p + 16), c = ld4(p + 32), d = ld4(p + 48);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        v[8] = c.x; v[9] = c.y; v[10] = c.z; v[11] = c.w;
+        v[12] = d.x; v[13] = d.y; v[14] = d.z; v[15] = d.w;
+        v[16] = ld1(p + 64);
+    }
+
+    // Contribution of block h (columns 32h..32h+31 of the unit).
+    __device__ __forceinline__ float half(int h, const float4* x, float /*sx*/) const
+    {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            const uint32_t q0 = h == 0 ? __builtin_amdgcn_alignbit(v[k + 1], v[k], 16) : v[9 + k];
+            const uint32_t q1 = h == 0 ? __builtin_amdgcn_alignbit(v[k + 2], v[k + 1], 16) : v[10 + k];
+            a0 = dot4_i8(q0, x[k], a0);
+            a1 = dot4_i8(q1, x[k + 1], a1);
+        }
+        const float d = h == 0 ? half_lo(v[0]) : half_hi(v[8]);
+        return d * (a0 + a1);
+    }
+};
+
+// Two Q4_0 blocks {fp16 d; u8 q[16]}: element j < 16 is the low nibble of
+// q[j], element j + 16 the high nibble, value d * (nibble - 8).
+// (nibble ^ 8) is (nibble - 8) as a signed 4-bit number; moved into the top
+// half of a byte it reads as the signed byte 16 * (nibble - 8), which one
+// sign-extending conversion turns into a float.  The factor 16 is folded
+// into the scale (d / 16 is exact), so no per-block sum of x is needed and
+// every product keeps the sign and class of the dequantised weight.
+template <>
+struct QUnit<FMT_Q4_0> {
+    static constexpr int UNIT_BYTES = 36;
+    uint32_t v[9];
+
+    __device__ __forceinline__ void load(const uint8_t* row, int u)
+    {
+        const uint8_t* p = row + u * UNIT_BYTES;
+        const u32x4 a = ld4(p), b = ld4(p + 16);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        v[8] = ld1(p + 32);
+    }
+
+    __device__ __forceinline__ float half(int h, const float4* x, float /*sx*/) const
+    {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t q = h == 0 ? __builtin_amdgcn_alignbit(v[k + 1], v[k], 16) : v[5 + k];
+            const uint32_t t = q ^ 0x88888888u;
+            a0 = dot4_i8((t << 4) & 0xf0f0f0f0u, x[k], a0);
+            a1 = dot4_i8(t & 0xf0f0f0f0u, x[4 + k], a1);
+        }
+        const float d = h == 0 ? half_lo(v[0]) : half_hi(v[4]);
+        return (d * 0.0625f) * (a0 + a1);
+    }
+};
+
+// Q4_K super-block {fp16 d; fp16 dmin; u8 scales[12]; u8 q[128]}; unit u is
+// chunk c = u % 4 (64 elements: low nibbles of q[32c..32c+31] are sub-block
+// 2c, high nibbles sub-block 2c+1), value (d*sc)*q - (dmin*m).
+template <>
+struct QUnit<FMT_Q4_K> {
+    static constexpr int UNIT_BYTES = 36;   // amortised: 144 bytes per 4 units
+    uint32_t hd[4];
+    uint32_t qs[8];
+    int chunk;
+
+    __device__ __forceinline__ void load(const uint8_t* row, int u)
+    {
+        chunk = u & 3;
+        const uint8_t* p = row + (u >> 2) * 144;
+        const u32x4 h = ld4(p), a = ld4(p + 16 + 32 * chunk), b = ld4(p + 32 + 32 * chunk);
+        hd[0] = h.x; hd[1] = h.y; hd[2] = h.z; hd[3] = h.w;
+        qs[0] = a.x; qs[1] = a.y; qs[2] = a.z; qs[3] = a.w;
+        qs[4] = b.x; qs[5] = b.y; qs[6] = b.z; qs[7] = b.w;
+    }
+
+    // 6-bit scale and min of sub-block j (GGML get_scale_min_k4), written
+    // with selects so lanes of different chunks do not diverge.
+    __device__ __forceinline__ void scale_min(int j, int& sc, int& m) const
+    {
+        const int jj = j & 3;
+        const uint32_t s0 = (hd[1] >> (8 * jj)) & 0xffu;   // scales[jj]
+        const uint32_t s1 = (hd[2] >> (8 * jj)) & 0xffu;   // scales[jj + 4]
+        const uint32_t s2 = (hd[3] >> (8 * jj)) & 0xffu;   // scales[jj + 8]
+        const bool low = j < 4;
+        sc = static_cast<int>(low ? (s0 & 63u) : ((s2 & 15u) | ((s0 >> 6) << 4)));
+        m = static_cast<int>(low ? (s1 & 63u) : ((s2 >> 4) | ((s1 >> 6) << 4)));
+    }
+
+    __device__ __forceinline__ float half(int h, const float4* x, float sx) const
+    {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            const uint32_t q0 = h == 0 ? (qs[k] & 0x0f0f0f0fu) : ((qs[k] >> 4) & 0x0f0f0f0fu);
+            const uint32_t q1 = h == 0 ? (qs[k + 1] & 0x0f0f0f0fu) : ((qs[k + 1] >> 4) & 0x0f0f0f0fu);
+            a0 = dot4_u8(opaque(q0), x[k], a0);
+            a1 = dot4_u8(opaque(q1), x[k + 1], a1);
+        }
+        int sc, m;
+        scale_min(2 * chunk + h, sc, m);
+        const float d1 = half_lo(hd[0]) * static_cast<float>(sc);
+        const float m1 = half_hi(hd[0]) * static_cast<float>(m);
+        return fmaf(d1, a0 + a1, -(m1 * sx));
+    }
+
+    // Same contribution with every weight decoded as the oracle does,
+    // w = (d*sc)*q - (dmin*m) rounded per operation, then w*x accumulated.
+    // Used when x holds non-finite or huge values, where the factored form
+    // above could change the IEEE class of the result (inf - inf).
+    __device__ float half_exact(int h, const float4* x) const
+    {
+        int sc, m;
+        scale_min(2 * chunk + h, sc, m);
+        const float d1 = __fmul_rn(half_lo(hd[0]), static_cast<float>(sc));
+        const float m1 = __fmul_rn(half_hi(hd[0]), static_cast<float>(m));
+        float a = 0.0f;
+        for (int k = 0; k < 8; k++) {
+            const uint32_t q = h == 0 ? (qs[k] & 0x0f0f0f0fu) : ((qs[k] >> 4) & 0x0f0f0f0fu);
+            const float xs[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+            for (int i = 0; i < 4; i++) {
+                const float w = __fsub_rn(__fmul_rn(d1, static_cast<float>((q >> (8 * i)) & 0xffu)), m1);
+                a = fmaf(w, xs[i], a);
+            }
+        }
+        return a;
+    }
+};
+
+template <int FMT, int LK, int UPL, int RL>
+__global__ __launch_bounds__(WG) void gemv_fast_kernel(const uint8_t* __restrict__ W,
+                                                         const float* __restrict__ x,
+                                                         float* __restrict__ y,
+                                                         const float* __restrict__ residual,
+                                                         int rows)
+{
+    constexpr int RS = 64 / LK;                   // row slots per wave
+    constexpr int ROWS_PER_WAVE = RS * RL;
+    constexpr int ROWS_PER_WG = ROWS_PER_WAVE * (WG / 64);
+    constexpr int UPR = LK * UPL;                 // units per row
+    constexpr int K = UPR * 64;
+    constexpr int64_t ROW_BYTES = static_cast<int64_t>(UPR) * QUnit<FMT>::UNIT_BYTES;
+
+    __shared__ float4 xs4[UPR * XS_UNIT / 4];
+    __shared__ float bs[UPR * 2];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lk = lane % LK;
+    const int lr = lane / LK;
+    const int row0 = blockIdx.x * ROWS_PER_WG + wave * ROWS_PER_WAVE + lr * RL;
+
+    // 1. issue every weight load of this lane
+    QUnit<FMT> w[UPL][RL];
+#pragma unroll
+    for (int t = 0; t < RL; t++) {
+        const int r = min(row0 + t, rows - 1);
+        const uint8_t* rp = W + static_cast<int64_t>(r) * ROW_BYTES;
+#pragma unroll
+        for (int i = 0; i < UPL; i++)
+            w[i][t].load(rp, lk + i * LK);
+    }
+
+    // 2. stage x into LDS (padded per unit) with per-32-column sums; all of
+    //    this thread's x loads are issued before the first LDS write
+    constexpr int XPT = K / 4 / WG;   // float4 of x per thread (K is a multiple of 1024)
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4 xr[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; j++)
+        xr[j] = x4[threadIdx.x + j * WG];
+#pragma unroll
+    for (int j = 0; j < XPT; j++) {
+        const int col = 4 * (threadIdx.x + j * WG);
+        xs4[(col >> 6) * (XS_UNIT / 4) + ((col & 63) >> 2)] = xr[j];
+    }
+    constexpr bool SUMS = FMT == FMT_Q4_K;   // the factored Q4_K form needs sum(x) per 32 columns
+    int any_wide = 0;
+    if constexpr (SUMS) {
+        bool wide = false;
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            const int i = threadIdx.x + j * WG;
+            // NaN fails every comparison, so it counts as wide too
+            wide |= !(fabsf(xr[j].x) <= 0x1p100f && fabsf(xr[j].y) <= 0x1p100f &&
+                      fabsf(xr[j].z) <= 0x1p100f && fabsf(xr[j].w) <= 0x1p100f);
+            float sum = (xr[j].x + xr[j].y) + (xr[j].z + xr[j].w);
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            sum += __shfl_xor(sum, 4);
+            if ((i & 7) == 0)
+                bs[i >> 3] = sum;
+        }
+        any_wide = __syncthreads_or(wide);
+    } else {
+        __syncthreads();
+    }
+
+    // 3. per-unit dot products, x read once per unit and reused for RL rows
+    float acc[RL];
+#pragma unroll
+    for (int t = 0; t < RL; t++)
+        acc[t] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = lk + i * LK;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float4 xv[8];
+            const float4* src = xs4 + u * (XS_UNIT / 4) + h * 8;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                xv[k] = src[k];
+            if constexpr (SUMS) {
+                const float sx = bs[2 * u + h];
+                if (any_wide) {
+                    for (int t = 0; t < RL; t++)
+                        acc[t] += w[i][t].half_exact(h, xv);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < RL; t++)
+                        acc[t] += w[i][t].half(h, xv, sx);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < RL; t++)
+                    acc[t] += w[i][t].half(h, xv, 0.0f);
+            }
+        }
+    }
+
+    // 4. reduce across the LK lanes of a row slot and store
+#pragma unroll
+    for (int t = 0; t < RL; t++) {
+#pragma unroll
+        for (int off = LK / 2; off > 0; off >>= 1)
+            acc[t] += __shfl_xor(acc[t], off);
+    }
+    if (lk == 0) {
+#pragma unroll
+        for (int t = 0; t < RL; t++) {
+            const int r = row0 + t;
+            if (r < rows)
+                y[r] = residual ? acc[t] + residual[r] : acc[t];
+        }
+    }
+}
+
+// ---- generic path: any whole number of blocks per row ------------------
+
+__device__ __forceinline__ float ld_half(const uint8_t* p)
+{
+    const unsigned short h = static_cast<unsigned short>(p[0] | (p[1] << 8));
+    return __half2float(__ushort_as_half(h));
+}
+
+template <int FMT>
+__device__ float block_dot(const uint8_t* b, const float* x);
+
+template <>
+__device__ float block_dot<FMT_Q8_0>(const uint8_t* b, const float* x)
+{
+    float a = 0.0f;
+    for (int i = 0; i < 32; i++)
+        a = fmaf(static_cast<float>(static_cast<int8_t>(b[2 + i])), x[i], a);
+    return ld_half(b) * a;
+}
+
+template <>
+__device__ float block_dot<FMT_Q4_0>(const uint8_t* b, const float* x)
+{
+    float a = 0.0f;
+    for (int i = 0; i < 16; i++) {
+        a = fmaf(static_cast<float>((b[2 + i] & 15) - 8), x[i], a);
+        a = fmaf(static_cast<float>((b[2 + i] >> 4) - 8), x[i + 16], a);
+    }
+    return ld_half(b) * a;
+}
+
+template <>
+__device__ float block_dot<FMT_Q4_K>(const uint8_t* b, const float* x)
+{
+    const float d = ld_half(b), dmin = ld_half(b + 2);
+    const uint8_t* s = b + 4;
+    const uint8_t* q = b + 16;
+    float a = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        if (j < 4) {
+            sc = s[j] & 63;
+            m = s[j + 4] & 63;
+        } else {
+            sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+            m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float d1 = __fmul_rn(d, static_cast<float>(sc));
+        const float m1 = __fmul_rn(dmin, static_cast<float>(m));
+        const uint8_t* qc = q + 32 * (j >> 1);
+        const int shift = 4 * (j & 1);
+        for (int l = 0; l < 32; l++) {
+            const float w = __fsub_rn(__fmul_rn(d1, static_cast<float>((qc[l] >> shift) & 15)), m1);
+            a = fmaf(w, x[32 * j + l], a);
+        }
+    }
+    return a;
+}
+
+// One wave per row, lanes stride over blocks, byte loads (no alignment needs).
+template <int FMT>
+__global__ __launch_bounds__(WG) void gemv_generic_kernel(const uint8_t* __restrict__ W,
+                                                            const float* __restrict__ x,
+                                                            float* __restrict__ y,
+                                                            const float* __restrict__ residual,
+                                                            int rows, int blocks_per_row)
+{
+    const int row = blockIdx.x * (WG / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows)
+        return;   // whole wave leaves together; no barrier follows
+    const uint8_t* rp = W + static_cast<int64_t>(row) * blocks_per_row * block_bytes(FMT);
+    float acc = 0.0f;
+    for (int b = lane; b < blocks_per_row; b += 64)
+        acc += block_dot<FMT>(rp + static_cast<int64_t>(b) * block_bytes(FMT), x + static_cast<int64_t>(b) * block_elems(FMT));
+    for (int off = 32; off > 0; off >>= 1)
+        acc += __shfl_xor(acc, off);
+    if (lane == 0)
+        y[row] = residual ? acc + residual[row] : acc;
+}
+
+// ---- block decoder (bit-exact dequantisation) ----------------------------
+
+template <int FMT>
+__global__ __launch_bounds__(WG) void dequant_kernel(const uint8_t* __restrict__ W, float* __restrict__ out,
+                                                       int64_t nblocks)
+{
+    const int64_t blk = static_cast<int64_t>(blockIdx.x) * WG + threadIdx.x;
+    if (blk >= nblocks)
+        return;
+    const uint8_t* b = W + blk * block_bytes(FMT);
+    float* o = out + blk * block_elems(FMT);
+    if constexpr (FMT == FMT_Q8_0) {
+        const float d = ld_half(b);
+        for (int i = 0; i < 32; i++)
+            o[i] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(b[2 + i])));
+    } else if constexpr (FMT == FMT_Q4_0) {
+        const float d = ld_half(b);
+        for (int i = 0; i < 16; i++) {
+            o[i] = __fmul_rn(d, static_cast<float>((b[2 + i] & 15) - 8));
+            o[i + 16] = __fmul_rn(d, static_cast<float>((b[2 + i] >> 4) - 8));
+        }
+    } else {
+        const float d = ld_half(b), dmin = ld_half(b + 2);
+        const uint8_t* s = b + 4;
+        const uint8_t* q = b + 16;
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            if (j < 4) {
+                sc = s[j] & 63;
+                m = s[j + 4] & 63;
+            } else {
+                sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+                m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+            }
+            const float d1 = __fmul_rn(d, static_cast<float>(sc));
+            const float m1 = __fmul_rn(dmin, static_cast<float>(m));
+            const uint8_t* qc = q + 32 * (j >> 1);
+            const int shift = 4 * (j & 1);
+            for (int l = 0; l < 32; l++)
+                o[32 * j + l] = __fsub_rn(__fmul_rn(d1, static_cast<float>((qc[l] >> shift) & 15)), m1);
+        }
+    }
+}
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, uint64_t count)
+{
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * WG + threadIdx.x;
+    if (i < count)
+        dst[i] = value;
+}
+
+// ---- dispatch --------------------------------------------------------------
+
+using FastFn = void (*)(const uint8_t*, const float*, float*, const float*, int);
+
+template <int FMT, int LK, int UPL, int RL>
+constexpr int rows_per_wg() { return (64 / LK) * RL * (WG / 64); }
+
+template <int FMT, int LK, int UPL>
+hipError_t launch_fast_rl(const uint8_t* w, const float* x, float* y, const float* res, int rows,
+                          hipStream_t s)
+{
+    // Two rows per lane once the grid would still give every CU several
+    // waves; one row per lane keeps small matrices spread over all CUs.
+    const int rows_per_wave_rl1 = 64 / LK;
+    const int64_t waves_rl1 = (rows + rows_per_wave_rl1 - 1) / rows_per_wave_rl1;
+    if (waves_rl1 >= 8192) {
+        constexpr int R = rows_per_wg<FMT, LK, UPL, 2>();
+        hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, 2>), dim3((rows + R - 1) / R), dim3(WG), 0, s,
+                           w, x, y, res, rows);
+    } else {
+        constexpr int R = rows_per_wg<FMT, LK, UPL, 1>();
+        hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, 1>), dim3((rows + R - 1) / R), dim3(WG), 0, s,
+                           w, x, y, res, rows);
+    }
+    return hipGetLastError();
+}
+
+template <int FMT>
+bool launch_fast(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows, int64_t cols,
+                 hipStream_t s, hipError_t* err)
+{
+    switch (cols) {
+    case 1024: *err = launch_fast_rl<FMT, 16, 1>(w, x, y, res, static_cast<int>(rows), s); return true;
+    case 2048: *err = launch_fast_rl<FMT, 16, 2>(w, x, y, res, static_cast<int>(rows), s); return true;
+    case 3072: *err = launch_fast_rl<FMT, 16, 3>(w, x, y, res, static_cast<int>(rows), s); return true;
+    case 4096: *err = launch_fast_rl<FMT, 16, 4>(w, x, y, res, static_cast<int>(rows), s); return true;
+    case 6144: *err = launch_fast_rl<FMT, 32, 3>(w, x, y, res, static_cast<int>(rows), s); return true;
+    case 8192: *err = launch_fast_rl<FMT, 64, 2>(w, x, y, res, static_cast<int>(rows), s); return true;
+    default: return false;
+    }
+}
+
+template <int FMT>
+hipError_t launch_generic(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows,
+                          int64_t cols, hipStream_t s)
+{
+    const int rows_per_wg = WG / 64;
+    hipLaunchKernelGGL((gemv_generic_kernel<FMT>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(WG), 0, s,
+                       w, x, y, res, static_cast<int>(rows), static_cast<int>(cols / block_elems(FMT)));
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_gemv_fmt(const void* wv, const float* x, float* y, int64_t rows, int64_t cols,
+                           const GemvEpilogue& epi, hipStream_t s, int* path)
+{
+    const uint8_t* w = static_cast<const uint8_t*>(wv);
+    const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    hipError_t err = hipSuccess;
+    if (aligned && launch_fast<FMT>(w, x, y, epi.residual, rows, cols, s, &err)) {
+        if (path) *path = PATH_FAST;
+        return err;
+    }
+    if (path) *path = PATH_GENERIC;
+    return launch_generic<FMT>(w, x, y, epi.residual, rows, cols, s);
+}
+
+}  // namespace
+
+hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
+                       const GemvEpilogue& epi, hipStream_t stream, int* path)
+{
+    switch (fmt) {
+    case FMT_Q8_0: return launch_gemv_fmt<FMT_Q8_0>(w, x, y, rows, cols, epi, stream, path);
+    case FMT_Q4_0: return launch_gemv_fmt<FMT_Q4_0>(w, x, y, rows, cols, epi, stream, path);
+    case FMT_Q4_K: return launch_gemv_fmt<FMT_Q4_K>(w, x, y, rows, cols, epi, stream, path);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dequant(int fmt, const void* wv, float* out, int64_t rows, int64_t cols, hipStream_t s)
+{
+    const uint8_t* w = static_cast<const uint8_t*>(wv);
+    const int be = block_elems(fmt);
+    if (be == 0)
+        return hipErrorInvalidValue;
+    const int64_t nblocks = rows * (cols / be);
+    const dim3 grid(static_cast<unsigned>((nblocks + WG - 1) / WG));
+    switch (fmt) {
+    case FMT_Q8_0: hipLaunchKernelGGL((dequant_kernel<FMT_Q8_0>), grid, dim3(WG), 0, s, w, out, nblocks); break;
+    case FMT_Q4_0: hipLaunchKernelGGL((dequant_kernel<FMT_Q4_0>), grid, dim3(WG), 0, s, w, out, nblocks); break;
+    case FMT_Q4_K: hipLaunchKernelGGL((dequant_kernel<FMT_Q4_K>), grid, dim3(WG), 0, s, w, out, nblocks); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(void* dst, uint32_t value, uint64_t count, hipStream_t s)
+{
+    if (count == 0)
+        return hipSuccess;
+    const dim3 grid(static_cast<unsigned>((count + WG - 1) / WG));
+    hipLaunchKernelGGL(fill_u32_kernel, grid, dim3(WG), 0, s, static_cast<uint32_t*>(dst), value, count);
+    return hipGetLastError();
+}
+
+}  // namespace si

@@ -1,0 +1,261 @@
+"""ctypes binding of libsharpinference_hip (include/sharpinference_hip.h).
+
+This is the Python face of the same C ABI the managed SharpInference host
+would P/Invoke.  It never substitutes another implementation: if the HIP
+library is missing or a call fails, it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libsharpinference_hip.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+
+# GGUF tensor type ids (GgufModelFile.cs:24-46)
+F32, F16, Q4_0, Q8_0, Q4_K, BF16 = 0, 1, 2, 8, 12, 30
+FORMAT_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", BF16: "bf16"}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+
+OK, ERR_ARGUMENT, ERR_UNSUPPORTED, ERR_ADAPTATION, ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_STATE = range(7)
+PATH_FAST, PATH_GENERIC = 1, 2
+
+# Every symbol include/sharpinference_hip.h declares, with its ctypes signature.
+_vp, _i32, _i64, _u32, _u64, _dbl = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32,
+                                     ctypes.c_uint64, ctypes.c_double)
+SIGNATURES = {
+    "si_hip_abi_version": ([], _i32),
+    "si_hip_device_count": ([ctypes.POINTER(_i32)], _i32),
+    "si_hip_init": ([_i32, ctypes.POINTER(_vp)], _i32),
+    "si_hip_destroy": ([_vp], _i32),
+    "si_hip_last_error": ([_vp], ctypes.c_char_p),
+    "si_hip_tensor_bytes": ([_i32, _i64, _i64, ctypes.POINTER(_u64)], _i32),
+    "si_hip_alloc": ([_vp, _u64, ctypes.POINTER(_vp)], _i32),
+    "si_hip_free": ([_vp, _vp], _i32),
+    "si_hip_upload": ([_vp, _vp, _vp, _u64], _i32),
+    "si_hip_readback": ([_vp, _vp, _vp, _u64], _i32),
+    "si_hip_copy": ([_vp, _vp, _vp, _u64], _i32),
+    "si_hip_fill_u32": ([_vp, _vp, _u32, _u64], _i32),
+    "si_hip_sync": ([_vp], _i32),
+    "si_hip_gemv": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_i32)], _i32),
+    "si_hip_dequant": ([_vp, _i32, _vp, _vp, _i64, _i64], _i32),
+    "si_hip_plan_begin": ([_vp], _i32),
+    "si_hip_plan_end": ([_vp, ctypes.POINTER(_vp)], _i32),
+    "si_hip_plan_destroy": ([_vp], _i32),
+    "si_hip_plan_launch": ([_vp], _i32),
+    "si_hip_plan_launch_sequence": ([ctypes.POINTER(_vp), _i32, _i64], _i32),
+    "si_hip_plan_measure_us": ([_vp, _i32, ctypes.POINTER(_dbl)], _i32),
+    "si_hip_timer_begin": ([_vp], _i32),
+    "si_hip_timer_end": ([_vp, ctypes.POINTER(_dbl)], _i32),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class HipError(RuntimeError):
+    """A failed C-ABI call; `status` is the si_hip_status code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[si_hip status {status}] {message}")
+        self.status = status
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the in-tree HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m sharpinference_amd.build` "
+                "(there is no fallback implementation)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = handle
+    return _lib
+
+
+def _check(rc: int, ctx=None) -> None:
+    if rc != OK:
+        msg = lib().si_hip_last_error(ctx)
+        raise HipError(rc, msg.decode() if msg else "")
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(lib().si_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def tensor_bytes(fmt: int, rows: int, cols: int) -> int:
+    out = ctypes.c_uint64(0)
+    _check(lib().si_hip_tensor_bytes(fmt, rows, cols, ctypes.byref(out)))
+    return out.value
+
+
+class DeviceBuffer:
+    """A device allocation owned by a HipContext."""
+
+    def __init__(self, ctx: "HipContext", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        ptr = ctypes.c_void_p()
+        ctx._call(lib().si_hip_alloc, ctypes.c_uint64(self.nbytes), ctypes.byref(ptr))
+        self.ptr = ptr.value
+
+    def upload(self, host: np.ndarray, offset: int = 0) -> None:
+        host = np.ascontiguousarray(host)
+        if offset < 0 or offset + host.nbytes > self.nbytes:
+            raise ValueError("upload exceeds the buffer")
+        self.ctx._call(lib().si_hip_upload, ctypes.c_void_p(self.ptr + offset), host.ctypes.data,
+                       ctypes.c_uint64(host.nbytes))
+
+    def readback(self, dtype=np.uint8, count: Optional[int] = None, offset: int = 0) -> np.ndarray:
+        itemsize = np.dtype(dtype).itemsize
+        if count is None:
+            count = (self.nbytes - offset) // itemsize
+        out = np.empty(count, dtype=dtype)
+        if offset < 0 or offset + out.nbytes > self.nbytes:
+            raise ValueError("readback exceeds the buffer")
+        self.ctx._call(lib().si_hip_readback, out.ctypes.data, ctypes.c_void_p(self.ptr + offset),
+                       ctypes.c_uint64(out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx._call(lib().si_hip_free, ctypes.c_void_p(self.ptr))
+            self.ptr = None
+
+    def __int__(self) -> int:
+        return int(self.ptr)
+
+
+class Plan:
+    """A recorded entry (HIP graph) replayed on its context's stream."""
+
+    def __init__(self, ctx: "HipContext", handle: int):
+        self.ctx = ctx
+        self.handle = handle
+
+    def launch(self) -> None:
+        self.ctx._call_plain(lib().si_hip_plan_launch(ctypes.c_void_p(self.handle)))
+
+    def measure_us(self, repetitions: int = 8) -> float:
+        us = ctypes.c_double(0.0)
+        self.ctx._call_plain(lib().si_hip_plan_measure_us(ctypes.c_void_p(self.handle), repetitions,
+                                                          ctypes.byref(us)))
+        return us.value
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().si_hip_plan_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+
+class HipContext:
+    """One device, one stream; mirrors how a HIP executor uses the shim."""
+
+    def __init__(self, device: int = 0):
+        handle = ctypes.c_void_p()
+        _check(lib().si_hip_init(device, ctypes.byref(handle)))
+        self.handle = handle
+        self.device = device
+
+    # -- plumbing ----------------------------------------------------------
+    def _call(self, fn, *args) -> None:
+        _check(fn(self.handle, *args), self.handle)
+
+    def _call_plain(self, rc: int) -> None:
+        _check(rc, self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().si_hip_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- memory ------------------------------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, host: np.ndarray) -> DeviceBuffer:
+        host = np.ascontiguousarray(host)
+        buf = DeviceBuffer(self, max(host.nbytes, 4))
+        buf.upload(host)
+        return buf
+
+    def copy(self, dst: int, src: int, nbytes: int) -> None:
+        self._call(lib().si_hip_copy, ctypes.c_void_p(int(dst)), ctypes.c_void_p(int(src)), ctypes.c_uint64(nbytes))
+
+    def fill_u32(self, dst: int, value: int, count: int) -> None:
+        self._call(lib().si_hip_fill_u32, ctypes.c_void_p(int(dst)), ctypes.c_uint32(value), ctypes.c_uint64(count))
+
+    def sync(self) -> None:
+        self._call(lib().si_hip_sync)
+
+    # -- hot path ------------------------------------------------------------
+    def gemv(self, fmt: int, w: int, x: int, y: int, rows: int, cols: int, residual: int = 0) -> int:
+        """y = W.x (+ residual); returns which kernel path ran (1 fast, 2 generic)."""
+        path = ctypes.c_int(0)
+        self._call(lib().si_hip_gemv, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(x)),
+                   ctypes.c_void_p(int(y)), rows, cols, ctypes.c_void_p(int(residual) or None), ctypes.byref(path))
+        return path.value
+
+    def dequant(self, fmt: int, w: int, out: int, rows: int, cols: int) -> None:
+        self._call(lib().si_hip_dequant, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(out)), rows, cols)
+
+    # -- plans and timing ----------------------------------------------------
+    def plan_begin(self) -> None:
+        self._call(lib().si_hip_plan_begin)
+
+    def plan_end(self) -> Plan:
+        handle = ctypes.c_void_p()
+        self._call(lib().si_hip_plan_end, ctypes.byref(handle))
+        return Plan(self, handle.value)
+
+    def record(self, body) -> Plan:
+        """Records everything `body()` launches into a plan."""
+        self.plan_begin()
+        try:
+            body()
+        except BaseException:
+            try:
+                self.plan_end().destroy()
+            except HipError:
+                pass
+            raise
+        return self.plan_end()
+
+    def launch_sequence(self, plans: Sequence[Plan], steps: int) -> None:
+        arr = (ctypes.c_void_p * len(plans))(*[p.handle for p in plans])
+        self._call_plain(lib().si_hip_plan_launch_sequence(arr, len(plans), steps))
+
+    def timer_begin(self) -> None:
+        self._call(lib().si_hip_timer_begin)
+
+    def timer_end(self) -> float:
+        ms = ctypes.c_double(0.0)
+        self._call(lib().si_hip_timer_end, ctypes.byref(ms))
+        return ms.value
+
+
+def exported_symbols(path: str = LIB_PATH) -> Iterable[str]:
+    """Names the shared library exports (dynamic symbol table), without loading it."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    for line in out.splitlines():
+        parts = line.split()
+        if len(parts) >= 3 and parts[1] in ("T", "W"):
+            yield parts[2]
