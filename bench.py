@@ -70,6 +70,9 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 640 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="before timing, copy this many MiB device-to-device once (a plain copy of "
+                         "known size that scales the HBM byte counters of a profiler run)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -127,6 +130,16 @@ def main() -> int:
                 hip.gemv(fmt, dev_w[c][k].ptr, xs[cols].ptr, ys[name].ptr, rows, cols)
         shape_plans[name] = hip.record(body)
 
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * 2 ** 20
+        src, dst = hip.alloc(n), hip.alloc(n)
+        hip.fill_u32(src.ptr, 0x3F800000, n // 4)
+        hip.copy(dst.ptr, src.ptr, n)
+        hip.sync()
+        src.free()
+        dst.free()
+        log(f"calibration copy of {args.copy_calibration_mib} MiB done")
+
     log(f"warmup {args.warmup} steps")
     hip.launch_sequence(plans, max(args.warmup, 1))
     hip.sync()
@@ -152,7 +165,15 @@ def main() -> int:
                          "GBs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         log(f"  {name:8s} {rows}x{cols}: {us:.3f} us/launch, {b / us / 1e3:.1f} GB/s")
 
-    # parity spot check of the last step's outputs against the CPU restatement
+    # dispatch floor: the same graph mechanism with 64 one-wave fill kernels
+    scratch = hip.alloc(4096)
+    floor_plan = hip.record(lambda: [hip.fill_u32(scratch.ptr, 0, 64) for _ in range(64)])
+    floor_plan.measure_us(2)
+    floor_us = sorted(floor_plan.measure_us(8) for _ in range(5))[2] / 64
+    floor_plan.destroy()
+    scratch.free()
+    log(f"dispatch floor: {floor_us:.3f} us per dependent launch")
+
     result = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -176,13 +197,14 @@ def main() -> int:
         },
         "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
         "kernels": kernels,
+        "dispatch_floor_us": round(floor_us, 3),
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": committed_traffic(args.config),
             "kernel": "gemv_fast_kernel (Q4_0), launch-averaged over the step's 4 GEMVs",
         },
     }
@@ -195,6 +217,20 @@ def main() -> int:
     hip.close()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def committed_traffic(config: str):
+    """HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE counter
+    runs recorded in profiles/ for this workload (None when absent)."""
+    path = os.path.join(ROOT, "profiles", {"layer_q4_0": "gemv_q4_0_layer_set.md"}.get(config, "-"))
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(fmt, shapes, host_w, xs, ys, hip, bytes_per_step, budget_s):

@@ -64,6 +64,25 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v)
     return v;
 }
 
+// Sum of v over aligned groups of N lanes (N = 2, 4, 8, 16), left in every
+// lane of the group, with DPP lane moves (no LDS traffic):
+// xor-1 and xor-2 swaps inside quads, then the mirror of each 8- and
+// 16-lane row, which pairs every lane with one in the other half.
+template <int N>
+__device__ __forceinline__ float group_sum(float v)
+{
+    if constexpr (N >= 2)
+        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    if constexpr (N >= 4)
+        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    if constexpr (N >= 8)
+        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    if constexpr (N >= 16)
+        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    static_assert(N <= 16, "groups wider than a DPP row use shuffles");
+    return v;
+}
+
 // 4 unsigned bytes (each < 256) of q times 4 floats, accumulated.
 __device__ __forceinline__ float dot4_u8(uint32_t q, const float4& x, float a)
 {
@@ -112,11 +131,10 @@ struct QUnit<FMT_Q8_0> {
 
 // Two Q4_0 blocks {fp16 d; u8 q[16]}: element j < 16 is the low nibble of
 // q[j], element j + 16 the high nibble, value d * (nibble - 8).
-// (nibble ^ 8) is (nibble - 8) as a signed 4-bit number; moved into the top
-// half of a byte it reads as the signed byte 16 * (nibble - 8), which one
-// sign-extending conversion turns into a float.  The factor 16 is folded
-// into the scale (d / 16 is exact), so no per-block sum of x is needed and
-// every product keeps the sign and class of the dequantised weight.
+// Fast form: the low nibbles are masked in place (q & 0x0f..) and the high
+// ones too (q & 0xf0.., i.e. 16 * nibble), each byte converted by one
+// v_cvt_f32_ubyteN; the factor 16 and the offset 8 are applied once per
+// block: d * (a_lo + a_hi / 16 - 8 * sum(x)).
 template <>
 struct QUnit<FMT_Q4_0> {
     static constexpr int UNIT_BYTES = 36;
@@ -131,18 +149,37 @@ struct QUnit<FMT_Q4_0> {
         v[8] = ld1(p + 32);
     }
 
-    __device__ __forceinline__ float half(int h, const float4* x, float /*sx*/) const
+    __device__ __forceinline__ uint32_t qword(int h, int k) const
     {
-        float a0 = 0.0f, a1 = 0.0f;
+        return h == 0 ? __builtin_amdgcn_alignbit(v[k + 1], v[k], 16) : v[5 + k];
+    }
+    __device__ __forceinline__ float scale(int h) const { return h == 0 ? half_lo(v[0]) : half_hi(v[4]); }
+
+    __device__ __forceinline__ float half(int h, const float4* x, float sx) const
+    {
+        float a_lo = 0.0f, a_hi = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t q = h == 0 ? __builtin_amdgcn_alignbit(v[k + 1], v[k], 16) : v[5 + k];
-            const uint32_t t = q ^ 0x88888888u;
-            a0 = dot4_i8((t << 4) & 0xf0f0f0f0u, x[k], a0);
-            a1 = dot4_i8(t & 0xf0f0f0f0u, x[4 + k], a1);
+            const uint32_t q = qword(h, k);
+            a_lo = dot4_u8(opaque(q & 0x0f0f0f0fu), x[k], a_lo);
+            a_hi = dot4_u8(opaque(q & 0xf0f0f0f0u), x[4 + k], a_hi);
         }
-        const float d = h == 0 ? half_lo(v[0]) : half_hi(v[4]);
-        return (d * 0.0625f) * (a0 + a1);
+        return scale(h) * fmaf(-8.0f, sx, fmaf(a_hi, 0.0625f, a_lo));
+    }
+
+    // Classification-exact form for non-finite or huge x: (nibble ^ 8) is
+    // (nibble - 8) as a signed 4-bit number; moved to the top of a byte it
+    // reads as the signed byte 16 * (nibble - 8), so every product carries
+    // the sign and class of the dequantised weight (no sum(x) term).
+    __device__ float half_exact(int h, const float4* x) const
+    {
+        float a = 0.0f;
+        for (int k = 0; k < 4; k++) {
+            const uint32_t t = qword(h, k) ^ 0x88888888u;
+            a = dot4_i8((t << 4) & 0xf0f0f0f0u, x[k], a);
+            a = dot4_i8(t & 0xf0f0f0f0u, x[4 + k], a);
+        }
+        return (scale(h) * 0.0625f) * a;
     }
 };
 
@@ -179,19 +216,20 @@ struct QUnit<FMT_Q4_K> {
         m = static_cast<int>(low ? (s1 & 63u) : ((s2 >> 4) | ((s1 >> 6) << 4)));
     }
 
+    // The high nibbles are masked in place (16 * q per byte); 1/16 goes
+    // into the sub-block scale, which stays exact (a power of two).
     __device__ __forceinline__ float half(int h, const float4* x, float sx) const
     {
+        const uint32_t mask = h == 0 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k += 2) {
-            const uint32_t q0 = h == 0 ? (qs[k] & 0x0f0f0f0fu) : ((qs[k] >> 4) & 0x0f0f0f0fu);
-            const uint32_t q1 = h == 0 ? (qs[k + 1] & 0x0f0f0f0fu) : ((qs[k + 1] >> 4) & 0x0f0f0f0fu);
-            a0 = dot4_u8(opaque(q0), x[k], a0);
-            a1 = dot4_u8(opaque(q1), x[k + 1], a1);
+            a0 = dot4_u8(opaque(qs[k] & mask), x[k], a0);
+            a1 = dot4_u8(opaque(qs[k + 1] & mask), x[k + 1], a1);
         }
         int sc, m;
         scale_min(2 * chunk + h, sc, m);
-        const float d1 = half_lo(hd[0]) * static_cast<float>(sc);
+        const float d1 = half_lo(hd[0]) * static_cast<float>(sc) * (h == 0 ? 1.0f : 0.0625f);
         const float m1 = half_hi(hd[0]) * static_cast<float>(m);
         return fmaf(d1, a0 + a1, -(m1 * sx));
     }
@@ -219,28 +257,45 @@ struct QUnit<FMT_Q4_K> {
     }
 };
 
-template <int FMT, int LK, int UPL, int RL>
-__global__ __launch_bounds__(WG) void gemv_fast_kernel(const uint8_t* __restrict__ W,
-                                                         const float* __restrict__ x,
-                                                         float* __restrict__ y,
-                                                         const float* __restrict__ residual,
-                                                         int rows)
+// Tiled kernel.  A workgroup of NW waves covers a group of rows; its waves
+// split the row's units into KS consecutive K slices (wave w takes slice
+// w % KS of row group w / KS).  Inside a wave, RS = 64 / LK row slots of LK
+// lanes; lane k of a slot takes units k, k + LK, ... (UPL of them) of its
+// slice for RL consecutive rows.  Partial sums are reduced across the LK
+// lanes with shuffles and across the KS slices through LDS in a fixed
+// order, so results do not depend on timing.
+template <int FMT, int LK, int UPL, int RL, int KS, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __restrict__ W,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y,
+                                                              const float* __restrict__ residual,
+                                                              int rows)
 {
+    static_assert(NW % KS == 0, "waves must cover whole row groups");
+    constexpr int THREADS = 64 * NW;
     constexpr int RS = 64 / LK;                   // row slots per wave
-    constexpr int ROWS_PER_WAVE = RS * RL;
-    constexpr int ROWS_PER_WG = ROWS_PER_WAVE * (WG / 64);
-    constexpr int UPR = LK * UPL;                 // units per row
+    constexpr int ROWS_PER_GROUP = RS * RL;
+    constexpr int GROUPS = NW / KS;
+    constexpr int ROWS_PER_WG = ROWS_PER_GROUP * GROUPS;
+    constexpr int UPS = LK * UPL;                 // units per slice
+    constexpr int UPR = UPS * KS;                 // units per row
     constexpr int K = UPR * 64;
     constexpr int64_t ROW_BYTES = static_cast<int64_t>(UPR) * QUnit<FMT>::UNIT_BYTES;
+    static_assert((K / 4) % THREADS == 0, "x staging assumes whole float4 rounds");
 
     __shared__ float4 xs4[UPR * XS_UNIT / 4];
     __shared__ float bs[UPR * 2];
+    __shared__ float part[KS > 1 ? ROWS_PER_WG * KS : 1];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int slice = wave % KS;
+    const int group = wave / KS;
     const int lk = lane % LK;
     const int lr = lane / LK;
-    const int row0 = blockIdx.x * ROWS_PER_WG + wave * ROWS_PER_WAVE + lr * RL;
+    const int local_row0 = group * ROWS_PER_GROUP + lr * RL;
+    const int row0 = blockIdx.x * ROWS_PER_WG + local_row0;
+    const int unit0 = slice * UPS + lk;
 
     // 1. issue every weight load of this lane
     QUnit<FMT> w[UPL][RL];
@@ -250,36 +305,33 @@ __global__ __launch_bounds__(WG) void gemv_fast_kernel(const uint8_t* __restrict
         const uint8_t* rp = W + static_cast<int64_t>(r) * ROW_BYTES;
 #pragma unroll
         for (int i = 0; i < UPL; i++)
-            w[i][t].load(rp, lk + i * LK);
+            w[i][t].load(rp, unit0 + i * LK);
     }
 
-    // 2. stage x into LDS (padded per unit) with per-32-column sums; all of
-    //    this thread's x loads are issued before the first LDS write
-    constexpr int XPT = K / 4 / WG;   // float4 of x per thread (K is a multiple of 1024)
+    // 2. stage x into LDS (padded per unit); all of this thread's x loads
+    //    are issued before the first LDS write
+    constexpr int XPT = K / 4 / THREADS;
     const float4* x4 = reinterpret_cast<const float4*>(x);
     float4 xr[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; j++)
-        xr[j] = x4[threadIdx.x + j * WG];
+        xr[j] = x4[threadIdx.x + j * THREADS];
 #pragma unroll
     for (int j = 0; j < XPT; j++) {
-        const int col = 4 * (threadIdx.x + j * WG);
+        const int col = 4 * (threadIdx.x + j * THREADS);
         xs4[(col >> 6) * (XS_UNIT / 4) + ((col & 63) >> 2)] = xr[j];
     }
-    constexpr bool SUMS = FMT == FMT_Q4_K;   // the factored Q4_K form needs sum(x) per 32 columns
+    constexpr bool SUMS = FMT != FMT_Q8_0;   // the factored Q4 forms need sum(x) per 32 columns
     int any_wide = 0;
     if constexpr (SUMS) {
         bool wide = false;
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
-            const int i = threadIdx.x + j * WG;
+            const int i = threadIdx.x + j * THREADS;
             // NaN fails every comparison, so it counts as wide too
             wide |= !(fabsf(xr[j].x) <= 0x1p100f && fabsf(xr[j].y) <= 0x1p100f &&
                       fabsf(xr[j].z) <= 0x1p100f && fabsf(xr[j].w) <= 0x1p100f);
-            float sum = (xr[j].x + xr[j].y) + (xr[j].z + xr[j].w);
-            sum += __shfl_xor(sum, 1);
-            sum += __shfl_xor(sum, 2);
-            sum += __shfl_xor(sum, 4);
+            const float sum = group_sum<8>((xr[j].x + xr[j].y) + (xr[j].z + xr[j].w));
             if ((i & 7) == 0)
                 bs[i >> 3] = sum;
         }
@@ -295,7 +347,7 @@ __global__ __launch_bounds__(WG) void gemv_fast_kernel(const uint8_t* __restrict
         acc[t] = 0.0f;
 #pragma unroll
     for (int i = 0; i < UPL; i++) {
-        const int u = lk + i * LK;
+        const int u = unit0 + i * LK;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             float4 xv[8];
@@ -321,19 +373,41 @@ __global__ __launch_bounds__(WG) void gemv_fast_kernel(const uint8_t* __restrict
         }
     }
 
-    // 4. reduce across the LK lanes of a row slot and store
+    // 4. reduce across the LK lanes of a row slot, then across K slices
 #pragma unroll
     for (int t = 0; t < RL; t++) {
+        if constexpr (LK <= 16) {
+            acc[t] = group_sum<LK>(acc[t]);
+        } else {
 #pragma unroll
-        for (int off = LK / 2; off > 0; off >>= 1)
-            acc[t] += __shfl_xor(acc[t], off);
+            for (int off = LK / 2; off > 0; off >>= 1)
+                acc[t] += __shfl_xor(acc[t], off);
+        }
     }
-    if (lk == 0) {
+    if constexpr (KS == 1) {
+        if (lk == 0) {
 #pragma unroll
-        for (int t = 0; t < RL; t++) {
-            const int r = row0 + t;
+            for (int t = 0; t < RL; t++) {
+                const int r = row0 + t;
+                if (r < rows)
+                    y[r] = residual ? acc[t] + residual[r] : acc[t];
+            }
+        }
+    } else {
+        if (lk == 0) {
+#pragma unroll
+            for (int t = 0; t < RL; t++)
+                part[(local_row0 + t) * KS + slice] = acc[t];
+        }
+        __syncthreads();
+        if (threadIdx.x < ROWS_PER_WG) {
+            const int r = blockIdx.x * ROWS_PER_WG + threadIdx.x;
+            float v = part[threadIdx.x * KS];
+#pragma unroll
+            for (int s2 = 1; s2 < KS; s2++)
+                v += part[threadIdx.x * KS + s2];
             if (r < rows)
-                y[r] = residual ? acc[t] + residual[r] : acc[t];
+                y[r] = residual ? v + residual[r] : v;
         }
     }
 }
@@ -472,42 +546,42 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, uint
 
 // ---- dispatch --------------------------------------------------------------
 
-using FastFn = void (*)(const uint8_t*, const float*, float*, const float*, int);
-
-template <int FMT, int LK, int UPL, int RL>
-constexpr int rows_per_wg() { return (64 / LK) * RL * (WG / 64); }
-
-template <int FMT, int LK, int UPL>
-hipError_t launch_fast_rl(const uint8_t* w, const float* x, float* y, const float* res, int rows,
-                          hipStream_t s)
+template <int FMT, int LK, int UPL, int RL, int KS, int NW>
+hipError_t launch_tiled(const uint8_t* w, const float* x, float* y, const float* res, int rows, hipStream_t s)
 {
-    // Two rows per lane once the grid would still give every CU several
-    // waves; one row per lane keeps small matrices spread over all CUs.
-    const int rows_per_wave_rl1 = 64 / LK;
-    const int64_t waves_rl1 = (rows + rows_per_wave_rl1 - 1) / rows_per_wave_rl1;
-    if (waves_rl1 >= 8192) {
-        constexpr int R = rows_per_wg<FMT, LK, UPL, 2>();
-        hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, 2>), dim3((rows + R - 1) / R), dim3(WG), 0, s,
-                           w, x, y, res, rows);
-    } else {
-        constexpr int R = rows_per_wg<FMT, LK, UPL, 1>();
-        hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, 1>), dim3((rows + R - 1) / R), dim3(WG), 0, s,
-                           w, x, y, res, rows);
-    }
+    constexpr int R = (64 / LK) * RL * (NW / KS);
+    hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW>), dim3((rows + R - 1) / R), dim3(64 * NW), 0, s,
+                       w, x, y, res, rows);
     return hipGetLastError();
 }
 
+// Shape table of the tiled kernel, from measurements on MI355X (rotating
+// weight copies larger than the Infinity Cache).  Matrices with few rows
+// are latency bound: the K slices spread each row over KS waves so every
+// lane handles one 64-column unit and the grid covers all CUs.  Tall
+// matrices are throughput bound: one wave per row group (KS = 1) with
+// several units and rows per lane amortises the x staging and the
+// reductions over more weights.
 template <int FMT>
-bool launch_fast(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows, int64_t cols,
+bool launch_fast(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows64, int64_t cols,
                  hipStream_t s, hipError_t* err)
 {
+    const int rows = static_cast<int>(rows64);
+    const bool mid = rows64 >= 12288, tall = rows64 >= 49152;
     switch (cols) {
-    case 1024: *err = launch_fast_rl<FMT, 16, 1>(w, x, y, res, static_cast<int>(rows), s); return true;
-    case 2048: *err = launch_fast_rl<FMT, 16, 2>(w, x, y, res, static_cast<int>(rows), s); return true;
-    case 3072: *err = launch_fast_rl<FMT, 16, 3>(w, x, y, res, static_cast<int>(rows), s); return true;
-    case 4096: *err = launch_fast_rl<FMT, 16, 4>(w, x, y, res, static_cast<int>(rows), s); return true;
-    case 6144: *err = launch_fast_rl<FMT, 32, 3>(w, x, y, res, static_cast<int>(rows), s); return true;
-    case 8192: *err = launch_fast_rl<FMT, 64, 2>(w, x, y, res, static_cast<int>(rows), s); return true;
+    case 1024: *err = mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(w, x, y, res, rows, s)
+                          : launch_tiled<FMT, 16, 1, 1, 1, 4>(w, x, y, res, rows, s); return true;
+    case 2048: *err = mid ? launch_tiled<FMT, 16, 2, 2, 1, 4>(w, x, y, res, rows, s)
+                          : launch_tiled<FMT, 16, 1, 1, 2, 4>(w, x, y, res, rows, s); return true;
+    case 3072: *err = tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(w, x, y, res, rows, s)
+                    : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(w, x, y, res, rows, s)
+                           : launch_tiled<FMT, 16, 1, 1, 3, 3>(w, x, y, res, rows, s); return true;
+    case 4096: *err = mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(w, x, y, res, rows, s)
+                          : launch_tiled<FMT, 16, 1, 1, 4, 4>(w, x, y, res, rows, s); return true;
+    case 6144: *err = mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(w, x, y, res, rows, s)
+                          : launch_tiled<FMT, 16, 1, 1, 6, 6>(w, x, y, res, rows, s); return true;
+    case 8192: *err = mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(w, x, y, res, rows, s)
+                          : launch_tiled<FMT, 16, 1, 1, 8, 8>(w, x, y, res, rows, s); return true;
     default: return false;
     }
 }

@@ -49,10 +49,15 @@ def run_gemv(hip, fmt, w_host, x_host, rows, cols, residual=None, w_offset=0):
 
 # ---- seeded data at the workload shapes --------------------------------------------
 
+# Every entry of the tiled kernel's shape table is covered: small, mid
+# (>= 12288 rows) and tall (>= 49152 rows) variants for each column count.
 SHAPES = {
-    native.Q8_0: [(3072, 3072), (2048, 2048), (8192, 2048), (2048, 8192), (4099, 3072), (1, 3072), (7, 8192)],
-    native.Q4_0: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (4099, 3072), (1, 4096), (33, 6144)],
-    native.Q4_K: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (4099, 1024), (1, 2048), (33, 6144)],
+    native.Q8_0: [(3072, 3072), (2048, 2048), (8192, 2048), (2048, 8192), (4099, 3072), (1, 3072), (7, 8192),
+                  (65536, 2048), (12288, 4096), (50000, 3072)],
+    native.Q4_0: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (4099, 3072), (1, 4096), (33, 6144),
+                  (16384, 8192), (12289, 6144), (49153, 3072)],
+    native.Q4_K: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (4099, 1024), (1, 2048), (33, 6144),
+                  (12288, 8192), (12300, 1024), (49160, 3072)],
 }
 CASES = [(f, r, c) for f in FORMATS for (r, c) in SHAPES[f]]
 
