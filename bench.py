@@ -70,6 +70,7 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0: enough for 640 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill (MFMA) measurement")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before timing, copy this many MiB device-to-device once (a plain copy of "
                          "known size that scales the HBM byte counters of a profiler run)")
@@ -165,6 +166,8 @@ def main() -> int:
                          "GBs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         log(f"  {name:8s} {rows}x{cols}: {us:.3f} us/launch, {b / us / 1e3:.1f} GB/s")
 
+    prefill = None if args.no_prefill else bench_prefill(hip, rng)
+
     # dispatch floor: the same graph mechanism with 64 one-wave fill kernels
     scratch = hip.alloc(4096)
     floor_plan = hip.record(lambda: [hip.fill_u32(scratch.ptr, 0, 64) for _ in range(64)])
@@ -198,6 +201,7 @@ def main() -> int:
         "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
         "kernels": kernels,
         "dispatch_floor_us": round(floor_us, 3),
+        "prefill": prefill,
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 1),
@@ -217,6 +221,36 @@ def main() -> int:
     hip.close()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def bench_prefill(hip, rng, m: int = 512):
+    """Batched prefill product at the same layer shapes: M = 512 tokens of
+    bf16 activations against the Q4_0 projections (MFMA), FP32 out."""
+    from sharpinference_amd import native
+    MFMA_BF16_PEAK_TFLOPS = 2500.0
+    out = {"tokens": m, "shapes": {}}
+    total_flops, total_us = 0.0, 0.0
+    for name, rows, cols in LAYER_Q4_0:
+        w = hip.to_device(synth_weights(native.Q4_0, rows, cols, rng))
+        xb = rng.standard_normal(m * cols).astype(np.float32).view(np.uint32)
+        xb = ((xb + 0x7FFF + ((xb >> 16) & 1)) >> 16).astype(np.uint16)
+        x = hip.to_device(xb)
+        y = hip.alloc(m * rows * 4)
+        plan = hip.record(lambda: hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols))
+        plan.measure_us(2)
+        us = sorted(plan.measure_us(8) for _ in range(5))[2]
+        flops = 2.0 * m * rows * cols
+        total_flops += flops
+        total_us += us
+        out["shapes"][name] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1)}
+        log(f"  prefill {name:8s} m={m} {rows}x{cols}: {us:.1f} us, {flops / us / 1e6:.1f} TFLOP/s")
+        plan.destroy()
+        for b in (w, x, y):
+            b.free()
+    tflops = total_flops / total_us / 1e6
+    out.update({"us_total": round(total_us, 1), "TFLOPs": round(tflops, 1),
+                "mfma_bf16_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+    return out
 
 
 def committed_traffic(config: str):

@@ -122,6 +122,17 @@ int si_hip_sync(si_hip_context* ctx);
 int si_hip_gemv(si_hip_context* ctx, int format, const void* w, const float* x, float* y,
                 int64_t rows, int64_t cols, const float* residual, int* path);
 
+/* Batched prefill product Y[m, rows] = X[m, cols] . W[rows, cols]^T: m token
+ * rows of bf16 activations (16-byte aligned) against a block-quantized W,
+ * FP32 output (one row of `rows` values per token), FP32 accumulation on
+ * MFMA; W is decoded exactly and rounded to bf16 for the matrix cores.
+ * Replaces: the transpose_right matrix multiply of the CpuVm path
+ * (CpuInstructionNumerics.MatrixMultiply, CpuInstructionNumerics.cs:66-77)
+ * and the batched prefill matvec of the D3D12 transformer program
+ * (GpuBatchTransformerInstructions.cs:224-279). */
+int si_hip_gemm_prefill(si_hip_context* ctx, int format, const void* w, const void* x_bf16, float* y,
+                        int64_t m, int64_t rows, int64_t cols);
+
 /* out[rows, cols] = exact FP32 values of the blocks of W.  Test and
  * inspection entry point for the block decoder used by the products.
  * Replaces: the FP16 -> FP32 row conversion step of the CPU matvec

@@ -27,6 +27,7 @@ ARCH = os.environ.get("SI_HIP_ARCH", "gfx950")
 SOURCES = [
     "si_abi.cpp",
     "si_gemv.hip",
+    "si_prefill.hip",
 ]
 
 

@@ -136,8 +136,8 @@ int si_hip_init(int device, si_hip_context** out)
     if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&ctx->t0)) != hipSuccess || (e = hipEventCreate(&ctx->t1)) != hipSuccess) {
         hip_fail(nullptr, e, "init");
-        if (ctx->t0) hipEventDestroy(ctx->t0);
-        if (ctx->stream) hipStreamDestroy(ctx->stream);
+        if (ctx->t0) (void)hipEventDestroy(ctx->t0);
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return SI_HIP_ERR_DEVICE;
     }
@@ -153,7 +153,7 @@ int si_hip_destroy(si_hip_context* ctx)
         Enter g(ctx);
         if (ctx->recording) {
             hipGraph_t graph = nullptr;
-            hipStreamEndCapture(ctx->stream, &graph);
+            (void)hipStreamEndCapture(ctx->stream, &graph);
             if (graph) (void)hipGraphDestroy(graph);
         }
         (void)hipStreamSynchronize(ctx->stream);
@@ -320,6 +320,31 @@ int si_hip_gemv(si_hip_context* ctx, int format, const void* w, const float* x, 
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv: output overlaps an input");
     const hipError_t e = si::launch_gemv(format, w, x, y, rows, cols, si::GemvEpilogue{residual}, ctx->stream, path);
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemv launch");
+}
+
+int si_hip_gemm_prefill(si_hip_context* ctx, int format, const void* w, const void* x_bf16, float* y, int64_t m,
+                        int64_t rows, int64_t cols)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "gemm_prefill: null context");
+    Enter g(ctx);
+    if (g.err != hipSuccess)
+        return hip_fail(ctx, g.err, "hipSetDevice");
+    uint64_t wbytes = 0;
+    if (const int rc = check_matrix(ctx, "gemm_prefill", format, w, rows, cols, &wbytes))
+        return rc;
+    if (m <= 0 || m > INT32_MAX)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: token count %lld out of range", static_cast<long long>(m));
+    if (!x_bf16 || !y)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: null input or output");
+    if ((reinterpret_cast<uintptr_t>(x_bf16) & 15u) || (reinterpret_cast<uintptr_t>(y) & 3u))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: X must be 16-byte aligned and Y 4-byte aligned");
+    const uint64_t ybytes = static_cast<uint64_t>(m) * static_cast<uint64_t>(rows) * 4;
+    const uint64_t xbytes = static_cast<uint64_t>(m) * static_cast<uint64_t>(cols) * 2;
+    if (overlaps(y, ybytes, w, wbytes) || overlaps(y, ybytes, x_bf16, xbytes))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: output overlaps an input");
+    const hipError_t e = si::launch_prefill(format, w, x_bf16, y, m, rows, cols, ctx->stream);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemm_prefill launch");
 }
 
 int si_hip_dequant(si_hip_context* ctx, int format, const void* w, float* out, int64_t rows, int64_t cols)

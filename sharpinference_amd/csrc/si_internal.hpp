@@ -46,6 +46,8 @@ enum GemvPath : int { PATH_FAST = 1, PATH_GENERIC = 2 };
 
 hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
                        const GemvEpilogue& epi, hipStream_t stream, int* path);
+hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, int64_t m, int64_t rows,
+                          int64_t cols, hipStream_t stream);
 hipError_t launch_dequant(int fmt, const void* w, float* out, int64_t rows, int64_t cols,
                           hipStream_t stream);
 hipError_t launch_fill_u32(void* dst, uint32_t value, uint64_t count, hipStream_t stream);

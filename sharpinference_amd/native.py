@@ -44,6 +44,7 @@ SIGNATURES = {
     "si_hip_sync": ([_vp], _i32),
     "si_hip_gemv": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_i32)], _i32),
     "si_hip_dequant": ([_vp, _i32, _vp, _vp, _i64, _i64], _i32),
+    "si_hip_gemm_prefill": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64], _i32),
     "si_hip_plan_begin": ([_vp], _i32),
     "si_hip_plan_end": ([_vp, ctypes.POINTER(_vp)], _i32),
     "si_hip_plan_destroy": ([_vp], _i32),
@@ -212,6 +213,11 @@ class HipContext:
         self._call(lib().si_hip_gemv, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(x)),
                    ctypes.c_void_p(int(y)), rows, cols, ctypes.c_void_p(int(residual) or None), ctypes.byref(path))
         return path.value
+
+    def gemm_prefill(self, fmt: int, w: int, x_bf16: int, y: int, m: int, rows: int, cols: int) -> None:
+        """Y[m, rows] = X[m, cols] . W^T with bf16 X, FP32 Y (MFMA)."""
+        self._call(lib().si_hip_gemm_prefill, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(x_bf16)),
+                   ctypes.c_void_p(int(y)), m, rows, cols)
 
     def dequant(self, fmt: int, w: int, out: int, rows: int, cols: int) -> None:
         self._call(lib().si_hip_dequant, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(out)), rows, cols)

@@ -1,0 +1,101 @@
+"""GPU parity of the batched prefill product Y = X . W^T (MFMA), through the C ABI.
+
+Gates: the BASELINE prefill tolerance, 2e-2 relative against the oracle's
+fp64 product over the exactly dequantised weights,
+|y - t| <= 2e-2 * max(|t|, rms(t)) elementwise and ||y - t|| / ||t|| <= 2e-2,
+and, to pin the matrix-core data layout itself, 1e-5 L2-relative against the
+fp64 product of the very operands the matrix cores see (bf16 X and the
+dequantised weights rounded to bf16).
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from sharpinference_amd import native
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [native.Q8_0, native.Q4_0, native.Q4_K]
+NAMES = {native.Q8_0: "q8_0", native.Q4_0: "q4_0", native.Q4_K: "q4_k"}
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 (round to nearest even) -> float32, numpy only."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return (u.astype(np.uint32) << 16).view(np.float32)
+
+
+def run_prefill(hip, fmt, w, x_bf16, m, rows, cols):
+    dw = hip.to_device(w)
+    dx = hip.to_device(x_bf16)
+    dy = hip.alloc(m * rows * 4)
+    hip.gemm_prefill(fmt, dw.ptr, dx.ptr, dy.ptr, m, rows, cols)
+    y = dy.readback(np.float32, m * rows).reshape(m, rows)
+    for b in (dw, dx, dy):
+        b.free()
+    return y
+
+
+def check(y, truth, tol, what):
+    y = np.asarray(y, np.float64)
+    truth = np.asarray(truth, np.float64)
+    guard = np.sqrt(np.mean(truth ** 2))
+    err = np.abs(y - truth)
+    assert np.all(err <= tol * np.maximum(np.abs(truth), guard)), what
+    l2 = np.linalg.norm(y - truth) / np.linalg.norm(truth)
+    assert l2 <= tol, f"{what}: L2-relative {l2:.3e}"
+
+
+SMALL = [(1, 32, 256), (7, 64, 256), (256, 96, 512), (300, 100, 768), (513, 33, 1024)]
+CASES = [(f, m, n, k) for f in FORMATS for (m, n, k) in SMALL]
+
+
+@pytest.mark.parametrize("fmt,m,rows,cols", CASES, ids=[f"{NAMES[f]}-m{m}-{n}x{k}" for f, m, n, k in CASES])
+def test_prefill_matches_oracle(hip, fmt, m, rows, cols):
+    w = orc.gen_quant(fmt, 50 + rows, rows, cols)
+    x = orc.gen_normal_bf16(60 + m, m * cols)
+    y = run_prefill(hip, fmt, w, x, m, rows, cols)
+    check(y, orc.gemm_prefill_f64(fmt, w, x, m, rows, cols), 2e-2, "vs fp64 oracle")
+    check(y, orc.gemm_prefill_cpuvm(fmt, w, x, m, rows, cols), 2e-2, "vs CpuVm order")
+    # the exact product of the matrix-core operands
+    wb = bf16_round(orc.dequant(fmt, w, rows, cols)).astype(np.float64)
+    xb = orc.bf16_to_f32(x).reshape(m, cols).astype(np.float64)
+    check(y, xb @ wb.T, 1e-5, "vs bf16-operand product")
+
+
+CONFIG4 = [("qkv", 5120, 3072), ("o_proj", 3072, 3072), ("gate_up", 16384, 3072), ("down", 3072, 8192)]
+
+
+@pytest.mark.parametrize("name,rows,cols", CONFIG4, ids=[c[0] for c in CONFIG4])
+def test_prefill_512_tokens_at_layer_shapes(hip, name, rows, cols):
+    """M = 512 tokens x the Phi-4-mini projections, Q4_0 weights, bf16 X; the
+    oracle checks a sample of 24 token rows spread over all 512."""
+    m = 512
+    w = orc.gen_quant(native.Q4_0, 7 + rows, rows, cols)
+    x = orc.gen_normal_bf16(8 + cols, m * cols)
+    y = run_prefill(hip, native.Q4_0, w, x, m, rows, cols)
+    sample = np.linspace(0, m - 1, 24).astype(int)
+    xs = np.ascontiguousarray(x.reshape(m, cols)[sample])
+    truth = orc.gemm_prefill_f64(native.Q4_0, w, xs, len(sample), rows, cols)
+    check(y[sample], truth, 2e-2, name)
+    wb = bf16_round(orc.dequant(native.Q4_0, w, rows, cols)).astype(np.float64)
+    check(y[sample], orc.bf16_to_f32(xs).astype(np.float64) @ wb.T, 1e-5, name + " bf16 operands")
+
+
+def test_prefill_rejects_bad_requests(hip):
+    w = hip.alloc(1 << 16)
+    x = hip.alloc(1 << 16)
+    y = hip.alloc(1 << 16)
+    for args, status in [
+        ((native.F16, w.ptr, x.ptr, y.ptr, 4, 32, 32), native.ERR_UNSUPPORTED),
+        ((native.Q4_0, w.ptr, x.ptr, y.ptr, 0, 32, 32), native.ERR_ARGUMENT),
+        ((native.Q4_0, w.ptr, x.ptr + 8, y.ptr, 4, 32, 32), native.ERR_ARGUMENT),   # X not 16-byte aligned
+        ((native.Q4_K, w.ptr, x.ptr, y.ptr, 4, 32, 128), native.ERR_ARGUMENT),      # partial super-block
+        ((native.Q4_0, w.ptr, x.ptr, x.ptr, 4, 32, 32), native.ERR_ARGUMENT),       # Y overlaps X
+    ]:
+        with pytest.raises(native.HipError) as e:
+            hip.gemm_prefill(*args)
+        assert e.value.status == status
+    for b in (w, x, y):
+        b.free()
