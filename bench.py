@@ -71,6 +71,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill (MFMA) measurement")
+    ap.add_argument("--no-decode", action="store_true", help="skip the Phi-4-mini decode-step measurement")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before timing, copy this many MiB device-to-device once (a plain copy of "
                          "known size that scales the HBM byte counters of a profiler run)")
@@ -167,6 +168,7 @@ def main() -> int:
         log(f"  {name:8s} {rows}x{cols}: {us:.3f} us/launch, {b / us / 1e3:.1f} GB/s")
 
     prefill = None if args.no_prefill else bench_prefill(hip, rng)
+    decode = None if args.no_decode else bench_decode(hip)
 
     # dispatch floor: the same graph mechanism with 64 one-wave fill kernels
     scratch = hip.alloc(4096)
@@ -202,6 +204,7 @@ def main() -> int:
         "kernels": kernels,
         "dispatch_floor_us": round(floor_us, 3),
         "prefill": prefill,
+        "decode": decode,
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 1),
@@ -251,6 +254,45 @@ def bench_prefill(hip, rng, m: int = 512):
     out.update({"us_total": round(total_us, 1), "TFLOPs": round(tflops, 1),
                 "mfma_bf16_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
     return out
+
+
+def bench_decode(hip, context: int = 2048, tokens: int = 64):
+    """Phi-4-mini-shaped decode step (32 layers, Q4_K layers, Q8_0 embedding
+    and head, fp16 KV cache holding `context` tokens), one new token per
+    step.  Steady state: the recorded step replayed back to back at position
+    `context`; loop: forward_token (control upload, replay, next-token
+    readback) over `tokens` consecutive positions."""
+    from sharpinference_amd import phi4
+    cfg = phi4.Phi4Config()
+    t0 = time.time()
+    weights = phi4.synth_weights(cfg, seed=7, distinct_layers=4)
+    sess = phi4.Phi4DecodeSession(hip, cfg, weights)
+    kv = phi4.synth_kv(phi4.Phi4Config(layers=1, capacity=cfg.capacity), context, seed=8)[0]
+    for l in range(cfg.layers):
+        sess.load_kv(l, *kv)
+    del weights
+    log(f"decode: model on device in {time.time() - t0:.1f} s")
+    sess.set_control(1, context)
+    sess.plan.launch()
+    hip.sync()
+    us = sorted(sess.plan.measure_us(16) for _ in range(5))[2]
+    step_bytes = cfg.weight_bytes_per_token() + cfg.kv_bytes(context + 1)
+    gbs = step_bytes / us / 1e3
+    t0 = time.perf_counter()
+    tok = 1
+    for i in range(tokens):
+        tok = sess.forward_token(tok, context + i)
+    loop_s = (time.perf_counter() - t0) / tokens
+    sess.close()
+    log(f"decode: {us:.1f} us/token on device ({1e6 / us:.0f} tok/s, {gbs:.0f} GB/s), "
+        f"{loop_s * 1e6:.1f} us/token with host round trips")
+    return {"workload": "Phi-4-mini decode step, 32 layers, Q4_K layers, Q8_0 embedding/head 200064x3072, "
+                        f"fp16 KV cache with {context} tokens, batch 1",
+            "us_per_token": round(us, 1), "tok_s": round(1e6 / us, 1),
+            "bytes_per_token": step_bytes, "GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
+            "loop_us_per_token": round(loop_s * 1e6, 1), "loop_tok_s": round(1.0 / loop_s, 1),
+            "layer_weights": "4 distinct layers uploaded as 32 separate device copies"}
 
 
 def committed_traffic(config: str):

@@ -139,6 +139,111 @@ int si_hip_gemm_prefill(si_hip_context* ctx, int format, const void* w, const vo
  * (CpuHalfMatrixOperators.cs:34-36), for quantized blocks. */
 int si_hip_dequant(si_hip_context* ctx, int format, const void* w, float* out, int64_t rows, int64_t cols);
 
+/* ---- decode-step operators ------------------------------------------------------ */
+
+/* Transforms of x fused into the staging of a GEMV. */
+typedef enum si_hip_xform {
+    SI_HIP_X_PLAIN = 0,
+    SI_HIP_X_RMSNORM = 1,   /* x_i * (1 / sqrt(sum(x^2) / cols + eps)) * norm_weight_i   */
+    SI_HIP_X_SWIGLU = 2,    /* x = [gate | up] (2 * cols values): gate / (1 + exp(-gate)) * up */
+} si_hip_xform;
+
+/* si_hip_gemv with a transform of x applied on the fly (x itself is not
+ * modified).  Replaces the RMSNorm (Phi4TextModel.cs:107-128) and SwiGLU
+ * (Phi4TextModel.cs:84-89) steps that precede a projection, and the
+ * transformer.rms-norm / swiglu dispatches of the D3D12 decode program
+ * (Phi4D3D12TextSession.cs:870-912).  Transforms need cols in {1024, 2048,
+ * 3072, 4096, 6144, 8192}. */
+int si_hip_gemv_fused(si_hip_context* ctx, int format, const void* w, const float* x, float* y,
+                      int64_t rows, int64_t cols, const float* residual, int xform,
+                      const float* norm_weight, float eps, int* path);
+
+/* out[cols] = FP32 values of row *index of a block-quantized [rows, cols]
+ * table; an index outside 0..rows-1 yields NaN values (no out-of-bounds
+ * read).  `index` is a device int32.  Replaces: core.gather-row
+ * (GpuTierZeroInstruction.cs:397-405, CpuInstructionNumerics.cs:25-30) for a
+ * quantized embedding table. */
+int si_hip_gather_row(si_hip_context* ctx, int format, const void* table, int64_t rows, int64_t cols,
+                      const int32_t* index, float* out);
+
+/* Grouped-query attention of one new token over an fp16 KV cache. */
+typedef struct si_hip_attention {
+    const float* qkv;          /* [heads*128 q | kv_heads*128 k | kv_heads*128 v], before the rotary embedding */
+    const int32_t* position;   /* device scalar: the new token's index = its cache slot */
+    void* k_cache;             /* fp16 [kv_heads][capacity][128], 16-byte aligned */
+    void* v_cache;             /* fp16 [kv_heads][capacity][128], 16-byte aligned */
+    float* out;                /* [heads * 128] */
+    float* workspace;          /* si_hip_attention_workspace_bytes */
+    int heads;
+    int kv_heads;              /* heads / kv_heads in 1..4 */
+    int head_dim;              /* 128 */
+    int rotary_dim;            /* rotate-half over the first rotary_dim values of each head */
+    int capacity;              /* 1..16384 */
+    float rope_base;
+    float rope_scale;
+} si_hip_attention;
+
+int si_hip_attention_workspace_bytes(int heads, int capacity, uint64_t* bytes);
+
+/* Applies the rotary embedding to q and k at *position, rounds k and v to
+ * fp16 and appends them at slot *position, then attends over slots
+ * 0..*position: out_h = softmax(q_h . K^T / sqrt(128)) . V for every query
+ * head h with KV head h / (heads / kv_heads).  A position outside
+ * 0..capacity-1 writes nothing and yields NaN.  Replaces: ApplyRotary +
+ * Phi4KeyValueCache.Append + ComputeAttention (Phi4TextModel.cs:64-72,
+ * 212-273) and the rope-kv-write / grouped-query-attention dispatches
+ * (Phi4D3D12TextSession.cs:873-890). */
+int si_hip_attention_decode(si_hip_context* ctx, const si_hip_attention* args);
+
+int si_hip_argmax_workspace_bytes(uint64_t* bytes);
+
+/* *index = first index of the maximum of values[0..n).  Replaces:
+ * transformer.argmax (GpuTransformerInstructionCollection.cs:697-748). */
+int si_hip_argmax(si_hip_context* ctx, const float* values, int64_t n, void* workspace, int32_t* index);
+
+/* ---- Phi-4 decode step ------------------------------------------------------------ */
+
+typedef struct si_hip_phi4_layer {
+    const float* attn_norm;    /* FP32 [hidden] */
+    const void* qkv;           /* [hidden + 2*kv_heads*128, hidden] */
+    const void* o;             /* [hidden, hidden] */
+    const float* ffn_norm;     /* FP32 [hidden] */
+    const void* up;            /* [2*ffn, hidden]: gate rows then up rows */
+    const void* down;          /* [hidden, ffn] */
+    void* k_cache;             /* fp16 [kv_heads][capacity][128] */
+    void* v_cache;
+} si_hip_phi4_layer;
+
+typedef struct si_hip_phi4_model {
+    int layers, hidden, heads, kv_heads, head_dim, rotary_dim, ffn, vocab, capacity;
+    int weight_format;         /* layer projections (e.g. Q4_K) */
+    int embed_format;          /* embedding table (e.g. Q8_0) */
+    int head_format;           /* vocabulary projection (e.g. Q8_0) */
+    float rms_eps, rope_base, rope_scale;
+    const void* embed;         /* [vocab, hidden] */
+    const void* lm_head;       /* [vocab, hidden] */
+    const float* output_norm;  /* FP32 [hidden] */
+    const si_hip_phi4_layer* layer;   /* host array of `layers` entries */
+    int32_t* control;          /* device [token, position] */
+    float* hidden_state;       /* [hidden] */
+    float* qkv;                /* [hidden + 2*kv_heads*128] */
+    float* attn;               /* [hidden] */
+    float* gate_up;            /* [2*ffn] */
+    float* logits;             /* [vocab] */
+    void* workspace;           /* si_hip_phi4_workspace_bytes */
+    int32_t* next_token;       /* device int32: argmax of the logits */
+} si_hip_phi4_model;
+
+int si_hip_phi4_workspace_bytes(const si_hip_phi4_model* model, uint64_t* bytes);
+
+/* Launches one decode step for token control[0] at position control[1]:
+ * embedding, every layer (updating the KV caches at control[1]), logits and
+ * next_token.  Inside si_hip_plan_begin/end it records the whole step as
+ * one plan (replayed per token with si_hip_plan_launch).  Replaces: the
+ * Phi-4 decode program (Phi4D3D12TextSession.Build, Phi4D3D12TextSession.cs:
+ * 866-919) and Phi4TextSession.ForwardToken (Phi4TextModel.cs:329-344). */
+int si_hip_phi4_decode(si_hip_context* ctx, const si_hip_phi4_model* model);
+
 /* ---- recorded entries and timing -------------------------------------------- */
 
 /* Starts recording: until si_hip_plan_end, launches on `ctx` are recorded

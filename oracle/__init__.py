@@ -27,6 +27,19 @@ NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
 _lib = None
 
 
+class Phi4Model(ctypes.Structure):
+    """orc_phi4_model (oracle.h)."""
+    _vpp = ctypes.POINTER(ctypes.c_void_p)
+    _fields_ = [("layers", ctypes.c_int), ("hidden", ctypes.c_int), ("heads", ctypes.c_int),
+                ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("rotary_dim", ctypes.c_int),
+                ("ffn", ctypes.c_int), ("vocab", ctypes.c_int), ("capacity", ctypes.c_int),
+                ("weight_format", ctypes.c_int), ("embed_format", ctypes.c_int), ("head_format", ctypes.c_int),
+                ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("rope_scale", ctypes.c_float),
+                ("embed", ctypes.c_void_p), ("lm_head", ctypes.c_void_p), ("output_norm", ctypes.c_void_p),
+                ("attn_norm", _vpp), ("qkv", _vpp), ("o", _vpp), ("ffn_norm", _vpp), ("up", _vpp),
+                ("down", _vpp), ("k_cache", _vpp), ("v_cache", _vpp)]
+
+
 def build() -> None:
     """Compile liboracle.so from oracle.c (gcc, via the Makefile)."""
     subprocess.run(["make", "-s", "-C", HERE], check=True)
@@ -77,6 +90,17 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_gemm_prefill_cpuvm.restype = i32
     l.orc_gemm_prefill_f64.argtypes = [i32, vp, vp, vp, i64, i64, i64]
     l.orc_gemm_prefill_f64.restype = i32
+    fp = ctypes.POINTER(ctypes.c_float)
+    l.orc_rmsnorm.argtypes = [vp, vp, i32, ctypes.c_float, vp]
+    l.orc_rmsnorm.restype = None
+    l.orc_rope.argtypes = [vp, i32, i32, i32, i32, ctypes.c_float, ctypes.c_float]
+    l.orc_rope.restype = None
+    l.orc_attention.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    l.orc_attention.restype = None
+    l.orc_argmax.argtypes = [vp, i64]
+    l.orc_argmax.restype = i32
+    l.orc_phi4_decode_step.argtypes = [ctypes.POINTER(Phi4Model), i32, i32, vp, i32]
+    l.orc_phi4_decode_step.restype = i32
     l.orc_now_seconds.restype = dbl
     l.orc_max_threads.restype = i32
 
@@ -198,3 +222,64 @@ def f32_to_f16_bits(x: float) -> int:
 
 def f16_bits_to_f32(h: int) -> float:
     return float(lib().orc_half_to_float(int(h)))
+
+
+# ---- Phi-4 decode step ----------------------------------------------------------
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+    return out
+
+
+def rope(values: np.ndarray, heads: int, head_dim: int, rotary_dim: int, position: int, base: float,
+         scale: float) -> np.ndarray:
+    v = np.ascontiguousarray(values, np.float32).copy()
+    lib().orc_rope(_ptr(v), heads, head_dim, rotary_dim, position, base, scale)
+    return v
+
+
+def attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, heads: int, kv_heads: int, head_dim: int,
+              capacity: int, length: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k_cache, np.uint16)
+    v = np.ascontiguousarray(v_cache, np.uint16)
+    out = np.empty(heads * head_dim, np.float32)
+    lib().orc_attention(_ptr(q), _ptr(k), _ptr(v), heads, kv_heads, head_dim, capacity, length, _ptr(out))
+    return out
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return int(lib().orc_argmax(_ptr(v), v.size))
+
+
+class Phi4Oracle:
+    """The oracle's copy of one model: host weights (shared with the device
+    upload) and its own fp16 KV caches, stepped by orc_phi4_decode_step."""
+
+    def __init__(self, cfg, weights):
+        self.cfg = cfg
+        self.w = weights
+        L = cfg.layers
+        shape = (cfg.kv_heads, cfg.capacity, cfg.head_dim)
+        self.k = [np.zeros(shape, np.uint16) for _ in range(L)]
+        self.v = [np.zeros(shape, np.uint16) for _ in range(L)]
+        vpp = lambda arrs: (ctypes.c_void_p * L)(*[a.ctypes.data for a in arrs])
+        self._keep = [vpp(weights.attn_norm), vpp(weights.qkv), vpp(weights.o), vpp(weights.ffn_norm),
+                      vpp(weights.up), vpp(weights.down), vpp(self.k), vpp(self.v)]
+        cast = lambda a: ctypes.cast(a, ctypes.POINTER(ctypes.c_void_p))
+        self.model = Phi4Model(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.rotary_dim, cfg.ffn,
+                               cfg.vocab, cfg.capacity, cfg.weight_format, cfg.embed_format, cfg.head_format,
+                               cfg.rms_eps, cfg.rope_base, cfg.rope_scale, weights.embed.ctypes.data,
+                               weights.lm_head.ctypes.data, weights.output_norm.ctypes.data,
+                               *[cast(a) for a in self._keep])
+
+    def step(self, token: int, position: int, threads: int = 0):
+        logits = np.empty(self.cfg.vocab, np.float32)
+        nxt = lib().orc_phi4_decode_step(ctypes.byref(self.model), token, position, _ptr(logits), threads)
+        if nxt < 0:
+            raise ValueError("token or position out of range")
+        return nxt, logits

@@ -452,6 +452,130 @@ int orc_gemm_prefill_f64(int format, const uint8_t* w, const uint16_t* x_bf16, d
 }
 
 /* ------------------------------------------------------------------------ */
+/* Phi-4 decode step                                                          */
+/* ------------------------------------------------------------------------ */
+
+void orc_rmsnorm(const float* x, const float* w, int n, float eps, float* out)
+{
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++)
+        sum += x[i] * x[i];
+    float scale = 1.0f / sqrtf(sum / (float)n + eps);
+    for (int i = 0; i < n; i++)
+        out[i] = x[i] * scale * w[i];
+}
+
+void orc_rope(float* values, int heads, int head_dim, int rotary_dim, int position, float base, float scale)
+{
+    int half = rotary_dim / 2;
+    for (int h = 0; h < heads; h++) {
+        float* hv = values + (int64_t)h * head_dim;
+        for (int i = 0; i < half; i++) {
+            float frequency = 1.0f / powf(base, 2.0f * (float)i / (float)rotary_dim);
+            float angle = (float)position * frequency;
+            float c = cosf(angle) * scale;
+            float sn = sinf(angle) * scale;
+            float left = hv[i], right = hv[i + half];
+            hv[i] = left * c - right * sn;
+            hv[i + half] = right * c + left * sn;
+        }
+    }
+}
+
+void orc_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
+                   int head_dim, int capacity, int length, float* out)
+{
+    int group = heads / kv_heads;
+    float* scores = (float*)malloc((size_t)length * sizeof(float));
+    for (int i = 0; i < heads * head_dim; i++)
+        out[i] = 0.0f;
+    for (int h = 0; h < heads; h++) {
+        int g = h / group;
+        const uint16_t* kc = k_cache + (int64_t)g * capacity * head_dim;
+        const uint16_t* vc = v_cache + (int64_t)g * capacity * head_dim;
+        float maximum = -INFINITY;
+        for (int t = 0; t < length; t++) {
+            float score = 0.0f;
+            for (int d = 0; d < head_dim; d++)
+                score += q[h * head_dim + d] * orc_half_to_float(kc[(int64_t)t * head_dim + d]);
+            score /= sqrtf((float)head_dim);
+            scores[t] = score;
+            maximum = fmaxf(maximum, score);
+        }
+        float denominator = 0.0f;
+        for (int t = 0; t < length; t++) {
+            scores[t] = expf(scores[t] - maximum);
+            denominator += scores[t];
+        }
+        for (int t = 0; t < length; t++) {
+            float p = scores[t] / denominator;
+            for (int d = 0; d < head_dim; d++)
+                out[h * head_dim + d] += p * orc_half_to_float(vc[(int64_t)t * head_dim + d]);
+        }
+    }
+    free(scores);
+}
+
+int orc_argmax(const float* v, int64_t n)
+{
+    /* first index of the maximum; NaN never wins; all-NaN gives 0 */
+    int64_t best = -1;
+    float bv = -INFINITY;
+    for (int64_t i = 0; i < n; i++)
+        if (v[i] > bv || (v[i] == bv && best < 0)) {
+            bv = v[i];
+            best = i;
+        }
+    return best < 0 ? 0 : (int)best;
+}
+
+int orc_phi4_decode_step(const orc_phi4_model* m, int token, int position, float* logits, int threads)
+{
+    int H = m->hidden, D = m->head_dim, KVH = m->kv_heads;
+    int qkv_rows = H + 2 * KVH * D;
+    if (token < 0 || token >= m->vocab || position < 0 || position >= m->capacity)
+        return -1;
+    float* hidden = (float*)malloc((size_t)H * sizeof(float));
+    float* normed = (float*)malloc((size_t)H * sizeof(float));
+    float* qkv = (float*)malloc((size_t)qkv_rows * sizeof(float));
+    float* attn = (float*)malloc((size_t)H * sizeof(float));
+    float* proj = (float*)malloc((size_t)H * sizeof(float));
+    float* gate_up = (float*)malloc((size_t)2 * m->ffn * sizeof(float));
+    /* Embed (:44-53): the token's row of the embedding table */
+    orc_dequant_row(m->embed_format, m->embed + (int64_t)token * orc_row_bytes(m->embed_format, H), H, hidden);
+    for (int l = 0; l < m->layers; l++) {
+        orc_rmsnorm(hidden, m->attn_norm[l], H, m->rms_eps, normed);
+        orc_gemv_cpuvm(m->weight_format, m->qkv[l], normed, qkv, qkv_rows, H, threads);
+        orc_rope(qkv, m->heads, D, m->rotary_dim, position, m->rope_base, m->rope_scale);
+        orc_rope(qkv + H, KVH, D, m->rotary_dim, position, m->rope_base, m->rope_scale);
+        /* Phi4KeyValueCache.Append with fp16 storage */
+        for (int g = 0; g < KVH; g++)
+            for (int d = 0; d < D; d++) {
+                int64_t slot = ((int64_t)g * m->capacity + position) * D + d;
+                m->k_cache[l][slot] = orc_float_to_half(qkv[H + g * D + d]);
+                m->v_cache[l][slot] = orc_float_to_half(qkv[H + KVH * D + g * D + d]);
+            }
+        orc_attention(qkv, m->k_cache[l], m->v_cache[l], m->heads, KVH, D, m->capacity, position + 1, attn);
+        orc_gemv_cpuvm(m->weight_format, m->o[l], attn, proj, H, H, threads);
+        for (int i = 0; i < H; i++)
+            hidden[i] += proj[i];
+        orc_rmsnorm(hidden, m->ffn_norm[l], H, m->rms_eps, normed);
+        orc_gemv_cpuvm(m->weight_format, m->up[l], normed, gate_up, 2 * m->ffn, H, threads);
+        for (int i = 0; i < m->ffn; i++) {
+            float gate = gate_up[i];
+            gate_up[i] = gate / (1.0f + expf(-gate)) * gate_up[m->ffn + i];
+        }
+        orc_gemv_cpuvm(m->weight_format, m->down[l], gate_up, proj, H, m->ffn, threads);
+        for (int i = 0; i < H; i++)
+            hidden[i] += proj[i];
+    }
+    orc_rmsnorm(hidden, m->output_norm, H, m->rms_eps, normed);
+    orc_gemv_cpuvm(m->head_format, m->lm_head, normed, logits, m->vocab, H, threads);
+    free(hidden); free(normed); free(qkv); free(attn); free(proj); free(gate_up);
+    return orc_argmax(logits, m->vocab);
+}
+
+/* ------------------------------------------------------------------------ */
 
 double orc_now_seconds(void)
 {

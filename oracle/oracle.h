@@ -98,6 +98,41 @@ int orc_gemm_prefill_cpuvm(int format, const uint8_t* w, const uint16_t* x_bf16,
 int orc_gemm_prefill_f64(int format, const uint8_t* w, const uint16_t* x_bf16, double* y,
                          int64_t m, int64_t rows, int64_t cols);
 
+/* ---- Phi-4 decode step (Phi4TextModel.cs) ------------------------------- */
+/* RmsNorm (:107-128): sum of squares in order, scale = 1/sqrt(sum/n + eps),
+ * out = x * scale * w. */
+void orc_rmsnorm(const float* x, const float* w, int n, float eps, float* out);
+/* ApplyRotary (:212-229) over `heads` heads of head_dim values in place. */
+void orc_rope(float* values, int heads, int head_dim, int rotary_dim, int position, float base, float scale);
+/* ComputeAttention (:231-273) for one token over `length` cached rows of an
+ * fp16 cache laid out [kv_heads][capacity][head_dim]. */
+void orc_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
+                   int head_dim, int capacity, int length, float* out);
+/* First index of the maximum (transformer.argmax). */
+int orc_argmax(const float* v, int64_t n);
+
+typedef struct orc_phi4_model {
+    int layers, hidden, heads, kv_heads, head_dim, rotary_dim, ffn, vocab, capacity;
+    int weight_format, embed_format, head_format;
+    float rms_eps, rope_base, rope_scale;
+    const uint8_t* embed;
+    const uint8_t* lm_head;
+    const float* output_norm;
+    const float* const* attn_norm;   /* per layer */
+    const uint8_t* const* qkv;
+    const uint8_t* const* o;
+    const float* const* ffn_norm;
+    const uint8_t* const* up;
+    const uint8_t* const* down;
+    uint16_t* const* k_cache;        /* fp16 [kv_heads][capacity][head_dim] per layer */
+    uint16_t* const* v_cache;
+} orc_phi4_model;
+
+/* One decode step (Phi4TextSession.ForwardToken, :329-344 with ForwardLayer
+ * :59-93 and GetLogits :95-105, untied Q8_0 head): writes logits[vocab],
+ * appends this token's fp16 K/V at `position`, returns the argmax. */
+int orc_phi4_decode_step(const orc_phi4_model* m, int token, int position, float* logits, int threads);
+
 /* ---- timing helper for the CPU baseline -------------------------------- */
 double orc_now_seconds(void);
 int orc_max_threads(void);

@@ -26,8 +26,10 @@ ARCH = os.environ.get("SI_HIP_ARCH", "gfx950")
 
 SOURCES = [
     "si_abi.cpp",
+    "si_model.cpp",
     "si_gemv.hip",
     "si_prefill.hip",
+    "si_decode.hip",
 ]
 
 

@@ -1,35 +1,17 @@
 // C ABI of libsharpinference_hip (declared in include/sharpinference_hip.h):
 // contexts, device memory, the quantized matrix-vector entry points,
 // recorded plans (HIP graphs) and event timing.
-#include "sharpinference_hip.h"
-#include "si_internal.hpp"
+#include "si_context.hpp"
 
-#include <cstdarg>
-#include <cstdio>
-#include <mutex>
-#include <string>
 #include <vector>
 
-struct si_hip_context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    hipEvent_t t0 = nullptr;
-    hipEvent_t t1 = nullptr;
-    bool timer_open = false;
-    bool recording = false;
-    std::string error;
-    std::recursive_mutex gate;
-};
-
-struct si_hip_plan {
-    si_hip_context* ctx = nullptr;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-};
+namespace si_abi {
 
 namespace {
-
 thread_local std::string g_thread_error;
+}
+
+const char* thread_error() { return g_thread_error.c_str(); }
 
 int fail(si_hip_context* ctx, int code, const char* fmt, ...)
 {
@@ -48,19 +30,6 @@ int hip_fail(si_hip_context* ctx, hipError_t e, const char* what)
 {
     return fail(ctx, e == hipErrorOutOfMemory ? SI_HIP_ERR_OUT_OF_MEMORY : SI_HIP_ERR_DEVICE, "%s: %s (%d)",
                 what, hipGetErrorString(e), static_cast<int>(e));
-}
-
-// Locks the context and makes its device current on this thread.
-struct Enter {
-    std::unique_lock<std::recursive_mutex> lock;
-    hipError_t err;
-    explicit Enter(si_hip_context* ctx) : lock(ctx->gate), err(hipSetDevice(ctx->device)) {}
-};
-
-bool overlaps(const void* a, uint64_t an, const void* b, uint64_t bn)
-{
-    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
-    return an != 0 && bn != 0 && pa < pb + bn && pb < pa + an;
 }
 
 bool is_quant(int fmt) { return fmt == si::FMT_Q8_0 || fmt == si::FMT_Q4_0 || fmt == si::FMT_Q4_K; }
@@ -98,7 +67,9 @@ int check_matrix(si_hip_context* ctx, const char* op, int fmt, const void* w, in
     return SI_HIP_OK;
 }
 
-}  // namespace
+}  // namespace si_abi
+
+using namespace si_abi;
 
 extern "C" {
 
@@ -167,7 +138,7 @@ int si_hip_destroy(si_hip_context* ctx)
 
 const char* si_hip_last_error(const si_hip_context* ctx)
 {
-    return ctx ? ctx->error.c_str() : g_thread_error.c_str();
+    return ctx ? ctx->error.c_str() : si_abi::thread_error();
 }
 
 int si_hip_tensor_bytes(int format, int64_t rows, int64_t cols, uint64_t* bytes)

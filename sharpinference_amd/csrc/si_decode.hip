@@ -1,0 +1,459 @@
+// Decode-step operators around the quantized products: embedding row
+// gather, grouped-query attention over an fp16 KV cache with the rotary
+// embedding and the cache append fused in, and argmax.
+//
+// Semantics follow the Phi-4 text model of the reference
+// (SharpInference.Architectures.Phi4/Phi4TextModel.cs): Embed :44-53,
+// ApplyRotary :212-229 (rotate-half over the first `rotary_dim` values of
+// each head, cos/sin scaled by rope_scale), ComputeAttention :231-273
+// (scores q.k / sqrt(head_dim) over every cached token including the new
+// one, softmax, weighted sum of values), and the D3D12 program's argmax
+// (GpuTransformerInstructionCollection.cs:697-748: first index of the
+// maximum) and gather-row (GpuTierZeroInstruction.cs:397-405: an index
+// outside the table yields NaN).  The BASELINE decode step keeps K and V in
+// fp16: new rows are rounded to fp16 when appended and attention reads the
+// rounded values back.
+#include "si_internal.hpp"
+#include "si_decode.hpp"
+
+#include <hip/hip_fp16.h>
+
+namespace si {
+namespace {
+
+constexpr int HEAD_DIM = 128;
+constexpr int CHUNK = 64;          // cache positions per attention workgroup
+constexpr int ATT_THREADS = 256;
+constexpr int PART = HEAD_DIM + 2; // per head and chunk: max, sum, 128 weighted values
+
+__device__ __forceinline__ float ld_half_u(const uint8_t* p)
+{
+    const unsigned short h = static_cast<unsigned short>(p[0] | (p[1] << 8));
+    return __half2float(__ushort_as_half(h));
+}
+
+// ---- embedding gather -------------------------------------------------------
+
+template <int FMT>
+__global__ __launch_bounds__(256) void gather_row_kernel(const uint8_t* __restrict__ table, int rows, int cols,
+                                                         int64_t row_bytes, const int32_t* __restrict__ index,
+                                                         float* __restrict__ out)
+{
+    const int row = *index;
+    const bool valid = row >= 0 && row < rows;
+    const uint8_t* rp = table + static_cast<int64_t>(valid ? row : 0) * row_bytes;
+    constexpr int BE = block_elems(FMT), BB = block_bytes(FMT);
+    for (int c = blockIdx.x * 256 + threadIdx.x; c < cols; c += gridDim.x * 256) {
+        float v;
+        if (!valid) {
+            v = __int_as_float(0x7fc00000);
+        } else {
+            const uint8_t* b = rp + (c / BE) * BB;
+            const int e = c % BE;
+            if constexpr (FMT == FMT_Q8_0) {
+                v = __fmul_rn(ld_half_u(b), static_cast<float>(static_cast<int8_t>(b[2 + e])));
+            } else if constexpr (FMT == FMT_Q4_0) {
+                const int q = e < 16 ? (b[2 + e] & 15) : (b[2 + e - 16] >> 4);
+                v = __fmul_rn(ld_half_u(b), static_cast<float>(q - 8));
+            } else {
+                const int j = e / 32, l = e % 32;
+                const uint8_t* s = b + 4;
+                int sc, m;
+                if (j < 4) {
+                    sc = s[j] & 63;
+                    m = s[j + 4] & 63;
+                } else {
+                    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+                    m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+                }
+                const float d1 = __fmul_rn(ld_half_u(b), static_cast<float>(sc));
+                const float m1 = __fmul_rn(ld_half_u(b + 2), static_cast<float>(m));
+                const int q = (b[16 + 32 * (j >> 1) + l] >> (4 * (j & 1))) & 15;
+                v = __fsub_rn(__fmul_rn(d1, static_cast<float>(q)), m1);
+            }
+        }
+        out[c] = v;
+    }
+}
+
+// ---- attention ------------------------------------------------------------------
+
+// Rotary embedding of one head in place (values in LDS), position p:
+// pairs (i, i + R/2) for i < R/2, frequency 1 / base^(2i / R).
+__device__ __forceinline__ void rotate_pair(float* h, int i, int rotary, float pos, float base, float scale)
+{
+    const float freq = 1.0f / powf(base, 2.0f * static_cast<float>(i) / static_cast<float>(rotary));
+    const float angle = pos * freq;
+    const float c = cosf(angle) * scale, s = sinf(angle) * scale;
+    const float left = h[i], right = h[i + rotary / 2];
+    h[i] = left * c - right * s;
+    h[i + rotary / 2] = right * c + left * s;
+}
+
+__device__ __forceinline__ void unpack8(const uint4& r, float* f)
+{
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] & 0xffffu)));
+        f[2 * i + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] >> 16)));
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float row_sum(float v)
+{
+    // sum over aligned groups of N (<= 16) lanes with DPP
+    if constexpr (N >= 2) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    if constexpr (N >= 4) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    if constexpr (N >= 8) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+    if constexpr (N >= 16) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+
+// One workgroup = one KV head x one chunk of 64 cache positions.  Writes
+// per query head of the group: (max score, sum of exp, sum of exp * v).
+// Every K and V row of the chunk is requested (16-byte loads, one 8-value
+// slice per lane) before q is staged, so the cache reads overlap the setup.
+template <int GROUP>
+__global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(AttentionArgs a)
+{
+    const int g = blockIdx.x;                 // KV head
+    const int chunk = blockIdx.y;
+    const int P = *a.position;                // index of the new token
+    const int start = chunk * CHUNK;
+    if (P < 0 || P >= a.capacity || start > P)
+        return;                               // whole workgroup leaves together
+    const int count = min(CHUNK, P + 1 - start);
+    const int newp = P - start;               // the new token's slot in this chunk (< CHUNK when owned)
+    const bool owns_new = newp < CHUNK;
+    const int koff = a.heads * HEAD_DIM, voff = koff + a.kv_heads * HEAD_DIM;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int dg = t & 15;                    // 8-value slice of a head row
+
+    __half* kc = a.k_cache + static_cast<int64_t>(g) * a.capacity * HEAD_DIM;
+    __half* vc = a.v_cache + static_cast<int64_t>(g) * a.capacity * HEAD_DIM;
+
+    // 1. K rows for the scores (wave w: positions 16w..16w+15) and V rows
+    //    for the weighted sum (position slot t/16 + 16j)
+    uint4 kr[4], vr[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int pk = wave * 16 + (lane >> 4) + 4 * j;
+        const int pv = (t >> 4) + 16 * j;
+        kr[j] = (pk < count && pk != newp)
+                    ? *reinterpret_cast<const uint4*>(kc + static_cast<int64_t>(start + pk) * HEAD_DIM + 8 * dg)
+                    : make_uint4(0, 0, 0, 0);
+        vr[j] = (pv < count && pv != newp)
+                    ? *reinterpret_cast<const uint4*>(vc + static_cast<int64_t>(start + pv) * HEAD_DIM + 8 * dg)
+                    : make_uint4(0, 0, 0, 0);
+    }
+
+    __shared__ float q[GROUP][HEAD_DIM];
+    __shared__ float knew[HEAD_DIM];
+    __shared__ float vnew[HEAD_DIM];
+    __shared__ float prob[GROUP][CHUNK];
+    __shared__ float mx[GROUP];
+    __shared__ float lsum[GROUP];
+    __shared__ float red[4][GROUP][HEAD_DIM];
+
+    // 2. rotated queries of the group; the new row, rotated, rounded, appended
+    const float pos = static_cast<float>(P);
+    for (int i = t; i < GROUP * HEAD_DIM; i += ATT_THREADS)
+        q[i / HEAD_DIM][i % HEAD_DIM] = a.qkv[(g * GROUP + i / HEAD_DIM) * HEAD_DIM + i % HEAD_DIM];
+    if (owns_new && t < HEAD_DIM) {
+        knew[t] = a.qkv[koff + g * HEAD_DIM + t];
+        vnew[t] = a.qkv[voff + g * HEAD_DIM + t];
+    }
+    __syncthreads();
+    const int half_rot = a.rotary_dim / 2;
+    for (int i = t; i < GROUP * half_rot; i += ATT_THREADS)
+        rotate_pair(q[i / half_rot], i % half_rot, a.rotary_dim, pos, a.rope_base, a.rope_scale);
+    if (owns_new && t < half_rot)
+        rotate_pair(knew, t, a.rotary_dim, pos, a.rope_base, a.rope_scale);
+    __syncthreads();
+    if (owns_new && t < HEAD_DIM) {
+        const __half kh = __float2half_rn(knew[t]), vh = __float2half_rn(vnew[t]);
+        kc[static_cast<int64_t>(P) * HEAD_DIM + t] = kh;
+        vc[static_cast<int64_t>(P) * HEAD_DIM + t] = vh;
+        knew[t] = __half2float(kh);
+        vnew[t] = __half2float(vh);
+    }
+    __syncthreads();
+
+    // 3. scores: a 16-lane row holds one position's 128 values
+    float qv[GROUP][8];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            qv[h][e] = q[h][8 * dg + e];
+    const float inv_scale = sqrtf(static_cast<float>(HEAD_DIM));
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int p = wave * 16 + (lane >> 4) + 4 * j;
+        float k8[8];
+        if (p == newp) {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                k8[e] = knew[8 * dg + e];
+        } else {
+            unpack8(kr[j], k8);
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            float sdot = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                sdot = fmaf(qv[h][e], k8[e], sdot);
+            sdot = row_sum<16>(sdot);
+            if (dg == 0)
+                prob[h][p] = p < count ? sdot / inv_scale : -INFINITY;
+        }
+    }
+    __syncthreads();
+
+    // 4. per-head max and exponentials (wave h takes head h)
+    if (wave < GROUP) {
+        const float v = prob[wave][lane];
+        float m = v;
+        for (int off = 32; off > 0; off >>= 1)
+            m = fmaxf(m, __shfl_xor(m, off));
+        const float e = lane < count ? expf(v - m) : 0.0f;
+        float l = e;
+        for (int off = 32; off > 0; off >>= 1)
+            l += __shfl_xor(l, off);
+        prob[wave][lane] = e;
+        if (lane == 0) {
+            mx[wave] = m;
+            lsum[wave] = l;
+        }
+    }
+    __syncthreads();
+
+    // 5. weighted values: thread (slot t/16, slice t%16) over 4 positions,
+    //    then a sum over the 16 position slots
+    float acc[GROUP][8];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            acc[h][e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int p = (t >> 4) + 16 * j;
+        float v8[8];
+        if (p == newp) {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                v8[e] = vnew[8 * dg + e];
+        } else {
+            unpack8(vr[j], v8);
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            const float w = prob[h][p];
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                acc[h][e] = fmaf(w, v8[e], acc[h][e]);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = acc[h][e];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[h][e] = v;
+        }
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < GROUP; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                red[wave][h][8 * dg + e] = acc[h][e];
+    }
+    __syncthreads();
+    float* part_out = a.workspace;
+    for (int i = t; i < GROUP * HEAD_DIM; i += ATT_THREADS) {
+        const int h = i / HEAD_DIM, d = i % HEAD_DIM;
+        const float o = (red[0][h][d] + red[1][h][d]) + (red[2][h][d] + red[3][h][d]);
+        float* dst = part_out + (static_cast<int64_t>(g * GROUP + h) * a.max_chunks + chunk) * PART;
+        dst[2 + d] = o;
+        if (d == 0) {
+            dst[0] = mx[h];
+            dst[1] = lsum[h];
+        }
+    }
+}
+
+// One workgroup per query head: merge the chunk partials
+// (m_c, l_c, o_c) into softmax-weighted values.
+constexpr int MAX_CHUNKS = 256;
+
+__global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
+{
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int P = *a.position;
+    if (P < 0 || P >= a.capacity) {
+        if (t < HEAD_DIM)
+            a.out[h * HEAD_DIM + t] = __int_as_float(0x7fc00000);   // position outside the cache
+        return;
+    }
+    const int chunks = P / CHUNK + 1;
+    const float* src = a.workspace + static_cast<int64_t>(h) * a.max_chunks * PART;
+    __shared__ float wts[MAX_CHUNKS];
+    __shared__ float lw[MAX_CHUNKS];
+    __shared__ float half_acc[2][HEAD_DIM];
+    __shared__ float stat[2];
+    for (int c = t; c < chunks; c += 256)
+        wts[c] = src[c * PART];
+    __syncthreads();
+    if (t < 64) {
+        float m = -INFINITY;
+        for (int c = t; c < chunks; c += 64)
+            m = fmaxf(m, wts[c]);
+        for (int off = 32; off > 0; off >>= 1)
+            m = fmaxf(m, __shfl_xor(m, off));
+        if (t == 0)
+            stat[0] = m;
+    }
+    __syncthreads();
+    const float M = stat[0];
+    for (int c = t; c < chunks; c += 256) {
+        const float w = expf(wts[c] - M);
+        wts[c] = w;
+        lw[c] = src[c * PART + 1] * w;
+    }
+    __syncthreads();
+    if (t < 64) {
+        float l = 0.0f;
+        for (int c = t; c < chunks; c += 64)
+            l += lw[c];
+        for (int off = 32; off > 0; off >>= 1)
+            l += __shfl_xor(l, off);
+        if (t == 0)
+            stat[1] = l;
+    }
+    const int d = t & (HEAD_DIM - 1), half = t >> 7;
+    float acc = 0.0f;
+#pragma unroll 4
+    for (int c = half; c < chunks; c += 2)
+        acc = fmaf(src[c * PART + 2 + d], wts[c], acc);
+    half_acc[half][d] = acc;
+    __syncthreads();
+    if (t < HEAD_DIM)
+        a.out[h * HEAD_DIM + t] = (half_acc[0][t] + half_acc[1][t]) / stat[1];
+}
+
+// ---- argmax ----------------------------------------------------------------------------
+
+constexpr int AM_BLOCKS = 256;
+
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i)
+{
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ v, int n,
+                                                             float* __restrict__ pv, int* __restrict__ pi)
+{
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += AM_BLOCKS * 256)
+        better(bv, bi, v[i], i);
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int step = 128; step > 0; step >>= 1) {
+        if (threadIdx.x < step)
+            better(sv[threadIdx.x], si[threadIdx.x], sv[threadIdx.x + step], si[threadIdx.x + step]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = sv[0];
+        pi[blockIdx.x] = si[0];
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                           int32_t* __restrict__ out)
+{
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[threadIdx.x] = pv[threadIdx.x];
+    si[threadIdx.x] = pi[threadIdx.x];
+    __syncthreads();
+    for (int step = 128; step > 0; step >>= 1) {
+        if (threadIdx.x < step)
+            better(sv[threadIdx.x], si[threadIdx.x], sv[threadIdx.x + step], si[threadIdx.x + step]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        *out = si[0] == 0x7fffffff ? 0 : si[0];
+}
+
+}  // namespace
+
+int64_t attention_workspace_floats(int heads, int capacity)
+{
+    return static_cast<int64_t>(heads) * ((capacity + CHUNK - 1) / CHUNK) * PART;
+}
+
+int64_t argmax_workspace_bytes() { return AM_BLOCKS * 8; }
+
+hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index, float* out,
+                             hipStream_t s)
+{
+    const int64_t rb = row_bytes(fmt, cols);
+    const int64_t nblk = (cols + 255) / 256;
+    const dim3 grid(static_cast<unsigned>(nblk < 64 ? nblk : 64));
+    const uint8_t* t = static_cast<const uint8_t*>(table);
+    switch (fmt) {
+    case FMT_Q8_0: hipLaunchKernelGGL((gather_row_kernel<FMT_Q8_0>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
+    case FMT_Q4_0: hipLaunchKernelGGL((gather_row_kernel<FMT_Q4_0>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
+    case FMT_Q4_K: hipLaunchKernelGGL((gather_row_kernel<FMT_Q4_K>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttentionArgs& a, hipStream_t s)
+{
+    if (a.head_dim != HEAD_DIM || a.kv_heads <= 0 || a.heads % a.kv_heads != 0 || a.max_chunks > MAX_CHUNKS)
+        return hipErrorInvalidValue;
+    const int group = a.heads / a.kv_heads;
+    const dim3 grid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>(a.max_chunks));
+    switch (group) {
+    case 1: hipLaunchKernelGGL((attention_partial_kernel<1>), grid, dim3(ATT_THREADS), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attention_partial_kernel<2>), grid, dim3(ATT_THREADS), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((attention_partial_kernel<3>), grid, dim3(ATT_THREADS), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attention_partial_kernel<4>), grid, dim3(ATT_THREADS), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* values, int64_t n, void* workspace, int32_t* out, hipStream_t s)
+{
+    float* pv = static_cast<float*>(workspace);
+    int* pi = reinterpret_cast<int*>(pv + AM_BLOCKS);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(AM_BLOCKS), dim3(256), 0, s, values, static_cast<int>(n), pv, pi);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, out);
+    return hipGetLastError();
+}
+
+}  // namespace si

@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y,
                                                               const float* __restrict__ residual,
-                                                              int rows)
+                                                              int rows, GemvXform xf)
 {
     static_assert(NW % KS == 0, "waves must cover whole row groups");
     constexpr int THREADS = 64 * NW;
@@ -286,6 +286,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     __shared__ float4 xs4[UPR * XS_UNIT / 4];
     __shared__ float bs[UPR * 2];
     __shared__ float part[KS > 1 ? ROWS_PER_WG * KS : 1];
+    __shared__ float red[NW];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -316,6 +317,42 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
 #pragma unroll
     for (int j = 0; j < XPT; j++)
         xr[j] = x4[threadIdx.x + j * THREADS];
+    if (xf.kind == XF_SWIGLU) {
+        // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            const float4 u = x4[K / 4 + threadIdx.x + j * THREADS];
+            xr[j].x = xr[j].x / (1.0f + expf(-xr[j].x)) * u.x;
+            xr[j].y = xr[j].y / (1.0f + expf(-xr[j].y)) * u.y;
+            xr[j].z = xr[j].z / (1.0f + expf(-xr[j].z)) * u.z;
+            xr[j].w = xr[j].w / (1.0f + expf(-xr[j].w)) * u.w;
+        }
+    } else if (xf.kind == XF_RMSNORM) {
+        // scale = 1 / sqrt(sum(x^2) / K + eps); x_i * scale * weight_i
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XPT; j++)
+            ss += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
+        for (int off = 32; off > 0; off >>= 1)
+            ss += __shfl_xor(ss, off);
+        if (lane == 0)
+            red[wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; i++)
+            total += red[i];
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(K) + xf.eps);
+        const float4* g4 = reinterpret_cast<const float4*>(xf.weight);
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            const float4 g = g4[threadIdx.x + j * THREADS];
+            xr[j].x = xr[j].x * scale * g.x;
+            xr[j].y = xr[j].y * scale * g.y;
+            xr[j].z = xr[j].z * scale * g.z;
+            xr[j].w = xr[j].w * scale * g.w;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < XPT; j++) {
         const int col = 4 * (threadIdx.x + j * THREADS);
@@ -547,11 +584,12 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, uint
 // ---- dispatch --------------------------------------------------------------
 
 template <int FMT, int LK, int UPL, int RL, int KS, int NW>
-hipError_t launch_tiled(const uint8_t* w, const float* x, float* y, const float* res, int rows, hipStream_t s)
+hipError_t launch_tiled(const uint8_t* w, const float* x, float* y, const float* res, int rows, const GemvXform& xf,
+                        hipStream_t s)
 {
     constexpr int R = (64 / LK) * RL * (NW / KS);
     hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW>), dim3((rows + R - 1) / R), dim3(64 * NW), 0, s,
-                       w, x, y, res, rows);
+                       w, x, y, res, rows, xf);
     return hipGetLastError();
 }
 
@@ -564,24 +602,24 @@ hipError_t launch_tiled(const uint8_t* w, const float* x, float* y, const float*
 // reductions over more weights.
 template <int FMT>
 bool launch_fast(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows64, int64_t cols,
-                 hipStream_t s, hipError_t* err)
+                 const GemvXform& xf, hipStream_t s, hipError_t* err)
 {
     const int rows = static_cast<int>(rows64);
     const bool mid = rows64 >= 12288, tall = rows64 >= 49152;
     switch (cols) {
-    case 1024: *err = mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(w, x, y, res, rows, s)
-                          : launch_tiled<FMT, 16, 1, 1, 1, 4>(w, x, y, res, rows, s); return true;
-    case 2048: *err = mid ? launch_tiled<FMT, 16, 2, 2, 1, 4>(w, x, y, res, rows, s)
-                          : launch_tiled<FMT, 16, 1, 1, 2, 4>(w, x, y, res, rows, s); return true;
-    case 3072: *err = tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(w, x, y, res, rows, s)
-                    : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(w, x, y, res, rows, s)
-                           : launch_tiled<FMT, 16, 1, 1, 3, 3>(w, x, y, res, rows, s); return true;
-    case 4096: *err = mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(w, x, y, res, rows, s)
-                          : launch_tiled<FMT, 16, 1, 1, 4, 4>(w, x, y, res, rows, s); return true;
-    case 6144: *err = mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(w, x, y, res, rows, s)
-                          : launch_tiled<FMT, 16, 1, 1, 6, 6>(w, x, y, res, rows, s); return true;
-    case 8192: *err = mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(w, x, y, res, rows, s)
-                          : launch_tiled<FMT, 16, 1, 1, 8, 8>(w, x, y, res, rows, s); return true;
+    case 1024: *err = mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(w, x, y, res, rows, xf, s)
+                          : launch_tiled<FMT, 16, 1, 1, 1, 4>(w, x, y, res, rows, xf, s); return true;
+    case 2048: *err = mid ? launch_tiled<FMT, 16, 2, 2, 1, 4>(w, x, y, res, rows, xf, s)
+                          : launch_tiled<FMT, 16, 1, 1, 2, 4>(w, x, y, res, rows, xf, s); return true;
+    case 3072: *err = tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(w, x, y, res, rows, xf, s)
+                    : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(w, x, y, res, rows, xf, s)
+                           : launch_tiled<FMT, 16, 1, 1, 3, 3>(w, x, y, res, rows, xf, s); return true;
+    case 4096: *err = mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(w, x, y, res, rows, xf, s)
+                          : launch_tiled<FMT, 16, 1, 1, 4, 4>(w, x, y, res, rows, xf, s); return true;
+    case 6144: *err = mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(w, x, y, res, rows, xf, s)
+                          : launch_tiled<FMT, 16, 1, 1, 6, 6>(w, x, y, res, rows, xf, s); return true;
+    case 8192: *err = mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(w, x, y, res, rows, xf, s)
+                          : launch_tiled<FMT, 16, 1, 1, 8, 8>(w, x, y, res, rows, xf, s); return true;
     default: return false;
     }
 }
@@ -598,30 +636,44 @@ hipError_t launch_generic(const uint8_t* w, const float* x, float* y, const floa
 
 template <int FMT>
 hipError_t launch_gemv_fmt(const void* wv, const float* x, float* y, int64_t rows, int64_t cols,
-                           const GemvEpilogue& epi, hipStream_t s, int* path)
+                           const GemvEpilogue& epi, const GemvXform& xf, hipStream_t s, int* path)
 {
     const uint8_t* w = static_cast<const uint8_t*>(wv);
-    const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(xf.weight) & 15u) == 0;
     hipError_t err = hipSuccess;
-    if (aligned && launch_fast<FMT>(w, x, y, epi.residual, rows, cols, s, &err)) {
+    if (aligned && launch_fast<FMT>(w, x, y, epi.residual, rows, cols, xf, s, &err)) {
         if (path) *path = PATH_FAST;
         return err;
     }
+    if (xf.kind != XF_PLAIN)
+        return hipErrorNotSupported;
     if (path) *path = PATH_GENERIC;
     return launch_generic<FMT>(w, x, y, epi.residual, rows, cols, s);
 }
 
 }  // namespace
 
+hipError_t launch_gemv_xform(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
+                             const GemvEpilogue& epi, const GemvXform& xf, hipStream_t stream, int* path)
+{
+    switch (fmt) {
+    case FMT_Q8_0: return launch_gemv_fmt<FMT_Q8_0>(w, x, y, rows, cols, epi, xf, stream, path);
+    case FMT_Q4_0: return launch_gemv_fmt<FMT_Q4_0>(w, x, y, rows, cols, epi, xf, stream, path);
+    case FMT_Q4_K: return launch_gemv_fmt<FMT_Q4_K>(w, x, y, rows, cols, epi, xf, stream, path);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
                        const GemvEpilogue& epi, hipStream_t stream, int* path)
 {
-    switch (fmt) {
-    case FMT_Q8_0: return launch_gemv_fmt<FMT_Q8_0>(w, x, y, rows, cols, epi, stream, path);
-    case FMT_Q4_0: return launch_gemv_fmt<FMT_Q4_0>(w, x, y, rows, cols, epi, stream, path);
-    case FMT_Q4_K: return launch_gemv_fmt<FMT_Q4_K>(w, x, y, rows, cols, epi, stream, path);
-    default: return hipErrorInvalidValue;
-    }
+    return launch_gemv_xform(fmt, w, x, y, rows, cols, epi, GemvXform{}, stream, path);
+}
+
+bool gemv_tiled_cols(int64_t cols)
+{
+    return cols == 1024 || cols == 2048 || cols == 3072 || cols == 4096 || cols == 6144 || cols == 8192;
 }
 
 hipError_t launch_dequant(int fmt, const void* wv, float* out, int64_t rows, int64_t cols, hipStream_t s)

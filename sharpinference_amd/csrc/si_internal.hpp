@@ -41,11 +41,29 @@ struct GemvEpilogue {
     const float* residual = nullptr;   // y = W.x + residual when non-null
 };
 
+// Transform applied to x while it is staged, before the product.
+enum XformKind : int {
+    XF_PLAIN = 0,
+    XF_RMSNORM = 1,   // x_i * (1 / sqrt(sum(x^2) / cols + eps)) * weight_i
+    XF_SWIGLU = 2,    // x holds [gate | up] (2 * cols values): gate / (1 + exp(-gate)) * up
+};
+struct GemvXform {
+    int kind = XF_PLAIN;
+    const float* weight = nullptr;
+    float eps = 0.0f;
+};
+
 // Which kernel a launch used; reported to the caller for tests and profiles.
 enum GemvPath : int { PATH_FAST = 1, PATH_GENERIC = 2 };
 
 hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
                        const GemvEpilogue& epi, hipStream_t stream, int* path);
+// Same product with a transform of x fused into the staging; only the tiled
+// kernel's column counts take a transform (returns hipErrorNotSupported
+// otherwise).
+hipError_t launch_gemv_xform(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
+                             const GemvEpilogue& epi, const GemvXform& xf, hipStream_t stream, int* path);
+bool gemv_tiled_cols(int64_t cols);
 hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, int64_t m, int64_t rows,
                           int64_t cols, hipStream_t stream);
 hipError_t launch_dequant(int fmt, const void* w, float* out, int64_t rows, int64_t cols,

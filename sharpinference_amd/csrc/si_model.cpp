@@ -1,0 +1,293 @@
+// C ABI of the decode-step operators (fused-norm GEMV, row gather,
+// attention, argmax) and the Phi-4 decode program recorder.
+//
+// The recorder is the HIP counterpart of the reference's hand-built Phi-4
+// decode program (SharpInference.Architectures.Phi4.D3D12/
+// Phi4D3D12TextSession.cs:866-919): embedding gather, 32 x (RMSNorm + qkv,
+// rotary + KV append + attention, o_proj + residual, RMSNorm + gate_up,
+// SwiGLU + down + residual), final RMSNorm + vocabulary projection, argmax,
+// recorded once into one plan and replayed per token with a single
+// submission (the ExecuteWithTransfers pattern, D3D12VmExecutor.cs:298).
+// The token and position come from a device control buffer [token, position]
+// written by the caller before each replay (Phi4D3D12TextSession.cs:212-226).
+#include "si_context.hpp"
+#include "si_decode.hpp"
+
+using namespace si_abi;
+
+namespace {
+
+int check_fp32(si_hip_context* ctx, const char* op, const void* p, const char* what)
+{
+    if (!p || !aligned(p, 4))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: %s must be a non-null 4-byte aligned pointer", op, what);
+    return SI_HIP_OK;
+}
+
+int attention_check(si_hip_context* ctx, const si_hip_attention* a)
+{
+    if (!a)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "attention: null arguments");
+    if (a->head_dim != 128)
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "attention: head_dim %d (only 128 is built)", a->head_dim);
+    if (a->kv_heads <= 0 || a->heads <= 0 || a->heads % a->kv_heads != 0 || a->heads / a->kv_heads > 4)
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "attention: %d query heads over %d KV heads (group of 1..4 is built)",
+                    a->heads, a->kv_heads);
+    if (a->rotary_dim < 0 || a->rotary_dim > a->head_dim || (a->rotary_dim & 1))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "attention: rotary_dim %d must be even and <= head_dim", a->rotary_dim);
+    if (a->capacity <= 0 || a->capacity > 16384)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "attention: capacity %d outside 1..16384", a->capacity);
+    if (!a->qkv || !a->position || !a->k_cache || !a->v_cache || !a->out || !a->workspace)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "attention: null pointer");
+    if (!aligned(a->qkv, 4) || !aligned(a->position, 4) || !aligned(a->k_cache, 16) || !aligned(a->v_cache, 16) ||
+        !aligned(a->out, 4) || !aligned(a->workspace, 4))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "attention: misaligned pointer");
+    return SI_HIP_OK;
+}
+
+si::AttentionArgs attention_args(const si_hip_attention* a)
+{
+    si::AttentionArgs r;
+    r.qkv = a->qkv;
+    r.position = a->position;
+    r.k_cache = static_cast<__half*>(a->k_cache);
+    r.v_cache = static_cast<__half*>(a->v_cache);
+    r.out = a->out;
+    r.workspace = a->workspace;
+    r.heads = a->heads;
+    r.kv_heads = a->kv_heads;
+    r.head_dim = a->head_dim;
+    r.rotary_dim = a->rotary_dim;
+    r.capacity = a->capacity;
+    r.max_chunks = (a->capacity + 63) / 64;
+    r.rope_base = a->rope_base;
+    r.rope_scale = a->rope_scale;
+    return r;
+}
+
+// Device scratch of one decode program: attention partials, then argmax.
+uint64_t phi4_workspace_bytes(const si_hip_phi4_model* m)
+{
+    const uint64_t att = static_cast<uint64_t>(si::attention_workspace_floats(m->heads, m->capacity)) * 4;
+    return ((att + 255) & ~uint64_t(255)) + static_cast<uint64_t>(si::argmax_workspace_bytes());
+}
+
+int phi4_check(si_hip_context* ctx, const si_hip_phi4_model* m)
+{
+    if (!m)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: null model");
+    if (m->layers <= 0 || !m->layer)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: no layers");
+    if (m->heads * m->head_dim != m->hidden)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: heads * head_dim (%d * %d) != hidden %d", m->heads, m->head_dim,
+                    m->hidden);
+    if (!si::gemv_tiled_cols(m->hidden) || !si::gemv_tiled_cols(m->ffn))
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                    "phi4: hidden %d and ffn %d must be tiled column counts (1024/2048/3072/4096/6144/8192) "
+                    "for the fused norms", m->hidden, m->ffn);
+    for (int fmt : {m->weight_format, m->embed_format, m->head_format})
+        if (!is_quant(fmt))
+            return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "phi4: tensor type %d is not block-quantized", fmt);
+    if (si::row_bytes(m->weight_format, m->hidden) < 0 || si::row_bytes(m->weight_format, m->ffn) < 0 ||
+        si::row_bytes(m->embed_format, m->hidden) < 0 || si::row_bytes(m->head_format, m->hidden) < 0)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: hidden/ffn are not whole blocks of the weight formats");
+    if (!m->embed || !m->lm_head || !m->output_norm || !m->control || !m->hidden_state || !m->qkv || !m->attn ||
+        !m->gate_up || !m->logits || !m->workspace || !m->next_token)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: null buffer");
+    for (int l = 0; l < m->layers; l++) {
+        const si_hip_phi4_layer& L = m->layer[l];
+        if (!L.attn_norm || !L.qkv || !L.o || !L.ffn_norm || !L.up || !L.down || !L.k_cache || !L.v_cache)
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: layer %d has a null tensor", l);
+    }
+    si_hip_attention a{};
+    a.head_dim = m->head_dim;
+    a.heads = m->heads;
+    a.kv_heads = m->kv_heads;
+    a.rotary_dim = m->rotary_dim;
+    a.capacity = m->capacity;
+    a.qkv = m->qkv;
+    a.position = m->control + 1;
+    a.k_cache = m->layer[0].k_cache;
+    a.v_cache = m->layer[0].v_cache;
+    a.out = m->attn;
+    a.workspace = static_cast<float*>(m->workspace);
+    return attention_check(ctx, &a);
+}
+
+// Launches one decode step on the context stream (recorded when capturing).
+hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
+{
+    hipStream_t s = ctx->stream;
+    const int H = m->hidden;
+    const int qkv_rows = H + 2 * m->kv_heads * m->head_dim;
+    float* att_ws = static_cast<float*>(m->workspace);
+    const uint64_t att_bytes = (static_cast<uint64_t>(si::attention_workspace_floats(m->heads, m->capacity)) * 4 + 255) &
+                               ~uint64_t(255);
+    void* am_ws = static_cast<uint8_t*>(m->workspace) + att_bytes;
+    hipError_t e = si::launch_gather_row(m->embed_format, m->embed, m->vocab, H, m->control, m->hidden_state, s);
+    for (int l = 0; e == hipSuccess && l < m->layers; l++) {
+        const si_hip_phi4_layer& L = m->layer[l];
+        si::GemvXform norm{si::XF_RMSNORM, L.attn_norm, m->rms_eps};
+        e = si::launch_gemv_xform(m->weight_format, L.qkv, m->hidden_state, m->qkv, qkv_rows, H, si::GemvEpilogue{},
+                                  norm, s, nullptr);
+        if (e != hipSuccess) break;
+        si_hip_attention a{};
+        a.qkv = m->qkv;
+        a.position = m->control + 1;
+        a.k_cache = L.k_cache;
+        a.v_cache = L.v_cache;
+        a.out = m->attn;
+        a.workspace = att_ws;
+        a.heads = m->heads;
+        a.kv_heads = m->kv_heads;
+        a.head_dim = m->head_dim;
+        a.rotary_dim = m->rotary_dim;
+        a.capacity = m->capacity;
+        a.rope_base = m->rope_base;
+        a.rope_scale = m->rope_scale;
+        e = si::launch_attention(attention_args(&a), s);
+        if (e != hipSuccess) break;
+        // hidden += W_o . attn
+        e = si::launch_gemv(m->weight_format, L.o, m->attn, m->hidden_state, H, H, si::GemvEpilogue{m->hidden_state}, s,
+                            nullptr);
+        if (e != hipSuccess) break;
+        si::GemvXform fnorm{si::XF_RMSNORM, L.ffn_norm, m->rms_eps};
+        e = si::launch_gemv_xform(m->weight_format, L.up, m->hidden_state, m->gate_up, 2 * m->ffn, H, si::GemvEpilogue{},
+                                  fnorm, s, nullptr);
+        if (e != hipSuccess) break;
+        // hidden += W_down . (silu(gate) * up)
+        si::GemvXform swiglu{si::XF_SWIGLU, nullptr, 0.0f};
+        e = si::launch_gemv_xform(m->weight_format, L.down, m->gate_up, m->hidden_state, H, m->ffn,
+                                  si::GemvEpilogue{m->hidden_state}, swiglu, s, nullptr);
+    }
+    if (e == hipSuccess) {
+        si::GemvXform onorm{si::XF_RMSNORM, m->output_norm, m->rms_eps};
+        e = si::launch_gemv_xform(m->head_format, m->lm_head, m->hidden_state, m->logits, m->vocab, H, si::GemvEpilogue{},
+                                  onorm, s, nullptr);
+    }
+    if (e == hipSuccess)
+        e = si::launch_argmax(m->logits, m->vocab, am_ws, m->next_token, s);
+    return e;
+}
+
+}  // namespace
+
+extern "C" {
+
+int si_hip_gemv_fused(si_hip_context* ctx, int format, const void* w, const float* x, float* y, int64_t rows,
+                      int64_t cols, const float* residual, int xform, const float* norm_weight, float eps, int* path)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "gemv_fused: null context");
+    Enter g(ctx);
+    if (g.err != hipSuccess)
+        return hip_fail(ctx, g.err, "hipSetDevice");
+    uint64_t wbytes = 0;
+    if (const int rc = check_matrix(ctx, "gemv_fused", format, w, rows, cols, &wbytes))
+        return rc;
+    if (xform != SI_HIP_X_PLAIN && xform != SI_HIP_X_RMSNORM && xform != SI_HIP_X_SWIGLU)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_fused: unknown transform %d", xform);
+    if (xform != SI_HIP_X_PLAIN && !si::gemv_tiled_cols(cols))
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                    "gemv_fused: a fused transform needs cols in {1024, 2048, 3072, 4096, 6144, 8192}, got %lld",
+                    static_cast<long long>(cols));
+    if (!x || !y || !aligned(y, 4) || (residual && !aligned(residual, 4)))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_fused: null or misaligned FP32 operand");
+    if (xform != SI_HIP_X_PLAIN && (!aligned(x, 16) || !aligned(w, 4)))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_fused: a fused transform needs x 16-byte and W 4-byte aligned");
+    if (xform == SI_HIP_X_RMSNORM && (!norm_weight || !aligned(norm_weight, 16)))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_fused: RMSNorm weight must be a 16-byte aligned pointer");
+    const uint64_t ybytes = static_cast<uint64_t>(rows) * 4;
+    const uint64_t xbytes = static_cast<uint64_t>(cols) * 4 * (xform == SI_HIP_X_SWIGLU ? 2 : 1);
+    if (overlaps(y, ybytes, w, wbytes) || overlaps(y, ybytes, x, xbytes) ||
+        (residual && residual != y && overlaps(y, ybytes, residual, ybytes)))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_fused: output overlaps an input");
+    si::GemvXform xf{xform, norm_weight, eps};
+    const hipError_t e = si::launch_gemv_xform(format, w, x, y, rows, cols, si::GemvEpilogue{residual}, xf, ctx->stream,
+                                               path);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemv_fused launch");
+}
+
+int si_hip_gather_row(si_hip_context* ctx, int format, const void* table, int64_t rows, int64_t cols,
+                      const int32_t* index, float* out)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "gather_row: null context");
+    Enter g(ctx);
+    uint64_t tbytes = 0;
+    if (const int rc = check_matrix(ctx, "gather_row", format, table, rows, cols, &tbytes))
+        return rc;
+    if (!index || !aligned(index, 4))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gather_row: index must be a 4-byte aligned device pointer");
+    if (const int rc = check_fp32(ctx, "gather_row", out, "out"))
+        return rc;
+    if (overlaps(out, static_cast<uint64_t>(cols) * 4, table, tbytes) ||
+        overlaps(out, static_cast<uint64_t>(cols) * 4, index, 4))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gather_row: output overlaps an input");
+    const hipError_t e = si::launch_gather_row(format, table, rows, cols, index, out, ctx->stream);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gather_row launch");
+}
+
+int si_hip_attention_workspace_bytes(int heads, int capacity, uint64_t* bytes)
+{
+    if (!bytes || heads <= 0 || capacity <= 0)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "attention_workspace_bytes: bad arguments");
+    *bytes = static_cast<uint64_t>(si::attention_workspace_floats(heads, capacity)) * 4;
+    return SI_HIP_OK;
+}
+
+int si_hip_attention_decode(si_hip_context* ctx, const si_hip_attention* args)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "attention: null context");
+    Enter g(ctx);
+    if (const int rc = attention_check(ctx, args))
+        return rc;
+    const hipError_t e = si::launch_attention(attention_args(args), ctx->stream);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "attention launch");
+}
+
+int si_hip_argmax_workspace_bytes(uint64_t* bytes)
+{
+    if (!bytes)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "argmax_workspace_bytes: null output");
+    *bytes = static_cast<uint64_t>(si::argmax_workspace_bytes());
+    return SI_HIP_OK;
+}
+
+int si_hip_argmax(si_hip_context* ctx, const float* values, int64_t n, void* workspace, int32_t* index)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "argmax: null context");
+    Enter g(ctx);
+    if (n <= 0 || n > INT32_MAX)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "argmax: count %lld out of range", static_cast<long long>(n));
+    if (check_fp32(ctx, "argmax", values, "values") || check_fp32(ctx, "argmax", workspace, "workspace") ||
+        check_fp32(ctx, "argmax", index, "index"))
+        return SI_HIP_ERR_ARGUMENT;
+    const hipError_t e = si::launch_argmax(values, n, workspace, index, ctx->stream);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "argmax launch");
+}
+
+int si_hip_phi4_workspace_bytes(const si_hip_phi4_model* model, uint64_t* bytes)
+{
+    if (!model || !bytes || model->heads <= 0 || model->capacity <= 0)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "phi4_workspace_bytes: bad arguments");
+    *bytes = phi4_workspace_bytes(model);
+    return SI_HIP_OK;
+}
+
+int si_hip_phi4_decode(si_hip_context* ctx, const si_hip_phi4_model* model)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "phi4_decode: null context");
+    Enter g(ctx);
+    if (g.err != hipSuccess)
+        return hip_fail(ctx, g.err, "hipSetDevice");
+    if (const int rc = phi4_check(ctx, model))
+        return rc;
+    const hipError_t e = phi4_step(ctx, model);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "phi4 decode step");
+}
+
+}  // extern "C"

@@ -55,6 +55,46 @@ SIGNATURES = {
     "si_hip_timer_end": ([_vp, ctypes.POINTER(_dbl)], _i32),
 }
 
+X_PLAIN, X_RMSNORM, X_SWIGLU = 0, 1, 2
+
+
+class AttentionArgs(ctypes.Structure):
+    """si_hip_attention."""
+    _fields_ = [("qkv", _vp), ("position", _vp), ("k_cache", _vp), ("v_cache", _vp), ("out", _vp),
+                ("workspace", _vp), ("heads", _i32), ("kv_heads", _i32), ("head_dim", _i32),
+                ("rotary_dim", _i32), ("capacity", _i32), ("rope_base", ctypes.c_float),
+                ("rope_scale", ctypes.c_float)]
+
+
+class Phi4Layer(ctypes.Structure):
+    """si_hip_phi4_layer."""
+    _fields_ = [("attn_norm", _vp), ("qkv", _vp), ("o", _vp), ("ffn_norm", _vp), ("up", _vp), ("down", _vp),
+                ("k_cache", _vp), ("v_cache", _vp)]
+
+
+class Phi4Model(ctypes.Structure):
+    """si_hip_phi4_model."""
+    _fields_ = [("layers", _i32), ("hidden", _i32), ("heads", _i32), ("kv_heads", _i32), ("head_dim", _i32),
+                ("rotary_dim", _i32), ("ffn", _i32), ("vocab", _i32), ("capacity", _i32),
+                ("weight_format", _i32), ("embed_format", _i32), ("head_format", _i32),
+                ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("rope_scale", ctypes.c_float),
+                ("embed", _vp), ("lm_head", _vp), ("output_norm", _vp), ("layer", ctypes.POINTER(Phi4Layer)),
+                ("control", _vp), ("hidden_state", _vp), ("qkv", _vp), ("attn", _vp), ("gate_up", _vp),
+                ("logits", _vp), ("workspace", _vp), ("next_token", _vp)]
+
+
+SIGNATURES.update({
+    "si_hip_gemv_fused": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp, ctypes.c_float,
+                           ctypes.POINTER(_i32)], _i32),
+    "si_hip_gather_row": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp], _i32),
+    "si_hip_attention_workspace_bytes": ([_i32, _i32, ctypes.POINTER(_u64)], _i32),
+    "si_hip_attention_decode": ([_vp, ctypes.POINTER(AttentionArgs)], _i32),
+    "si_hip_argmax_workspace_bytes": ([ctypes.POINTER(_u64)], _i32),
+    "si_hip_argmax": ([_vp, _vp, _i64, _vp, _vp], _i32),
+    "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
+    "si_hip_phi4_decode": ([_vp, ctypes.POINTER(Phi4Model)], _i32),
+})
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -219,6 +259,28 @@ class HipContext:
         self._call(lib().si_hip_gemm_prefill, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(x_bf16)),
                    ctypes.c_void_p(int(y)), m, rows, cols)
 
+    def gemv_fused(self, fmt: int, w: int, x: int, y: int, rows: int, cols: int, residual: int = 0,
+                   xform: int = X_PLAIN, norm_weight: int = 0, eps: float = 0.0) -> int:
+        path = ctypes.c_int(0)
+        self._call(lib().si_hip_gemv_fused, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(x)),
+                   ctypes.c_void_p(int(y)), rows, cols, ctypes.c_void_p(int(residual) or None), xform,
+                   ctypes.c_void_p(int(norm_weight) or None), ctypes.c_float(eps), ctypes.byref(path))
+        return path.value
+
+    def gather_row(self, fmt: int, table: int, rows: int, cols: int, index: int, out: int) -> None:
+        self._call(lib().si_hip_gather_row, fmt, ctypes.c_void_p(int(table)), rows, cols,
+                   ctypes.c_void_p(int(index)), ctypes.c_void_p(int(out)))
+
+    def attention(self, args: AttentionArgs) -> None:
+        self._call(lib().si_hip_attention_decode, ctypes.byref(args))
+
+    def argmax(self, values: int, n: int, workspace: int, index: int) -> None:
+        self._call(lib().si_hip_argmax, ctypes.c_void_p(int(values)), n, ctypes.c_void_p(int(workspace)),
+                   ctypes.c_void_p(int(index)))
+
+    def phi4_decode(self, model: Phi4Model) -> None:
+        self._call(lib().si_hip_phi4_decode, ctypes.byref(model))
+
     def dequant(self, fmt: int, w: int, out: int, rows: int, cols: int) -> None:
         self._call(lib().si_hip_dequant, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(out)), rows, cols)
 
@@ -255,6 +317,24 @@ class HipContext:
         ms = ctypes.c_double(0.0)
         self._call(lib().si_hip_timer_end, ctypes.byref(ms))
         return ms.value
+
+
+def attention_workspace_bytes(heads: int, capacity: int) -> int:
+    out = ctypes.c_uint64(0)
+    _check(lib().si_hip_attention_workspace_bytes(heads, capacity, ctypes.byref(out)))
+    return out.value
+
+
+def argmax_workspace_bytes() -> int:
+    out = ctypes.c_uint64(0)
+    _check(lib().si_hip_argmax_workspace_bytes(ctypes.byref(out)))
+    return out.value
+
+
+def phi4_workspace_bytes(model: Phi4Model) -> int:
+    out = ctypes.c_uint64(0)
+    _check(lib().si_hip_phi4_workspace_bytes(ctypes.byref(model), ctypes.byref(out)))
+    return out.value
 
 
 def exported_symbols(path: str = LIB_PATH) -> Iterable[str]:

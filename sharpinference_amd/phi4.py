@@ -1,0 +1,246 @@
+"""Phi-4-mini-shaped decode session on the HIP backend.
+
+The host half of the reference's Phi4D3D12TextSession
+(SharpInference.Architectures.Phi4.D3D12/Phi4D3D12TextSession.cs): it owns
+the device tensors of one model (block-quantized weights kept in their GGUF
+bytes, FP32 norms, fp16 KV caches), records the whole decode step once as a
+plan through si_hip_phi4_decode, and runs ForwardToken (:212-226) as
+control upload -> one plan replay -> next-token readback.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from . import native
+
+
+@dataclass
+class Phi4Config:
+    """Phi-4-mini text shapes (Phi4TextModel.cs:14-21) with the BASELINE
+    storage formats: Q4_K layer weights, Q8_0 embedding and vocabulary head."""
+    layers: int = 32
+    hidden: int = 3072
+    heads: int = 24
+    kv_heads: int = 8
+    head_dim: int = 128
+    rotary_dim: int = 96
+    ffn: int = 8192
+    vocab: int = 200064
+    capacity: int = 4096
+    weight_format: int = native.Q4_K
+    embed_format: int = native.Q8_0
+    head_format: int = native.Q8_0
+    rms_eps: float = 1e-5
+    rope_base: float = 10000.0
+    rope_scale: float = 1.0
+
+    @property
+    def qkv_rows(self) -> int:
+        return self.hidden + 2 * self.kv_heads * self.head_dim
+
+    def layer_shapes(self) -> Dict[str, tuple]:
+        return {"qkv": (self.qkv_rows, self.hidden), "o": (self.hidden, self.hidden),
+                "up": (2 * self.ffn, self.hidden), "down": (self.hidden, self.ffn)}
+
+    def weight_bytes_per_token(self) -> int:
+        """HBM bytes one decode step must read at least: every layer weight,
+        the vocabulary head, one embedding row, norms, and the KV cache rows
+        up to the current position (counted at full capacity by callers that
+        want the bound at a given position)."""
+        total = 0
+        for rows, cols in self.layer_shapes().values():
+            total += native.tensor_bytes(self.weight_format, rows, cols) * self.layers
+        total += native.tensor_bytes(self.head_format, self.vocab, self.hidden)
+        total += native.tensor_bytes(self.embed_format, 1, self.hidden)
+        total += 4 * self.hidden * (2 * self.layers + 1)
+        return total
+
+    def kv_bytes(self, length: int) -> int:
+        return 2 * 2 * self.layers * self.kv_heads * self.head_dim * length
+
+
+@dataclass
+class Phi4Weights:
+    """Host tensors of one model.  Layer lists hold one array per layer."""
+    embed: np.ndarray
+    lm_head: np.ndarray
+    output_norm: np.ndarray
+    attn_norm: List[np.ndarray]
+    qkv: List[np.ndarray]
+    o: List[np.ndarray]
+    ffn_norm: List[np.ndarray]
+    up: List[np.ndarray]
+    down: List[np.ndarray]
+
+
+class Phi4DecodeSession:
+    """Device-resident model + one recorded decode plan."""
+
+    def __init__(self, hip: native.HipContext, cfg: Phi4Config, weights: Phi4Weights):
+        self.hip = hip
+        self.cfg = cfg
+        self._bufs: List[native.DeviceBuffer] = []
+        up = self._upload
+        self.embed = up(weights.embed)
+        self.lm_head = up(weights.lm_head)
+        self.output_norm = up(weights.output_norm.astype(np.float32))
+        kv_bytes = 2 * cfg.kv_heads * cfg.capacity * cfg.head_dim
+        self.layers = []
+        for l in range(cfg.layers):
+            L = {
+                "attn_norm": up(weights.attn_norm[l].astype(np.float32)),
+                "qkv": up(weights.qkv[l]), "o": up(weights.o[l]),
+                "ffn_norm": up(weights.ffn_norm[l].astype(np.float32)),
+                "up": up(weights.up[l]), "down": up(weights.down[l]),
+                "k_cache": self._alloc(kv_bytes), "v_cache": self._alloc(kv_bytes),
+            }
+            self.layers.append(L)
+        self.control = self._alloc(8)
+        self.hidden_state = self._alloc(4 * cfg.hidden)
+        self.qkv = self._alloc(4 * cfg.qkv_rows)
+        self.attn = self._alloc(4 * cfg.hidden)
+        self.gate_up = self._alloc(8 * cfg.ffn)
+        self.logits = self._alloc(4 * cfg.vocab)
+        self.next_token = self._alloc(4)
+        self._layer_array = (native.Phi4Layer * cfg.layers)()
+        for l, L in enumerate(self.layers):
+            self._layer_array[l] = native.Phi4Layer(
+                L["attn_norm"].ptr, L["qkv"].ptr, L["o"].ptr, L["ffn_norm"].ptr, L["up"].ptr, L["down"].ptr,
+                L["k_cache"].ptr, L["v_cache"].ptr)
+        self.model = native.Phi4Model(
+            cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.rotary_dim, cfg.ffn, cfg.vocab,
+            cfg.capacity, cfg.weight_format, cfg.embed_format, cfg.head_format, cfg.rms_eps, cfg.rope_base,
+            cfg.rope_scale, self.embed.ptr, self.lm_head.ptr, self.output_norm.ptr,
+            ctypes.cast(self._layer_array, ctypes.POINTER(native.Phi4Layer)),
+            self.control.ptr, self.hidden_state.ptr, self.qkv.ptr, self.attn.ptr, self.gate_up.ptr,
+            self.logits.ptr, 0, self.next_token.ptr)
+        self.workspace = self._alloc(native.phi4_workspace_bytes(self.model))
+        self.model.workspace = self.workspace.ptr
+        self.plan = hip.record(lambda: hip.phi4_decode(self.model))
+        self.position = 0
+
+    # -- buffers -------------------------------------------------------------------
+    def _alloc(self, nbytes: int) -> native.DeviceBuffer:
+        b = self.hip.alloc(max(int(nbytes), 4))
+        self._bufs.append(b)
+        return b
+
+    def _upload(self, arr: np.ndarray) -> native.DeviceBuffer:
+        b = self._alloc(arr.nbytes)
+        b.upload(np.ascontiguousarray(arr))
+        return b
+
+    def load_kv(self, layer: int, k_fp16: np.ndarray, v_fp16: np.ndarray) -> None:
+        """Fills a layer's caches (uint16 fp16 bits [kv_heads, capacity, head_dim])."""
+        L = self.layers[layer]
+        L["k_cache"].upload(np.ascontiguousarray(k_fp16, np.uint16))
+        L["v_cache"].upload(np.ascontiguousarray(v_fp16, np.uint16))
+
+    def read_kv(self, layer: int):
+        cfg = self.cfg
+        shape = (cfg.kv_heads, cfg.capacity, cfg.head_dim)
+        L = self.layers[layer]
+        return L["k_cache"].readback(np.uint16).reshape(shape), L["v_cache"].readback(np.uint16).reshape(shape)
+
+    # -- decoding -------------------------------------------------------------------
+    def set_control(self, token: int, position: int) -> None:
+        self.control.upload(np.array([token, position], np.int32))
+
+    def forward_token(self, token: int, position: Optional[int] = None) -> int:
+        """One decode step; returns the argmax token (greedy next token)."""
+        if position is None:
+            position = self.position
+        if not 0 <= position < self.cfg.capacity:
+            raise ValueError(f"position {position} outside the KV capacity {self.cfg.capacity}")
+        self.set_control(token, position)
+        self.plan.launch()
+        nxt = int(self.next_token.readback(np.int32, 1)[0])
+        self.position = position + 1
+        return nxt
+
+    def read_logits(self) -> np.ndarray:
+        return self.logits.readback(np.float32, self.cfg.vocab)
+
+    def close(self) -> None:
+        if self.plan is not None:
+            self.plan.destroy()
+            self.plan = None
+        for b in self._bufs:
+            b.free()
+        self._bufs = []
+
+
+# ---- synthetic weights --------------------------------------------------------------
+
+def _fp16_bytes(v: np.ndarray) -> np.ndarray:
+    return v.astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+
+def synth_blocks(fmt: int, rows: int, cols: int, rng: np.random.Generator, sigma: float = 0.02) -> np.ndarray:
+    """GGUF blocks with the BASELINE distributions: Q8_0 q ~ U{-127..127},
+    d = |N(0, sigma)| / 127; Q4_0 nibbles ~ U{0..15}, d = |N(0, sigma)| / 8;
+    Q4_K q ~ U{0..15}, 6-bit sc, m ~ U{0..63}, d = |N(0, sigma)| / 504,
+    dmin = |N(0, sigma)| / 63."""
+    if fmt == native.Q8_0:
+        nb = rows * cols // 32
+        out = np.empty((nb, 34), np.uint8)
+        out[:, :2] = _fp16_bytes(np.abs(rng.standard_normal(nb)) * sigma / 127)
+        out[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+        return out.reshape(-1)
+    if fmt == native.Q4_0:
+        nb = rows * cols // 32
+        out = np.empty((nb, 18), np.uint8)
+        out[:, :2] = _fp16_bytes(np.abs(rng.standard_normal(nb)) * sigma / 8)
+        out[:, 2:] = rng.integers(0, 256, size=(nb, 16), dtype=np.uint8)
+        return out.reshape(-1)
+    if fmt == native.Q4_K:
+        nb = rows * cols // 256
+        out = np.empty((nb, 144), np.uint8)
+        out[:, 0:2] = _fp16_bytes(np.abs(rng.standard_normal(nb)) * sigma / 504)
+        out[:, 2:4] = _fp16_bytes(np.abs(rng.standard_normal(nb)) * sigma / 63)
+        sc = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        m = rng.integers(0, 64, size=(nb, 8), dtype=np.uint8)
+        out[:, 4:8] = (sc[:, :4] & 63) | ((sc[:, 4:] >> 4) << 6)
+        out[:, 8:12] = (m[:, :4] & 63) | ((m[:, 4:] >> 4) << 6)
+        out[:, 12:16] = (sc[:, 4:] & 15) | ((m[:, 4:] & 15) << 4)
+        out[:, 16:] = rng.integers(0, 256, size=(nb, 128), dtype=np.uint8)
+        return out.reshape(-1)
+    raise ValueError(f"format {fmt}")
+
+
+def synth_weights(cfg: Phi4Config, seed: int = 0, distinct_layers: int = 0) -> Phi4Weights:
+    """Random Phi-4-shaped weights.  distinct_layers = 0 gives every layer
+    its own tensors; n > 0 generates n layers and reuses them cyclically
+    (each layer still gets its own device copy when uploaded)."""
+    rng = np.random.default_rng(seed)
+    n = cfg.layers if distinct_layers <= 0 else min(distinct_layers, cfg.layers)
+    shapes = cfg.layer_shapes()
+    gen = {k: [synth_blocks(cfg.weight_format, r, c, rng) for _ in range(n)] for k, (r, c) in shapes.items()}
+    norm = lambda: (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+    attn_norm = [norm() for _ in range(n)]
+    ffn_norm = [norm() for _ in range(n)]
+    pick = lambda lst: [lst[i % n] for i in range(cfg.layers)]
+    return Phi4Weights(
+        embed=synth_blocks(cfg.embed_format, cfg.vocab, cfg.hidden, rng),
+        lm_head=synth_blocks(cfg.head_format, cfg.vocab, cfg.hidden, rng),
+        output_norm=norm(), attn_norm=pick(attn_norm), qkv=pick(gen["qkv"]), o=pick(gen["o"]),
+        ffn_norm=pick(ffn_norm), up=pick(gen["up"]), down=pick(gen["down"]))
+
+
+def synth_kv(cfg: Phi4Config, length: int, seed: int = 1):
+    """fp16 N(0, 1) cache rows for positions < length (zeros beyond), per
+    layer: (k, v) uint16 arrays [kv_heads, capacity, head_dim]."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(cfg.layers):
+        pair = []
+        for _ in range(2):
+            a = np.zeros((cfg.kv_heads, cfg.capacity, cfg.head_dim), np.float16)
+            a[:, :length] = rng.standard_normal((cfg.kv_heads, length, cfg.head_dim)).astype(np.float16)
+            pair.append(a.view(np.uint16))
+        out.append(tuple(pair))
+    return out

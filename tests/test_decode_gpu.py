@@ -1,0 +1,257 @@
+"""GPU parity of the decode-step operators and of the whole Phi-4 decode
+step, through the C ABI, against the oracle.
+
+Gates: row gather bit-exact; fused-norm GEMVs with the GEMV gate
+(1e-3 * max(|t|, rms(t)) elementwise, 1e-5 L2) against the oracle's norm
+followed by the fp64 product; attention 5e-5 L2-relative against an fp64
+evaluation of the same operands (a softmax-weighted sum of ~2000 N(0,1) rows
+cancels to ~1/30 of its terms, which lifts plain FP32 error to ~1e-5);
+appended V rows exact, K rows within one fp16 step; decode-step logits within the reference's model gate
+|d| <= 3e-4 + 3e-4 * |t| (doc/gpu-matvec-performance.md:118-120) and the
+same greedy token.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from sharpinference_amd import native, phi4
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [native.Q8_0, native.Q4_0, native.Q4_K]
+
+
+def close(y, t, rel, l2, what=""):
+    y = np.asarray(y, np.float64)
+    t = np.asarray(t, np.float64)
+    guard = np.sqrt(np.mean(t * t))
+    err = np.abs(y - t)
+    assert np.all(err <= rel * np.maximum(np.abs(t), guard)), f"{what}: max rel {np.max(err / np.maximum(np.abs(t), guard)):.2e}"
+    assert np.linalg.norm(y - t) / np.linalg.norm(t) <= l2, f"{what}: L2 {np.linalg.norm(y - t) / np.linalg.norm(t):.2e}"
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_gather_row_is_exact_and_out_of_range_is_nan(hip, fmt):
+    rows, cols = 300, 3072
+    w = orc.gen_quant(fmt, 9, rows, cols)
+    table = hip.to_device(w)
+    out = hip.alloc(cols * 4)
+    idx = hip.alloc(4)
+    ref = orc.dequant(fmt, w, rows, cols)
+    for row in (0, 17, rows - 1):
+        idx.upload(np.array([row], np.int32))
+        hip.gather_row(fmt, table.ptr, rows, cols, idx.ptr, out.ptr)
+        assert np.array_equal(out.readback(np.float32).view(np.uint32), ref[row].view(np.uint32))
+    for row in (-1, rows):
+        idx.upload(np.array([row], np.int32))
+        hip.gather_row(fmt, table.ptr, rows, cols, idx.ptr, out.ptr)
+        assert np.all(np.isnan(out.readback(np.float32)))
+    for b in (table, out, idx):
+        b.free()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("rows,cols", [(5120, 3072), (16384, 3072), (3072, 1024)])
+def test_rmsnorm_fused_gemv(hip, fmt, rows, cols):
+    w = orc.gen_quant(fmt, rows, rows, cols)
+    x = orc.gen_normal_f32(1 + cols, cols, 0.0, 3.0)
+    g = orc.gen_normal_f32(2 + cols, cols, 1.0, 0.1)
+    dw, dx, dg, dy = hip.to_device(w), hip.to_device(x), hip.to_device(g), hip.alloc(rows * 4)
+    hip.gemv_fused(fmt, dw.ptr, dx.ptr, dy.ptr, rows, cols, xform=native.X_RMSNORM, norm_weight=dg.ptr, eps=1e-5)
+    truth = orc.gemv_f64(fmt, w, orc.rmsnorm(x, g, 1e-5), rows, cols)
+    close(dy.readback(np.float32), truth, 1e-3, 1e-5, "rmsnorm gemv")
+    assert np.array_equal(dx.readback(np.float32), x)        # x is not modified
+    for b in (dw, dx, dg, dy):
+        b.free()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_swiglu_fused_gemv_with_residual(hip, fmt):
+    rows, cols = 3072, 8192
+    w = orc.gen_quant(fmt, 11, rows, cols)
+    gu = orc.gen_normal_f32(12, 2 * cols, 0.0, 2.0)
+    r = orc.gen_normal_f32(13, rows)
+    dw, dx, dy = hip.to_device(w), hip.to_device(gu), hip.to_device(r)
+    hip.gemv_fused(fmt, dw.ptr, dx.ptr, dy.ptr, rows, cols, residual=dy.ptr, xform=native.X_SWIGLU)
+    gate, up = gu[:cols].astype(np.float32), gu[cols:].astype(np.float32)
+    act = (gate / (np.float32(1) + np.exp(-gate)) * up).astype(np.float32)
+    truth = orc.gemv_f64(fmt, w, act, rows, cols) + r.astype(np.float64)
+    close(dy.readback(np.float32), truth, 1e-3, 1e-5, "swiglu gemv")
+    for b in (dw, dx, dy):
+        b.free()
+
+
+def test_fused_transform_rejects_untiled_shapes(hip):
+    w, x, y = hip.alloc(1 << 20), hip.alloc(1 << 16), hip.alloc(1 << 16)
+    with pytest.raises(native.HipError) as e:
+        hip.gemv_fused(native.Q8_0, w.ptr, x.ptr, y.ptr, 8, 96, xform=native.X_SWIGLU)
+    assert e.value.status == native.ERR_UNSUPPORTED
+    with pytest.raises(native.HipError) as e:
+        hip.gemv_fused(native.Q8_0, w.ptr, x.ptr, y.ptr, 8, 1024, xform=native.X_RMSNORM, norm_weight=0)
+    assert e.value.status == native.ERR_ARGUMENT
+    for b in (w, x, y):
+        b.free()
+
+
+def _attention_case(hip, heads, kv_heads, capacity, position, seed):
+    d = 128
+    rng = np.random.default_rng(seed)
+    qkv = rng.standard_normal(heads * d + 2 * kv_heads * d).astype(np.float32)
+    k = np.zeros((kv_heads, capacity, d), np.float16)
+    v = np.zeros((kv_heads, capacity, d), np.float16)
+    k[:, :position] = rng.standard_normal((kv_heads, position, d))
+    v[:, :position] = rng.standard_normal((kv_heads, position, d))
+    k, v = k.view(np.uint16), v.view(np.uint16)
+    dq, dk, dv = hip.to_device(qkv), hip.to_device(k), hip.to_device(v)
+    dout = hip.alloc(heads * d * 4)
+    dpos = hip.to_device(np.array([position], np.int32))
+    ws = hip.alloc(native.attention_workspace_bytes(heads, capacity))
+    args = native.AttentionArgs(dq.ptr, dpos.ptr, dk.ptr, dv.ptr, dout.ptr, ws.ptr, heads, kv_heads, d, 96,
+                                capacity, 10000.0, 1.0)
+    hip.attention(args)
+    out = dout.readback(np.float32)
+    kg, vg = dk.readback(np.uint16).reshape(k.shape), dv.readback(np.uint16).reshape(v.shape)
+    # oracle: rotary on q and k, fp16 append, attention over position + 1 rows
+    H = heads * d
+    q = orc.rope(qkv[:H], heads, d, 96, position, 10000.0, 1.0)
+    knew = orc.rope(qkv[H:H + kv_heads * d], kv_heads, d, 96, position, 10000.0, 1.0)
+    kk, vv = k.copy(), v.copy()
+    kk[:, position] = knew.reshape(kv_heads, d).astype(np.float16).view(np.uint16)
+    vv[:, position] = qkv[H + kv_heads * d:].reshape(kv_heads, d).astype(np.float16).view(np.uint16)
+    truth = orc.attention(q, kk, vv, heads, kv_heads, d, capacity, position + 1)
+    # fp64 evaluation of the same rounded operands
+    group = heads // kv_heads
+    kf = kk.view(np.float16).astype(np.float64)[:, :position + 1]
+    vf = vv.view(np.float16).astype(np.float64)[:, :position + 1]
+    q64 = q.astype(np.float64).reshape(heads, d)
+    t64 = np.empty((heads, d))
+    for h in range(heads):
+        sc = kf[h // group] @ q64[h] / np.sqrt(d)
+        p = np.exp(sc - sc.max())
+        t64[h] = (p / p.sum()) @ vf[h // group]
+    for b in (dq, dk, dv, dout, dpos, ws):
+        b.free()
+    return out, truth, t64.reshape(-1), kg, vg, kk, vv, qkv
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(24, 8), (8, 2), (4, 4)])
+@pytest.mark.parametrize("position", [0, 1, 63, 64, 65, 2048])
+def test_attention_matches_oracle(hip, heads, kv_heads, position):
+    capacity = 2112
+    out, truth, t64, kg, vg, kk, vv, qkv = _attention_case(hip, heads, kv_heads, capacity, position, 100 + position)
+    # against the fp64 evaluation of the same operands: the GEMV gates
+    close(out, t64, 1e-3, 5e-5, "attention vs fp64")
+    # against the oracle's FP32 sequential softmax: both carry FP32 error
+    close(out, truth, 1e-3, 5e-5, "attention vs oracle")
+    # appended rows: V exactly; K within one fp16 step plus the rotation's
+    # FP32 error: pow/cos/sin of two math libraries may differ in the last
+    # bit at angles up to `position` radians, and l*cos - r*sin can cancel
+    # to a small fraction of |l| + |r|; an angle of up to `position` rad
+    # carries about position * 2^-24 rad of error per library, so the bound
+    # is (|l| + |r|) * (position + 1) * 2^-21 on top of one fp16 step
+    assert np.array_equal(vg[:, position], vv[:, position])
+    a = kg[:, position].view(np.float16).astype(np.float32)
+    b = kk[:, position].view(np.float16).astype(np.float32)
+    raw = qkv[heads * 128: heads * 128 + kv_heads * 128].reshape(kv_heads, 128)
+    pair = np.abs(raw).copy()
+    pair[:, :48] += np.abs(raw[:, 48:96])
+    pair[:, 48:96] += np.abs(raw[:, :48])
+    bad = np.argwhere(~(np.abs(a - b) <= 2.0 ** -10 * np.maximum(np.abs(a), np.abs(b)) + 2.0 ** -21 * (position + 1) * pair))
+    assert bad.size == 0, [(tuple(i), float(a[tuple(i)]), float(b[tuple(i)])) for i in bad[:8]]
+    # nothing else in the cache changed
+    mask = np.ones(capacity, bool)
+    mask[position] = False
+    assert np.array_equal(kg[:, mask], kk[:, mask]), np.argwhere(kg[:, mask] != kk[:, mask])[:8]
+    assert np.array_equal(vg[:, mask], vv[:, mask]), np.argwhere(vg[:, mask] != vv[:, mask])[:8]
+
+
+def test_attention_position_outside_cache_yields_nan_and_writes_nothing(hip):
+    heads, kv_heads, capacity, d = 8, 2, 128, 128
+    qkv = np.ones(heads * d + 2 * kv_heads * d, np.float32)
+    dq = hip.to_device(qkv)
+    dk = hip.to_device(np.zeros(kv_heads * capacity * d, np.uint16))
+    dv = hip.to_device(np.zeros(kv_heads * capacity * d, np.uint16))
+    dout, dpos = hip.alloc(heads * d * 4), hip.to_device(np.array([capacity], np.int32))
+    ws = hip.alloc(native.attention_workspace_bytes(heads, capacity))
+    hip.attention(native.AttentionArgs(dq.ptr, dpos.ptr, dk.ptr, dv.ptr, dout.ptr, ws.ptr, heads, kv_heads, d, 96,
+                                       capacity, 10000.0, 1.0))
+    assert np.all(np.isnan(dout.readback(np.float32)))
+    assert not dk.readback(np.uint16).any() and not dv.readback(np.uint16).any()
+    for b in (dq, dk, dv, dout, dpos, ws):
+        b.free()
+
+
+def test_argmax_matches_first_index_rule(hip):
+    ws = hip.alloc(native.argmax_workspace_bytes())
+    out = hip.alloc(4)
+    rng = np.random.default_rng(5)
+    cases = [rng.standard_normal(200064).astype(np.float32), np.array([1, 5, 5, 2], np.float32),
+             np.array([np.nan, 1, 3, np.nan, 3], np.float32), np.full(1000, -np.inf, np.float32),
+             np.full(77, np.nan, np.float32)]
+    big = rng.standard_normal(200064).astype(np.float32)
+    big[150000] = big[190000] = 99.0
+    cases.append(big)
+    for v in cases:
+        dv = hip.to_device(v)
+        hip.argmax(dv.ptr, v.size, ws.ptr, out.ptr)
+        assert int(out.readback(np.int32, 1)[0]) == orc.argmax(v)
+        dv.free()
+    ws.free()
+    out.free()
+
+
+# ---- the decode step -------------------------------------------------------------------
+
+def _run_steps(hip, cfg, weights, kv, steps):
+    """(GPU next tokens + logits, oracle next tokens + logits) for `steps`
+    = [(token, position), ...] on the same weights and starting caches."""
+    sess = phi4.Phi4DecodeSession(hip, cfg, weights)
+    ref = orc.Phi4Oracle(cfg, weights)
+    for l, (k, v) in enumerate(kv):
+        sess.load_kv(l, k, v)
+        ref.k[l][...] = k
+        ref.v[l][...] = v
+    results = []
+    for token, pos in steps:
+        g = sess.forward_token(token, pos)
+        gl = sess.read_logits()
+        o, ol = ref.step(token, pos)
+        results.append((g, gl, o, ol))
+    kv_gpu = [sess.read_kv(l) for l in range(cfg.layers)]
+    sess.close()
+    return results, kv_gpu, ref
+
+
+def _check_logits(g, gl, o, ol, what):
+    d = np.abs(gl.astype(np.float64) - ol)
+    assert np.all(d <= 3e-4 + 3e-4 * np.abs(ol)), f"{what}: worst {np.max(d / (3e-4 + 3e-4 * np.abs(ol))):.2f} of gate"
+    top2 = np.sort(ol)[-2:]
+    if top2[1] - top2[0] > 1e-3 * max(1.0, abs(top2[1])):
+        assert g == o, what
+
+
+def test_small_phi4_decode_steps_match_oracle(hip):
+    cfg = phi4.Phi4Config(layers=3, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=5000, capacity=256)
+    weights = phi4.synth_weights(cfg, seed=21)
+    kv = phi4.synth_kv(cfg, length=70, seed=22)
+    steps = [(11, 70), (4999, 71), (0, 72), (123, 0)]       # continuing context, then an overwrite at 0
+    results, kv_gpu, ref = _run_steps(hip, cfg, weights, kv, steps)
+    for i, (g, gl, o, ol) in enumerate(results):
+        _check_logits(g, gl, o, ol, f"step {i}")
+    for l in range(cfg.layers):
+        for which in (0, 1):
+            a = kv_gpu[l][which].view(np.float16).astype(np.float32)
+            b = (ref.k if which == 0 else ref.v)[l].view(np.float16).astype(np.float32)
+            assert np.allclose(a, b, rtol=2e-3, atol=2e-3), (l, which)
+
+
+def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
+    """32 layers, Phi-4-mini shapes, Q4_K layers, Q8_0
+    embedding and head (200064 x 3072), fp16 KV cache with 2048 tokens of
+    N(0, 1) context, one new token."""
+    cfg = phi4.Phi4Config()
+    weights = phi4.synth_weights(cfg, seed=31)
+    kv = phi4.synth_kv(cfg, length=2048, seed=32)
+    results, _, _ = _run_steps(hip, cfg, weights, kv, [(4242, 2048)])
+    g, gl, o, ol = results[0]
+    _check_logits(g, gl, o, ol, "phi4-mini step")
