@@ -144,19 +144,62 @@ int si_hip_dequant(si_hip_context* ctx, int format, const void* w, float* out, i
 /* Transforms of x fused into the staging of a GEMV. */
 typedef enum si_hip_xform {
     SI_HIP_X_PLAIN = 0,
-    SI_HIP_X_RMSNORM = 1,   /* x_i * (1 / sqrt(sum(x^2) / cols + eps)) * norm_weight_i   */
-    SI_HIP_X_SWIGLU = 2,    /* x = [gate | up] (2 * cols values): gate / (1 + exp(-gate)) * up */
+    SI_HIP_X_RMSNORM = 1,        /* x_i * (1 / sqrt(sum(x^2) / cols + eps)) * norm_weight_i   */
+    SI_HIP_X_SWIGLU = 2,         /* x = [gate | up] (2 * cols values): gate / (1 + exp(-gate)) * up */
+    SI_HIP_X_LAYERNORM = 3,      /* ((x - mean) * (1 / sqrt(var + eps))) * norm_weight + norm_bias */
+    SI_HIP_X_LAYERNORM_MIX = 4,  /* ln = LAYERNORM(x); ln + (prev - ln) * mix                   */
 } si_hip_xform;
+
+/* Functions applied to each output value of a GEMV. */
+typedef enum si_hip_output {
+    SI_HIP_OUT_PLAIN = 0,        /* y = W.x (+ residual)                                        */
+    SI_HIP_OUT_SWIGLU_ROWS = 1,  /* W = [gate rows; up rows] (2 * rows rows): g / (1 + exp(-g)) * u */
+    SI_HIP_OUT_RELU_SQUARE = 2,  /* max(v, 0)^2, NaN kept                                       */
+    SI_HIP_OUT_TANH = 3,
+    SI_HIP_OUT_SIGMOID = 4,      /* 1 / (1 + exp(-v))                                            */
+} si_hip_output;
 
 /* si_hip_gemv with a transform of x applied on the fly (x itself is not
  * modified).  Replaces the RMSNorm (Phi4TextModel.cs:107-128) and SwiGLU
  * (Phi4TextModel.cs:84-89) steps that precede a projection, and the
  * transformer.rms-norm / swiglu dispatches of the D3D12 decode program
- * (Phi4D3D12TextSession.cs:870-912).  Transforms need cols in {1024, 2048,
- * 3072, 4096, 6144, 8192}. */
+ * (Phi4D3D12TextSession.cs:870-912).  xform is PLAIN, RMSNORM or SWIGLU;
+ * transforms need cols in {1024, 2048, 3072, 4096, 6144, 8192}. */
 int si_hip_gemv_fused(si_hip_context* ctx, int format, const void* w, const float* x, float* y,
                       int64_t rows, int64_t cols, const float* residual, int xform,
                       const float* norm_weight, float eps, int* path);
+
+/* One product of si_hip_gemv_batch: y = output(W . input_xform(x)). */
+typedef struct si_hip_gemv_op {
+    int32_t format;              /* SI_HIP_Q8_0 / Q4_0 / Q4_K                                  */
+    int32_t input_xform;         /* si_hip_xform                                               */
+    int32_t output;              /* si_hip_output                                              */
+    int32_t reserved;            /* 0                                                          */
+    const void* weight;          /* [rows (2 * rows for SWIGLU_ROWS), cols] GGUF blocks         */
+    const float* x;              /* [cols] ([2 * cols] for SI_HIP_X_SWIGLU)                    */
+    float* y;                    /* [rows]                                                     */
+    const float* residual;       /* SI_HIP_OUT_PLAIN only: y = W.x + residual; may equal y     */
+    const float* norm_weight;    /* RMSNORM, LAYERNORM*: [cols]                                */
+    const float* norm_bias;      /* LAYERNORM*: [cols]                                         */
+    const float* mix;            /* LAYERNORM_MIX: [cols]                                      */
+    const float* prev;           /* LAYERNORM_MIX: [cols]                                      */
+    float* norm_out;             /* LAYERNORM*, optional: receives the normalised x (pre-mix)  */
+    int64_t rows;
+    int64_t cols;
+    float eps;
+    int32_t reserved2;           /* 0                                                          */
+} si_hip_gemv_op;
+
+/* Runs `count` (1..64) products that have no data dependence on each other:
+ * no op may read or write what another op of the batch writes (y,
+ * norm_out).  Consecutive ops with the same format (and, for the tiled
+ * kernel, the same cols) share one launch, up to 8 per launch.  Replaces a
+ * run of core.mat-vec dispatches between two barriers of a D3D12 entry
+ * (D3D12VmSchedule.cs:74-99, whose pending-write rule this batch enforces),
+ * e.g. the RWKV-7 r/k/v and LoRA projections of one layer
+ * (PortableRwkv7GraphProvider.cs:219-233).  paths (optional) receives
+ * each op's kernel as si_hip_gemv reports it (1 tiled, 2 any-shape). */
+int si_hip_gemv_batch(si_hip_context* ctx, const si_hip_gemv_op* ops, int count, int* paths);
 
 /* out[cols] = FP32 values of row *index of a block-quantized [rows, cols]
  * table; an index outside 0..rows-1 yields NaN values (no out-of-bounds
@@ -228,7 +271,7 @@ typedef struct si_hip_phi4_model {
     float* hidden_state;       /* [hidden] */
     float* qkv;                /* [hidden + 2*kv_heads*128] */
     float* attn;               /* [hidden] */
-    float* gate_up;            /* [2*ffn] */
+    float* gate_up;            /* [2*ffn] scratch (the step uses the first ffn values) */
     float* logits;             /* [vocab] */
     void* workspace;           /* si_hip_phi4_workspace_bytes */
     int32_t* next_token;       /* device int32: argmax of the logits */
@@ -243,6 +286,92 @@ int si_hip_phi4_workspace_bytes(const si_hip_phi4_model* model, uint64_t* bytes)
  * Phi-4 decode program (Phi4D3D12TextSession.Build, Phi4D3D12TextSession.cs:
  * 866-919) and Phi4TextSession.ForwardToken (Phi4TextModel.cs:329-344). */
 int si_hip_phi4_decode(si_hip_context* ctx, const si_hip_phi4_model* model);
+
+/* ---- RWKV-7 decode step ------------------------------------------------------------ */
+
+/* out[b][r] = sum_c matrix[b][r][c] * vector[b][c], FP32.  Replaces:
+ * core.tensor.batched-mat-vec (CpuPrimitiveGraphExecutor.cs:780-791,
+ * GpuTierZeroInstruction.cs:447-451). */
+int si_hip_batched_matvec(si_hip_context* ctx, const float* matrix, const float* vector, float* out,
+                          int batch, int rows, int cols);
+
+/* out = ((x - mean) * (1 / sqrt(var + eps))) * weight + bias over n <= 8192
+ * values (mean and var over the n values).  Replaces: the Normalize +
+ * Affine node chain of the RWKV-7 graph (PortableRwkv7GraphProvider.cs:
+ * 163-170, 180-182). */
+int si_hip_layernorm(si_hip_context* ctx, const float* x, const float* weight, const float* bias, int n,
+                     float eps, float* out);
+
+/* Time-mix core of one RWKV-7 layer after its projections, vectors
+ * [heads * 64]:
+ *   decay = exp(-0.606531 * sigmoid(w_lora + w0)), a = sigmoid(a_lora + a0)
+ *   kn = per-head unit vector of k * k_k;  key = (k + a * (k * k_a)) - k * k_a
+ *   value = v (first layer, also stored to v_first) or
+ *           v + (v_first - v) * sigmoid(v_lora + v0)
+ *   S'[h,i,j] = (S[h,i,j] * decay[j] + value[i] * key[j]) - (S[h,i,:].kn) * kn[j] * a[j]
+ *   y = S' . r;  out = (GroupNorm64e-5(y) * lnx_weight + lnx_bias + value * sum(key * r * r_k)) * gate
+ * with the state updated in place.  Replaces the WKV node chain
+ * (PortableRwkv7GraphProvider.cs:224-276: batched mat-vecs, head outer
+ * products, broadcasts and the pointwise ops around them). */
+typedef struct si_hip_rwkv7_wkv_args {
+    int32_t heads;             /* head size is 64 */
+    int32_t first_layer;
+    const float* r, *k, *v;
+    const float* w_lora, *a_lora, *gate, *v_lora;   /* v_lora unused when first_layer */
+    const float* w0, *a0, *v0, *k_k, *k_a, *r_k, *lnx_weight, *lnx_bias;
+    float* v_first;            /* [heads * 64] */
+    float* state;              /* FP32 [heads][64][64], 16-byte aligned */
+    float* out;                /* [heads * 64] */
+} si_hip_rwkv7_wkv_args;
+
+int si_hip_rwkv7_wkv(si_hip_context* ctx, const si_hip_rwkv7_wkv_args* args);
+
+typedef struct si_hip_rwkv7_layer {
+    const float* ln1_weight, *ln1_bias, *ln2_weight, *ln2_bias;   /* FP32 [hidden] */
+    const float* mix;          /* att.x_rwkvag FP32 [6][hidden]: r, w, k, v, a, g */
+    const void* receptance, *key, *value, *output;   /* [hidden, hidden] */
+    const void* w1, *w2;       /* [rank_w, hidden], [hidden, rank_w] */
+    const void* a1, *a2;       /* [rank_a, hidden], [hidden, rank_a] */
+    const void* g1, *g2;       /* [rank_g, hidden], [hidden, rank_g] */
+    const void* v1, *v2;       /* [rank_v, hidden], [hidden, rank_v]; unused in layer 0 */
+    const float* w0, *a0, *v0, *k_k, *k_a, *r_k, *lnx_weight, *lnx_bias;   /* FP32 [hidden] */
+    const float* ffn_mix;      /* ffn.x_k FP32 [hidden] */
+    const void* ffn_key;       /* [ffn, hidden] */
+    const void* ffn_value;     /* [hidden, ffn] */
+    float* att_prev;           /* state FP32 [hidden] */
+    float* ffn_prev;           /* state FP32 [hidden] */
+    float* wkv;                /* state FP32 [heads][64][64] */
+} si_hip_rwkv7_layer;
+
+typedef struct si_hip_rwkv7_model {
+    int32_t layers, hidden, heads, ffn, vocab;   /* hidden = heads * 64 */
+    int32_t rank_w, rank_a, rank_v, rank_g;
+    int32_t weight_format;     /* every projection, LoRA included (e.g. Q8_0) */
+    int32_t embed_format, head_format;
+    const void* embed;         /* [vocab, hidden] */
+    const float* ln0_weight, *ln0_bias;
+    const si_hip_rwkv7_layer* layer;   /* host array of `layers` entries */
+    const float* ln_out_weight, *ln_out_bias;
+    const void* head;          /* [vocab, hidden] */
+    const int32_t* control;    /* device [token] */
+    float* hidden_state;       /* [hidden] */
+    float* logits;             /* [vocab] */
+    void* workspace;           /* si_hip_rwkv7_workspace_bytes */
+    int32_t* next_token;       /* device int32: argmax of the logits */
+} si_hip_rwkv7_model;
+
+int si_hip_rwkv7_workspace_bytes(const si_hip_rwkv7_model* model, uint64_t* bytes);
+
+/* Launches one RWKV-7 token step for token control[0]: ln0(embedding),
+ * every layer (updating its att_prev / ffn_prev / wkv state), ln_out +
+ * head, argmax.  Six launches per layer: the seven time-mix projections
+ * with LayerNorm + token mix fused (one launch), the four LoRA outputs (one
+ * launch), the time-mix core, the output projection, the channel-mix key
+ * projection with LayerNorm + mix + relu^2 fused, and the value projection.
+ * Inside si_hip_plan_begin/end it records the step as one plan.  Replaces:
+ * the portable RWKV-7 forward-token graph (PortableRwkv7GraphProvider.cs:
+ * 190-292) run by a VM executor. */
+int si_hip_rwkv7_decode(si_hip_context* ctx, const si_hip_rwkv7_model* model);
 
 /* ---- recorded entries and timing -------------------------------------------- */
 

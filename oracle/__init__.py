@@ -40,6 +40,36 @@ class Phi4Model(ctypes.Structure):
                 ("down", _vpp), ("k_cache", _vpp), ("v_cache", _vpp)]
 
 
+_fp = ctypes.c_void_p
+
+
+class Rwkv7WkvArgs(ctypes.Structure):
+    """orc_rwkv7_wkv_args (oracle.h)."""
+    _fields_ = [("heads", ctypes.c_int), ("head_size", ctypes.c_int), ("first_layer", ctypes.c_int)] + \
+        [(n, _fp) for n in ("r", "k", "v", "w_lora", "a_lora", "gate", "v_lora", "w0", "a0", "v0", "k_k", "k_a",
+                            "r_k", "lnx_weight", "lnx_bias", "v_first", "state", "out")]
+
+
+RWKV7_LAYER_FIELDS = ("ln1_weight", "ln1_bias", "ln2_weight", "ln2_bias", "mix", "receptance", "key", "value",
+                      "output", "w1", "w2", "a1", "a2", "g1", "g2", "v1", "v2", "w0", "a0", "v0", "k_k", "k_a",
+                      "r_k", "lnx_weight", "lnx_bias", "ffn_mix", "ffn_key", "ffn_value", "att_prev", "ffn_prev",
+                      "wkv")
+
+
+class Rwkv7Layer(ctypes.Structure):
+    """orc_rwkv7_layer (oracle.h)."""
+    _fields_ = [(n, _fp) for n in RWKV7_LAYER_FIELDS]
+
+
+class Rwkv7Model(ctypes.Structure):
+    """orc_rwkv7_model (oracle.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("layers", "hidden", "heads", "head_size", "ffn", "vocab", "rank_w",
+                                            "rank_a", "rank_v", "rank_g", "weight_format", "embed_format",
+                                            "head_format")] + \
+        [("embed", _fp), ("ln0_weight", _fp), ("ln0_bias", _fp), ("layer", ctypes.POINTER(Rwkv7Layer)),
+         ("ln_out_weight", _fp), ("ln_out_bias", _fp), ("head", _fp)]
+
+
 def build() -> None:
     """Compile liboracle.so from oracle.c (gcc, via the Makefile)."""
     subprocess.run(["make", "-s", "-C", HERE], check=True)
@@ -101,6 +131,16 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_argmax.restype = i32
     l.orc_phi4_decode_step.argtypes = [ctypes.POINTER(Phi4Model), i32, i32, vp, i32]
     l.orc_phi4_decode_step.restype = i32
+    l.orc_sum_f32.argtypes = [vp, i64]
+    l.orc_sum_f32.restype = ctypes.c_float
+    l.orc_layernorm.argtypes = [vp, vp, vp, i32, ctypes.c_float, vp]
+    l.orc_layernorm.restype = None
+    l.orc_rwkv7_wkv_update.argtypes = [i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
+    l.orc_rwkv7_wkv_update.restype = None
+    l.orc_rwkv7_wkv.argtypes = [ctypes.POINTER(Rwkv7WkvArgs)]
+    l.orc_rwkv7_wkv.restype = None
+    l.orc_rwkv7_decode_step.argtypes = [ctypes.POINTER(Rwkv7Model), i32, vp, i32]
+    l.orc_rwkv7_decode_step.restype = i32
     l.orc_now_seconds.restype = dbl
     l.orc_max_threads.restype = i32
 
@@ -282,4 +322,92 @@ class Phi4Oracle:
         nxt = lib().orc_phi4_decode_step(ctypes.byref(self.model), token, position, _ptr(logits), threads)
         if nxt < 0:
             raise ValueError("token or position out of range")
+        return nxt, logits
+
+
+# ---- RWKV-7 ------------------------------------------------------------------
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float32)
+
+
+def sum_f32(a: np.ndarray) -> float:
+    a = _f32(a)
+    return float(lib().orc_sum_f32(_ptr(a), a.size))
+
+
+def layernorm(x: np.ndarray, w=None, b=None, eps: float = 1e-5) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    w = None if w is None else _f32(w)
+    b = None if b is None else _f32(b)
+    lib().orc_layernorm(_ptr(x), None if w is None else _ptr(w), None if b is None else _ptr(b), x.size, eps,
+                        _ptr(out))
+    return out
+
+
+def rwkv7_wkv_update(state: np.ndarray, r, decay, key, value, kn, adapt) -> np.ndarray:
+    """State update + readout (orc_rwkv7_wkv_update); `state` [heads, n, n]
+    float32 is updated in place; returns out [heads * n]."""
+    assert state.dtype == np.float32 and state.flags.c_contiguous and state.ndim == 3
+    heads, n, _ = state.shape
+    vecs = [_f32(v) for v in (r, decay, key, value, kn, adapt)]
+    out = np.empty(heads * n, np.float32)
+    lib().orc_rwkv7_wkv_update(heads, n, _ptr(state), *[_ptr(v) for v in vecs], _ptr(out))
+    return out
+
+
+WKV_VECTORS = ("r", "k", "v", "w_lora", "a_lora", "gate", "v_lora", "w0", "a0", "v0", "k_k", "k_a", "r_k",
+               "lnx_weight", "lnx_bias")
+
+
+def rwkv7_wkv(vec: dict, state: np.ndarray, v_first: np.ndarray, first_layer: bool) -> np.ndarray:
+    """Time-mix core (orc_rwkv7_wkv).  vec maps WKV_VECTORS names to [D]
+    arrays; state [heads, n, n] and v_first [D] float32 are updated in place;
+    returns out [D]."""
+    heads, n, _ = state.shape
+    keep = {k: _f32(vec[k]) for k in WKV_VECTORS}
+    out = np.empty(heads * n, np.float32)
+    args = Rwkv7WkvArgs(heads, n, int(first_layer), *[_ptr(keep[k]) for k in WKV_VECTORS], _ptr(v_first),
+                        _ptr(state), _ptr(out))
+    lib().orc_rwkv7_wkv(ctypes.byref(args))
+    return out
+
+
+class Rwkv7Oracle:
+    """The oracle's copy of one RWKV-7 model: host weights (shared with the
+    device upload) and its own recurrent state, stepped by
+    orc_rwkv7_decode_step.  `weights.layers[l]` maps the layer field names
+    of oracle.h (weights only); `state` is a list of per-layer
+    (att_prev [D], ffn_prev [D], wkv [H, N, N]) arrays, copied."""
+
+    def __init__(self, cfg, weights, state):
+        self.cfg = cfg
+        self.w = weights
+        self.state = [(np.array(a, np.float32), np.array(f, np.float32), np.array(s, np.float32))
+                      for a, f, s in state]
+        self._layers = (Rwkv7Layer * cfg.layers)()
+        for l in range(cfg.layers):
+            L = weights.layers[l]
+            vals = {}
+            for name in RWKV7_LAYER_FIELDS:
+                if name in ("att_prev", "ffn_prev", "wkv"):
+                    continue
+                vals[name] = L[name].ctypes.data if L.get(name) is not None else None
+            att, ffn, wkv = self.state[l]
+            vals.update(att_prev=att.ctypes.data, ffn_prev=ffn.ctypes.data, wkv=wkv.ctypes.data)
+            self._layers[l] = Rwkv7Layer(**vals)
+        self.model = Rwkv7Model(cfg.layers, cfg.hidden, cfg.heads, cfg.head_size, cfg.ffn, cfg.vocab, cfg.rank_w,
+                                cfg.rank_a, cfg.rank_v, cfg.rank_g, cfg.weight_format, cfg.embed_format,
+                                cfg.head_format, weights.embed.ctypes.data, weights.ln0_weight.ctypes.data,
+                                weights.ln0_bias.ctypes.data,
+                                ctypes.cast(self._layers, ctypes.POINTER(Rwkv7Layer)),
+                                weights.ln_out_weight.ctypes.data, weights.ln_out_bias.ctypes.data,
+                                weights.head.ctypes.data)
+
+    def step(self, token: int, threads: int = 0):
+        logits = np.empty(self.cfg.vocab, np.float32)
+        nxt = lib().orc_rwkv7_decode_step(ctypes.byref(self.model), token, _ptr(logits), threads)
+        if nxt < 0:
+            raise ValueError("token out of range")
         return nxt, logits

@@ -576,6 +576,197 @@ int orc_phi4_decode_step(const orc_phi4_model* m, int token, int position, float
 }
 
 /* ------------------------------------------------------------------------ */
+/* RWKV-7 decode step (PortableRwkv7GraphProvider.cs)                        */
+/* ------------------------------------------------------------------------ */
+
+float orc_sum_f32(const float* a, int64_t n)
+{
+    float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int k = 0; k < 8; k++)
+            lane[k] += a[i + k];
+    for (int k = 0; i < n; i++, k++)
+        lane[k] += a[i];
+    return ((lane[0] + lane[4]) + (lane[2] + lane[6])) + ((lane[1] + lane[5]) + (lane[3] + lane[7]));
+}
+
+void orc_layernorm(const float* x, const float* w, const float* b, int n, float eps, float* out)
+{
+    float* c = (float*)malloc((size_t)n * sizeof(float));
+    float mean = orc_sum_f32(x, n) / (float)n;                     /* ReduceMean :129 */
+    for (int i = 0; i < n; i++)
+        c[i] = x[i] - mean;                                        /* centered */
+    for (int i = 0; i < n; i++)
+        out[i] = c[i] * c[i];                                      /* Square */
+    float var = orc_sum_f32(out, n) / (float)n;
+    float inv = 1.0f / sqrtf(var + eps);                           /* ReciprocalSquareRoot(var + eps) */
+    for (int i = 0; i < n; i++) {
+        float v = c[i] * inv;
+        if (w) v = v * w[i];                                       /* Affine :180-182 */
+        if (b) v = v + b[i];
+        out[i] = v;
+    }
+    free(c);
+}
+
+static float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+void orc_rwkv7_wkv_update(int heads, int n, float* state, const float* r, const float* decay, const float* key,
+                          const float* value, const float* kn, const float* adapt, float* out)
+{
+    float* proj = (float*)malloc((size_t)n * sizeof(float));
+    float* ak = (float*)malloc((size_t)n * sizeof(float));
+    for (int h = 0; h < heads; h++) {
+        float* S = state + (int64_t)h * n * n;
+        const int o = h * n;
+        for (int j = 0; j < n; j++)
+            ak[j] = kn[o + j] * adapt[o + j];                      /* adaptedKey :254 */
+        for (int i = 0; i < n; i++)
+            proj[i] = orc_dot_f32(S + (int64_t)i * n, kn + o, n);  /* BatchedMatVec(state, kn) :256 */
+        for (int i = 0; i < n; i++)
+            for (int j = 0; j < n; j++) {
+                float* s = S + (int64_t)i * n + j;
+                float negp = 0.0f - proj[i];
+                *s = (*s * decay[o + j] + value[o + i] * key[o + j]) + negp * ak[j];
+            }
+        for (int i = 0; i < n; i++)
+            out[o + i] = orc_dot_f32(S + (int64_t)i * n, r + o, n); /* BatchedMatVec(updated, r) :270 */
+    }
+    free(proj);
+    free(ak);
+}
+
+void orc_rwkv7_wkv(const orc_rwkv7_wkv_args* a)
+{
+    const int H = a->heads, N = a->head_size, D = H * N;
+    float* decay = (float*)calloc((size_t)D, sizeof(float));
+    float* adapt = (float*)calloc((size_t)D, sizeof(float));
+    float* kn = (float*)calloc((size_t)D, sizeof(float));
+    float* key = (float*)calloc((size_t)D, sizeof(float));
+    float* value = (float*)calloc((size_t)D, sizeof(float));
+    float* tmp = (float*)calloc((size_t)D, sizeof(float));
+    float* y = (float*)calloc((size_t)D, sizeof(float));
+    for (int i = 0; i < D; i++) {
+        decay[i] = expf(-0.606531f * sigmoidf_(a->w_lora[i] + a->w0[i]));   /* :232-234 */
+        adapt[i] = sigmoidf_(a->a_lora[i] + a->a0[i]);                      /* :235-237 */
+    }
+    for (int h = 0; h < H; h++) {                                           /* :241-246 */
+        const int o = h * N;
+        for (int j = 0; j < N; j++) {
+            float sk = a->k[o + j] * a->k_k[o + j];
+            tmp[o + j] = sk * sk;
+        }
+        float squares = orc_sum_f32(tmp + o, N);
+        float inv = 1.0f / sqrtf(squares > 1e-24f ? squares : 1e-24f);
+        for (int j = 0; j < N; j++)
+            kn[o + j] = (a->k[o + j] * a->k_k[o + j]) * inv;
+    }
+    for (int i = 0; i < D; i++) {
+        float ka = a->k[i] * a->k_a[i];                                     /* :247-248 */
+        key[i] = (a->k[i] + adapt[i] * ka) - ka;
+        if (a->first_layer) {                                               /* :249-257 */
+            value[i] = a->v[i];
+            a->v_first[i] = a->v[i];
+        } else {
+            float vg = sigmoidf_(a->v_lora[i] + a->v0[i]);
+            value[i] = a->v[i] + (a->v_first[i] - a->v[i]) * vg;
+        }
+    }
+    orc_rwkv7_wkv_update(H, N, a->state, a->r, decay, key, value, kn, adapt, y);
+    for (int h = 0; h < H; h++) {
+        const int o = h * N;
+        orc_layernorm(y + o, a->lnx_weight + o, a->lnx_bias + o, N, 64e-5f, tmp + o);   /* :272-273, :171-178 */
+        for (int j = 0; j < N; j++)
+            y[o + j] = (key[o + j] * a->r[o + j]) * a->r_k[o + j];         /* bonus factors :274 */
+        float bonus = orc_sum_f32(y + o, N);
+        for (int j = 0; j < N; j++)
+            a->out[o + j] = (tmp[o + j] + value[o + j] * bonus) * a->gate[o + j];   /* :276 */
+    }
+    free(decay); free(adapt); free(kn); free(key); free(value); free(tmp); free(y);
+}
+
+static void mix_(const float* x, const float* prev, const float* mix, int n, float* out)
+{
+    for (int i = 0; i < n; i++)
+        out[i] = x[i] + (prev[i] - x[i]) * mix[i];                      /* Mix :183-184 */
+}
+
+int orc_rwkv7_decode_step(const orc_rwkv7_model* m, int token, float* logits, int threads)
+{
+    const int D = m->hidden, F = m->ffn, fmt = m->weight_format;
+    if (token < 0 || token >= m->vocab)
+        return -1;
+    const int rmax = m->rank_g > m->rank_w ? m->rank_g : m->rank_w;
+    float* x = (float*)malloc((size_t)D * sizeof(float));
+    float* row = (float*)malloc((size_t)D * sizeof(float));
+    float* normed = (float*)malloc((size_t)D * sizeof(float));
+    float* xm = (float*)malloc((size_t)6 * D * sizeof(float));
+    float* r = (float*)malloc((size_t)D * sizeof(float));
+    float* k = (float*)malloc((size_t)D * sizeof(float));
+    float* v = (float*)malloc((size_t)D * sizeof(float));
+    float* wl = (float*)malloc((size_t)D * sizeof(float));
+    float* al = (float*)malloc((size_t)D * sizeof(float));
+    float* g = (float*)malloc((size_t)D * sizeof(float));
+    float* vl = (float*)malloc((size_t)D * sizeof(float));
+    float* h1 = (float*)malloc((size_t)(rmax > m->rank_v ? rmax : m->rank_v) * sizeof(float) + 4 * (size_t)m->rank_a);
+    float* att = (float*)malloc((size_t)D * sizeof(float));
+    float* proj = (float*)malloc((size_t)D * sizeof(float));
+    float* v_first = (float*)malloc((size_t)D * sizeof(float));
+    float* hid = (float*)malloc((size_t)F * sizeof(float));
+    /* x = ln0(emb[token]) (:191-193) */
+    orc_dequant_row(m->embed_format, m->embed + (int64_t)token * orc_row_bytes(m->embed_format, D), D, row);
+    orc_layernorm(row, m->ln0_weight, m->ln0_bias, D, 1e-5f, x);
+    for (int l = 0; l < m->layers; l++) {
+        const orc_rwkv7_layer* L = &m->layer[l];
+        orc_layernorm(x, L->ln1_weight, L->ln1_bias, D, 1e-5f, normed);   /* :202-203 */
+        for (int t = 0; t < 6; t++)                                     /* xr, xw, xk, xv, xa, xg :205-210 */
+            mix_(normed, L->att_prev, L->mix + (int64_t)t * D, D, xm + (int64_t)t * D);
+        const float* xr = xm, *xw = xm + D, *xk = xm + 2 * D, *xv = xm + 3 * D, *xa = xm + 4 * D, *xg = xm + 5 * D;
+        orc_gemv_cpuvm(fmt, L->receptance, xr, r, D, D, threads);
+        orc_gemv_cpuvm(fmt, L->key, xk, k, D, D, threads);
+        orc_gemv_cpuvm(fmt, L->value, xv, v, D, D, threads);
+        orc_gemv_cpuvm(fmt, L->w1, xw, h1, m->rank_w, D, threads);          /* decay LoRA :214-216 */
+        for (int i = 0; i < m->rank_w; i++)
+            h1[i] = tanhf(h1[i]);
+        orc_gemv_cpuvm(fmt, L->w2, h1, wl, D, m->rank_w, threads);
+        orc_gemv_cpuvm(fmt, L->a1, xa, h1, m->rank_a, D, threads);          /* adaptation LoRA :220-222 */
+        orc_gemv_cpuvm(fmt, L->a2, h1, al, D, m->rank_a, threads);
+        orc_gemv_cpuvm(fmt, L->g1, xg, h1, m->rank_g, D, threads);          /* gate LoRA :223-224 */
+        for (int i = 0; i < m->rank_g; i++)
+            h1[i] = sigmoidf_(h1[i]);
+        orc_gemv_cpuvm(fmt, L->g2, h1, g, D, m->rank_g, threads);
+        if (l > 0) {                                                        /* value LoRA :252-254 */
+            orc_gemv_cpuvm(fmt, L->v1, xv, h1, m->rank_v, D, threads);
+            orc_gemv_cpuvm(fmt, L->v2, h1, vl, D, m->rank_v, threads);
+        }
+        orc_rwkv7_wkv_args wa = {m->heads, m->head_size, l == 0, r, k, v, wl, al, g, vl, L->w0, L->a0, L->v0,
+                                 L->k_k, L->k_a, L->r_k, L->lnx_weight, L->lnx_bias, v_first, L->wkv, att};
+        orc_rwkv7_wkv(&wa);
+        orc_gemv_cpuvm(fmt, L->output, att, proj, D, D, threads);           /* :277 */
+        for (int i = 0; i < D; i++)
+            x[i] += proj[i];
+        memcpy(L->att_prev, normed, (size_t)D * sizeof(float));             /* Store :278 */
+        orc_layernorm(x, L->ln2_weight, L->ln2_bias, D, 1e-5f, normed);     /* :280-281 */
+        mix_(normed, L->ffn_prev, L->ffn_mix, D, row);                      /* :282-283 */
+        orc_gemv_cpuvm(fmt, L->ffn_key, row, hid, F, D, threads);
+        for (int i = 0; i < F; i++) {
+            float h = hid[i] > 0.0f ? hid[i] : (hid[i] != hid[i] ? hid[i] : 0.0f);   /* Relu :284-285 */
+            hid[i] = h * h;                                                 /* Square :287 */
+        }
+        orc_gemv_cpuvm(fmt, L->ffn_value, hid, proj, D, F, threads);
+        for (int i = 0; i < D; i++)
+            x[i] += proj[i];
+        memcpy(L->ffn_prev, normed, (size_t)D * sizeof(float));             /* Store :288 */
+    }
+    orc_layernorm(x, m->ln_out_weight, m->ln_out_bias, D, 1e-5f, normed);   /* :290 */
+    orc_gemv_cpuvm(m->head_format, m->head, normed, logits, m->vocab, D, threads);
+    free(x); free(row); free(normed); free(xm); free(r); free(k); free(v); free(wl); free(al); free(g); free(vl);
+    free(h1); free(att); free(proj); free(v_first); free(hid);
+    return orc_argmax(logits, m->vocab);
+}
+
+/* ------------------------------------------------------------------------ */
 
 double orc_now_seconds(void)
 {

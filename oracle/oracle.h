@@ -133,6 +133,67 @@ typedef struct orc_phi4_model {
  * appends this token's fp16 K/V at `position`, returns the argmax. */
 int orc_phi4_decode_step(const orc_phi4_model* m, int token, int position, float* logits, int threads);
 
+/* ---- RWKV-7 decode step (PortableRwkv7GraphProvider.cs:199-290) -------- */
+/* Sum of n floats: 8 lanes in order, fixed merge (the SIMD shape of
+ * TensorPrimitives.Sum, whose exact order the reference does not fix). */
+float orc_sum_f32(const float* a, int64_t n);
+/* Normalize + Affine (:163-170, :180-182): mean = sum/n, c = x - mean,
+ * var = sum(c*c)/n, out = (c * (1/sqrt(var + eps))) * w + b.  w and b may
+ * be NULL (no affine). */
+void orc_layernorm(const float* x, const float* w, const float* b, int n, float eps, float* out);
+
+/* WKV state update of `heads` heads of size n (:255-269), state
+ * [heads][n][n] updated in place:
+ *   proj[i] = sum_l S[i][l] kn[l]
+ *   S'[i][j] = (S[i][j] * decay[j] + value[i] * key[j]) + (-proj[i]) * (kn[j] * adapt[j])
+ *   out[i] = sum_j S'[i][j] r[j]            (BatchedMatVec, :270) */
+void orc_rwkv7_wkv_update(int heads, int n, float* state, const float* r, const float* decay, const float* key,
+                          const float* value, const float* kn, const float* adapt, float* out);
+
+/* The whole time-mix core of one layer after its projections (:224-275):
+ * decay, adaptation, key normalisation, key/value adjustment, the state
+ * update above, GroupNorm (eps 64e-5) + ln_x affine, the r_k bonus and the
+ * gate.  Vectors are [heads * n]; v_first is written when first_layer and
+ * read otherwise. */
+typedef struct orc_rwkv7_wkv_args {
+    int heads, head_size, first_layer;
+    const float* r, *k, *v;
+    const float* w_lora, *a_lora, *gate, *v_lora;     /* w2.tanh(w1.xw), a2.(a1.xa), g2.sigmoid(g1.xg), v2.(v1.xv) */
+    const float* w0, *a0, *v0, *k_k, *k_a, *r_k, *lnx_weight, *lnx_bias;
+    float* v_first;
+    float* state;
+    float* out;
+} orc_rwkv7_wkv_args;
+void orc_rwkv7_wkv(const orc_rwkv7_wkv_args* a);
+
+typedef struct orc_rwkv7_layer {
+    const float* ln1_weight, *ln1_bias, *ln2_weight, *ln2_bias;
+    const float* mix;                                   /* x_rwkvag [6][hidden]: r, w, k, v, a, g */
+    const uint8_t* receptance, *key, *value, *output;   /* [hidden, hidden] */
+    const uint8_t* w1, *w2, *a1, *a2, *g1, *g2, *v1, *v2;   /* [rank, hidden] / [hidden, rank] */
+    const float* w0, *a0, *v0, *k_k, *k_a, *r_k, *lnx_weight, *lnx_bias;
+    const float* ffn_mix;                               /* ffn.x_k [hidden] */
+    const uint8_t* ffn_key, *ffn_value;                 /* [ffn, hidden], [hidden, ffn] */
+    float* att_prev, *ffn_prev;                         /* state [hidden] */
+    float* wkv;                                         /* state [heads][head_size][head_size] */
+} orc_rwkv7_layer;
+
+typedef struct orc_rwkv7_model {
+    int layers, hidden, heads, head_size, ffn, vocab;
+    int rank_w, rank_a, rank_v, rank_g;
+    int weight_format, embed_format, head_format;
+    const uint8_t* embed;                               /* [vocab, hidden] */
+    const float* ln0_weight, *ln0_bias;
+    const orc_rwkv7_layer* layer;
+    const float* ln_out_weight, *ln_out_bias;
+    const uint8_t* head;                                /* [vocab, hidden] */
+} orc_rwkv7_model;
+
+/* One token through the graph (:190-290): writes logits[vocab], updates
+ * every layer's state, returns the argmax, or -1 for a token outside the
+ * vocabulary. */
+int orc_rwkv7_decode_step(const orc_rwkv7_model* m, int token, float* logits, int threads);
+
 /* ---- timing helper for the CPU baseline -------------------------------- */
 double orc_now_seconds(void);
 int orc_max_threads(void);

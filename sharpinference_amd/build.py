@@ -30,6 +30,8 @@ SOURCES = [
     "si_gemv.hip",
     "si_prefill.hip",
     "si_decode.hip",
+    "si_rwkv.hip",
+    "si_rwkv_program.cpp",
 ]
 
 

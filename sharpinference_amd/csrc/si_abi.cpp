@@ -289,7 +289,7 @@ int si_hip_gemv(si_hip_context* ctx, int format, const void* w, const float* x, 
     if (overlaps(y, ybytes, w, wbytes) || overlaps(y, ybytes, x, xbytes) ||
         (residual && residual != y && overlaps(y, ybytes, residual, ybytes)))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv: output overlaps an input");
-    const hipError_t e = si::launch_gemv(format, w, x, y, rows, cols, si::GemvEpilogue{residual}, ctx->stream, path);
+    const hipError_t e = si::launch_gemv(format, w, x, y, rows, cols, residual, ctx->stream, path);
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemv launch");
 }
 

@@ -10,7 +10,7 @@
 // one, softmax, weighted sum of values), and the D3D12 program's argmax
 // (GpuTransformerInstructionCollection.cs:697-748: first index of the
 // maximum) and gather-row (GpuTierZeroInstruction.cs:397-405: an index
-// outside the table yields NaN).  The BASELINE decode step keeps K and V in
+// outside the table yields NaN).  The benchmark decode step keeps K and V in
 // fp16: new rows are rounded to fp16 when appended and attention reads the
 // rounded values back.
 #include "si_internal.hpp"

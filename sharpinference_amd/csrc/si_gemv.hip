@@ -264,12 +264,95 @@ struct QUnit<FMT_Q4_K> {
 // slice for RL consecutive rows.  Partial sums are reduced across the LK
 // lanes with shuffles and across the KS slices through LDS in a fixed
 // order, so results do not depend on timing.
+// ---- launch descriptors -----------------------------------------------------
+
+// Device copy of one GemvOp.  A launch carries up to MAX_SEGS of them by
+// value; op i owns workgroups [wg0_i, wg0_{i+1}).
+struct Seg {
+    const uint8_t* w;
+    const float* x;
+    float* y;
+    const float* residual;
+    const float* nw;        // norm weight
+    const float* nb;        // norm bias
+    const float* mix;
+    const float* prev;
+    float* norm_out;
+    const float* copy_src;
+    float* copy_dst;
+    int rows;               // output rows
+    int wg0;                // first workgroup of this op
+    int in;                 // XformKind
+    int out;                // OutKind
+    int copy_n;
+    int blocks;             // blocks per row (generic kernel)
+    float eps;
+};
+constexpr int MAX_SEGS = 8;
+struct Segs {
+    Seg s[MAX_SEGS];
+    int count;
+};
+
+// Index of the op that owns this workgroup (uniform across the workgroup).
+__device__ __forceinline__ int seg_index(const Segs& t)
+{
+    int si = 0;
+    for (int i = 1; i < t.count; i++)
+        si = static_cast<int>(blockIdx.x) >= t.s[i].wg0 ? i : si;
+    return si;
+}
+
+// Output function of one row (OUT_SWIGLU_ROWS is handled by the callers,
+// which hold both halves).
+__device__ __forceinline__ float finish(const Seg& sg, float v, int r)
+{
+    switch (sg.out) {
+    case OUT_RELU_SQUARE: {
+        const float h = v > 0.0f ? v : (v != v ? v : 0.0f);   // max(v, 0) with NaN kept
+        return h * h;
+    }
+    case OUT_TANH: return tanhf(v);
+    case OUT_SIGMOID: return 1.0f / (1.0f + expf(-v));
+    default: return sg.residual ? v + sg.residual[r] : v;
+    }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+    return g / (1.0f + expf(-g)) * u;
+}
+
+// The op's first workgroup copies copy_n floats (a state store that must
+// happen after every reader of the destination has run).
+__device__ __forceinline__ void side_copy(const Seg& sg, int b, int threads)
+{
+    if (sg.copy_n > 0 && b == 0)
+        for (int i = threadIdx.x; i < sg.copy_n; i += threads)
+            sg.copy_dst[i] = sg.copy_src[i];
+}
+
+// Sum of v over the workgroup, returned to every thread; red holds one
+// float per wave and is not reused before the next barrier.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red)
+{
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4(a.x - m, a.y - m, a.z - m, a.w - m); }
+
 template <int FMT, int LK, int UPL, int RL, int KS, int NW>
-__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __restrict__ W,
-                                                              const float* __restrict__ x,
-                                                              float* __restrict__ y,
-                                                              const float* __restrict__ residual,
-                                                              int rows, GemvXform xf)
+__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
 {
     static_assert(NW % KS == 0, "waves must cover whole row groups");
     constexpr int THREADS = 64 * NW;
@@ -277,6 +360,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     constexpr int ROWS_PER_GROUP = RS * RL;
     constexpr int GROUPS = NW / KS;
     constexpr int ROWS_PER_WG = ROWS_PER_GROUP * GROUPS;
+    constexpr int HALF = ROWS_PER_WG / 2;         // OUT_SWIGLU_ROWS: gate rows, then up rows
+    static_assert(HALF % RL == 0, "a lane's rows stay in one half");
     constexpr int UPS = LK * UPL;                 // units per slice
     constexpr int UPR = UPS * KS;                 // units per row
     constexpr int K = UPR * 64;
@@ -285,8 +370,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
 
     __shared__ float4 xs4[UPR * XS_UNIT / 4];
     __shared__ float bs[UPR * 2];
-    __shared__ float part[KS > 1 ? ROWS_PER_WG * KS : 1];
-    __shared__ float red[NW];
+    __shared__ float part[ROWS_PER_WG * KS];
+    __shared__ float red[NW], red2[NW];
+
+    const Seg& sg = segs.s[seg_index(segs)];
+    const int b = static_cast<int>(blockIdx.x) - sg.wg0;
+    const int rows = sg.rows;
+    const bool swiglu = sg.out == OUT_SWIGLU_ROWS;
+    const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -295,55 +386,55 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     const int lk = lane % LK;
     const int lr = lane / LK;
     const int local_row0 = group * ROWS_PER_GROUP + lr * RL;
-    const int row0 = blockIdx.x * ROWS_PER_WG + local_row0;
     const int unit0 = slice * UPS + lk;
 
-    // 1. issue every weight load of this lane
+    // 1. issue every weight load of this lane (rows past the end are
+    //    clamped into the matrix; their results are dropped)
     QUnit<FMT> w[UPL][RL];
 #pragma unroll
     for (int t = 0; t < RL; t++) {
-        const int r = min(row0 + t, rows - 1);
-        const uint8_t* rp = W + static_cast<int64_t>(r) * ROW_BYTES;
+        const int l = local_row0 + t;
+        int r;
+        if (swiglu) {
+            const int o = min(rb + l % HALF, rows - 1);
+            r = l < HALF ? o : o + rows;
+        } else {
+            r = min(rb + l, rows - 1);
+        }
+        const uint8_t* rp = sg.w + static_cast<int64_t>(r) * ROW_BYTES;
 #pragma unroll
         for (int i = 0; i < UPL; i++)
             w[i][t].load(rp, unit0 + i * LK);
     }
+    side_copy(sg, b, THREADS);
 
     // 2. stage x into LDS (padded per unit); all of this thread's x loads
     //    are issued before the first LDS write
     constexpr int XPT = K / 4 / THREADS;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* x4 = reinterpret_cast<const float4*>(sg.x);
     float4 xr[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; j++)
         xr[j] = x4[threadIdx.x + j * THREADS];
-    if (xf.kind == XF_SWIGLU) {
+    if (sg.in == XF_SWIGLU) {
         // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             const float4 u = x4[K / 4 + threadIdx.x + j * THREADS];
-            xr[j].x = xr[j].x / (1.0f + expf(-xr[j].x)) * u.x;
-            xr[j].y = xr[j].y / (1.0f + expf(-xr[j].y)) * u.y;
-            xr[j].z = xr[j].z / (1.0f + expf(-xr[j].z)) * u.z;
-            xr[j].w = xr[j].w / (1.0f + expf(-xr[j].w)) * u.w;
+            xr[j].x = silu_mul(xr[j].x, u.x);
+            xr[j].y = silu_mul(xr[j].y, u.y);
+            xr[j].z = silu_mul(xr[j].z, u.z);
+            xr[j].w = silu_mul(xr[j].w, u.w);
         }
-    } else if (xf.kind == XF_RMSNORM) {
+    } else if (sg.in == XF_RMSNORM) {
         // scale = 1 / sqrt(sum(x^2) / K + eps); x_i * scale * weight_i
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < XPT; j++)
             ss += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
-        for (int off = 32; off > 0; off >>= 1)
-            ss += __shfl_xor(ss, off);
-        if (lane == 0)
-            red[wave] = ss;
-        __syncthreads();
-        float total = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NW; i++)
-            total += red[i];
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(K) + xf.eps);
-        const float4* g4 = reinterpret_cast<const float4*>(xf.weight);
+        const float total = block_sum<NW>(ss, red);
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(K) + sg.eps);
+        const float4* g4 = reinterpret_cast<const float4*>(sg.nw);
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             const float4 g = g4[threadIdx.x + j * THREADS];
@@ -351,6 +442,48 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             xr[j].y = xr[j].y * scale * g.y;
             xr[j].z = xr[j].z * scale * g.z;
             xr[j].w = xr[j].w * scale * g.w;
+        }
+    } else if (sg.in == XF_LAYERNORM || sg.in == XF_LAYERNORM_MIX) {
+        // mean = sum(x) / K; c = x - mean; var = sum(c^2) / K;
+        // ln = (c * (1 / sqrt(var + eps))) * weight + bias
+        float s1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XPT; j++)
+            s1 += (xr[j].x + xr[j].y) + (xr[j].z + xr[j].w);
+        const float mean = block_sum<NW>(s1, red) / static_cast<float>(K);
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            xr[j] = f4_sub(xr[j], mean);
+            s2 += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
+        }
+        const float var = block_sum<NW>(s2, red2) / static_cast<float>(K);
+        const float inv = 1.0f / sqrtf(var + sg.eps);
+        const float4* g4 = reinterpret_cast<const float4*>(sg.nw);
+        const float4* b4 = reinterpret_cast<const float4*>(sg.nb);
+        const bool store = sg.norm_out != nullptr && b == 0;
+        const bool mixing = sg.in == XF_LAYERNORM_MIX;
+        const float4* m4 = reinterpret_cast<const float4*>(sg.mix);
+        const float4* p4 = reinterpret_cast<const float4*>(sg.prev);
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            const int i = threadIdx.x + j * THREADS;
+            const float4 g = g4[i], bb = b4[i];
+            float4 v;
+            v.x = xr[j].x * inv * g.x + bb.x;
+            v.y = xr[j].y * inv * g.y + bb.y;
+            v.z = xr[j].z * inv * g.z + bb.z;
+            v.w = xr[j].w * inv * g.w + bb.w;
+            if (store)
+                reinterpret_cast<float4*>(sg.norm_out)[i] = v;
+            if (mixing) {
+                const float4 m = m4[i], p = p4[i];
+                v.x = v.x + (p.x - v.x) * m.x;
+                v.y = v.y + (p.y - v.y) * m.y;
+                v.z = v.z + (p.z - v.z) * m.z;
+                v.w = v.w + (p.w - v.w) * m.w;
+            }
+            xr[j] = v;
         }
     }
 #pragma unroll
@@ -421,13 +554,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
                 acc[t] += __shfl_xor(acc[t], off);
         }
     }
-    if constexpr (KS == 1) {
+    if (KS == 1 && !swiglu) {
         if (lk == 0) {
 #pragma unroll
             for (int t = 0; t < RL; t++) {
-                const int r = row0 + t;
+                const int r = rb + local_row0 + t;
                 if (r < rows)
-                    y[r] = residual ? acc[t] + residual[r] : acc[t];
+                    sg.y[r] = finish(sg, acc[t], r);
             }
         }
     } else {
@@ -437,14 +570,23 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
                 part[(local_row0 + t) * KS + slice] = acc[t];
         }
         __syncthreads();
-        if (threadIdx.x < ROWS_PER_WG) {
-            const int r = blockIdx.x * ROWS_PER_WG + threadIdx.x;
-            float v = part[threadIdx.x * KS];
+        const int t = threadIdx.x;
+        if (t < (swiglu ? HALF : ROWS_PER_WG)) {
+            float v = part[t * KS];
 #pragma unroll
             for (int s2 = 1; s2 < KS; s2++)
-                v += part[threadIdx.x * KS + s2];
-            if (r < rows)
-                y[r] = residual ? v + residual[r] : v;
+                v += part[t * KS + s2];
+            const int r = rb + t;
+            if (swiglu) {
+                float u = part[(t + HALF) * KS];
+#pragma unroll
+                for (int s2 = 1; s2 < KS; s2++)
+                    u += part[(t + HALF) * KS + s2];
+                if (r < rows)
+                    sg.y[r] = silu_mul(v, u);
+            } else if (r < rows) {
+                sg.y[r] = finish(sg, v, r);
+            }
         }
     }
 }
@@ -508,26 +650,38 @@ __device__ float block_dot<FMT_Q4_K>(const uint8_t* b, const float* x)
     return a;
 }
 
-// One wave per row, lanes stride over blocks, byte loads (no alignment needs).
 template <int FMT>
-__global__ __launch_bounds__(WG) void gemv_generic_kernel(const uint8_t* __restrict__ W,
-                                                            const float* __restrict__ x,
-                                                            float* __restrict__ y,
-                                                            const float* __restrict__ residual,
-                                                            int rows, int blocks_per_row)
+__device__ __forceinline__ float row_dot(const uint8_t* rp, const float* x, int blocks, int lane)
 {
-    const int row = blockIdx.x * (WG / 64) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows)
-        return;   // whole wave leaves together; no barrier follows
-    const uint8_t* rp = W + static_cast<int64_t>(row) * blocks_per_row * block_bytes(FMT);
     float acc = 0.0f;
-    for (int b = lane; b < blocks_per_row; b += 64)
-        acc += block_dot<FMT>(rp + static_cast<int64_t>(b) * block_bytes(FMT), x + static_cast<int64_t>(b) * block_elems(FMT));
+    for (int k = lane; k < blocks; k += 64)
+        acc += block_dot<FMT>(rp + static_cast<int64_t>(k) * block_bytes(FMT), x + static_cast<int64_t>(k) * block_elems(FMT));
     for (int off = 32; off > 0; off >>= 1)
         acc += __shfl_xor(acc, off);
-    if (lane == 0)
-        y[row] = residual ? acc + residual[row] : acc;
+    return acc;
+}
+
+// One wave per output row, lanes stride over blocks, byte loads (no
+// alignment needs); x is taken as is (no input transform).
+template <int FMT>
+__global__ __launch_bounds__(WG) void gemv_generic_kernel(Segs segs)
+{
+    const Seg& sg = segs.s[seg_index(segs)];
+    const int b = static_cast<int>(blockIdx.x) - sg.wg0;
+    side_copy(sg, b, WG);
+    const int row = b * (WG / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= sg.rows)
+        return;   // whole wave leaves together; no barrier follows
+    const int64_t rbytes = static_cast<int64_t>(sg.blocks) * block_bytes(FMT);
+    const float acc = row_dot<FMT>(sg.w + row * rbytes, sg.x, sg.blocks, lane);
+    if (sg.out == OUT_SWIGLU_ROWS) {
+        const float u = row_dot<FMT>(sg.w + (static_cast<int64_t>(row) + sg.rows) * rbytes, sg.x, sg.blocks, lane);
+        if (lane == 0)
+            sg.y[row] = silu_mul(acc, u);
+    } else if (lane == 0) {
+        sg.y[row] = finish(sg, acc, row);
+    }
 }
 
 // ---- block decoder (bit-exact dequantisation) ----------------------------
@@ -583,13 +737,53 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, uint
 
 // ---- dispatch --------------------------------------------------------------
 
+Seg to_seg(const GemvOp& op)
+{
+    Seg g{};
+    g.w = static_cast<const uint8_t*>(op.w);
+    g.x = op.x;
+    g.y = op.y;
+    g.residual = op.residual;
+    g.nw = op.norm_weight;
+    g.nb = op.norm_bias;
+    g.mix = op.mix;
+    g.prev = op.prev;
+    g.norm_out = op.norm_out;
+    g.copy_src = op.copy_src;
+    g.copy_dst = op.copy_dst;
+    g.copy_n = static_cast<int>(op.copy_n);
+    g.rows = static_cast<int>(op.rows);
+    g.in = op.in;
+    g.out = op.out;
+    g.blocks = static_cast<int>(op.cols / block_elems(op.fmt));
+    g.eps = op.eps;
+    return g;
+}
+
+// Builds the descriptor table of n ops, each taking ceil(rows / rows_per_wg)
+// workgroups; with halve_swiglu, an OUT_SWIGLU_ROWS op puts half as many
+// output rows in a workgroup (its gate and up rows share the tile).
+unsigned fill_segs(Segs& t, const GemvOp* ops, int n, int rows_per_wg, bool halve_swiglu)
+{
+    int wg = 0;
+    t = Segs{};
+    t.count = n;
+    for (int i = 0; i < n; i++) {
+        t.s[i] = to_seg(ops[i]);
+        t.s[i].wg0 = wg;
+        const int per = halve_swiglu && ops[i].out == OUT_SWIGLU_ROWS ? rows_per_wg / 2 : rows_per_wg;
+        wg += static_cast<int>((ops[i].rows + per - 1) / per);
+    }
+    return static_cast<unsigned>(wg);
+}
+
 template <int FMT, int LK, int UPL, int RL, int KS, int NW>
-hipError_t launch_tiled(const uint8_t* w, const float* x, float* y, const float* res, int rows, const GemvXform& xf,
-                        hipStream_t s)
+hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
 {
     constexpr int R = (64 / LK) * RL * (NW / KS);
-    hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW>), dim3((rows + R - 1) / R), dim3(64 * NW), 0, s,
-                       w, x, y, res, rows, xf);
+    Segs t;
+    const unsigned grid = fill_segs(t, ops, n, R, true);
+    hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW>), dim3(grid), dim3(64 * NW), 0, s, t);
     return hipGetLastError();
 }
 
@@ -599,76 +793,103 @@ hipError_t launch_tiled(const uint8_t* w, const float* x, float* y, const float*
 // lane handles one 64-column unit and the grid covers all CUs.  Tall
 // matrices are throughput bound: one wave per row group (KS = 1) with
 // several units and rows per lane amortises the x staging and the
-// reductions over more weights.
+// reductions over more weights.  `rows64` counts the weight rows of every
+// op of the launch.
 template <int FMT>
-bool launch_fast(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows64, int64_t cols,
-                 const GemvXform& xf, hipStream_t s, hipError_t* err)
+hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, hipStream_t s)
 {
-    const int rows = static_cast<int>(rows64);
     const bool mid = rows64 >= 12288, tall = rows64 >= 49152;
     switch (cols) {
-    case 1024: *err = mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(w, x, y, res, rows, xf, s)
-                          : launch_tiled<FMT, 16, 1, 1, 1, 4>(w, x, y, res, rows, xf, s); return true;
-    case 2048: *err = mid ? launch_tiled<FMT, 16, 2, 2, 1, 4>(w, x, y, res, rows, xf, s)
-                          : launch_tiled<FMT, 16, 1, 1, 2, 4>(w, x, y, res, rows, xf, s); return true;
-    case 3072: *err = tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(w, x, y, res, rows, xf, s)
-                    : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(w, x, y, res, rows, xf, s)
-                           : launch_tiled<FMT, 16, 1, 1, 3, 3>(w, x, y, res, rows, xf, s); return true;
-    case 4096: *err = mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(w, x, y, res, rows, xf, s)
-                          : launch_tiled<FMT, 16, 1, 1, 4, 4>(w, x, y, res, rows, xf, s); return true;
-    case 6144: *err = mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(w, x, y, res, rows, xf, s)
-                          : launch_tiled<FMT, 16, 1, 1, 6, 6>(w, x, y, res, rows, xf, s); return true;
-    case 8192: *err = mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(w, x, y, res, rows, xf, s)
-                          : launch_tiled<FMT, 16, 1, 1, 8, 8>(w, x, y, res, rows, xf, s); return true;
-    default: return false;
+    case 1024: return mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
+    case 2048: return mid ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
+    case 3072: return tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s)
+                    : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s)
+                           : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+    case 4096: return mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
+    case 6144: return mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
+    case 8192: return mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
+    default: return hipErrorNotSupported;
     }
 }
 
 template <int FMT>
-hipError_t launch_generic(const uint8_t* w, const float* x, float* y, const float* res, int64_t rows,
-                          int64_t cols, hipStream_t s)
+hipError_t launch_generic(const GemvOp* ops, int n, hipStream_t s)
 {
-    const int rows_per_wg = WG / 64;
-    hipLaunchKernelGGL((gemv_generic_kernel<FMT>), dim3((rows + rows_per_wg - 1) / rows_per_wg), dim3(WG), 0, s,
-                       w, x, y, res, static_cast<int>(rows), static_cast<int>(cols / block_elems(FMT)));
+    Segs t;
+    const unsigned grid = fill_segs(t, ops, n, WG / 64, false);   // one output row per wave
+    hipLaunchKernelGGL((gemv_generic_kernel<FMT>), dim3(grid), dim3(WG), 0, s, t);
     return hipGetLastError();
 }
 
-template <int FMT>
-hipError_t launch_gemv_fmt(const void* wv, const float* x, float* y, int64_t rows, int64_t cols,
-                           const GemvEpilogue& epi, const GemvXform& xf, hipStream_t s, int* path)
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The tiled kernel takes the op: column count in its table, whole-dword
+// weight rows and 16-byte aligned float operands.
+bool tiled_ok(const GemvOp& op)
 {
-    const uint8_t* w = static_cast<const uint8_t*>(wv);
-    const bool aligned = (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
-                         (reinterpret_cast<uintptr_t>(xf.weight) & 15u) == 0;
-    hipError_t err = hipSuccess;
-    if (aligned && launch_fast<FMT>(w, x, y, epi.residual, rows, cols, xf, s, &err)) {
-        if (path) *path = PATH_FAST;
-        return err;
-    }
-    if (xf.kind != XF_PLAIN)
-        return hipErrorNotSupported;
-    if (path) *path = PATH_GENERIC;
-    return launch_generic<FMT>(w, x, y, epi.residual, rows, cols, s);
+    return gemv_tiled_cols(op.cols) && (reinterpret_cast<uintptr_t>(op.w) & 3u) == 0 && aligned16(op.x) &&
+           aligned16(op.norm_weight) && aligned16(op.norm_bias) && aligned16(op.mix) && aligned16(op.prev) &&
+           aligned16(op.norm_out);
 }
 
-}  // namespace
-
-hipError_t launch_gemv_xform(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
-                             const GemvEpilogue& epi, const GemvXform& xf, hipStream_t stream, int* path)
+hipError_t launch_group(const GemvOp* ops, int n, bool tiled, hipStream_t s)
 {
+    const int fmt = ops[0].fmt;
+    if (!tiled) {
+        switch (fmt) {
+        case FMT_Q8_0: return launch_generic<FMT_Q8_0>(ops, n, s);
+        case FMT_Q4_0: return launch_generic<FMT_Q4_0>(ops, n, s);
+        case FMT_Q4_K: return launch_generic<FMT_Q4_K>(ops, n, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
+    int64_t wrows = 0;
+    for (int i = 0; i < n; i++)
+        wrows += ops[i].out == OUT_SWIGLU_ROWS ? 2 * ops[i].rows : ops[i].rows;
     switch (fmt) {
-    case FMT_Q8_0: return launch_gemv_fmt<FMT_Q8_0>(w, x, y, rows, cols, epi, xf, stream, path);
-    case FMT_Q4_0: return launch_gemv_fmt<FMT_Q4_0>(w, x, y, rows, cols, epi, xf, stream, path);
-    case FMT_Q4_K: return launch_gemv_fmt<FMT_Q4_K>(w, x, y, rows, cols, epi, xf, stream, path);
+    case FMT_Q8_0: return launch_fast<FMT_Q8_0>(ops, n, wrows, ops[0].cols, s);
+    case FMT_Q4_0: return launch_fast<FMT_Q4_0>(ops, n, wrows, ops[0].cols, s);
+    case FMT_Q4_K: return launch_fast<FMT_Q4_K>(ops, n, wrows, ops[0].cols, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
-                       const GemvEpilogue& epi, hipStream_t stream, int* path)
+}  // namespace
+
+hipError_t launch_gemv_ops(const GemvOp* ops, int count, hipStream_t stream, int* paths)
 {
-    return launch_gemv_xform(fmt, w, x, y, rows, cols, epi, GemvXform{}, stream, path);
+    int i = 0;
+    while (i < count) {
+        const bool tiled = tiled_ok(ops[i]);
+        if (!tiled && ops[i].in != XF_PLAIN)
+            return hipErrorNotSupported;
+        int n = 1;
+        while (i + n < count && n < MAX_SEGS && ops[i + n].fmt == ops[i].fmt && tiled_ok(ops[i + n]) == tiled &&
+               (!tiled || ops[i + n].cols == ops[i].cols))
+            n++;
+        const hipError_t e = launch_group(ops + i, n, tiled, stream);
+        if (e != hipSuccess)
+            return e;
+        if (paths)
+            for (int k = 0; k < n; k++)
+                paths[i + k] = tiled ? PATH_FAST : PATH_GENERIC;
+        i += n;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
+                       const float* residual, hipStream_t stream, int* path)
+{
+    GemvOp op;
+    op.fmt = fmt;
+    op.w = w;
+    op.x = x;
+    op.y = y;
+    op.rows = rows;
+    op.cols = cols;
+    op.residual = residual;
+    return launch_gemv_ops(&op, 1, stream, path);
 }
 
 bool gemv_tiled_cols(int64_t cols)

@@ -36,33 +36,59 @@ inline int64_t row_bytes(int fmt, int64_t cols)
     return cols / be * block_bytes(fmt);
 }
 
-// Optional work fused around the product y = W . x.
-struct GemvEpilogue {
-    const float* residual = nullptr;   // y = W.x + residual when non-null
-};
-
 // Transform applied to x while it is staged, before the product.
 enum XformKind : int {
     XF_PLAIN = 0,
-    XF_RMSNORM = 1,   // x_i * (1 / sqrt(sum(x^2) / cols + eps)) * weight_i
-    XF_SWIGLU = 2,    // x holds [gate | up] (2 * cols values): gate / (1 + exp(-gate)) * up
+    XF_RMSNORM = 1,        // x_i * (1 / sqrt(sum(x^2) / cols + eps)) * weight_i
+    XF_SWIGLU = 2,         // x holds [gate | up] (2 * cols values): gate / (1 + exp(-gate)) * up
+    XF_LAYERNORM = 3,      // ((x - mean) * (1 / sqrt(var + eps))) * weight + bias
+    XF_LAYERNORM_MIX = 4,  // ln = LAYERNORM(x); ln + (prev - ln) * mix
 };
-struct GemvXform {
-    int kind = XF_PLAIN;
-    const float* weight = nullptr;
+
+// Function applied to each output value (OUT_PLAIN also adds the residual).
+enum OutKind : int {
+    OUT_PLAIN = 0,
+    OUT_SWIGLU_ROWS = 1,   // weight holds [gate rows; up rows]: y_r = g_r / (1 + exp(-g_r)) * u_r
+    OUT_RELU_SQUARE = 2,   // max(v, 0)^2 (NaN stays NaN)
+    OUT_TANH = 3,
+    OUT_SIGMOID = 4,       // 1 / (1 + exp(-v))
+};
+
+// One quantized product y = out(W . in(x)) of a launch.  Several products
+// without data dependences between them share one launch.
+struct GemvOp {
+    int fmt = 0;
+    const void* w = nullptr;
+    const float* x = nullptr;
+    float* y = nullptr;
+    int64_t rows = 0;                    // output rows (OUT_SWIGLU_ROWS reads 2 * rows weight rows)
+    int64_t cols = 0;
+    const float* residual = nullptr;     // OUT_PLAIN: y = W.x + residual (residual may be y)
+    int in = XF_PLAIN;
+    int out = OUT_PLAIN;
+    const float* norm_weight = nullptr;
+    const float* norm_bias = nullptr;
+    const float* mix = nullptr;
+    const float* prev = nullptr;
     float eps = 0.0f;
+    float* norm_out = nullptr;           // XF_LAYERNORM*: the normalised x (before the mix), stored once
+    const float* copy_src = nullptr;     // side job of the op's first workgroup:
+    float* copy_dst = nullptr;           //   copy_dst[0..copy_n) = copy_src[0..copy_n)
+    int64_t copy_n = 0;
 };
 
 // Which kernel a launch used; reported to the caller for tests and profiles.
 enum GemvPath : int { PATH_FAST = 1, PATH_GENERIC = 2 };
 
+// Launches `count` independent products (no op reads what another writes).
+// Consecutive ops that share a format and, for the tiled kernel, a column
+// count go into one launch (up to 8 per launch).  Input transforms need the
+// tiled kernel's column counts and alignment (hipErrorNotSupported
+// otherwise).  paths[i] (optional) receives each op's kernel.
+hipError_t launch_gemv_ops(const GemvOp* ops, int count, hipStream_t stream, int* paths);
+// Plain product with an optional residual.
 hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
-                       const GemvEpilogue& epi, hipStream_t stream, int* path);
-// Same product with a transform of x fused into the staging; only the tiled
-// kernel's column counts take a transform (returns hipErrorNotSupported
-// otherwise).
-hipError_t launch_gemv_xform(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
-                             const GemvEpilogue& epi, const GemvXform& xf, hipStream_t stream, int* path);
+                       const float* residual, hipStream_t stream, int* path);
 bool gemv_tiled_cols(int64_t cols);
 hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, int64_t m, int64_t rows,
                           int64_t cols, hipStream_t stream);

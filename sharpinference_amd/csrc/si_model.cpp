@@ -13,6 +13,8 @@
 #include "si_context.hpp"
 #include "si_decode.hpp"
 
+#include <vector>
+
 using namespace si_abi;
 
 namespace {
@@ -127,9 +129,17 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
     hipError_t e = si::launch_gather_row(m->embed_format, m->embed, m->vocab, H, m->control, m->hidden_state, s);
     for (int l = 0; e == hipSuccess && l < m->layers; l++) {
         const si_hip_phi4_layer& L = m->layer[l];
-        si::GemvXform norm{si::XF_RMSNORM, L.attn_norm, m->rms_eps};
-        e = si::launch_gemv_xform(m->weight_format, L.qkv, m->hidden_state, m->qkv, qkv_rows, H, si::GemvEpilogue{},
-                                  norm, s, nullptr);
+        si::GemvOp qkv;
+        qkv.fmt = m->weight_format;
+        qkv.w = L.qkv;
+        qkv.x = m->hidden_state;
+        qkv.y = m->qkv;
+        qkv.rows = qkv_rows;
+        qkv.cols = H;
+        qkv.in = si::XF_RMSNORM;
+        qkv.norm_weight = L.attn_norm;
+        qkv.eps = m->rms_eps;
+        e = si::launch_gemv_ops(&qkv, 1, s, nullptr);
         if (e != hipSuccess) break;
         si_hip_attention a{};
         a.qkv = m->qkv;
@@ -148,22 +158,38 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
         e = si::launch_attention(attention_args(&a), s);
         if (e != hipSuccess) break;
         // hidden += W_o . attn
-        e = si::launch_gemv(m->weight_format, L.o, m->attn, m->hidden_state, H, H, si::GemvEpilogue{m->hidden_state}, s,
+        e = si::launch_gemv(m->weight_format, L.o, m->attn, m->hidden_state, H, H, m->hidden_state, s, nullptr);
+        if (e != hipSuccess) break;
+        // act = silu(gate) * up, gate and up rows of W_up on RMSNorm(hidden)
+        si::GemvOp up;
+        up.fmt = m->weight_format;
+        up.w = L.up;
+        up.x = m->hidden_state;
+        up.y = m->gate_up;
+        up.rows = m->ffn;
+        up.cols = H;
+        up.in = si::XF_RMSNORM;
+        up.out = si::OUT_SWIGLU_ROWS;
+        up.norm_weight = L.ffn_norm;
+        up.eps = m->rms_eps;
+        e = si::launch_gemv_ops(&up, 1, s, nullptr);
+        if (e != hipSuccess) break;
+        // hidden += W_down . act
+        e = si::launch_gemv(m->weight_format, L.down, m->gate_up, m->hidden_state, H, m->ffn, m->hidden_state, s,
                             nullptr);
-        if (e != hipSuccess) break;
-        si::GemvXform fnorm{si::XF_RMSNORM, L.ffn_norm, m->rms_eps};
-        e = si::launch_gemv_xform(m->weight_format, L.up, m->hidden_state, m->gate_up, 2 * m->ffn, H, si::GemvEpilogue{},
-                                  fnorm, s, nullptr);
-        if (e != hipSuccess) break;
-        // hidden += W_down . (silu(gate) * up)
-        si::GemvXform swiglu{si::XF_SWIGLU, nullptr, 0.0f};
-        e = si::launch_gemv_xform(m->weight_format, L.down, m->gate_up, m->hidden_state, H, m->ffn,
-                                  si::GemvEpilogue{m->hidden_state}, swiglu, s, nullptr);
     }
     if (e == hipSuccess) {
-        si::GemvXform onorm{si::XF_RMSNORM, m->output_norm, m->rms_eps};
-        e = si::launch_gemv_xform(m->head_format, m->lm_head, m->hidden_state, m->logits, m->vocab, H, si::GemvEpilogue{},
-                                  onorm, s, nullptr);
+        si::GemvOp head;
+        head.fmt = m->head_format;
+        head.w = m->lm_head;
+        head.x = m->hidden_state;
+        head.y = m->logits;
+        head.rows = m->vocab;
+        head.cols = H;
+        head.in = si::XF_RMSNORM;
+        head.norm_weight = m->output_norm;
+        head.eps = m->rms_eps;
+        e = si::launch_gemv_ops(&head, 1, s, nullptr);
     }
     if (e == hipSuccess)
         e = si::launch_argmax(m->logits, m->vocab, am_ws, m->next_token, s);
@@ -202,10 +228,120 @@ int si_hip_gemv_fused(si_hip_context* ctx, int format, const void* w, const floa
     if (overlaps(y, ybytes, w, wbytes) || overlaps(y, ybytes, x, xbytes) ||
         (residual && residual != y && overlaps(y, ybytes, residual, ybytes)))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_fused: output overlaps an input");
-    si::GemvXform xf{xform, norm_weight, eps};
-    const hipError_t e = si::launch_gemv_xform(format, w, x, y, rows, cols, si::GemvEpilogue{residual}, xf, ctx->stream,
-                                               path);
+    si::GemvOp op;
+    op.fmt = format;
+    op.w = w;
+    op.x = x;
+    op.y = y;
+    op.rows = rows;
+    op.cols = cols;
+    op.residual = residual;
+    op.in = xform;
+    op.norm_weight = norm_weight;
+    op.eps = eps;
+    const hipError_t e = si::launch_gemv_ops(&op, 1, ctx->stream, path);
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemv_fused launch");
+}
+
+int si_hip_gemv_batch(si_hip_context* ctx, const si_hip_gemv_op* ops, int count, int* paths)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "gemv_batch: null context");
+    Enter g(ctx);
+    if (g.err != hipSuccess)
+        return hip_fail(ctx, g.err, "hipSetDevice");
+    if (!ops || count < 1 || count > 64)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: need 1..64 ops, got %d", count);
+    struct Range {
+        const void* p;
+        uint64_t n;
+    };
+    std::vector<std::vector<Range>> reads(count), writes(count);
+    std::vector<si::GemvOp> launch(count);
+    for (int i = 0; i < count; i++) {
+        const si_hip_gemv_op& o = ops[i];
+        if (o.reserved != 0 || o.reserved2 != 0)
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: reserved fields must be 0", i);
+        if (o.output < SI_HIP_OUT_PLAIN || o.output > SI_HIP_OUT_SIGMOID)
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: unknown output function %d", i, o.output);
+        if (o.input_xform < SI_HIP_X_PLAIN || o.input_xform > SI_HIP_X_LAYERNORM_MIX)
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: unknown transform %d", i, o.input_xform);
+        const bool swiglu_rows = o.output == SI_HIP_OUT_SWIGLU_ROWS;
+        const bool ln = o.input_xform == SI_HIP_X_LAYERNORM || o.input_xform == SI_HIP_X_LAYERNORM_MIX;
+        uint64_t wbytes = 0;
+        if (const int rc = check_matrix(ctx, "gemv_batch", o.format, o.weight, swiglu_rows ? 2 * o.rows : o.rows,
+                                        o.cols, &wbytes))
+            return rc;
+        if (!o.x || !o.y || !aligned(o.y, 4) || !aligned(o.x, 4) || (o.residual && !aligned(o.residual, 4)))
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: null or misaligned FP32 operand", i);
+        if (o.residual && o.output != SI_HIP_OUT_PLAIN)
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: a residual needs the plain output", i);
+        if (o.input_xform != SI_HIP_X_PLAIN) {
+            if (!si::gemv_tiled_cols(o.cols))
+                return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                            "gemv_batch: op %d: a fused transform needs cols in {1024, 2048, 3072, 4096, 6144, 8192}, "
+                            "got %lld", i, static_cast<long long>(o.cols));
+            if (!aligned(o.x, 16) || !aligned(o.weight, 4))
+                return fail(ctx, SI_HIP_ERR_ARGUMENT,
+                            "gemv_batch: op %d: a fused transform needs x 16-byte and W 4-byte aligned", i);
+        }
+        const bool need_w = o.input_xform == SI_HIP_X_RMSNORM || ln;
+        if (need_w && (!o.norm_weight || !aligned(o.norm_weight, 16)))
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: norm weight must be a 16-byte aligned pointer", i);
+        if (ln && (!o.norm_bias || !aligned(o.norm_bias, 16)))
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: norm bias must be a 16-byte aligned pointer", i);
+        if (o.input_xform == SI_HIP_X_LAYERNORM_MIX &&
+            (!o.mix || !o.prev || !aligned(o.mix, 16) || !aligned(o.prev, 16)))
+            return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d: mix and prev must be 16-byte aligned pointers", i);
+        if (o.norm_out && (!ln || !aligned(o.norm_out, 16)))
+            return fail(ctx, SI_HIP_ERR_ARGUMENT,
+                        "gemv_batch: op %d: norm_out needs a layer-norm transform and 16-byte alignment", i);
+        const uint64_t cb = static_cast<uint64_t>(o.cols) * 4, yb = static_cast<uint64_t>(o.rows) * 4;
+        reads[i] = {{o.weight, wbytes}, {o.x, o.input_xform == SI_HIP_X_SWIGLU ? 2 * cb : cb}};
+        if (need_w) reads[i].push_back({o.norm_weight, cb});
+        if (ln) reads[i].push_back({o.norm_bias, cb});
+        if (o.input_xform == SI_HIP_X_LAYERNORM_MIX) {
+            reads[i].push_back({o.mix, cb});
+            reads[i].push_back({o.prev, cb});
+        }
+        writes[i] = {{o.y, yb}};
+        if (o.norm_out) writes[i].push_back({o.norm_out, cb});
+        // the residual may be y itself (an in-place accumulate); any other
+        // overlap with a write is rejected below
+        if (o.residual && o.residual != o.y) reads[i].push_back({o.residual, yb});
+
+        si::GemvOp& op = launch[i];
+        op.fmt = o.format;
+        op.w = o.weight;
+        op.x = o.x;
+        op.y = o.y;
+        op.rows = o.rows;
+        op.cols = o.cols;
+        op.residual = o.residual;
+        op.in = o.input_xform;
+        op.out = o.output;
+        op.norm_weight = o.norm_weight;
+        op.norm_bias = o.norm_bias;
+        op.mix = o.mix;
+        op.prev = o.prev;
+        op.norm_out = o.norm_out;
+        op.eps = o.eps;
+    }
+    // Pending-write rule of one barrier interval (D3D12VmSchedule.cs:74-99):
+    // nothing an op writes may be read or written by any op of the batch,
+    // the op itself included (except its own residual == y).
+    for (int i = 0; i < count; i++)
+        for (const Range& wr : writes[i])
+            for (int j = 0; j < count; j++) {
+                for (const Range& rd : reads[j])
+                    if (overlaps(wr.p, wr.n, rd.p, rd.n))
+                        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: op %d writes what op %d reads", i, j);
+                for (const Range& w2 : writes[j])
+                    if (&w2 != &wr && overlaps(wr.p, wr.n, w2.p, w2.n))
+                        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemv_batch: ops %d and %d write overlapping memory", i, j);
+            }
+    const hipError_t e = si::launch_gemv_ops(launch.data(), count, ctx->stream, paths);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemv_batch launch");
 }
 
 int si_hip_gather_row(si_hip_context* ctx, int format, const void* table, int64_t rows, int64_t cols,

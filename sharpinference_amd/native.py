@@ -55,7 +55,25 @@ SIGNATURES = {
     "si_hip_timer_end": ([_vp, ctypes.POINTER(_dbl)], _i32),
 }
 
-X_PLAIN, X_RMSNORM, X_SWIGLU = 0, 1, 2
+X_PLAIN, X_RMSNORM, X_SWIGLU, X_LAYERNORM, X_LAYERNORM_MIX = 0, 1, 2, 3, 4
+OUT_PLAIN, OUT_SWIGLU_ROWS, OUT_RELU_SQUARE, OUT_TANH, OUT_SIGMOID = 0, 1, 2, 3, 4
+
+
+class GemvOp(ctypes.Structure):
+    """si_hip_gemv_op."""
+    _fields_ = [("format", _i32), ("input_xform", _i32), ("output", _i32), ("reserved", _i32),
+                ("weight", _vp), ("x", _vp), ("y", _vp), ("residual", _vp), ("norm_weight", _vp),
+                ("norm_bias", _vp), ("mix", _vp), ("prev", _vp), ("norm_out", _vp), ("rows", _i64),
+                ("cols", _i64), ("eps", ctypes.c_float), ("reserved2", _i32)]
+
+
+def gemv_op(fmt: int, w: int, x: int, y: int, rows: int, cols: int, *, xform: int = X_PLAIN,
+            output: int = OUT_PLAIN, residual: int = 0, norm_weight: int = 0, norm_bias: int = 0,
+            mix: int = 0, prev: int = 0, norm_out: int = 0, eps: float = 0.0) -> GemvOp:
+    """One product for HipContext.gemv_batch (device pointers as ints)."""
+    p = lambda v: int(v) or None
+    return GemvOp(fmt, xform, output, 0, p(w), p(x), p(y), p(residual), p(norm_weight), p(norm_bias),
+                  p(mix), p(prev), p(norm_out), rows, cols, eps, 0)
 
 
 class AttentionArgs(ctypes.Structure):
@@ -83,9 +101,40 @@ class Phi4Model(ctypes.Structure):
                 ("logits", _vp), ("workspace", _vp), ("next_token", _vp)]
 
 
+RWKV7_WKV_VECTORS = ("r", "k", "v", "w_lora", "a_lora", "gate", "v_lora", "w0", "a0", "v0", "k_k", "k_a", "r_k",
+                     "lnx_weight", "lnx_bias")
+
+
+class Rwkv7WkvArgs(ctypes.Structure):
+    """si_hip_rwkv7_wkv_args."""
+    _fields_ = [("heads", _i32), ("first_layer", _i32)] + [(n, _vp) for n in RWKV7_WKV_VECTORS] + \
+        [("v_first", _vp), ("state", _vp), ("out", _vp)]
+
+
+RWKV7_LAYER_FIELDS = ("ln1_weight", "ln1_bias", "ln2_weight", "ln2_bias", "mix", "receptance", "key", "value",
+                      "output", "w1", "w2", "a1", "a2", "g1", "g2", "v1", "v2", "w0", "a0", "v0", "k_k", "k_a",
+                      "r_k", "lnx_weight", "lnx_bias", "ffn_mix", "ffn_key", "ffn_value", "att_prev", "ffn_prev",
+                      "wkv")
+
+
+class Rwkv7Layer(ctypes.Structure):
+    """si_hip_rwkv7_layer."""
+    _fields_ = [(n, _vp) for n in RWKV7_LAYER_FIELDS]
+
+
+class Rwkv7Model(ctypes.Structure):
+    """si_hip_rwkv7_model."""
+    _fields_ = [(n, _i32) for n in ("layers", "hidden", "heads", "ffn", "vocab", "rank_w", "rank_a", "rank_v",
+                                    "rank_g", "weight_format", "embed_format", "head_format")] + \
+        [("embed", _vp), ("ln0_weight", _vp), ("ln0_bias", _vp), ("layer", ctypes.POINTER(Rwkv7Layer)),
+         ("ln_out_weight", _vp), ("ln_out_bias", _vp), ("head", _vp), ("control", _vp), ("hidden_state", _vp),
+         ("logits", _vp), ("workspace", _vp), ("next_token", _vp)]
+
+
 SIGNATURES.update({
     "si_hip_gemv_fused": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp, ctypes.c_float,
                            ctypes.POINTER(_i32)], _i32),
+    "si_hip_gemv_batch": ([_vp, ctypes.POINTER(GemvOp), _i32, ctypes.POINTER(_i32)], _i32),
     "si_hip_gather_row": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp], _i32),
     "si_hip_attention_workspace_bytes": ([_i32, _i32, ctypes.POINTER(_u64)], _i32),
     "si_hip_attention_decode": ([_vp, ctypes.POINTER(AttentionArgs)], _i32),
@@ -93,6 +142,11 @@ SIGNATURES.update({
     "si_hip_argmax": ([_vp, _vp, _i64, _vp, _vp], _i32),
     "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
     "si_hip_phi4_decode": ([_vp, ctypes.POINTER(Phi4Model)], _i32),
+    "si_hip_batched_matvec": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
+    "si_hip_layernorm": ([_vp, _vp, _vp, _vp, _i32, ctypes.c_float, _vp], _i32),
+    "si_hip_rwkv7_wkv": ([_vp, ctypes.POINTER(Rwkv7WkvArgs)], _i32),
+    "si_hip_rwkv7_workspace_bytes": ([ctypes.POINTER(Rwkv7Model), ctypes.POINTER(_u64)], _i32),
+    "si_hip_rwkv7_decode": ([_vp, ctypes.POINTER(Rwkv7Model)], _i32),
 })
 
 _lib: Optional[ctypes.CDLL] = None
@@ -267,6 +321,13 @@ class HipContext:
                    ctypes.c_void_p(int(norm_weight) or None), ctypes.c_float(eps), ctypes.byref(path))
         return path.value
 
+    def gemv_batch(self, ops: Sequence[GemvOp]) -> list:
+        """Runs independent products (si_hip_gemv_batch); returns each op's path."""
+        arr = (GemvOp * len(ops))(*ops)
+        paths = (ctypes.c_int * len(ops))()
+        self._call(lib().si_hip_gemv_batch, arr, len(ops), paths)
+        return list(paths)
+
     def gather_row(self, fmt: int, table: int, rows: int, cols: int, index: int, out: int) -> None:
         self._call(lib().si_hip_gather_row, fmt, ctypes.c_void_p(int(table)), rows, cols,
                    ctypes.c_void_p(int(index)), ctypes.c_void_p(int(out)))
@@ -280,6 +341,20 @@ class HipContext:
 
     def phi4_decode(self, model: Phi4Model) -> None:
         self._call(lib().si_hip_phi4_decode, ctypes.byref(model))
+
+    def batched_matvec(self, matrix: int, vector: int, out: int, batch: int, rows: int, cols: int) -> None:
+        self._call(lib().si_hip_batched_matvec, ctypes.c_void_p(int(matrix)), ctypes.c_void_p(int(vector)),
+                   ctypes.c_void_p(int(out)), batch, rows, cols)
+
+    def layernorm(self, x: int, weight: int, bias: int, n: int, eps: float, out: int) -> None:
+        self._call(lib().si_hip_layernorm, ctypes.c_void_p(int(x)), ctypes.c_void_p(int(weight)),
+                   ctypes.c_void_p(int(bias)), n, ctypes.c_float(eps), ctypes.c_void_p(int(out)))
+
+    def rwkv7_wkv(self, args: Rwkv7WkvArgs) -> None:
+        self._call(lib().si_hip_rwkv7_wkv, ctypes.byref(args))
+
+    def rwkv7_decode(self, model: Rwkv7Model) -> None:
+        self._call(lib().si_hip_rwkv7_decode, ctypes.byref(model))
 
     def dequant(self, fmt: int, w: int, out: int, rows: int, cols: int) -> None:
         self._call(lib().si_hip_dequant, fmt, ctypes.c_void_p(int(w)), ctypes.c_void_p(int(out)), rows, cols)
@@ -334,6 +409,12 @@ def argmax_workspace_bytes() -> int:
 def phi4_workspace_bytes(model: Phi4Model) -> int:
     out = ctypes.c_uint64(0)
     _check(lib().si_hip_phi4_workspace_bytes(ctypes.byref(model), ctypes.byref(out)))
+    return out.value
+
+
+def rwkv7_workspace_bytes(model: Rwkv7Model) -> int:
+    out = ctypes.c_uint64(0)
+    _check(lib().si_hip_rwkv7_workspace_bytes(ctypes.byref(model), ctypes.byref(out)))
     return out.value
 
 

@@ -246,7 +246,7 @@ def test_small_phi4_decode_steps_match_oracle(hip):
 
 
 def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
-    """32 layers, Phi-4-mini shapes, Q4_K layers, Q8_0
+    """The full decode workload: 32 layers, Phi-4-mini shapes, Q4_K layers, Q8_0
     embedding and head (200064 x 3072), fp16 KV cache with 2048 tokens of
     N(0, 1) context, one new token."""
     cfg = phi4.Phi4Config()

@@ -1,6 +1,6 @@
 """GPU parity of the quantized matrix-vector product, through the C ABI.
 
-Gates (BASELINE north star): dequantised weights bit-exact; GEMV
+Gates: dequantised weights bit-exact; GEMV
 |y - t| <= 1e-3 * max(|t|, rms(t)) elementwise (the rms term is the near-zero
 guard) and ||y - t|| / ||t|| <= 1e-5, where t is the oracle's fp64 product
 over the exactly dequantised weights.  The reference fixtures keep their own

@@ -1,6 +1,6 @@
 """GPU parity of the batched prefill product Y = X . W^T (MFMA), through the C ABI.
 
-Gates: the BASELINE prefill tolerance, 2e-2 relative against the oracle's
+Gates: the prefill tolerance, 2e-2 relative against the oracle's
 fp64 product over the exactly dequantised weights,
 |y - t| <= 2e-2 * max(|t|, rms(t)) elementwise and ||y - t|| / ||t|| <= 2e-2,
 and, to pin the matrix-core data layout itself, 1e-5 L2-relative against the
