@@ -72,6 +72,12 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill (MFMA) measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the Phi-4-mini decode-step measurement")
+    ap.add_argument("--no-rwkv", action="store_true", help="skip the RWKV-7 token-step measurement")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the Phi-4 and RWKV-7 token loops (one token at a time, no back-to-back "
+                         "replays, no CPU leg); prints their JSON; for kernel-trace profiles")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --decode-only: launch each step kernel by kernel instead of replaying its graph")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before timing, copy this many MiB device-to-device once (a plain copy of "
                          "known size that scales the HBM byte counters of a profiler run)")
@@ -86,6 +92,16 @@ def main() -> int:
         return 2
 
     from sharpinference_amd import native
+
+    if args.decode_only:
+        hip = native.HipContext(0)
+        res = {"decode": None if args.no_decode else bench_decode(hip, cpu=False, replay_timing=False,
+                                                                   eager=args.eager),
+               "decode_rwkv7": None if args.no_rwkv else bench_rwkv_decode(hip, cpu=False, replay_timing=False,
+                                                                           eager=args.eager)}
+        hip.close()
+        print(json.dumps(res), flush=True)
+        return 0
 
     desc, fmt, shapes = CONFIGS[args.config]
     rng = np.random.default_rng(20250101)
@@ -168,7 +184,8 @@ def main() -> int:
         log(f"  {name:8s} {rows}x{cols}: {us:.3f} us/launch, {b / us / 1e3:.1f} GB/s")
 
     prefill = None if args.no_prefill else bench_prefill(hip, rng)
-    decode = None if args.no_decode else bench_decode(hip)
+    decode = None if args.no_decode else bench_decode(hip, cpu=not args.no_cpu)
+    rwkv = None if args.no_rwkv else bench_rwkv_decode(hip, cpu=not args.no_cpu)
 
     # dispatch floor: the same graph mechanism with 64 one-wave fill kernels
     scratch = hip.alloc(4096)
@@ -205,6 +222,7 @@ def main() -> int:
         "dispatch_floor_us": round(floor_us, 3),
         "prefill": prefill,
         "decode": decode,
+        "decode_rwkv7": rwkv,
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 1),
@@ -256,12 +274,34 @@ def bench_prefill(hip, rng, m: int = 512):
     return out
 
 
-def bench_decode(hip, context: int = 2048, tokens: int = 64):
+def cpu_threads() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+
+
+def r1(v):
+    """Rounded value, None for a measurement that was not taken (NaN)."""
+    return None if v != v else round(v, 1)
+
+
+def time_cpu_steps(step, samples: int = 3) -> float:
+    """Median seconds of `samples` oracle token steps after one warm-up."""
+    step()
+    times = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, replay_timing: bool = True,
+                 eager: bool = False):
     """Phi-4-mini-shaped decode step (32 layers, Q4_K layers, Q8_0 embedding
     and head, fp16 KV cache holding `context` tokens), one new token per
     step.  Steady state: the recorded step replayed back to back at position
     `context`; loop: forward_token (control upload, replay, next-token
-    readback) over `tokens` consecutive positions."""
+    readback) over `tokens` consecutive positions.  CPU: the oracle's decode
+    step (CpuVm restatement) on the same weights and cache."""
     from sharpinference_amd import phi4
     cfg = phi4.Phi4Config()
     t0 = time.time()
@@ -270,29 +310,103 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64):
     kv = phi4.synth_kv(phi4.Phi4Config(layers=1, capacity=cfg.capacity), context, seed=8)[0]
     for l in range(cfg.layers):
         sess.load_kv(l, *kv)
-    del weights
     log(f"decode: model on device in {time.time() - t0:.1f} s")
     sess.set_control(1, context)
     sess.plan.launch()
     hip.sync()
-    us = sorted(sess.plan.measure_us(16) for _ in range(5))[2]
+    us = sorted(sess.plan.measure_us(16) for _ in range(5))[2] if replay_timing else float("nan")
     step_bytes = cfg.weight_bytes_per_token() + cfg.kv_bytes(context + 1)
     gbs = step_bytes / us / 1e3
     t0 = time.perf_counter()
     tok = 1
     for i in range(tokens):
-        tok = sess.forward_token(tok, context + i)
+        if eager:   # the same step launched kernel by kernel instead of as one graph replay
+            sess.set_control(tok, context + i)
+            hip.phi4_decode(sess.model)
+            tok = int(sess.next_token.readback(np.int32, 1)[0])
+        else:
+            tok = sess.forward_token(tok, context + i)
     loop_s = (time.perf_counter() - t0) / tokens
     sess.close()
     log(f"decode: {us:.1f} us/token on device ({1e6 / us:.0f} tok/s, {gbs:.0f} GB/s), "
         f"{loop_s * 1e6:.1f} us/token with host round trips")
-    return {"workload": "Phi-4-mini decode step, 32 layers, Q4_K layers, Q8_0 embedding/head 200064x3072, "
-                        f"fp16 KV cache with {context} tokens, batch 1",
-            "us_per_token": round(us, 1), "tok_s": round(1e6 / us, 1),
-            "bytes_per_token": step_bytes, "GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
-            "loop_us_per_token": round(loop_s * 1e6, 1), "loop_tok_s": round(1.0 / loop_s, 1),
-            "layer_weights": "4 distinct layers uploaded as 32 separate device copies"}
+    out = {"workload": "Phi-4-mini decode step, 32 layers, Q4_K layers, Q8_0 embedding/head 200064x3072, "
+                       f"fp16 KV cache with {context} tokens, batch 1",
+           "us_per_token": r1(us), "tok_s": r1(1e6 / us),
+           "bytes_per_token": step_bytes, "GBs": r1(gbs), "hbm_frac": None if gbs != gbs else round(gbs / HBM_PEAK_GBS, 4),
+           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
+           "loop_us_per_token": round(loop_s * 1e6, 1), "loop_tok_s": round(1.0 / loop_s, 1),
+           "layer_weights": "4 distinct layers uploaded as 32 separate device copies"}
+    if cpu:
+        import oracle as orc
+        model = orc.Phi4Oracle(cfg, weights)
+        for l in range(cfg.layers):
+            model.k[l][...] = kv[0]
+            model.v[l][...] = kv[1]
+        threads = cpu_threads()
+        sec = time_cpu_steps(lambda: model.step(1, context, threads))
+        out["cpu"] = {"tok_s": round(1.0 / sec, 3), "ms_per_token": round(sec * 1e3, 1), "cores": threads,
+                      "kind": "port", "sample": "1 warm-up + 3 oracle decode steps (median) at position "
+                                                f"{context}, same weights and cache"}
+        log(f"decode cpu: {sec * 1e3:.1f} ms/token on {threads} threads")
+        del model
+    del weights
+    return out
+
+
+def bench_rwkv_decode(hip, tokens: int = 64, cpu: bool = True, replay_timing: bool = True, eager: bool = False):
+    """RWKV-7-shaped token step (24 layers, width 2048 in 32 heads of 64,
+    FFN 8192, Q8_0 projections and LoRA, Q8_0 embedding/head 65536x2048,
+    FP32 state with WKV matrices N(0, 0.1)).  Steady state: the recorded step
+    replayed back to back; loop: forward_token over `tokens` tokens.  CPU:
+    the oracle's token step on the same weights and state."""
+    from sharpinference_amd import rwkv7
+    cfg = rwkv7.Rwkv7Config()
+    t0 = time.time()
+    weights = rwkv7.synth_weights(cfg, seed=9, distinct_layers=4)
+    state = rwkv7.synth_state(cfg, seed=10)
+    sess = rwkv7.Rwkv7DecodeSession(hip, cfg, weights, state)
+    log(f"rwkv7: model on device in {time.time() - t0:.1f} s")
+    sess.control.upload(np.array([1], np.int32))
+    sess.plan.launch()
+    hip.sync()
+    us = sorted(sess.plan.measure_us(16) for _ in range(5))[2] if replay_timing else float("nan")
+    step_bytes = cfg.weight_bytes_per_token()
+    gbs = step_bytes / us / 1e3
+    t0 = time.perf_counter()
+    tok = 1
+    for _ in range(tokens):
+        if eager:
+            sess.control.upload(np.array([tok], np.int32))
+            hip.rwkv7_decode(sess.model)
+            tok = int(sess.next_token.readback(np.int32, 1)[0])
+        else:
+            tok = sess.forward_token(tok)
+    loop_s = (time.perf_counter() - t0) / tokens
+    sess.close()
+    log(f"rwkv7: {us:.1f} us/token on device ({1e6 / us:.0f} tok/s, {gbs:.0f} GB/s), "
+        f"{loop_s * 1e6:.1f} us/token with host round trips")
+    out = {"workload": "RWKV-7 token step, 24 layers, width 2048 (32 heads x 64), FFN 8192, Q8_0 projections "
+                       "and LoRA (ranks 96/96/64/256), Q8_0 embedding/head 65536x2048, batch 1",
+           "us_per_token": r1(us), "tok_s": r1(1e6 / us), "bytes_per_token": step_bytes,
+           "GBs": r1(gbs), "hbm_frac": None if gbs != gbs else round(gbs / HBM_PEAK_GBS, 4),
+           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
+           "loop_us_per_token": round(loop_s * 1e6, 1), "loop_tok_s": round(1.0 / loop_s, 1),
+           "layer_weights": "4 distinct layers uploaded as 24 separate device copies"}
+    if cpu:
+        import oracle as orc
+        from types import SimpleNamespace
+        ocfg = SimpleNamespace(**{k: getattr(cfg, k) for k in (
+            "layers", "hidden", "heads", "head_size", "ffn", "vocab", "rank_w", "rank_a", "rank_v", "rank_g",
+            "weight_format", "embed_format", "head_format")})
+        model = orc.Rwkv7Oracle(ocfg, weights, state)
+        threads = cpu_threads()
+        sec = time_cpu_steps(lambda: model.step(1, threads))
+        out["cpu"] = {"tok_s": round(1.0 / sec, 3), "ms_per_token": round(sec * 1e3, 1), "cores": threads,
+                      "kind": "port", "sample": "1 warm-up + 3 oracle token steps (median), same weights and "
+                                                "state"}
+        log(f"rwkv7 cpu: {sec * 1e3:.1f} ms/token on {threads} threads")
+    return out
 
 
 def committed_traffic(config: str):
@@ -313,7 +427,7 @@ def cpu_baseline(fmt, shapes, host_w, xs, ys, hip, bytes_per_step, budget_s):
     """The oracle's CpuVm restatement (dequantise row -> FP32 dot, rows in
     parallel) timed on this host over a bounded sample of the same steps."""
     import oracle as orc
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     x_host = {cols: xs[cols].readback(np.float32) for cols in xs}
 
     def step(n_threads):

@@ -289,18 +289,26 @@ struct Seg {
     float eps;
 };
 constexpr int MAX_SEGS = 8;
+// A launch of one op carries a one-entry table, so its kernel reads its
+// descriptor at fixed kernel-argument offsets (no dependent lookup).
+template <int NS>
 struct Segs {
-    Seg s[MAX_SEGS];
+    Seg s[NS];
     int count;
 };
 
-// Index of the op that owns this workgroup (uniform across the workgroup).
-__device__ __forceinline__ int seg_index(const Segs& t)
+// The op that owns this workgroup (uniform across the workgroup).
+template <int NS>
+__device__ __forceinline__ const Seg& seg_of(const Segs<NS>& t)
 {
-    int si = 0;
-    for (int i = 1; i < t.count; i++)
-        si = static_cast<int>(blockIdx.x) >= t.s[i].wg0 ? i : si;
-    return si;
+    if constexpr (NS == 1) {
+        return t.s[0];
+    } else {
+        int si = 0;
+        for (int i = 1; i < t.count; i++)
+            si = static_cast<int>(blockIdx.x) >= t.s[i].wg0 ? i : si;
+        return t.s[si];
+    }
 }
 
 // Output function of one row (OUT_SWIGLU_ROWS is handled by the callers,
@@ -351,8 +359,11 @@ __device__ __forceinline__ float block_sum(float v, float* red)
 
 __device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4(a.x - m, a.y - m, a.z - m, a.w - m); }
 
-template <int FMT, int LK, int UPL, int RL, int KS, int NW>
-__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
+// FULL = false compiles the plain product (no input transform, plain
+// output with an optional residual, no side copy): the hot decode GEMV keeps
+// the registers and the instruction stream it had before the fused forms.
+template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL>
+__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
 {
     static_assert(NW % KS == 0, "waves must cover whole row groups");
     constexpr int THREADS = 64 * NW;
@@ -373,10 +384,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
     __shared__ float part[ROWS_PER_WG * KS];
     __shared__ float red[NW], red2[NW];
 
-    const Seg& sg = segs.s[seg_index(segs)];
+    const Seg& sg = seg_of(segs);
     const int b = static_cast<int>(blockIdx.x) - sg.wg0;
     const int rows = sg.rows;
-    const bool swiglu = sg.out == OUT_SWIGLU_ROWS;
+    const bool swiglu = FULL && sg.out == OUT_SWIGLU_ROWS;
+    const int in_kind = FULL ? sg.in : static_cast<int>(XF_PLAIN);
     const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
 
     const int lane = threadIdx.x & 63;
@@ -406,7 +418,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
         for (int i = 0; i < UPL; i++)
             w[i][t].load(rp, unit0 + i * LK);
     }
-    side_copy(sg, b, THREADS);
+    if constexpr (FULL)
+        side_copy(sg, b, THREADS);
 
     // 2. stage x into LDS (padded per unit); all of this thread's x loads
     //    are issued before the first LDS write
@@ -416,7 +429,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
 #pragma unroll
     for (int j = 0; j < XPT; j++)
         xr[j] = x4[threadIdx.x + j * THREADS];
-    if (sg.in == XF_SWIGLU) {
+    if (in_kind == XF_SWIGLU) {
         // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
@@ -426,7 +439,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
             xr[j].z = silu_mul(xr[j].z, u.z);
             xr[j].w = silu_mul(xr[j].w, u.w);
         }
-    } else if (sg.in == XF_RMSNORM) {
+    } else if (in_kind == XF_RMSNORM) {
         // scale = 1 / sqrt(sum(x^2) / K + eps); x_i * scale * weight_i
         float ss = 0.0f;
 #pragma unroll
@@ -443,7 +456,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
             xr[j].z = xr[j].z * scale * g.z;
             xr[j].w = xr[j].w * scale * g.w;
         }
-    } else if (sg.in == XF_LAYERNORM || sg.in == XF_LAYERNORM_MIX) {
+    } else if (in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX) {
         // mean = sum(x) / K; c = x - mean; var = sum(c^2) / K;
         // ln = (c * (1 / sqrt(var + eps))) * weight + bias
         float s1 = 0.0f;
@@ -462,7 +475,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
         const float4* g4 = reinterpret_cast<const float4*>(sg.nw);
         const float4* b4 = reinterpret_cast<const float4*>(sg.nb);
         const bool store = sg.norm_out != nullptr && b == 0;
-        const bool mixing = sg.in == XF_LAYERNORM_MIX;
+        const bool mixing = in_kind == XF_LAYERNORM_MIX;
         const float4* m4 = reinterpret_cast<const float4*>(sg.mix);
         const float4* p4 = reinterpret_cast<const float4*>(sg.prev);
 #pragma unroll
@@ -560,7 +573,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
             for (int t = 0; t < RL; t++) {
                 const int r = rb + local_row0 + t;
                 if (r < rows)
-                    sg.y[r] = finish(sg, acc[t], r);
+                    sg.y[r] = FULL ? finish(sg, acc[t], r) : (sg.residual ? acc[t] + sg.residual[r] : acc[t]);
             }
         }
     } else {
@@ -585,7 +598,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs segs)
                 if (r < rows)
                     sg.y[r] = silu_mul(v, u);
             } else if (r < rows) {
-                sg.y[r] = finish(sg, v, r);
+                sg.y[r] = FULL ? finish(sg, v, r) : (sg.residual ? v + sg.residual[r] : v);
             }
         }
     }
@@ -663,10 +676,10 @@ __device__ __forceinline__ float row_dot(const uint8_t* rp, const float* x, int 
 
 // One wave per output row, lanes stride over blocks, byte loads (no
 // alignment needs); x is taken as is (no input transform).
-template <int FMT>
-__global__ __launch_bounds__(WG) void gemv_generic_kernel(Segs segs)
+template <int FMT, int NS>
+__global__ __launch_bounds__(WG) void gemv_generic_kernel(Segs<NS> segs)
 {
-    const Seg& sg = segs.s[seg_index(segs)];
+    const Seg& sg = seg_of(segs);
     const int b = static_cast<int>(blockIdx.x) - sg.wg0;
     side_copy(sg, b, WG);
     const int row = b * (WG / 64) + (threadIdx.x >> 6);
@@ -763,10 +776,16 @@ Seg to_seg(const GemvOp& op)
 // Builds the descriptor table of n ops, each taking ceil(rows / rows_per_wg)
 // workgroups; with halve_swiglu, an OUT_SWIGLU_ROWS op puts half as many
 // output rows in a workgroup (its gate and up rows share the tile).
-unsigned fill_segs(Segs& t, const GemvOp* ops, int n, int rows_per_wg, bool halve_swiglu)
+bool is_plain(const GemvOp& op)
+{
+    return op.in == XF_PLAIN && op.out == OUT_PLAIN && op.copy_n == 0;
+}
+
+template <int NS>
+unsigned fill_segs(Segs<NS>& t, const GemvOp* ops, int n, int rows_per_wg, bool halve_swiglu)
 {
     int wg = 0;
-    t = Segs{};
+    t = Segs<NS>{};
     t.count = n;
     for (int i = 0; i < n; i++) {
         t.s[i] = to_seg(ops[i]);
@@ -781,9 +800,21 @@ template <int FMT, int LK, int UPL, int RL, int KS, int NW>
 hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
 {
     constexpr int R = (64 / LK) * RL * (NW / KS);
-    Segs t;
-    const unsigned grid = fill_segs(t, ops, n, R, true);
-    hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW>), dim3(grid), dim3(64 * NW), 0, s, t);
+    if (n == 1) {
+        Segs<1> t;
+        const unsigned grid = fill_segs(t, ops, n, R, true);
+        if (is_plain(ops[0]))
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), dim3(grid), dim3(64 * NW), 0,
+                               s, t);
+        else
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true>), dim3(grid), dim3(64 * NW), 0,
+                               s, t);
+    } else {
+        Segs<MAX_SEGS> t;
+        const unsigned grid = fill_segs(t, ops, n, R, true);
+        hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true>), dim3(grid), dim3(64 * NW),
+                           0, s, t);
+    }
     return hipGetLastError();
 }
 
@@ -815,9 +846,15 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
 template <int FMT>
 hipError_t launch_generic(const GemvOp* ops, int n, hipStream_t s)
 {
-    Segs t;
-    const unsigned grid = fill_segs(t, ops, n, WG / 64, false);   // one output row per wave
-    hipLaunchKernelGGL((gemv_generic_kernel<FMT>), dim3(grid), dim3(WG), 0, s, t);
+    if (n == 1) {   // one output row per wave
+        Segs<1> t;
+        const unsigned grid = fill_segs(t, ops, n, WG / 64, false);
+        hipLaunchKernelGGL((gemv_generic_kernel<FMT, 1>), dim3(grid), dim3(WG), 0, s, t);
+    } else {
+        Segs<MAX_SEGS> t;
+        const unsigned grid = fill_segs(t, ops, n, WG / 64, false);
+        hipLaunchKernelGGL((gemv_generic_kernel<FMT, MAX_SEGS>), dim3(grid), dim3(WG), 0, s, t);
+    }
     return hipGetLastError();
 }
 
