@@ -44,6 +44,8 @@ typedef enum si_hip_status {
     SI_HIP_ERR_DEVICE = 4,        /* HIP runtime failure */
     SI_HIP_ERR_OUT_OF_MEMORY = 5,
     SI_HIP_ERR_STATE = 6,         /* call not valid in the context's current state */
+    SI_HIP_ERR_FORMAT = 7,        /* InvalidDataException: malformed or truncated GGUF data */
+    SI_HIP_ERR_IO = 8,            /* the file cannot be opened or mapped */
 } si_hip_status;
 
 /* GGUF tensor type ids, as GgufModelTensorType (GgufModelFile.cs:24-46). */
@@ -372,6 +374,72 @@ int si_hip_rwkv7_workspace_bytes(const si_hip_rwkv7_model* model, uint64_t* byte
  * the portable RWKV-7 forward-token graph (PortableRwkv7GraphProvider.cs:
  * 190-292) run by a VM executor. */
 int si_hip_rwkv7_decode(si_hip_context* ctx, const si_hip_rwkv7_model* model);
+
+/* ---- GGUF model files ------------------------------------------------------------ */
+
+/* A GGUF v3 file mapped read-only: metadata, tensor directory and the
+ * tensors' bytes.  Replaces: GgufModelFile (SharpInference.Gguf/
+ * GgufModelFile.cs:49-199) with the same validation (magic, version 3,
+ * counts, unique non-blank keys and names, rank 1..8, non-empty dimensions,
+ * power-of-two general.alignment, every tensor inside the file), plus byte
+ * lengths for the K-quant types (256-element super-blocks: Q2_K 84, Q3_K
+ * 110, Q4_K 144, Q5_K 176, Q6_K 210, Q8_K 292 bytes) and tensors above
+ * 2 GiB.  Errors: SI_HIP_ERR_IO (open/map), SI_HIP_ERR_FORMAT (malformed),
+ * SI_HIP_ERR_UNSUPPORTED (tensor type without a byte length); the message is
+ * si_hip_last_error(NULL). */
+typedef struct si_gguf si_gguf;
+
+typedef enum si_gguf_value_type {
+    SI_GGUF_U8 = 0, SI_GGUF_I8 = 1, SI_GGUF_U16 = 2, SI_GGUF_I16 = 3, SI_GGUF_U32 = 4, SI_GGUF_I32 = 5,
+    SI_GGUF_F32 = 6, SI_GGUF_BOOL = 7, SI_GGUF_STRING = 8, SI_GGUF_ARRAY = 9, SI_GGUF_U64 = 10,
+    SI_GGUF_I64 = 11, SI_GGUF_F64 = 12,
+} si_gguf_value_type;
+
+typedef struct si_gguf_file_info {
+    uint32_t version;
+    uint32_t reserved;
+    uint64_t alignment;        /* general.alignment or 32 */
+    uint64_t data_start;       /* file offset of the tensor data section */
+    uint64_t file_bytes;
+    int64_t tensor_count;
+    int64_t metadata_count;
+} si_gguf_file_info;
+
+typedef struct si_gguf_tensor {
+    const char* name;          /* valid until si_gguf_close */
+    int32_t type;              /* GGUF tensor type id (si_hip_format values and the other GGML ids) */
+    int32_t rank;
+    uint64_t dims[8];          /* dims[0] is the contiguous axis (columns); unused entries are 1 */
+    uint64_t offset;           /* absolute file offset of the first byte */
+    uint64_t bytes;
+    const void* data;          /* host address inside the read-only mapping */
+} si_gguf_tensor;
+
+typedef struct si_gguf_value {
+    const char* key;
+    int32_t type;              /* si_gguf_value_type */
+    int32_t array_type;        /* element type when type == SI_GGUF_ARRAY, else -1 */
+    uint64_t count;            /* elements (1 for a scalar) */
+    const void* data;          /* numbers and bools: count values in native layout (bool = uint8);
+                                  strings: count const char* (NUL-terminated UTF-8) */
+    const uint64_t* lengths;   /* strings: byte length of each; NULL otherwise */
+} si_gguf_value;
+
+int si_gguf_open(const char* path, si_gguf** out);
+int si_gguf_close(si_gguf* file);
+int si_gguf_info(const si_gguf* file, si_gguf_file_info* info);
+int si_gguf_tensor_at(const si_gguf* file, int64_t index, si_gguf_tensor* out);
+/* *index = the tensor's index, or -1 when the file has no such tensor. */
+int si_gguf_find_tensor(const si_gguf* file, const char* name, int64_t* index);
+int si_gguf_metadata_at(const si_gguf* file, int64_t index, si_gguf_value* out);
+/* *index = the key's index, or -1 when absent. */
+int si_gguf_find_metadata(const si_gguf* file, const char* key, int64_t* index);
+
+/* Copies tensor `index`'s bytes, unchanged, from the mapping into device
+ * memory at device_dst (dst_bytes >= the tensor's bytes) and waits.
+ * Replaces: executor.Upload(slot, tensor.Bytes) of the model tensors
+ * (Phi4D3D12TextSession.cs:55-58, D3D12VmExecutor.cs:595-625). */
+int si_gguf_upload(si_hip_context* ctx, const si_gguf* file, int64_t index, void* device_dst, uint64_t dst_bytes);
 
 /* ---- recorded entries and timing -------------------------------------------- */
 

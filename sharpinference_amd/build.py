@@ -32,6 +32,7 @@ SOURCES = [
     "si_decode.hip",
     "si_rwkv.hip",
     "si_rwkv_program.cpp",
+    "si_gguf.cpp",
 ]
 
 

@@ -22,7 +22,7 @@ FORMAT_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"
 BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
 
-OK, ERR_ARGUMENT, ERR_UNSUPPORTED, ERR_ADAPTATION, ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_STATE = range(7)
+OK, ERR_ARGUMENT, ERR_UNSUPPORTED, ERR_ADAPTATION, ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_STATE, ERR_FORMAT, ERR_IO = range(9)
 PATH_FAST, PATH_GENERIC = 1, 2
 
 # Every symbol include/sharpinference_hip.h declares, with its ctypes signature.
@@ -130,6 +130,35 @@ class Rwkv7Model(ctypes.Structure):
          ("ln_out_weight", _vp), ("ln_out_bias", _vp), ("head", _vp), ("control", _vp), ("hidden_state", _vp),
          ("logits", _vp), ("workspace", _vp), ("next_token", _vp)]
 
+
+class GgufFileInfo(ctypes.Structure):
+    """si_gguf_file_info."""
+    _fields_ = [("version", _u32), ("reserved", _u32), ("alignment", _u64), ("data_start", _u64),
+                ("file_bytes", _u64), ("tensor_count", _i64), ("metadata_count", _i64)]
+
+
+class GgufTensor(ctypes.Structure):
+    """si_gguf_tensor."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", _i32), ("rank", _i32), ("dims", _u64 * 8),
+                ("offset", _u64), ("bytes", _u64), ("data", _vp)]
+
+
+class GgufValue(ctypes.Structure):
+    """si_gguf_value."""
+    _fields_ = [("key", ctypes.c_char_p), ("type", _i32), ("array_type", _i32), ("count", _u64),
+                ("data", _vp), ("lengths", ctypes.POINTER(_u64))]
+
+
+SIGNATURES.update({
+    "si_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], _i32),
+    "si_gguf_close": ([_vp], _i32),
+    "si_gguf_info": ([_vp, ctypes.POINTER(GgufFileInfo)], _i32),
+    "si_gguf_tensor_at": ([_vp, _i64, ctypes.POINTER(GgufTensor)], _i32),
+    "si_gguf_find_tensor": ([_vp, ctypes.c_char_p, ctypes.POINTER(_i64)], _i32),
+    "si_gguf_metadata_at": ([_vp, _i64, ctypes.POINTER(GgufValue)], _i32),
+    "si_gguf_find_metadata": ([_vp, ctypes.c_char_p, ctypes.POINTER(_i64)], _i32),
+    "si_gguf_upload": ([_vp, _vp, _i64, _vp, _u64], _i32),
+})
 
 SIGNATURES.update({
     "si_hip_gemv_fused": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp, ctypes.c_float,

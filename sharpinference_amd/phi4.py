@@ -43,6 +43,28 @@ class Phi4Config:
     def qkv_rows(self) -> int:
         return self.hidden + 2 * self.kv_heads * self.head_dim
 
+    @classmethod
+    def from_gguf(cls, g, capacity: int = 4096) -> "Phi4Config":
+        """Shapes and constants from a phi3 GGUF's metadata and tensor types."""
+        if g.get("general.architecture") != "phi3":
+            raise ValueError("not a phi3-architecture GGUF")
+        hidden = int(g.get("phi3.embedding_length"))
+        heads = int(g.get("phi3.attention.head_count"))
+        emb = g.tensor("token_embd.weight")
+        head = g.tensors.get("output.weight", emb)
+        layer_types = {g.tensor(f"blk.{l}.{n}.weight").type for l in range(int(g.get("phi3.block_count")))
+                       for n in ("attn_qkv", "attn_output", "ffn_up", "ffn_down")}
+        if len(layer_types) != 1:
+            raise ValueError(f"layer projections use several formats {sorted(layer_types)}; one is supported")
+        return cls(layers=int(g.get("phi3.block_count")), hidden=hidden, heads=heads,
+                   kv_heads=int(g.get("phi3.attention.head_count_kv")), head_dim=hidden // heads,
+                   rotary_dim=int(g.metadata.get("phi3.rope.dimension_count", hidden // heads)),
+                   ffn=int(g.get("phi3.feed_forward_length")), vocab=emb.rows, capacity=capacity,
+                   weight_format=layer_types.pop(), embed_format=emb.type, head_format=head.type,
+                   rms_eps=float(g.get("phi3.attention.layer_norm_rms_epsilon")),
+                   rope_base=float(g.get("phi3.rope.freq_base")),
+                   rope_scale=float(g.metadata.get("phi3.rope.scaling.attn_factor", 1.0)))
+
     def layer_shapes(self) -> Dict[str, tuple]:
         return {"qkv": (self.qkv_rows, self.hidden), "o": (self.hidden, self.hidden),
                 "up": (2 * self.ffn, self.hidden), "down": (self.hidden, self.ffn)}
@@ -86,16 +108,17 @@ class Phi4DecodeSession:
         self.cfg = cfg
         self._bufs: List[native.DeviceBuffer] = []
         up = self._upload
+        f32 = lambda a: a if isinstance(a, native.DeviceBuffer) else np.ascontiguousarray(a, np.float32)
         self.embed = up(weights.embed)
-        self.lm_head = up(weights.lm_head)
-        self.output_norm = up(weights.output_norm.astype(np.float32))
+        self.lm_head = self.embed if weights.lm_head is weights.embed else up(weights.lm_head)
+        self.output_norm = up(f32(weights.output_norm))
         kv_bytes = 2 * cfg.kv_heads * cfg.capacity * cfg.head_dim
         self.layers = []
         for l in range(cfg.layers):
             L = {
-                "attn_norm": up(weights.attn_norm[l].astype(np.float32)),
+                "attn_norm": up(f32(weights.attn_norm[l])),
                 "qkv": up(weights.qkv[l]), "o": up(weights.o[l]),
-                "ffn_norm": up(weights.ffn_norm[l].astype(np.float32)),
+                "ffn_norm": up(f32(weights.ffn_norm[l])),
                 "up": up(weights.up[l]), "down": up(weights.down[l]),
                 "k_cache": self._alloc(kv_bytes), "v_cache": self._alloc(kv_bytes),
             }
@@ -130,10 +153,30 @@ class Phi4DecodeSession:
         self._bufs.append(b)
         return b
 
-    def _upload(self, arr: np.ndarray) -> native.DeviceBuffer:
+    def _upload(self, arr) -> native.DeviceBuffer:
+        if isinstance(arr, native.DeviceBuffer):   # already resident (e.g. uploaded from a GGUF mapping)
+            self._bufs.append(arr)
+            return arr
         b = self._alloc(arr.nbytes)
         b.upload(np.ascontiguousarray(arr))
         return b
+
+    @classmethod
+    def from_gguf(cls, hip: native.HipContext, g, capacity: int = 4096) -> "Phi4DecodeSession":
+        """A session over a phi3-architecture GGUF file (the Phi-4-mini text
+        backbone, Phi4ModelPackage.cs:108-113, Phi4TextModel.cs:40-42,53,
+        67-99): every tensor is uploaded once, unchanged, from the mapping."""
+        cfg = Phi4Config.from_gguf(g, capacity)
+        up = lambda name: g.upload(hip, name)
+        embed = up("token_embd.weight")
+        lm_head = up("output.weight") if "output.weight" in g.tensors else embed   # tied (Phi4TextModel.cs:99)
+        L = range(cfg.layers)
+        weights = Phi4Weights(
+            embed=embed, lm_head=lm_head, output_norm=up("output_norm.weight"),
+            attn_norm=[up(f"blk.{l}.attn_norm.weight") for l in L], qkv=[up(f"blk.{l}.attn_qkv.weight") for l in L],
+            o=[up(f"blk.{l}.attn_output.weight") for l in L], ffn_norm=[up(f"blk.{l}.ffn_norm.weight") for l in L],
+            up=[up(f"blk.{l}.ffn_up.weight") for l in L], down=[up(f"blk.{l}.ffn_down.weight") for l in L])
+        return cls(hip, cfg, weights)
 
     def load_kv(self, layer: int, k_fp16: np.ndarray, v_fp16: np.ndarray) -> None:
         """Fills a layer's caches (uint16 fp16 bits [kv_heads, capacity, head_dim])."""
