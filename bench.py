@@ -230,7 +230,13 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": committed_traffic(args.config),
-            "kernel": "gemv_fast_kernel (Q4_0), launch-averaged over the step's 4 GEMVs",
+            "kernel": f"gemv_fast_kernel ({native.FORMAT_NAMES[fmt]}), launch-averaged over the step's "
+                      f"{len(shapes)} GEMVs",
+            # the event-timed launch includes the dependent-launch floor;
+            # without it, the launch time matches a kernel trace's duration
+            "launch_us": round(s_per_step * 1e6 / len(shapes), 3),
+            "dispatch_floor_us": round(floor_us, 3),
+            "kernel_us": round(s_per_step * 1e6 / len(shapes) - floor_us, 3),
         },
     }
 
