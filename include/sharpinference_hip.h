@@ -218,7 +218,9 @@ typedef struct si_hip_attention {
     void* k_cache;             /* fp16 [kv_heads][capacity][128], 16-byte aligned */
     void* v_cache;             /* fp16 [kv_heads][capacity][128], 16-byte aligned */
     float* out;                /* [heads * 128] */
-    float* workspace;          /* si_hip_attention_workspace_bytes */
+    float* workspace;          /* si_hip_attention_workspace_bytes: chunk partials and the rotary table; any
+                                  contents on entry (each call prepares it); calls that share one workspace
+                                  must not overlap on the GPU */
     int heads;
     int kv_heads;              /* heads / kv_heads in 1..4 */
     int head_dim;              /* 128 */

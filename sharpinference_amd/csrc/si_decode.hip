@@ -78,13 +78,19 @@ __global__ __launch_bounds__(256) void gather_row_kernel(const uint8_t* __restri
 
 // ---- attention ------------------------------------------------------------------
 
-// Rotary embedding of one head in place (values in LDS), position p:
-// pairs (i, i + R/2) for i < R/2, frequency 1 / base^(2i / R).
-__device__ __forceinline__ void rotate_pair(float* h, int i, int rotary, float pos, float base, float scale)
+// Workspace of one attention launch: per query head and chunk the partial
+// (max, sum, 128 weighted values), then the rotary table of the current
+// position (cos at [0, R/2), sin at [64, 64 + R/2), both already scaled).
+__host__ __device__ inline int64_t att_rope(int heads, int max_chunks)
 {
-    const float freq = 1.0f / powf(base, 2.0f * static_cast<float>(i) / static_cast<float>(rotary));
-    const float angle = pos * freq;
-    const float c = cosf(angle) * scale, s = sinf(angle) * scale;
+    return (static_cast<int64_t>(heads) * max_chunks * PART + 63) / 64 * 64;
+}
+
+// Rotary embedding of one pair in place (values in LDS): pairs (i, i + R/2)
+// for i < R/2 with the precomputed cos / sin of the position.
+__device__ __forceinline__ void rotate_pair(float* h, int i, int rotary, const float* rope)
+{
+    const float c = rope[i], s = rope[64 + i];
     const float left = h[i], right = h[i + rotary / 2];
     h[i] = left * c - right * s;
     h[i + rotary / 2] = right * c + left * s;
@@ -109,6 +115,83 @@ __device__ __forceinline__ float row_sum(float v)
     if constexpr (N >= 8) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
     if constexpr (N >= 16) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
     return v;
+}
+
+// Once per step: the rotary table of the new position (frequency
+// 1 / base^(2i / R), cos / sin scaled by rope_scale), shared by every layer
+// that attends at that position.
+__global__ __launch_bounds__(64) void attention_prep_kernel(AttentionArgs a)
+{
+    const int t = threadIdx.x;
+    const int P = *a.position;
+    float* rope = a.workspace + att_rope(a.heads, a.max_chunks);
+    if (t < a.rotary_dim / 2) {
+        const float freq = 1.0f / powf(a.rope_base, 2.0f * static_cast<float>(t) / static_cast<float>(a.rotary_dim));
+        const float angle = static_cast<float>(P) * freq;
+        rope[t] = cosf(angle) * a.rope_scale;
+        rope[64 + t] = sinf(angle) * a.rope_scale;
+    }
+}
+
+constexpr int MAX_CHUNKS = 256;
+
+// One workgroup per query head: merge the chunk partials (m_c, l_c, o_c)
+// into softmax-weighted values.  (Merging inside the last partial
+// workgroup instead needs a device-scope release per workgroup, which
+// writes back the XCD's L2 and costs far more than this launch.)
+__global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
+{
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int P = *a.position;
+    if (P < 0 || P >= a.capacity) {
+        if (t < HEAD_DIM)
+            a.out[h * HEAD_DIM + t] = __int_as_float(0x7fc00000);   // position outside the cache
+        return;
+    }
+    const int chunks = P / CHUNK + 1;
+    const float* src = a.workspace + static_cast<int64_t>(h) * a.max_chunks * PART;
+    __shared__ float wts[MAX_CHUNKS];
+    __shared__ float lw[MAX_CHUNKS];
+    __shared__ float half_acc[2][HEAD_DIM];
+    __shared__ float stat[2];
+    for (int c = t; c < chunks; c += 256)
+        wts[c] = src[c * PART];
+    __syncthreads();
+    if (t < 64) {
+        float m = -INFINITY;
+        for (int c = t; c < chunks; c += 64)
+            m = fmaxf(m, wts[c]);
+        for (int off = 32; off > 0; off >>= 1)
+            m = fmaxf(m, __shfl_xor(m, off));
+        if (t == 0)
+            stat[0] = m;
+    }
+    __syncthreads();
+    const float M = stat[0];
+    for (int c = t; c < chunks; c += 256) {
+        const float w = expf(wts[c] - M);
+        wts[c] = w;
+        lw[c] = src[c * PART + 1] * w;
+    }
+    __syncthreads();
+    if (t < 64) {
+        float l = 0.0f;
+        for (int c = t; c < chunks; c += 64)
+            l += lw[c];
+        for (int off = 32; off > 0; off >>= 1)
+            l += __shfl_xor(l, off);
+        if (t == 0)
+            stat[1] = l;
+    }
+    const int d = t & (HEAD_DIM - 1), half = t >> 7;
+    float acc = 0.0f;
+#pragma unroll 4
+    for (int c = half; c < chunks; c += 2)
+        acc = fmaf(src[c * PART + 2 + d], wts[c], acc);
+    half_acc[half][d] = acc;
+    __syncthreads();
+    if (t < HEAD_DIM)
+        a.out[h * HEAD_DIM + t] = (half_acc[0][t] + half_acc[1][t]) / stat[1];
 }
 
 // One workgroup = one KV head x one chunk of 64 cache positions.  Writes
@@ -158,7 +241,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(Attentio
     __shared__ float red[4][GROUP][HEAD_DIM];
 
     // 2. rotated queries of the group; the new row, rotated, rounded, appended
-    const float pos = static_cast<float>(P);
+    const float* rope = a.workspace + att_rope(a.heads, a.max_chunks);
     for (int i = t; i < GROUP * HEAD_DIM; i += ATT_THREADS)
         q[i / HEAD_DIM][i % HEAD_DIM] = a.qkv[(g * GROUP + i / HEAD_DIM) * HEAD_DIM + i % HEAD_DIM];
     if (owns_new && t < HEAD_DIM) {
@@ -168,9 +251,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(Attentio
     __syncthreads();
     const int half_rot = a.rotary_dim / 2;
     for (int i = t; i < GROUP * half_rot; i += ATT_THREADS)
-        rotate_pair(q[i / half_rot], i % half_rot, a.rotary_dim, pos, a.rope_base, a.rope_scale);
+        rotate_pair(q[i / half_rot], i % half_rot, a.rotary_dim, rope);
     if (owns_new && t < half_rot)
-        rotate_pair(knew, t, a.rotary_dim, pos, a.rope_base, a.rope_scale);
+        rotate_pair(knew, t, a.rotary_dim, rope);
     __syncthreads();
     if (owns_new && t < HEAD_DIM) {
         const __half kh = __float2half_rn(knew[t]), vh = __float2half_rn(vnew[t]);
@@ -288,65 +371,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(Attentio
     }
 }
 
-// One workgroup per query head: merge the chunk partials
-// (m_c, l_c, o_c) into softmax-weighted values.
-constexpr int MAX_CHUNKS = 256;
-
-__global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
-{
-    const int h = blockIdx.x, t = threadIdx.x;
-    const int P = *a.position;
-    if (P < 0 || P >= a.capacity) {
-        if (t < HEAD_DIM)
-            a.out[h * HEAD_DIM + t] = __int_as_float(0x7fc00000);   // position outside the cache
-        return;
-    }
-    const int chunks = P / CHUNK + 1;
-    const float* src = a.workspace + static_cast<int64_t>(h) * a.max_chunks * PART;
-    __shared__ float wts[MAX_CHUNKS];
-    __shared__ float lw[MAX_CHUNKS];
-    __shared__ float half_acc[2][HEAD_DIM];
-    __shared__ float stat[2];
-    for (int c = t; c < chunks; c += 256)
-        wts[c] = src[c * PART];
-    __syncthreads();
-    if (t < 64) {
-        float m = -INFINITY;
-        for (int c = t; c < chunks; c += 64)
-            m = fmaxf(m, wts[c]);
-        for (int off = 32; off > 0; off >>= 1)
-            m = fmaxf(m, __shfl_xor(m, off));
-        if (t == 0)
-            stat[0] = m;
-    }
-    __syncthreads();
-    const float M = stat[0];
-    for (int c = t; c < chunks; c += 256) {
-        const float w = expf(wts[c] - M);
-        wts[c] = w;
-        lw[c] = src[c * PART + 1] * w;
-    }
-    __syncthreads();
-    if (t < 64) {
-        float l = 0.0f;
-        for (int c = t; c < chunks; c += 64)
-            l += lw[c];
-        for (int off = 32; off > 0; off >>= 1)
-            l += __shfl_xor(l, off);
-        if (t == 0)
-            stat[1] = l;
-    }
-    const int d = t & (HEAD_DIM - 1), half = t >> 7;
-    float acc = 0.0f;
-#pragma unroll 4
-    for (int c = half; c < chunks; c += 2)
-        acc = fmaf(src[c * PART + 2 + d], wts[c], acc);
-    half_acc[half][d] = acc;
-    __syncthreads();
-    if (t < HEAD_DIM)
-        a.out[h * HEAD_DIM + t] = (half_acc[0][t] + half_acc[1][t]) / stat[1];
-}
-
 // ---- argmax ----------------------------------------------------------------------------
 
 constexpr int AM_BLOCKS = 256;
@@ -403,7 +427,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restri
 
 int64_t attention_workspace_floats(int heads, int capacity)
 {
-    return static_cast<int64_t>(heads) * ((capacity + CHUNK - 1) / CHUNK) * PART;
+    return att_rope(heads, (capacity + CHUNK - 1) / CHUNK) + 2 * 64;
 }
 
 int64_t argmax_workspace_bytes() { return AM_BLOCKS * 8; }
@@ -424,10 +448,22 @@ hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t c
     return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttentionArgs& a, hipStream_t s)
+hipError_t launch_attention_prep(const AttentionArgs& a, hipStream_t s)
 {
-    if (a.head_dim != HEAD_DIM || a.kv_heads <= 0 || a.heads % a.kv_heads != 0 || a.max_chunks > MAX_CHUNKS)
+    hipLaunchKernelGGL(attention_prep_kernel, dim3(1), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
+{
+    if (a.head_dim != HEAD_DIM || a.kv_heads <= 0 || a.heads % a.kv_heads != 0 || a.max_chunks > MAX_CHUNKS ||
+        a.rotary_dim > HEAD_DIM)
         return hipErrorInvalidValue;
+    if (prep) {
+        const hipError_t e = launch_attention_prep(a, s);
+        if (e != hipSuccess)
+            return e;
+    }
     const int group = a.heads / a.kv_heads;
     const dim3 grid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>(a.max_chunks));
     switch (group) {
@@ -437,7 +473,7 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s)
     case 4: hipLaunchKernelGGL((attention_partial_kernel<4>), grid, dim3(ATT_THREADS), 0, s, a); break;
     default: return hipErrorInvalidValue;
     }
-    hipError_t e = hipGetLastError();
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
     hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a);

@@ -32,7 +32,11 @@ int64_t attention_workspace_floats(int heads, int capacity);
 int64_t argmax_workspace_bytes();
 hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index, float* out,
                              hipStream_t s);
-hipError_t launch_attention(const AttentionArgs& a, hipStream_t s);
+// The per-step preparation (rotary table of the position) runs first when
+// `prep`; a program that attends several layers at one position prepares
+// once and passes prep = false afterwards.
+hipError_t launch_attention_prep(const AttentionArgs& a, hipStream_t s);
+hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep = true);
 hipError_t launch_argmax(const float* values, int64_t n, void* workspace, int32_t* out, hipStream_t s);
 
 }  // namespace si

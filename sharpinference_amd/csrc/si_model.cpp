@@ -127,6 +127,21 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
                                ~uint64_t(255);
     void* am_ws = static_cast<uint8_t*>(m->workspace) + att_bytes;
     hipError_t e = si::launch_gather_row(m->embed_format, m->embed, m->vocab, H, m->control, m->hidden_state, s);
+    // every layer attends at the same position: one rotary table per step
+    si_hip_attention a{};
+    a.qkv = m->qkv;
+    a.position = m->control + 1;
+    a.out = m->attn;
+    a.workspace = att_ws;
+    a.heads = m->heads;
+    a.kv_heads = m->kv_heads;
+    a.head_dim = m->head_dim;
+    a.rotary_dim = m->rotary_dim;
+    a.capacity = m->capacity;
+    a.rope_base = m->rope_base;
+    a.rope_scale = m->rope_scale;
+    if (e == hipSuccess)
+        e = si::launch_attention_prep(attention_args(&a), s);
     for (int l = 0; e == hipSuccess && l < m->layers; l++) {
         const si_hip_phi4_layer& L = m->layer[l];
         si::GemvOp qkv;
@@ -141,21 +156,9 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
         qkv.eps = m->rms_eps;
         e = si::launch_gemv_ops(&qkv, 1, s, nullptr);
         if (e != hipSuccess) break;
-        si_hip_attention a{};
-        a.qkv = m->qkv;
-        a.position = m->control + 1;
         a.k_cache = L.k_cache;
         a.v_cache = L.v_cache;
-        a.out = m->attn;
-        a.workspace = att_ws;
-        a.heads = m->heads;
-        a.kv_heads = m->kv_heads;
-        a.head_dim = m->head_dim;
-        a.rotary_dim = m->rotary_dim;
-        a.capacity = m->capacity;
-        a.rope_base = m->rope_base;
-        a.rope_scale = m->rope_scale;
-        e = si::launch_attention(attention_args(&a), s);
+        e = si::launch_attention(attention_args(&a), s, false);
         if (e != hipSuccess) break;
         // hidden += W_o . attn
         e = si::launch_gemv(m->weight_format, L.o, m->attn, m->hidden_state, H, H, m->hidden_state, s, nullptr);
