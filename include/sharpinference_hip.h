@@ -116,7 +116,9 @@ int si_hip_sync(si_hip_context* ctx);
 /* y[rows] = W[rows, cols] . x[cols] (+ residual[rows] when residual != NULL),
  * W in GGUF Q8_0 / Q4_0 / Q4_K block layout, x, y, residual FP32.  FP32
  * arithmetic and accumulation.  `path` (optional) receives 1 for the tiled
- * gfx950 kernel and 2 for the any-shape kernel.
+ * gfx950 kernel, 2 for the any-shape kernel (one wave per row) and 3 for the
+ * short-row kernel (rows of at most 32 blocks and 2048 columns, one lane per
+ * block).
  * Replaces: the core.mat-vec instruction (cooperative form
  * GpuTierZeroInstruction.cs:44-89 on D3D12, CpuInstructionNumerics.MatVec
  * CpuInstructionNumerics.cs:16-23 on CpuVm) for block-quantized weights,
@@ -200,7 +202,8 @@ typedef struct si_hip_gemv_op {
  * (D3D12VmSchedule.cs:74-99, whose pending-write rule this batch enforces),
  * e.g. the RWKV-7 r/k/v and LoRA projections of one layer
  * (PortableRwkv7GraphProvider.cs:219-233).  paths (optional) receives
- * each op's kernel as si_hip_gemv reports it (1 tiled, 2 any-shape). */
+ * each op's kernel as si_hip_gemv reports it (1 tiled, 2 any-shape,
+ * 3 short rows). */
 int si_hip_gemv_batch(si_hip_context* ctx, const si_hip_gemv_op* ops, int count, int* paths);
 
 /* out[cols] = FP32 values of row *index of a block-quantized [rows, cols]

@@ -697,6 +697,53 @@ __global__ __launch_bounds__(WG) void gemv_generic_kernel(Segs<NS> segs)
     }
 }
 
+// Short rows (at most SHORT_MAX_BLOCKS blocks and SHORT_MAX_COLS columns,
+// e.g. the K = 64..256 LoRA outputs of RWKV-7): one lane per block, a wave
+// holds 64 / blocks rows, x is staged once per workgroup, and the blocks of
+// a row are summed in order by the row's first lane.
+constexpr int SHORT_MAX_BLOCKS = 32;
+constexpr int SHORT_MAX_COLS = 2048;
+
+template <int FMT, int NS>
+__global__ __launch_bounds__(WG) void gemv_short_kernel(Segs<NS> segs)
+{
+    __shared__ float xs[SHORT_MAX_COLS];
+    __shared__ float part[2][WG];
+    const Seg& sg = seg_of(segs);
+    const int b = static_cast<int>(blockIdx.x) - sg.wg0;
+    side_copy(sg, b, WG);
+    const int nb = sg.blocks;
+    const int rpw = 64 / nb;                       // row slots per wave
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int slot = lane / nb, blk = lane - slot * nb;
+    const int row = (b * (WG / 64) + wave) * rpw + slot;
+    const int K = nb * block_elems(FMT);
+    for (int i = threadIdx.x; i < K; i += WG)
+        xs[i] = sg.x[i];
+    __syncthreads();
+    const bool swiglu = sg.out == OUT_SWIGLU_ROWS;
+    const bool active = slot < rpw && row < sg.rows;
+    float acc = 0.0f, accu = 0.0f;
+    if (active) {
+        const int64_t rb = static_cast<int64_t>(nb) * block_bytes(FMT);
+        const int64_t off = static_cast<int64_t>(blk) * block_bytes(FMT);
+        acc = block_dot<FMT>(sg.w + row * rb + off, xs + blk * block_elems(FMT));
+        if (swiglu)
+            accu = block_dot<FMT>(sg.w + (static_cast<int64_t>(row) + sg.rows) * rb + off, xs + blk * block_elems(FMT));
+    }
+    part[0][threadIdx.x] = acc;
+    part[1][threadIdx.x] = accu;
+    __syncthreads();
+    if (active && blk == 0) {
+        float v = 0.0f, u = 0.0f;
+        for (int k = 0; k < nb; k++) {
+            v += part[0][threadIdx.x + k];
+            u += part[1][threadIdx.x + k];
+        }
+        sg.y[row] = swiglu ? silu_mul(v, u) : finish(sg, v, row);
+    }
+}
+
 // ---- block decoder (bit-exact dequantisation) ----------------------------
 
 template <int FMT>
@@ -773,16 +820,15 @@ Seg to_seg(const GemvOp& op)
     return g;
 }
 
-// Builds the descriptor table of n ops, each taking ceil(rows / rows_per_wg)
-// workgroups; with halve_swiglu, an OUT_SWIGLU_ROWS op puts half as many
-// output rows in a workgroup (its gate and up rows share the tile).
 bool is_plain(const GemvOp& op)
 {
     return op.in == XF_PLAIN && op.out == OUT_PLAIN && op.copy_n == 0;
 }
 
-template <int NS>
-unsigned fill_segs(Segs<NS>& t, const GemvOp* ops, int n, int rows_per_wg, bool halve_swiglu)
+// Builds the descriptor table of n ops, op i taking ceil(rows / per_wg(op))
+// workgroups.
+template <int NS, typename PerWg>
+unsigned fill_segs(Segs<NS>& t, const GemvOp* ops, int n, PerWg per_wg)
 {
     int wg = 0;
     t = Segs<NS>{};
@@ -790,7 +836,7 @@ unsigned fill_segs(Segs<NS>& t, const GemvOp* ops, int n, int rows_per_wg, bool 
     for (int i = 0; i < n; i++) {
         t.s[i] = to_seg(ops[i]);
         t.s[i].wg0 = wg;
-        const int per = halve_swiglu && ops[i].out == OUT_SWIGLU_ROWS ? rows_per_wg / 2 : rows_per_wg;
+        const int per = per_wg(ops[i]);
         wg += static_cast<int>((ops[i].rows + per - 1) / per);
     }
     return static_cast<unsigned>(wg);
@@ -800,9 +846,12 @@ template <int FMT, int LK, int UPL, int RL, int KS, int NW>
 hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
 {
     constexpr int R = (64 / LK) * RL * (NW / KS);
+    // an OUT_SWIGLU_ROWS op puts half as many output rows in a workgroup
+    // (its gate and up rows share the tile)
+    auto per = [](const GemvOp& op) { return op.out == OUT_SWIGLU_ROWS ? R / 2 : R; };
     if (n == 1) {
         Segs<1> t;
-        const unsigned grid = fill_segs(t, ops, n, R, true);
+        const unsigned grid = fill_segs(t, ops, n, per);
         if (is_plain(ops[0]))
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), dim3(grid), dim3(64 * NW), 0,
                                s, t);
@@ -811,7 +860,7 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
                                s, t);
     } else {
         Segs<MAX_SEGS> t;
-        const unsigned grid = fill_segs(t, ops, n, R, true);
+        const unsigned grid = fill_segs(t, ops, n, per);
         hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true>), dim3(grid), dim3(64 * NW),
                            0, s, t);
     }
@@ -832,7 +881,9 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     const bool mid = rows64 >= 12288, tall = rows64 >= 49152;
     switch (cols) {
     case 1024: return mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
-    case 2048: return mid ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
+    case 2048: return mid    ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s)
+                    : rows64 >= 8192 ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s)
+                                     : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
     case 3072: return tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s)
                     : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s)
                            : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
@@ -846,14 +897,31 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
 template <int FMT>
 hipError_t launch_generic(const GemvOp* ops, int n, hipStream_t s)
 {
-    if (n == 1) {   // one output row per wave
+    auto per = [](const GemvOp&) { return WG / 64; };   // one output row per wave
+    if (n == 1) {
         Segs<1> t;
-        const unsigned grid = fill_segs(t, ops, n, WG / 64, false);
+        const unsigned grid = fill_segs(t, ops, n, per);
         hipLaunchKernelGGL((gemv_generic_kernel<FMT, 1>), dim3(grid), dim3(WG), 0, s, t);
     } else {
         Segs<MAX_SEGS> t;
-        const unsigned grid = fill_segs(t, ops, n, WG / 64, false);
+        const unsigned grid = fill_segs(t, ops, n, per);
         hipLaunchKernelGGL((gemv_generic_kernel<FMT, MAX_SEGS>), dim3(grid), dim3(WG), 0, s, t);
+    }
+    return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_short(const GemvOp* ops, int n, hipStream_t s)
+{
+    auto per = [](const GemvOp& op) { return (WG / 64) * (64 / static_cast<int>(op.cols / block_elems(FMT))); };
+    if (n == 1) {
+        Segs<1> t;
+        const unsigned grid = fill_segs(t, ops, n, per);
+        hipLaunchKernelGGL((gemv_short_kernel<FMT, 1>), dim3(grid), dim3(WG), 0, s, t);
+    } else {
+        Segs<MAX_SEGS> t;
+        const unsigned grid = fill_segs(t, ops, n, per);
+        hipLaunchKernelGGL((gemv_short_kernel<FMT, MAX_SEGS>), dim3(grid), dim3(WG), 0, s, t);
     }
     return hipGetLastError();
 }
@@ -869,14 +937,23 @@ bool tiled_ok(const GemvOp& op)
            aligned16(op.norm_out);
 }
 
-hipError_t launch_group(const GemvOp* ops, int n, bool tiled, hipStream_t s)
+int kind_of(const GemvOp& op)
+{
+    if (tiled_ok(op))
+        return PATH_FAST;
+    const int64_t nb = op.cols / block_elems(op.fmt);
+    return nb <= SHORT_MAX_BLOCKS && op.cols <= SHORT_MAX_COLS ? PATH_SHORT : PATH_GENERIC;
+}
+
+hipError_t launch_group(const GemvOp* ops, int n, int kind, hipStream_t s)
 {
     const int fmt = ops[0].fmt;
-    if (!tiled) {
+    if (kind == PATH_GENERIC || kind == PATH_SHORT) {
+        const bool sh = kind == PATH_SHORT;
         switch (fmt) {
-        case FMT_Q8_0: return launch_generic<FMT_Q8_0>(ops, n, s);
-        case FMT_Q4_0: return launch_generic<FMT_Q4_0>(ops, n, s);
-        case FMT_Q4_K: return launch_generic<FMT_Q4_K>(ops, n, s);
+        case FMT_Q8_0: return sh ? launch_short<FMT_Q8_0>(ops, n, s) : launch_generic<FMT_Q8_0>(ops, n, s);
+        case FMT_Q4_0: return sh ? launch_short<FMT_Q4_0>(ops, n, s) : launch_generic<FMT_Q4_0>(ops, n, s);
+        case FMT_Q4_K: return sh ? launch_short<FMT_Q4_K>(ops, n, s) : launch_generic<FMT_Q4_K>(ops, n, s);
         default: return hipErrorInvalidValue;
         }
     }
@@ -897,19 +974,19 @@ hipError_t launch_gemv_ops(const GemvOp* ops, int count, hipStream_t stream, int
 {
     int i = 0;
     while (i < count) {
-        const bool tiled = tiled_ok(ops[i]);
-        if (!tiled && ops[i].in != XF_PLAIN)
+        const int kind = kind_of(ops[i]);
+        if (kind != PATH_FAST && ops[i].in != XF_PLAIN)
             return hipErrorNotSupported;
         int n = 1;
-        while (i + n < count && n < MAX_SEGS && ops[i + n].fmt == ops[i].fmt && tiled_ok(ops[i + n]) == tiled &&
-               (!tiled || ops[i + n].cols == ops[i].cols))
+        while (i + n < count && n < MAX_SEGS && ops[i + n].fmt == ops[i].fmt && kind_of(ops[i + n]) == kind &&
+               (kind != PATH_FAST || ops[i + n].cols == ops[i].cols))
             n++;
-        const hipError_t e = launch_group(ops + i, n, tiled, stream);
+        const hipError_t e = launch_group(ops + i, n, kind, stream);
         if (e != hipSuccess)
             return e;
         if (paths)
             for (int k = 0; k < n; k++)
-                paths[i + k] = tiled ? PATH_FAST : PATH_GENERIC;
+                paths[i + k] = kind;
         i += n;
     }
     return hipSuccess;

@@ -78,7 +78,7 @@ struct GemvOp {
 };
 
 // Which kernel a launch used; reported to the caller for tests and profiles.
-enum GemvPath : int { PATH_FAST = 1, PATH_GENERIC = 2 };
+enum GemvPath : int { PATH_FAST = 1, PATH_GENERIC = 2, PATH_SHORT = 3 };
 
 // Launches `count` independent products (no op reads what another writes).
 // Consecutive ops that share a format and, for the tiled kernel, a column

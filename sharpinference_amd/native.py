@@ -23,7 +23,7 @@ BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
 
 OK, ERR_ARGUMENT, ERR_UNSUPPORTED, ERR_ADAPTATION, ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_STATE, ERR_FORMAT, ERR_IO = range(9)
-PATH_FAST, PATH_GENERIC = 1, 2
+PATH_FAST, PATH_GENERIC, PATH_SHORT = 1, 2, 3
 
 # Every symbol include/sharpinference_hip.h declares, with its ctypes signature.
 _vp, _i32, _i64, _u32, _u64, _dbl = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32,

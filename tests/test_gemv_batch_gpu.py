@@ -138,7 +138,7 @@ def test_swiglu_rows(hip, fmt, cols):
     op = native.gemv_op(fmt, dw.ptr, dx.ptr, dy.ptr, F, cols, output=native.OUT_SWIGLU_ROWS,
                         xform=native.X_RMSNORM if tiled else native.X_PLAIN, norm_weight=dg.ptr if tiled else 0,
                         eps=1e-5)
-    assert hip.gemv_batch([op]) == [native.PATH_FAST if tiled else native.PATH_GENERIC]
+    assert hip.gemv_batch([op]) == [native.PATH_FAST if tiled else native.PATH_SHORT]
     xs = orc.rmsnorm(x, g, 1e-5) if tiled else x
     gu = fp64_product(fmt, w, 2 * F, cols, xs)
     t = gu[:F] / (1 + np.exp(-gu[:F])) * gu[F:]
@@ -147,7 +147,7 @@ def test_swiglu_rows(hip, fmt, cols):
 
 
 def test_any_shape_batch_of_short_products(hip):
-    """The RWKV-7 LoRA outputs: K = 96, 96, 256, 64 in one any-shape launch."""
+    """The RWKV-7 LoRA outputs: K = 96, 96, 256, 64 in one short-row launch."""
     fmt, D = native.Q8_0, 2048
     B = Bufs(hip)
     ops, ref, ys = [], [], []
@@ -158,7 +158,7 @@ def test_any_shape_batch_of_short_products(hip):
         ops.append(native.gemv_op(fmt, dw.ptr, dx.ptr, dy.ptr, D, K))
         ref.append(fp64_product(fmt, w, D, K, x))
         ys.append(dy)
-    assert hip.gemv_batch(ops) == [native.PATH_GENERIC] * 4
+    assert hip.gemv_batch(ops) == [native.PATH_SHORT] * 4
     for i in range(4):
         close(ys[i].readback(np.float32), ref[i], 1e-3, 1e-5, f"op {i}")
     B.free()

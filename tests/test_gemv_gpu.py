@@ -82,7 +82,9 @@ def test_q8_0_vocabulary_head_matches_oracle(hip):
     assert_gemv_close(y, orc.gemv_f64(native.Q8_0, w, x, rows, cols), "head")
 
 
-GENERIC = [(native.Q8_0, 513, 4160), (native.Q4_0, 65, 96), (native.Q4_K, 9, 2304), (native.Q8_0, 300, 3072)]
+GENERIC = [(native.Q8_0, 513, 4160), (native.Q4_0, 65, 96), (native.Q4_K, 9, 2304), (native.Q8_0, 300, 3072),
+           (native.Q8_0, 2048, 96), (native.Q8_0, 33, 64), (native.Q4_0, 7, 992), (native.Q4_K, 100, 512),
+           (native.Q4_K, 5, 1792), (native.Q8_0, 1000, 1056)]
 
 
 @pytest.mark.parametrize("fmt,rows,cols", GENERIC, ids=[f"{NAMES[f]}-{r}x{c}" for f, r, c in GENERIC])
@@ -92,7 +94,8 @@ def test_any_shape_path_matches_oracle(hip, fmt, rows, cols):
     # a 2-byte offset leaves W without dword alignment, which routes 3072
     # columns to the any-shape kernel as well
     y, path = run_gemv(hip, fmt, w, x, rows, cols, w_offset=2 if cols == 3072 else 0)
-    assert path == native.PATH_GENERIC
+    short = cols // native.BLOCK_ELEMS[fmt] <= 32 and cols <= 2048
+    assert path == (native.PATH_SHORT if short else native.PATH_GENERIC)
     assert_gemv_close(y, orc.gemv_f64(fmt, w, x, rows, cols))
 
 
