@@ -22,6 +22,8 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD_DIR = os.path.join(PKG, "_build")
 LIB_NAME = "libsharpinference_hip.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
+HOST_DIR = os.path.join(PKG, "host")
+HOST_LIB_PATH = os.path.join(PKG, "libsharpinference_hip_host.so")
 ARCH = os.environ.get("SI_HIP_ARCH", "gfx950")
 
 SOURCES = [
@@ -84,9 +86,28 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_host()
     if verbose:
         print(f"built {LIB_PATH}")
+        print(f"built {HOST_LIB_PATH}")
     return LIB_PATH
+
+
+def build_host() -> str:
+    """The C++ host interface (instruction contract, registry, VM executor)
+    as libsharpinference_hip_host.so, linked against the HIP library in the
+    same directory (found through an $ORIGIN run path)."""
+    tmp = HOST_LIB_PATH + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+           f"-I{os.path.join(ROOT, 'include')}", os.path.join(HOST_DIR, "si_host.cpp"),
+           f"-L{PKG}", "-lsharpinference_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"host library build failed:\n{proc.stderr}")
+    if proc.stderr.strip():
+        sys.stderr.write(proc.stderr)
+    os.replace(tmp, HOST_LIB_PATH)
+    return HOST_LIB_PATH
 
 
 if __name__ == "__main__":

@@ -1,0 +1,615 @@
+// Host side of the HIP backend: instruction contract, registry, the HIP
+// quantized instruction collection, and the VM program executor, over the
+// C ABI of libsharpinference_hip.  See si_host.hpp for the mapping to the
+// reference's managed types.
+#include "si_host.hpp"
+
+#include <algorithm>
+#include <set>
+#include <sstream>
+
+namespace sharpinference {
+
+namespace {
+
+std::string TypeName(GraphElementType t)
+{
+    switch (t) {
+    case GraphElementType::Float32: return "Float32";
+    case GraphElementType::Float16: return "Float16";
+    case GraphElementType::UInt8: return "UInt8";
+    case GraphElementType::Int32: return "Int32";
+    }
+    return "?";
+}
+
+bool Blank(const std::string& s)
+{
+    return std::all_of(s.begin(), s.end(), [](char c) { return c == ' ' || c == '\t' || c == '\n' || c == '\r'; });
+}
+
+const InstructionParameter* Find(const std::vector<InstructionParameter>& parameters, const std::string& name)
+{
+    for (const auto& p : parameters)
+        if (p.name == name)
+            return &p;
+    return nullptr;
+}
+
+}  // namespace
+
+InstructionAdaptationException::InstructionAdaptationException(const std::string& collection, const std::string& name,
+                                                               const std::string& reason)
+    : InvalidOperationException("Instruction '" + collection + "/" + name + "' cannot adapt parameters: " + reason)
+{
+}
+
+void Check(int status, const si_hip_context* context)
+{
+    if (status == SI_HIP_OK)
+        return;
+    const char* m = si_hip_last_error(context);
+    const std::string message = m ? m : "";
+    switch (status) {
+    case SI_HIP_ERR_ARGUMENT: throw ArgumentException(message);
+    case SI_HIP_ERR_UNSUPPORTED: throw NotSupportedException(message);
+    case SI_HIP_ERR_ADAPTATION: throw InvalidOperationException(message);
+    case SI_HIP_ERR_OUT_OF_MEMORY: throw OutOfMemoryException(message);
+    case SI_HIP_ERR_STATE: throw InvalidOperationException(message);
+    case SI_HIP_ERR_FORMAT: throw InvalidDataException(message);
+    case SI_HIP_ERR_IO: throw IOException(message);
+    default: throw DeviceException(message);
+    }
+}
+
+int ElementSize(GraphElementType type)
+{
+    switch (type) {
+    case GraphElementType::Float32: return 4;
+    case GraphElementType::Float16: return 2;
+    case GraphElementType::UInt8: return 1;
+    case GraphElementType::Int32: return 4;
+    }
+    return 0;
+}
+
+bool Satisfies(GraphElementType provided, GraphElementType required)
+{
+    auto rank = [](GraphElementType t) { return t == GraphElementType::Float16 ? 1 : t == GraphElementType::Float32 ? 2 : 0; };
+    if (rank(provided) == 0 || rank(required) == 0)
+        return provided == required;
+    return rank(provided) >= rank(required);
+}
+
+uint64_t TensorDescriptor::ElementCount() const
+{
+    uint64_t n = 1;
+    for (int64_t d : dimensions)
+        n *= static_cast<uint64_t>(d);
+    return n;
+}
+
+uint64_t TensorDescriptor::ByteLength() const { return ElementCount() * static_cast<uint64_t>(ElementSize(element_type)); }
+
+InstructionParameter InstructionParameter::Tensor(std::string name, TensorDescriptor tensor, GraphResourceAccess access,
+                                                  std::string source, uint64_t byte_offset)
+{
+    InstructionParameter p;
+    p.kind = Kind::Tensor;
+    p.name = std::move(name);
+    p.tensor = std::move(tensor);
+    p.access = access;
+    p.source = std::move(source);
+    p.byte_offset = byte_offset;
+    return p;
+}
+
+InstructionParameter InstructionParameter::Attribute(std::string name, std::string value)
+{
+    InstructionParameter p;
+    p.kind = Kind::Attribute;
+    p.name = std::move(name);
+    p.value = std::move(value);
+    return p;
+}
+
+// ---- Instruction ---------------------------------------------------------------------------
+
+void Instruction::Fail(const std::string& reason) const { throw InstructionAdaptationException(CollectionId(), Name(), reason); }
+
+void Instruction::Invoke(IInstructionRecorder& recorder, const std::vector<InstructionParameter>& parameters,
+                         const PrecisionRequirement& precision) const
+{
+    if (recorder.Target() != Target())
+        Fail("requires " + Target().architecture + ", recorder is " + recorder.Target().architecture + ".");
+    Adapt(parameters, precision);
+    recorder.Record(Generate(parameters));
+}
+
+InstructionSignature Instruction::Adapt(const std::vector<InstructionParameter>& parameters,
+                                        const PrecisionRequirement& precision) const
+{
+    InstructionSignature signature = GetSignature(parameters, precision);
+    Validate(parameters);
+    return signature;
+}
+
+InstructionSignature Instruction::GetSignature(const std::vector<InstructionParameter>& parameters,
+                                               const PrecisionRequirement& precision) const
+{
+    std::set<std::string> names;
+    for (const auto& p : parameters)
+        names.insert(p.name);
+    if (names.size() != parameters.size())
+        Fail("Invalid or duplicate parameters.");
+    std::vector<const InstructionParameter*> tensors;
+    std::set<std::string> attributes;
+    for (const auto& p : parameters) {
+        if (p.kind == InstructionParameter::Kind::Tensor)
+            tensors.push_back(&p);
+        else
+            attributes.insert(p.name);
+    }
+    std::vector<InstructionSignature> matches;
+    for (const auto& sig : Signatures()) {
+        if (sig.ports.size() != tensors.size())
+            continue;
+        if (std::set<std::string>(sig.attributes.begin(), sig.attributes.end()) != attributes)
+            continue;
+        bool all = true;
+        for (const auto& port : sig.ports) {
+            bool found = false;
+            for (const auto* t : tensors)
+                if (t->name == port.name && t->tensor.element_type == port.element_type &&
+                    (port.access == GraphResourceAccess::Read || t->access != GraphResourceAccess::Read))
+                    found = true;
+            all &= found;
+        }
+        if (all)
+            matches.push_back(sig);
+    }
+    if (matches.empty())
+        Fail("No supported parameter signature.");
+    std::vector<InstructionSignature> compatible;
+    for (const auto& sig : matches)
+        if (Satisfies(sig.precision.arithmetic_type, precision.minimum_arithmetic_type) &&
+            Satisfies(sig.precision.accumulator_type, precision.minimum_accumulator_type))
+            compatible.push_back(sig);
+    if (compatible.empty()) {
+        std::ostringstream os;
+        os << "On " << Target().architecture << ", required arithmetic=" << TypeName(precision.minimum_arithmetic_type)
+           << ", accumulator=" << TypeName(precision.minimum_accumulator_type) << "; provided ";
+        for (size_t i = 0; i < matches.size(); i++)
+            os << (i ? "; " : "") << "arithmetic=" << TypeName(matches[i].precision.arithmetic_type)
+               << ", accumulator=" << TypeName(matches[i].precision.accumulator_type);
+        os << ".";
+        Fail(os.str());
+    }
+    if (compatible.size() != 1)
+        Fail("Ambiguous supported parameter/precision signatures.");
+    return compatible[0];
+}
+
+// ---- InstructionRegistry -------------------------------------------------------------------
+
+InstructionRegistry::InstructionRegistry(std::vector<std::shared_ptr<const IInstructionCollectionProvider>> providers)
+    : providers_(std::move(providers))
+{
+    for (const auto& p : providers_)
+        if (!p)
+            throw ArgumentException("IC providers cannot contain null.");
+    std::vector<InstructionCollectionDescription> all;
+    for (const auto& p : providers_)
+        for (const auto& d : p->QueryInstructionCollection())
+            all.push_back(d);
+    for (size_t i = 0; i < all.size(); i++)
+        for (size_t j = i + 1; j < all.size(); j++)
+            if (all[i].id == all[j].id && all[i].architecture == all[j].architecture && !(all[i] == all[j]))
+                throw InvalidDataException("Conflicting IC descriptions for '" + all[i].id + "'.");
+    for (const auto& d : all)
+        if (Blank(d.name) || d.tier < 0 || Blank(d.architecture.architecture))
+            throw InvalidDataException("IC descriptions require a name and non-negative Tier.");
+    for (const auto& d : all)
+        if (std::find(collections_.begin(), collections_.end(), d) == collections_.end())
+            collections_.push_back(d);
+    std::sort(collections_.begin(), collections_.end(), [](const auto& a, const auto& b) {
+        return a.id != b.id ? a.id < b.id : a.architecture.architecture < b.architecture.architecture;
+    });
+}
+
+std::vector<std::shared_ptr<const Instruction>> InstructionRegistry::QueryInstruction(const std::string& collection_id,
+                                                                                     const std::string& name) const
+{
+    if (Blank(name))
+        throw ArgumentException("instructionName cannot be empty.");
+    const bool installed = std::any_of(collections_.begin(), collections_.end(),
+                                       [&](const auto& c) { return c.id == collection_id; });
+    if (!installed)
+        throw NotSupportedException("Instruction collection '" + collection_id + "' is not installed.");
+    std::vector<std::shared_ptr<const Instruction>> values;
+    for (const auto& p : providers_) {
+        const auto cs = p->QueryInstructionCollection();
+        if (std::none_of(cs.begin(), cs.end(), [&](const auto& c) { return c.id == collection_id; }))
+            continue;
+        for (const auto& v : p->QueryInstruction(collection_id, name))
+            values.push_back(v);
+    }
+    for (const auto& v : values) {
+        const bool known = std::any_of(collections_.begin(), collections_.end(), [&](const auto& c) {
+            return c.id == collection_id && c.architecture == v->Target();
+        });
+        if (!v || v->CollectionId() != collection_id || v->Name() != name || !known)
+            throw InvalidDataException("Provider returned an instruction with a different identity.");
+    }
+    for (size_t i = 0; i < values.size(); i++)
+        for (size_t j = i + 1; j < values.size(); j++)
+            if (values[i]->Target() == values[j]->Target())
+                throw InvalidDataException("Ambiguous implementations for '" + collection_id + "/" + name + "'.");
+    for (const auto& v : values)
+        for (const auto& sig : v->Signatures()) {
+            std::set<std::string> ports, attrs(sig.attributes.begin(), sig.attributes.end());
+            for (const auto& port : sig.ports) {
+                if (Blank(port.name))
+                    throw InvalidDataException("Invalid signatures for '" + collection_id + "/" + name + "'.");
+                ports.insert(port.name);
+            }
+            if (ports.size() != sig.ports.size() || attrs.size() != sig.attributes.size())
+                throw InvalidDataException("Invalid signatures for '" + collection_id + "/" + name + "'.");
+        }
+    return values;
+}
+
+std::shared_ptr<const Instruction> InstructionRegistry::Resolve(const std::string& collection_id,
+                                                                const std::string& name,
+                                                                const InstructionTarget& target) const
+{
+    for (const auto& v : QueryInstruction(collection_id, name))
+        if (v->Target() == target)
+            return v;
+    throw NotSupportedException("No " + target.architecture + " implementation for '" + collection_id + "/" + name +
+                                "'.");
+}
+
+// ---- the HIP quantized collection ----------------------------------------------------------
+
+int FormatId(const std::string& name)
+{
+    if (name == "q8_0") return SI_HIP_Q8_0;
+    if (name == "q4_0") return SI_HIP_Q4_0;
+    if (name == "q4_k") return SI_HIP_Q4_K;
+    return -1;
+}
+
+namespace {
+
+constexpr KernelPrecisionProfile FP32{GraphElementType::Float32, GraphElementType::Float32};
+
+// format and columns attributes, and the weight row length they imply
+struct QuantShape {
+    int format;
+    int64_t columns;
+    uint64_t row_bytes;
+};
+
+QuantShape ReadQuantShape(const Instruction& self, const std::vector<InstructionParameter>& parameters)
+{
+    auto fail = [&](const std::string& why) -> QuantShape {
+        throw InstructionAdaptationException(self.CollectionId(), self.Name(), why);
+    };
+    const auto* f = Find(parameters, "format");
+    const auto* c = Find(parameters, "columns");
+    const int format = FormatId(f->value);
+    if (format < 0)
+        return fail("format '" + f->value + "' is not q8_0, q4_0 or q4_k.");
+    int64_t columns = 0;
+    try {
+        size_t used = 0;
+        columns = std::stoll(c->value, &used);
+        if (used != c->value.size())
+            columns = -1;
+    } catch (const std::exception&) {
+        columns = -1;
+    }
+    uint64_t row_bytes = 0;
+    if (columns < 1 || si_hip_tensor_bytes(format, 1, columns, &row_bytes) != SI_HIP_OK)
+        return fail("columns '" + c->value + "' is not a positive whole number of " + f->value + " blocks.");
+    return {format, columns, row_bytes};
+}
+
+}  // namespace
+
+std::vector<InstructionSignature> QuantizedMatVecInstruction::Signatures() const
+{
+    std::vector<InstructionSignature> s;
+    for (const char* weight : {"weight", "matrix"})
+        s.push_back({{{weight, GraphElementType::UInt8, GraphResourceAccess::Read},
+                      {"input", GraphElementType::Float32, GraphResourceAccess::Read},
+                      {"output", GraphElementType::Float32, GraphResourceAccess::ReadWrite}},
+                     {"format", "columns"},
+                     FP32});
+    return s;
+}
+
+void QuantizedMatVecInstruction::Validate(const std::vector<InstructionParameter>& parameters) const
+{
+    const QuantShape q = ReadQuantShape(*this, parameters);
+    const auto* w = Find(parameters, "weight");
+    if (!w)
+        w = Find(parameters, "matrix");
+    const auto* x = Find(parameters, "input");
+    const auto* y = Find(parameters, "output");
+    if (w->tensor.dimensions.size() != 2 || w->tensor.dimensions[1] != static_cast<int64_t>(q.row_bytes) ||
+        w->tensor.dimensions[0] < 1)
+        Fail("the weight must be [rows, " + std::to_string(q.row_bytes) + "] bytes for " +
+             std::to_string(q.columns) + " columns.");
+    if (x->tensor.ElementCount() != static_cast<uint64_t>(q.columns))
+        Fail("input has " + std::to_string(x->tensor.ElementCount()) + " elements, columns is " +
+             std::to_string(q.columns) + ".");
+    if (y->tensor.ElementCount() != static_cast<uint64_t>(w->tensor.dimensions[0]))
+        Fail("output has " + std::to_string(y->tensor.ElementCount()) + " elements for " +
+             std::to_string(w->tensor.dimensions[0]) + " weight rows.");
+}
+
+InstructionRecording QuantizedMatVecInstruction::Generate(const std::vector<InstructionParameter>& parameters) const
+{
+    return {"si_hip_gemv", parameters};
+}
+
+std::vector<InstructionSignature> QuantizedGatherRowInstruction::Signatures() const
+{
+    return {{{{"table", GraphElementType::UInt8, GraphResourceAccess::Read},
+              {"index", GraphElementType::Int32, GraphResourceAccess::Read},
+              {"output", GraphElementType::Float32, GraphResourceAccess::ReadWrite}},
+             {"format", "columns"},
+             FP32}};
+}
+
+void QuantizedGatherRowInstruction::Validate(const std::vector<InstructionParameter>& parameters) const
+{
+    const QuantShape q = ReadQuantShape(*this, parameters);
+    const auto* t = Find(parameters, "table");
+    const auto* i = Find(parameters, "index");
+    const auto* y = Find(parameters, "output");
+    if (t->tensor.dimensions.size() != 2 || t->tensor.dimensions[1] != static_cast<int64_t>(q.row_bytes) ||
+        t->tensor.dimensions[0] < 1)
+        Fail("the table must be [rows, " + std::to_string(q.row_bytes) + "] bytes.");
+    if (i->tensor.ElementCount() != 1)
+        Fail("index must hold one element.");
+    if (y->tensor.ElementCount() != static_cast<uint64_t>(q.columns))
+        Fail("output must hold the " + std::to_string(q.columns) + " columns of a row.");
+}
+
+InstructionRecording QuantizedGatherRowInstruction::Generate(const std::vector<InstructionParameter>& parameters) const
+{
+    return {"si_hip_gather_row", parameters};
+}
+
+std::vector<InstructionCollectionDescription> HipQuantizedInstructions::QueryInstructionCollection() const
+{
+    return {{HipInstructionCollectionIds::QuantizedFloat32, "HIP quantized products", 0, InstructionTarget::Hip()}};
+}
+
+std::vector<std::shared_ptr<const Instruction>> HipQuantizedInstructions::QueryInstruction(
+    const std::string& collection_id, const std::string& name) const
+{
+    if (collection_id != HipInstructionCollectionIds::QuantizedFloat32)
+        return {};
+    if (name == "quant.mat-vec")
+        return {std::make_shared<QuantizedMatVecInstruction>()};
+    if (name == "quant.gather-row")
+        return {std::make_shared<QuantizedGatherRowInstruction>()};
+    return {};
+}
+
+// ---- HipVmProgram --------------------------------------------------------------------------
+
+namespace {
+
+class EntryRecorder : public IInstructionRecorder {
+public:
+    InstructionTarget Target() const override { return InstructionTarget::Hip(); }
+    void Record(InstructionRecording recording) override { recordings.push_back(std::move(recording)); }
+    std::vector<InstructionRecording> recordings;
+};
+
+}  // namespace
+
+int HipVmProgram::SlotIndex(const std::string& id) const
+{
+    for (size_t i = 0; i < slots_.size(); i++)
+        if (slots_[i].id == id)
+            return static_cast<int>(i);
+    return -1;
+}
+
+void HipVmProgram::AddSlot(HipVmSlot slot)
+{
+    if (Blank(slot.id) || SlotIndex(slot.id) >= 0)
+        throw InvalidDataException("Empty or duplicate slot '" + slot.id + "'.");
+    if (slot.tensor.ByteLength() == 0)
+        throw InvalidDataException("Slot '" + slot.id + "' is empty.");
+    slots_.push_back(std::move(slot));
+}
+
+void HipVmProgram::AddDispatch(const std::string& entry, std::shared_ptr<const Instruction> instruction,
+                               const std::vector<InstructionParameter>& parameters,
+                               const PrecisionRequirement& precision)
+{
+    if (!instruction)
+        throw ArgumentException("instruction cannot be null.");
+    if (Blank(entry))
+        throw ArgumentException("entry cannot be empty.");
+    std::vector<const InstructionParameter*> tensors;
+    for (const auto& p : parameters) {
+        if (p.kind != InstructionParameter::Kind::Tensor)
+            continue;
+        const int s = SlotIndex(p.source);
+        if (s < 0)
+            throw ArgumentException("Parameter '" + p.name + "' names unknown slot '" + p.source + "'.");
+        const uint64_t end = p.byte_offset + p.tensor.ByteLength();
+        if (end < p.byte_offset || end > slots_[s].tensor.ByteLength())
+            throw InvalidDataException("Parameter '" + p.name + "' does not fit in slot '" + p.source + "'.");
+        if (p.access == GraphResourceAccess::ReadWrite && slots_[s].access != GraphResourceAccess::ReadWrite)
+            throw InvalidDataException("Parameter '" + p.name + "' writes read-only slot '" + p.source + "'.");
+        tensors.push_back(&p);
+    }
+    for (size_t i = 0; i < tensors.size(); i++)
+        for (size_t j = i + 1; j < tensors.size(); j++) {
+            const auto* a = tensors[i];
+            const auto* b = tensors[j];
+            if (a->source == b->source &&
+                (a->access == GraphResourceAccess::ReadWrite || b->access == GraphResourceAccess::ReadWrite) &&
+                a->byte_offset < b->byte_offset + b->tensor.ByteLength() &&
+                b->byte_offset < a->byte_offset + a->tensor.ByteLength())
+                throw NotSupportedException("Dispatch '" + entry + "' aliases writable kernel parameters.");
+        }
+    EntryRecorder recorder;
+    instruction->Invoke(recorder, parameters, precision);
+    for (auto& r : recorder.recordings)
+        entries_[entry].push_back({instruction, std::move(r)});
+}
+
+// ---- HipVmExecutor -------------------------------------------------------------------------
+
+HipVmExecutor::HipVmExecutor(HipVmProgram program, int device) : program_(std::move(program))
+{
+    Check(si_hip_init(device, &context_));
+    try {
+        for (const auto& slot : program_.Slots()) {
+            void* p = nullptr;
+            const uint64_t bytes = slot.tensor.ByteLength();
+            Check(si_hip_alloc(context_, bytes < 4 ? 4 : bytes, &p), context_);
+            buffers_.push_back(p);
+            Check(si_hip_fill_u32(context_, p, 0, (bytes + 3) / 4), context_);
+        }
+        Check(si_hip_sync(context_), context_);
+    } catch (...) {
+        for (void* p : buffers_)
+            si_hip_free(context_, p);
+        si_hip_destroy(context_);
+        throw;
+    }
+}
+
+HipVmExecutor::~HipVmExecutor()
+{
+    for (auto& kv : plans_)
+        si_hip_plan_destroy(kv.second);
+    for (void* p : buffers_)
+        si_hip_free(context_, p);
+    si_hip_destroy(context_);
+}
+
+void HipVmExecutor::Upload(const std::string& slot, const void* bytes, uint64_t length)
+{
+    const int s = program_.SlotIndex(slot);
+    if (s < 0)
+        throw ArgumentException("Unknown slot '" + slot + "'.");
+    const uint64_t expected = program_.Slots()[s].tensor.ByteLength();
+    if (length != expected)
+        throw ArgumentException("Expected " + std::to_string(expected) + " bytes for slot '" + slot + "', received " +
+                                std::to_string(length) + ".");
+    if (!bytes)
+        throw ArgumentException("bytes cannot be null.");
+    Check(si_hip_upload(context_, buffers_[s], bytes, length), context_);
+}
+
+std::vector<uint8_t> HipVmExecutor::Readback(const std::string& slot)
+{
+    const int s = program_.SlotIndex(slot);
+    if (s < 0)
+        throw ArgumentException("Unknown slot '" + slot + "'.");
+    std::vector<uint8_t> out(program_.Slots()[s].tensor.ByteLength());
+    Check(si_hip_readback(context_, out.data(), buffers_[s], out.size()), context_);
+    return out;
+}
+
+void* HipVmExecutor::Address(const InstructionParameter& p) const
+{
+    return static_cast<uint8_t*>(buffers_[program_.SlotIndex(p.source)]) + p.byte_offset;
+}
+
+void HipVmExecutor::Launch(const InstructionRecording& r)
+{
+    const auto attr = [&](const char* n) { return Find(r.parameters, n)->value; };
+    if (r.operation == "si_hip_gemv") {
+        const auto* w = Find(r.parameters, "weight");
+        if (!w)
+            w = Find(r.parameters, "matrix");
+        const auto* x = Find(r.parameters, "input");
+        const auto* y = Find(r.parameters, "output");
+        Check(si_hip_gemv(context_, FormatId(attr("format")), Address(*w), static_cast<const float*>(Address(*x)),
+                          static_cast<float*>(Address(*y)), w->tensor.dimensions[0], std::stoll(attr("columns")),
+                          nullptr, nullptr),
+              context_);
+    } else if (r.operation == "si_hip_gather_row") {
+        const auto* t = Find(r.parameters, "table");
+        const auto* i = Find(r.parameters, "index");
+        const auto* y = Find(r.parameters, "output");
+        Check(si_hip_gather_row(context_, FormatId(attr("format")), Address(*t), t->tensor.dimensions[0],
+                                std::stoll(attr("columns")), static_cast<const int32_t*>(Address(*i)),
+                                static_cast<float*>(Address(*y))),
+              context_);
+    } else {
+        throw NotSupportedException("No HIP launch for recording '" + r.operation + "'.");
+    }
+}
+
+si_hip_plan* HipVmExecutor::PrepareEntry(const std::string& entry)
+{
+    const auto it = program_.Entries().find(entry);
+    if (it == program_.Entries().end())
+        throw ArgumentException("Unknown entry '" + entry + "'.");
+    const auto cached = plans_.find(entry);
+    if (cached != plans_.end())
+        return cached->second;
+    Check(si_hip_plan_begin(context_), context_);
+    try {
+        for (const auto& d : it->second)
+            Launch(d.recording);
+    } catch (...) {
+        si_hip_plan* broken = nullptr;
+        if (si_hip_plan_end(context_, &broken) == SI_HIP_OK)
+            si_hip_plan_destroy(broken);
+        throw;
+    }
+    si_hip_plan* plan = nullptr;
+    Check(si_hip_plan_end(context_, &plan), context_);
+    plans_[entry] = plan;
+    return plan;
+}
+
+void HipVmExecutor::Execute(const std::string& entry)
+{
+    si_hip_plan* plan = PrepareEntry(entry);
+    Check(si_hip_plan_launch(plan), context_);
+    Check(si_hip_sync(context_), context_);
+}
+
+void HipVmExecutor::ExecuteWithTransfers(const std::string& entry, const std::string& upload_slot,
+                                         const std::vector<uint8_t>& upload_bytes, const std::string& readback_slot,
+                                         std::vector<uint8_t>& readback_bytes)
+{
+    const int r = program_.SlotIndex(readback_slot);
+    if (r < 0)
+        throw ArgumentException("Unknown slot '" + readback_slot + "'.");
+    if (readback_bytes.size() != program_.Slots()[r].tensor.ByteLength())
+        throw ArgumentException("Expected a " + std::to_string(program_.Slots()[r].tensor.ByteLength()) +
+                                "-byte readback buffer for slot '" + readback_slot + "'.");
+    si_hip_plan* plan = PrepareEntry(entry);
+    Upload(upload_slot, upload_bytes);
+    Check(si_hip_plan_launch(plan), context_);
+    Check(si_hip_readback(context_, readback_bytes.data(), buffers_[r], readback_bytes.size()), context_);
+}
+
+double HipVmExecutor::MeasureGpuMicroseconds(const std::string& entry, int repetitions)
+{
+    if (repetitions < 1 || repetitions > 1024)
+        throw ArgumentOutOfRangeException("repetitions");
+    si_hip_plan* plan = PrepareEntry(entry);
+    double us = 0.0;
+    Check(si_hip_plan_measure_us(plan, repetitions, &us), context_);
+    return us;
+}
+
+}  // namespace sharpinference

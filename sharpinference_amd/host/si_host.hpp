@@ -1,0 +1,330 @@
+// Host side of the HIP backend in C++: the instruction/plugin interface and
+// the VM executor of the reference, restated over the C ABI of
+// libsharpinference_hip (include/sharpinference_hip.h).
+//
+// The reference's managed host (C#) declares the operator contract in
+// SharpInference.Instructions/InstructionCollection.cs (Instruction,
+// signatures, adaptation, the collection registry) and runs VM programs
+// through executors such as SharpInference.Backends.D3D12Vm/
+// D3D12VmExecutor.cs (slots, Upload / Readback / Execute /
+// MeasureGpuMicroseconds).  This header keeps those names, argument
+// meanings and failure types, so the parity tests read like the
+// reference's own tests:
+//
+//   .NET exception                   C++ exception here
+//   ArgumentException                ArgumentException
+//   ArgumentOutOfRangeException      ArgumentOutOfRangeException
+//   InvalidOperationException        InvalidOperationException
+//   InstructionAdaptationException   InstructionAdaptationException
+//   NotSupportedException            NotSupportedException
+//   InvalidDataException             InvalidDataException
+//
+// The HIP target records launch descriptors instead of shader source: an
+// InstructionRecording names the C ABI operation and carries the adapted
+// parameters, and the executor turns each recording into one library call
+// inside a recorded plan.
+#pragma once
+
+#include "sharpinference_hip.h"
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace sharpinference {
+
+// ---- .NET exception types --------------------------------------------------------------
+
+struct ArgumentException : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+struct ArgumentOutOfRangeException : ArgumentException {
+    using ArgumentException::ArgumentException;
+};
+struct InvalidOperationException : std::logic_error {
+    using std::logic_error::logic_error;
+};
+struct NotSupportedException : std::logic_error {
+    using std::logic_error::logic_error;
+};
+struct InvalidDataException : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct OutOfMemoryException : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct IOException : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+// A HIP runtime failure (SI_HIP_ERR_DEVICE).
+struct DeviceException : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// Instruction '{collection}/{name}' cannot adapt parameters: {reason}
+// (InstructionCollection.cs:155-159).
+struct InstructionAdaptationException : InvalidOperationException {
+    InstructionAdaptationException(const std::string& collection, const std::string& name, const std::string& reason);
+};
+
+// Throws the exception that corresponds to a library status (no-op for OK).
+void Check(int status, const si_hip_context* context = nullptr);
+
+// ---- operator contract (InstructionCollection.cs) ----------------------------------------
+
+enum class GraphElementType { Float32, Float16, UInt8, Int32 };
+enum class GraphResourceAccess { Read, ReadWrite };
+
+int ElementSize(GraphElementType type);
+// Width order used by precision checks: Float16 < Float32 (integers compare
+// only with themselves).
+bool Satisfies(GraphElementType provided, GraphElementType required);
+
+struct InstructionTarget {
+    std::string architecture;
+    bool operator==(const InstructionTarget& o) const { return architecture == o.architecture; }
+    bool operator!=(const InstructionTarget& o) const { return !(*this == o); }
+    static InstructionTarget Hip() { return {"hip.gfx950"}; }
+};
+
+struct InstructionCollectionDescription {
+    std::string id;             // GUID text
+    std::string name;
+    int tier;
+    InstructionTarget architecture;
+    bool operator==(const InstructionCollectionDescription& o) const
+    {
+        return id == o.id && name == o.name && tier == o.tier && architecture == o.architecture;
+    }
+};
+
+struct InstructionPort {
+    std::string name;
+    GraphElementType element_type;
+    GraphResourceAccess access;
+};
+
+struct KernelPrecisionProfile {
+    GraphElementType arithmetic_type;
+    GraphElementType accumulator_type;
+};
+
+struct PrecisionRequirement {
+    GraphElementType minimum_arithmetic_type;
+    GraphElementType minimum_accumulator_type;
+};
+
+struct InstructionSignature {
+    std::vector<InstructionPort> ports;
+    std::vector<std::string> attributes;
+    KernelPrecisionProfile precision;
+};
+
+struct TensorDescriptor {
+    GraphElementType element_type = GraphElementType::Float32;
+    std::vector<int64_t> dimensions;
+    uint64_t ElementCount() const;
+    uint64_t ByteLength() const;
+};
+
+// InstructionTensorParameter / InstructionAttributeParameter in one value.
+struct InstructionParameter {
+    enum class Kind { Tensor, Attribute } kind = Kind::Tensor;
+    std::string name;
+    TensorDescriptor tensor;                    // Tensor
+    GraphResourceAccess access = GraphResourceAccess::Read;
+    std::string source;                         // Tensor: the slot it is bound to
+    uint64_t byte_offset = 0;                   // Tensor: offset inside the slot
+    std::string value;                          // Attribute
+
+    static InstructionParameter Tensor(std::string name, TensorDescriptor tensor, GraphResourceAccess access,
+                                       std::string source, uint64_t byte_offset = 0);
+    static InstructionParameter Attribute(std::string name, std::string value);
+};
+
+// The HIP target's recording: the C ABI operation to launch and the
+// adapted parameters it binds.
+struct InstructionRecording {
+    std::string operation;
+    std::vector<InstructionParameter> parameters;
+};
+
+class IInstructionRecorder {
+public:
+    virtual ~IInstructionRecorder() = default;
+    virtual InstructionTarget Target() const = 0;
+    virtual void Record(InstructionRecording recording) = 0;
+};
+
+class Instruction {
+public:
+    virtual ~Instruction() = default;
+    virtual std::string CollectionId() const = 0;
+    virtual std::string Name() const = 0;
+    virtual InstructionTarget Target() const = 0;
+    virtual std::vector<InstructionSignature> Signatures() const = 0;
+
+    // Adapt, then record (Instruction.Invoke, InstructionCollection.cs:114-122).
+    void Invoke(IInstructionRecorder& recorder, const std::vector<InstructionParameter>& parameters,
+                const PrecisionRequirement& precision) const;
+    // The one signature the parameters match, after Validate (:124-130).
+    InstructionSignature Adapt(const std::vector<InstructionParameter>& parameters,
+                               const PrecisionRequirement& precision) const;
+    // Signature selection (:143-172): unique names, ports matched by name,
+    // element type and access, attribute set equality, precision.
+    InstructionSignature GetSignature(const std::vector<InstructionParameter>& parameters,
+                                      const PrecisionRequirement& precision) const;
+
+protected:
+    virtual void Validate(const std::vector<InstructionParameter>&) const {}
+    virtual InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const = 0;
+    [[noreturn]] void Fail(const std::string& reason) const;
+};
+
+class IInstructionCollectionProvider {
+public:
+    virtual ~IInstructionCollectionProvider() = default;
+    virtual std::vector<InstructionCollectionDescription> QueryInstructionCollection() const = 0;
+    virtual std::vector<std::shared_ptr<const Instruction>> QueryInstruction(const std::string& collection_id,
+                                                                            const std::string& name) const = 0;
+};
+
+// InstructionRegistry (InstructionCollection.cs:161-230).
+class InstructionRegistry : public IInstructionCollectionProvider {
+public:
+    explicit InstructionRegistry(std::vector<std::shared_ptr<const IInstructionCollectionProvider>> providers);
+    std::vector<InstructionCollectionDescription> QueryInstructionCollection() const override { return collections_; }
+    std::vector<std::shared_ptr<const Instruction>> QueryInstruction(const std::string& collection_id,
+                                                                    const std::string& name) const override;
+    std::shared_ptr<const Instruction> Resolve(const std::string& collection_id, const std::string& name,
+                                               const InstructionTarget& target) const;
+
+private:
+    std::vector<std::shared_ptr<const IInstructionCollectionProvider>> providers_;
+    std::vector<InstructionCollectionDescription> collections_;
+};
+
+// ---- the HIP quantized instruction collection -------------------------------------------
+
+namespace HipInstructionCollectionIds {
+// New collection: block-quantized matrix-vector products (the T0 mat-vec
+// rejects attributes and non-dense weights, TierZeroOperationContracts.cs:70-91,161).
+inline const std::string QuantizedFloat32 = "5c2f7b1e-9a4d-4f0e-8e61-3b7f2d9c4a10";
+}
+
+// quant.mat-vec: output[rows] = weight[rows, columns] . input[columns]; the
+// weight port is a UInt8 tensor [rows, row_bytes] of GGUF blocks, attributes
+// format (q8_0 | q4_0 | q4_k) and columns; port names as core.mat-vec
+// (weight or matrix, input, output); FP32 arithmetic and accumulation.
+class QuantizedMatVecInstruction : public Instruction {
+public:
+    std::string CollectionId() const override { return HipInstructionCollectionIds::QuantizedFloat32; }
+    std::string Name() const override { return "quant.mat-vec"; }
+    InstructionTarget Target() const override { return InstructionTarget::Hip(); }
+    std::vector<InstructionSignature> Signatures() const override;
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& parameters) const override;
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
+};
+
+// quant.gather-row: output[columns] = row index[0] of table[rows, columns]
+// (GpuTierZeroInstruction.cs:397-405 for a quantized table); NaN for an index
+// outside the table.
+class QuantizedGatherRowInstruction : public Instruction {
+public:
+    std::string CollectionId() const override { return HipInstructionCollectionIds::QuantizedFloat32; }
+    std::string Name() const override { return "quant.gather-row"; }
+    InstructionTarget Target() const override { return InstructionTarget::Hip(); }
+    std::vector<InstructionSignature> Signatures() const override;
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& parameters) const override;
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
+};
+
+class HipQuantizedInstructions : public IInstructionCollectionProvider {
+public:
+    std::vector<InstructionCollectionDescription> QueryInstructionCollection() const override;
+    std::vector<std::shared_ptr<const Instruction>> QueryInstruction(const std::string& collection_id,
+                                                                    const std::string& name) const override;
+};
+
+// GGUF format name of the quant attribute -> GGUF type id (-1 if unknown).
+int FormatId(const std::string& name);
+
+// ---- program and executor (VmProgram, D3D12VmExecutor) ------------------------------------
+
+struct HipVmSlot {
+    std::string id;
+    TensorDescriptor tensor;
+    GraphResourceAccess access = GraphResourceAccess::ReadWrite;
+};
+
+struct HipVmDispatch {
+    std::shared_ptr<const Instruction> instruction;
+    InstructionRecording recording;
+};
+
+// Slots and named entries; each entry is a list of dispatches separated by
+// barriers (every dispatch here is followed by one, as in the reference's
+// generated schedules).
+class HipVmProgram {
+public:
+    void AddSlot(HipVmSlot slot);
+    // Invokes the instruction on the entry's recorder.  Binding rules
+    // (D3D12VmSchedule.cs:74-99): every tensor names an existing slot and
+    // fits inside it at its byte offset; a ReadWrite port needs a writable
+    // slot; writable parameters of one dispatch may not overlap others
+    // (NotSupportedException).
+    void AddDispatch(const std::string& entry, std::shared_ptr<const Instruction> instruction,
+                     const std::vector<InstructionParameter>& parameters, const PrecisionRequirement& precision);
+
+    const std::vector<HipVmSlot>& Slots() const { return slots_; }
+    const std::map<std::string, std::vector<HipVmDispatch>>& Entries() const { return entries_; }
+    int SlotIndex(const std::string& id) const;   // -1 if absent
+
+private:
+    std::vector<HipVmSlot> slots_;
+    std::map<std::string, std::vector<HipVmDispatch>> entries_;
+};
+
+// The executor of a HipVmProgram on one device (D3D12VmExecutor.cs): one
+// persistent device buffer per slot, exact-size uploads, entries recorded
+// once into plans and replayed with one submission.
+class HipVmExecutor {
+public:
+    explicit HipVmExecutor(HipVmProgram program, int device = 0);
+    ~HipVmExecutor();
+    HipVmExecutor(const HipVmExecutor&) = delete;
+    HipVmExecutor& operator=(const HipVmExecutor&) = delete;
+
+    const HipVmProgram& Program() const { return program_; }
+    void Upload(const std::string& slot, const void* bytes, uint64_t length);
+    void Upload(const std::string& slot, const std::vector<uint8_t>& bytes) { Upload(slot, bytes.data(), bytes.size()); }
+    std::vector<uint8_t> Readback(const std::string& slot);
+    void Execute(const std::string& entry);
+    // Uploads one control slot, replays the entry, reads one result slot
+    // (D3D12VmExecutor.cs:298).
+    void ExecuteWithTransfers(const std::string& entry, const std::string& upload_slot,
+                              const std::vector<uint8_t>& upload_bytes, const std::string& readback_slot,
+                              std::vector<uint8_t>& readback_bytes);
+    // GPU microseconds per replay over `repetitions` (1..1024) back-to-back
+    // replays (D3D12VmExecutor.cs:452-478).
+    double MeasureGpuMicroseconds(const std::string& entry, int repetitions = 8);
+
+private:
+    si_hip_plan* PrepareEntry(const std::string& entry);
+    void Launch(const InstructionRecording& recording);
+    void* Address(const InstructionParameter& parameter) const;
+
+    HipVmProgram program_;
+    si_hip_context* context_ = nullptr;
+    std::vector<void*> buffers_;
+    std::map<std::string, si_hip_plan*> plans_;
+};
+
+}  // namespace sharpinference

@@ -1,0 +1,572 @@
+// Tests of the C++ host interface (sharpinference_amd/host/si_host.hpp):
+// the instruction contract and registry, program binding rules, and the VM
+// executor running quantized mat-vec and gather-row programs on the GPU.
+//
+// Mirrors SharpInference.Tests/GpuMatVecTests.cs for block-quantized
+// weights: tails, views with sentinel padding and repeated invocation
+// (:13-39, :283-310), non-finite sums (:54-67), compiler rejections
+// (:87-114), resident timestamp measurement (:116-127) and span upload
+// (:129-142).  Expected values come from the oracle's fp64 product over the
+// exactly dequantised weights (test infrastructure, linked only here).
+//
+//   test_host cpu    contract, registry and binding tests (no device)
+//   test_host gpu    executor tests on device 0
+#include "si_host.hpp"
+
+#include "oracle.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <typeinfo>
+#include <vector>
+
+using namespace sharpinference;
+
+namespace {
+
+struct TestCase {
+    const char* group;
+    const char* name;
+    std::function<void()> body;
+};
+
+std::vector<TestCase>& Registry()
+{
+    static std::vector<TestCase> tests;
+    return tests;
+}
+
+struct Register {
+    Register(const char* group, const char* name, std::function<void()> body)
+    {
+        Registry().push_back({group, name, std::move(body)});
+    }
+};
+
+struct Failure : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define TEST(group, name)                                                                                         \
+    void name();                                                                                                  \
+    const Register register_##name(#group, #name, name);                                                         \
+    void name()
+
+#define ASSERT_TRUE(cond)                                                                                         \
+    do {                                                                                                          \
+        if (!(cond))                                                                                              \
+            throw Failure(std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " #cond);                     \
+    } while (0)
+
+// Assert.Throws<T>: the exact exception type, not a subclass.
+template <typename T, typename F>
+void ThrowsExactly(F&& f, const char* what, int line)
+{
+    try {
+        f();
+    } catch (const std::exception& e) {
+        if (typeid(e) == typeid(T))
+            return;
+        throw Failure(std::string("line ") + std::to_string(line) + ": " + what + " threw " + typeid(e).name() +
+                      " (" + e.what() + "), expected " + typeid(T).name());
+    }
+    throw Failure(std::string("line ") + std::to_string(line) + ": " + what + " did not throw");
+}
+#define ASSERT_THROWS(T, expr) ThrowsExactly<T>([&] { (void)(expr); }, #expr, __LINE__)
+
+const PrecisionRequirement kFp32{GraphElementType::Float32, GraphElementType::Float32};
+
+std::shared_ptr<const InstructionRegistry> DefaultRegistry()
+{
+    return std::make_shared<InstructionRegistry>(
+        std::vector<std::shared_ptr<const IInstructionCollectionProvider>>{std::make_shared<HipQuantizedInstructions>()});
+}
+
+std::shared_ptr<const Instruction> MatVec()
+{
+    return DefaultRegistry()->Resolve(HipInstructionCollectionIds::QuantizedFloat32, "quant.mat-vec",
+                                      InstructionTarget::Hip());
+}
+
+std::shared_ptr<const Instruction> GatherRow()
+{
+    return DefaultRegistry()->Resolve(HipInstructionCollectionIds::QuantizedFloat32, "quant.gather-row",
+                                      InstructionTarget::Hip());
+}
+
+int Elems(int fmt) { return fmt == SI_HIP_Q4_K ? 256 : 32; }
+
+const char* Name(int fmt) { return fmt == SI_HIP_Q8_0 ? "q8_0" : fmt == SI_HIP_Q4_0 ? "q4_0" : "q4_k"; }
+
+uint64_t RowBytes(int fmt, int64_t columns)
+{
+    uint64_t b = 0;
+    Check(si_hip_tensor_bytes(fmt, 1, columns, &b));
+    return b;
+}
+
+TensorDescriptor U8(int64_t rows, int64_t bytes) { return {GraphElementType::UInt8, {rows, bytes}}; }
+TensorDescriptor F32(int64_t n) { return {GraphElementType::Float32, {n}}; }
+
+// The parameters of one quant.mat-vec dispatch over a view `padding`
+// elements into each slot (weight padding counts bytes).
+std::vector<InstructionParameter> MatVecParameters(int fmt, int64_t rows, int64_t columns, int64_t padding,
+                                                   const char* weight_port = "weight")
+{
+    return {InstructionParameter::Tensor(weight_port, U8(rows, RowBytes(fmt, columns)), GraphResourceAccess::Read,
+                                         "weight", padding),
+            InstructionParameter::Tensor("input", F32(columns), GraphResourceAccess::Read, "input", 4 * padding),
+            InstructionParameter::Tensor("output", F32(rows), GraphResourceAccess::ReadWrite, "output", 4 * padding),
+            InstructionParameter::Attribute("format", Name(fmt)),
+            InstructionParameter::Attribute("columns", std::to_string(columns))};
+}
+
+// GpuMatVecReferencePrograms.Create(rows, columns, ..., padding, weightPort)
+// for a block-quantized weight: three slots, one "forward" entry.
+HipVmProgram MatVecProgram(int fmt, int64_t rows, int64_t columns, int64_t padding = 0,
+                           const char* weight_port = "weight")
+{
+    HipVmProgram p;
+    p.AddSlot({"weight", U8(1, static_cast<int64_t>(rows * RowBytes(fmt, columns)) + 2 * padding),
+               GraphResourceAccess::Read});
+    p.AddSlot({"input", F32(columns + 2 * padding), GraphResourceAccess::Read});
+    p.AddSlot({"output", F32(rows + 2 * padding), GraphResourceAccess::ReadWrite});
+    p.AddDispatch("forward", MatVec(), MatVecParameters(fmt, rows, columns, padding, weight_port), kFp32);
+    return p;
+}
+
+HipVmProgram GatherProgram(int fmt, int64_t rows, int64_t columns)
+{
+    HipVmProgram p;
+    p.AddSlot({"table", U8(rows, RowBytes(fmt, columns)), GraphResourceAccess::Read});
+    p.AddSlot({"index", {GraphElementType::Int32, {1}}, GraphResourceAccess::ReadWrite});
+    p.AddSlot({"output", F32(columns), GraphResourceAccess::ReadWrite});
+    p.AddDispatch("forward", GatherRow(),
+                  {InstructionParameter::Tensor("table", U8(rows, RowBytes(fmt, columns)), GraphResourceAccess::Read,
+                                                "table"),
+                   InstructionParameter::Tensor("index", {GraphElementType::Int32, {1}}, GraphResourceAccess::Read,
+                                                "index"),
+                   InstructionParameter::Tensor("output", F32(columns), GraphResourceAccess::ReadWrite, "output"),
+                   InstructionParameter::Attribute("format", Name(fmt)),
+                   InstructionParameter::Attribute("columns", std::to_string(columns))},
+                  kFp32);
+    return p;
+}
+
+std::vector<uint8_t> Quant(int fmt, uint64_t seed, int64_t rows, int64_t columns)
+{
+    std::vector<uint8_t> w(rows * RowBytes(fmt, columns));
+    orc_gen_quant(fmt, seed, rows, columns, 0.02, w.data());
+    return w;
+}
+
+// A [rows, columns] matrix whose every weight decodes to exactly 1.
+std::vector<uint8_t> Ones(int fmt, int64_t rows, int64_t columns)
+{
+    const int64_t blocks = rows * columns / Elems(fmt);
+    std::vector<uint8_t> w;
+    for (int64_t b = 0; b < blocks; b++) {
+        if (fmt == SI_HIP_Q8_0) {           // d = 1, q = 1
+            w.insert(w.end(), {0x00, 0x3c});
+            w.insert(w.end(), 32, 0x01);
+        } else if (fmt == SI_HIP_Q4_0) {    // d = 1, q - 8 = 1
+            w.insert(w.end(), {0x00, 0x3c});
+            w.insert(w.end(), 16, 0x99);
+        } else {                            // d = 1, dmin = 0, sc = 1, m = 0, q = 1
+            w.insert(w.end(), {0x00, 0x3c, 0x00, 0x00, 1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1});
+            w.insert(w.end(), 128, 0x11);
+        }
+    }
+    return w;
+}
+
+template <typename T>
+std::vector<uint8_t> Bytes(const std::vector<T>& v)
+{
+    std::vector<uint8_t> b(v.size() * sizeof(T));
+    std::memcpy(b.data(), v.data(), b.size());
+    return b;
+}
+
+std::vector<float> Floats(const std::vector<uint8_t>& b)
+{
+    std::vector<float> v(b.size() / 4);
+    std::memcpy(v.data(), b.data(), b.size());
+    return v;
+}
+
+// The GEMV gate: |y - t| <= 1e-3 * max(|t|, rms(t)) elementwise and
+// ||y - t|| / ||t|| <= 1e-5.
+void AssertGemvClose(const float* y, const std::vector<double>& t)
+{
+    double ss = 0, es = 0;
+    for (double v : t)
+        ss += v * v;
+    const double rms = std::sqrt(ss / t.size());
+    for (size_t i = 0; i < t.size(); i++) {
+        const double e = std::fabs(y[i] - t[i]);
+        if (!(e <= 1e-3 * std::max(std::fabs(t[i]), rms)))
+            throw Failure("row " + std::to_string(i) + ": " + std::to_string(y[i]) + " vs " + std::to_string(t[i]));
+        es += e * e;
+    }
+    if (ss > 0 && !(std::sqrt(es / ss) <= 1e-5))
+        throw Failure("L2-relative error " + std::to_string(std::sqrt(es / ss)));
+}
+
+// ---- contract and registry (no device) ---------------------------------------------------
+
+TEST(cpu, RegistryResolvesTheQuantizedCollection)
+{
+    const auto registry = DefaultRegistry();
+    const auto collections = registry->QueryInstructionCollection();
+    ASSERT_TRUE(collections.size() == 1);
+    ASSERT_TRUE(collections[0].id == HipInstructionCollectionIds::QuantizedFloat32);
+    ASSERT_TRUE(collections[0].architecture == InstructionTarget::Hip());
+    ASSERT_TRUE(MatVec()->Name() == "quant.mat-vec");
+    ASSERT_TRUE(GatherRow()->Name() == "quant.gather-row");
+    ASSERT_THROWS(NotSupportedException, registry->QueryInstruction("00000000-0000-0000-0000-000000000000", "x"));
+    ASSERT_THROWS(ArgumentException, registry->QueryInstruction(HipInstructionCollectionIds::QuantizedFloat32, " "));
+    ASSERT_THROWS(NotSupportedException,
+                  registry->Resolve(HipInstructionCollectionIds::QuantizedFloat32, "core.mat-vec", InstructionTarget::Hip()));
+    ASSERT_THROWS(NotSupportedException, registry->Resolve(HipInstructionCollectionIds::QuantizedFloat32,
+                                                           "quant.mat-vec", InstructionTarget{"direct3d12"}));
+    ASSERT_TRUE(registry->QueryInstruction(HipInstructionCollectionIds::QuantizedFloat32, "quant.other").empty());
+}
+
+struct FixedProvider : IInstructionCollectionProvider {
+    std::vector<InstructionCollectionDescription> descriptions;
+    std::vector<std::shared_ptr<const Instruction>> instructions;
+    std::vector<InstructionCollectionDescription> QueryInstructionCollection() const override { return descriptions; }
+    std::vector<std::shared_ptr<const Instruction>> QueryInstruction(const std::string&,
+                                                                    const std::string&) const override
+    {
+        return instructions;
+    }
+};
+
+struct RenamedMatVec : QuantizedMatVecInstruction {
+    std::string Name() const override { return "quant.renamed"; }
+};
+
+TEST(cpu, RegistryRejectsConflictsForeignIdentitiesAndAmbiguity)
+{
+    using Providers = std::vector<std::shared_ptr<const IInstructionCollectionProvider>>;
+    ASSERT_THROWS(ArgumentException, InstructionRegistry(Providers{nullptr}));
+    auto renamed = std::make_shared<FixedProvider>();
+    renamed->descriptions = {{HipInstructionCollectionIds::QuantizedFloat32, "HIP quantized products v2", 0,
+                              InstructionTarget::Hip()}};
+    ASSERT_THROWS(InvalidDataException,
+                  InstructionRegistry(Providers{std::make_shared<HipQuantizedInstructions>(), renamed}));
+    auto nameless = std::make_shared<FixedProvider>();
+    nameless->descriptions = {{"11111111-2222-3333-4444-555555555555", " ", 0, InstructionTarget::Hip()}};
+    ASSERT_THROWS(InvalidDataException, InstructionRegistry(Providers{nameless}));
+    auto foreign = std::make_shared<FixedProvider>();
+    foreign->descriptions = {{HipInstructionCollectionIds::QuantizedFloat32, "HIP quantized products", 0,
+                              InstructionTarget::Hip()}};
+    foreign->instructions = {std::make_shared<RenamedMatVec>()};
+    ASSERT_THROWS(InvalidDataException, InstructionRegistry(Providers{foreign}).QueryInstruction(
+                                            HipInstructionCollectionIds::QuantizedFloat32, "quant.mat-vec"));
+    auto twice = std::make_shared<FixedProvider>();
+    twice->descriptions = foreign->descriptions;
+    twice->instructions = {std::make_shared<QuantizedMatVecInstruction>(),
+                           std::make_shared<QuantizedMatVecInstruction>()};
+    ASSERT_THROWS(InvalidDataException, InstructionRegistry(Providers{twice}).QueryInstruction(
+                                            HipInstructionCollectionIds::QuantizedFloat32, "quant.mat-vec"));
+}
+
+TEST(cpu, AdaptationSelectsTheSignatureAndRejectsMismatches)
+{
+    const auto mv = MatVec();
+    const auto ok = MatVecParameters(SI_HIP_Q4_K, 7, 512, 0);
+    ASSERT_TRUE(mv->Adapt(ok, kFp32).ports[0].name == "weight");
+    ASSERT_TRUE(mv->Adapt(MatVecParameters(SI_HIP_Q8_0, 7, 64, 0, "matrix"), kFp32).ports[0].name == "matrix");
+    // a weaker requirement is satisfied by FP32 arithmetic
+    ASSERT_TRUE(mv->Adapt(ok, {GraphElementType::Float16, GraphElementType::Float16}).precision.arithmetic_type ==
+                GraphElementType::Float32);
+    auto with = [&](std::function<void(std::vector<InstructionParameter>&)> change) {
+        auto p = ok;
+        change(p);
+        return p;
+    };
+    using P = std::vector<InstructionParameter>;
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p.pop_back(); }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p.push_back(p[3]); }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(with([](P& p) { p[0].tensor.element_type = GraphElementType::Float32; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(with([](P& p) { p[2].access = GraphResourceAccess::Read; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(with([](P& p) { p[0].name = "matrix2"; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(ok, {GraphElementType::Int32, GraphElementType::Float32}));
+    // Validate: format, columns, and tensor shapes
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p[3].value = "q5_0"; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p[4].value = "500"; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p[4].value = "512x"; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p[4].value = "-256"; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(with([](P& p) { p[0].tensor.dimensions = {7, 287}; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(with([](P& p) { p[1].tensor.dimensions = {511}; }), kFp32));
+    ASSERT_THROWS(InstructionAdaptationException,
+                  mv->Adapt(with([](P& p) { p[2].tensor.dimensions = {8}; }), kFp32));
+    try {
+        mv->Adapt(with([](P& p) { p[3].value = "f16"; }), kFp32);
+        throw Failure("f16 format adapted");
+    } catch (const InstructionAdaptationException& e) {
+        const std::string m = e.what();
+        ASSERT_TRUE(m.find("Instruction '" + HipInstructionCollectionIds::QuantizedFloat32 + "/quant.mat-vec'") == 0);
+    }
+}
+
+struct OtherTargetRecorder : IInstructionRecorder {
+    InstructionTarget Target() const override { return {"direct3d12"}; }
+    void Record(InstructionRecording) override { throw Failure("recorded on a foreign target"); }
+};
+
+TEST(cpu, InvokeRequiresTheRecordersTarget)
+{
+    OtherTargetRecorder r;
+    ASSERT_THROWS(InstructionAdaptationException, MatVec()->Invoke(r, MatVecParameters(SI_HIP_Q8_0, 3, 64, 0), kFp32));
+}
+
+TEST(cpu, ProgramRejectsUnknownSlotsOversizedViewsWritesToReadSlotsAndAliasing)
+{
+    auto program = MatVecProgram(SI_HIP_Q8_0, 7, 65 * 32, 3);
+    ASSERT_TRUE(program.Entries().at("forward").size() == 1);
+    ASSERT_TRUE(program.Entries().at("forward")[0].recording.operation == "si_hip_gemv");
+    ASSERT_THROWS(InvalidDataException, program.AddSlot({"input", F32(4), GraphResourceAccess::Read}));
+    ASSERT_THROWS(InvalidDataException, program.AddSlot({"empty", F32(0), GraphResourceAccess::Read}));
+    auto p = MatVecParameters(SI_HIP_Q8_0, 7, 65 * 32, 3);
+    auto unknown = p;
+    unknown[1].source = "missing";
+    ASSERT_THROWS(ArgumentException, program.AddDispatch("second", MatVec(), unknown, kFp32));
+    auto oversized = p;
+    oversized[2].byte_offset = 4 * 7;       // 7 + 7 > 7 + 2 * 3 floats
+    ASSERT_THROWS(InvalidDataException, program.AddDispatch("second", MatVec(), oversized, kFp32));
+    auto readonly = p;
+    readonly[2].source = "input";
+    ASSERT_THROWS(InvalidDataException, program.AddDispatch("second", MatVec(), readonly, kFp32));
+    // the output aliasing the input inside one writable slot
+    HipVmProgram shared;
+    shared.AddSlot({"weight", U8(7, RowBytes(SI_HIP_Q8_0, 64)), GraphResourceAccess::Read});
+    shared.AddSlot({"buffer", F32(64), GraphResourceAccess::ReadWrite});
+    auto aliased = MatVecParameters(SI_HIP_Q8_0, 7, 64, 0);
+    aliased[1].source = aliased[2].source = "buffer";
+    aliased[2].byte_offset = 4 * 32;
+    ASSERT_THROWS(NotSupportedException, shared.AddDispatch("forward", MatVec(), aliased, kFp32));
+    aliased[2].byte_offset = 4 * 58;        // 58 + 7 floats do not fit in the 64-float slot
+    ASSERT_THROWS(InvalidDataException, shared.AddDispatch("forward", MatVec(), aliased, kFp32));
+    ASSERT_THROWS(ArgumentException, shared.AddDispatch("forward", nullptr, p, kFp32));
+    ASSERT_THROWS(ArgumentException, shared.AddDispatch(" ", MatVec(), p, kFp32));
+    // a rejected dispatch leaves the program unchanged
+    ASSERT_TRUE(shared.Entries().empty());
+}
+
+TEST(cpu, ExecutorWithoutADeviceFailsLoudly)
+{
+    int n = 0;
+    if (si_hip_device_count(&n) == SI_HIP_OK && n > 0)
+        return;   // a device is present: the GPU group covers the executor
+    ASSERT_THROWS(DeviceException, HipVmExecutor(MatVecProgram(SI_HIP_Q8_0, 3, 32)));
+}
+
+// ---- executor (device 0) -----------------------------------------------------------------
+
+// Execute (GpuMatVecTests.cs:283-310): every slot is filled with 13 outside
+// the views, executed three times, the padding is left untouched and the
+// inputs read back unchanged.
+void ExecuteView(int fmt, int64_t rows, int64_t columns, const char* weight_port, uint64_t seed)
+{
+    const int64_t padding = 3;
+    auto program = MatVecProgram(fmt, rows, columns, padding, weight_port);
+    HipVmExecutor executor(program);
+    const auto w = Quant(fmt, seed, rows, columns);
+    std::vector<float> x(columns);
+    orc_gen_normal_f32(seed + 1, columns, 0.0, 1.0, x.data());
+    std::vector<uint8_t> weight(w.size() + 2 * padding, 13);
+    std::copy(w.begin(), w.end(), weight.begin() + padding);
+    std::vector<float> input(columns + 2 * padding, 13.0f), output(rows + 2 * padding, 13.0f);
+    std::copy(x.begin(), x.end(), input.begin() + padding);
+    executor.Upload("weight", weight);
+    executor.Upload("input", Bytes(input));
+    executor.Upload("output", Bytes(output));
+    std::vector<double> t(rows);
+    Check(orc_gemv_f64(fmt, w.data(), x.data(), t.data(), rows, columns) == 0 ? SI_HIP_OK : SI_HIP_ERR_ARGUMENT);
+    for (int repeat = 0; repeat < 3; repeat++) {
+        executor.Execute("forward");
+        const auto actual = Floats(executor.Readback("output"));
+        for (int64_t i = 0; i < padding; i++)
+            ASSERT_TRUE(actual[i] == 13.0f && actual[rows + padding + i] == 13.0f);
+        AssertGemvClose(actual.data() + padding, t);
+    }
+    ASSERT_TRUE(executor.Readback("weight") == weight);
+    ASSERT_TRUE(executor.Readback("input") == Bytes(input));
+    // a new input is read by the recorded entry
+    for (auto& v : x)
+        v = -2.0f * v;
+    std::copy(x.begin(), x.end(), input.begin() + padding);
+    executor.Upload("input", Bytes(input));
+    executor.Execute("forward");
+    Check(orc_gemv_f64(fmt, w.data(), x.data(), t.data(), rows, columns) == 0 ? SI_HIP_OK : SI_HIP_ERR_ARGUMENT);
+    AssertGemvClose(Floats(executor.Readback("output")).data() + padding, t);
+}
+
+TEST(gpu, QuantizedSignaturesHandleTailsViewsAndRepeatedInvocation)
+{
+    // (rows, blocks per row), as (rows, columns) of GpuMatVecTests.cs:14-21
+    const int64_t shapes[][2] = {{1, 1}, {7, 17}, {7, 63}, {7, 64}, {7, 65}, {3, -1}, {65536, 3}, {65537, 3}};
+    uint64_t seed = 500;
+    for (int fmt : {SI_HIP_Q8_0, SI_HIP_Q4_0, SI_HIP_Q4_K})
+        for (const auto& s : shapes) {
+            const int64_t columns = s[1] < 0 ? 4096 : s[1] * Elems(fmt);
+            std::printf("    %s %lld x %lld\n", Name(fmt), static_cast<long long>(s[0]),
+                        static_cast<long long>(columns));
+            std::fflush(stdout);
+            ExecuteView(fmt, s[0], columns, (seed / 2) % 2 ? "matrix" : "weight", seed);
+            seed += 2;
+        }
+}
+
+TEST(gpu, AlignedSlotsMeetTheGate)
+{
+    // Views at offset 0 of 256-byte aligned slots: the 3072-column product
+    // runs on the tiled kernel (the views above run on the any-shape ones).
+    for (int fmt : {SI_HIP_Q8_0, SI_HIP_Q4_0, SI_HIP_Q4_K}) {
+        const int64_t rows = 3072, columns = 3072;
+        HipVmExecutor executor(MatVecProgram(fmt, rows, columns));
+        const auto w = Quant(fmt, 900 + fmt, rows, columns);
+        std::vector<float> x(columns);
+        orc_gen_normal_f32(901 + fmt, columns, 0.0, 1.0, x.data());
+        executor.Upload("weight", w);
+        executor.Upload("input", Bytes(x));
+        executor.Execute("forward");
+        std::vector<double> t(rows);
+        orc_gemv_f64(fmt, w.data(), x.data(), t.data(), rows, columns);
+        AssertGemvClose(Floats(executor.Readback("output")).data(), t);
+    }
+}
+
+TEST(gpu, QuantizedNonfiniteSumsRetainClassification)
+{
+    const float inf = INFINITY;
+    const std::vector<std::vector<float>> inputs = {{inf, 1}, {-inf, 1}, {inf, -inf}, {NAN, 1}};
+    for (int fmt : {SI_HIP_Q8_0, SI_HIP_Q4_0, SI_HIP_Q4_K})
+        for (int64_t columns : {int64_t(Elems(fmt)), int64_t(3072)}) {
+            HipVmExecutor executor(MatVecProgram(fmt, 3, columns));
+            executor.Upload("weight", Ones(fmt, 3, columns));
+            for (const auto& head : inputs) {
+                std::vector<float> x(columns, 0.0f);
+                std::copy(head.begin(), head.end(), x.begin());
+                executor.Upload("input", Bytes(x));
+                executor.Execute("forward");
+                const float expected = head[0] + head[1];
+                for (float v : Floats(executor.Readback("output")))
+                    ASSERT_TRUE(std::isnan(expected) ? std::isnan(v) : v == expected);
+            }
+        }
+}
+
+TEST(gpu, ResidentTimestampMeasurementExecutesAndRejectsInvalidRequests)
+{
+    HipVmExecutor executor(MatVecProgram(SI_HIP_Q8_0, 3, 65 * 32));
+    executor.Upload("weight", Ones(SI_HIP_Q8_0, 3, 65 * 32));
+    executor.Upload("input", Bytes(std::vector<float>(65 * 32, 1.0f)));
+    const double elapsed = executor.MeasureGpuMicroseconds("forward", 4);
+    ASSERT_TRUE(std::isfinite(elapsed) && elapsed > 0);
+    for (float v : Floats(executor.Readback("output")))
+        ASSERT_TRUE(v == 65 * 32);
+    ASSERT_THROWS(ArgumentOutOfRangeException, executor.MeasureGpuMicroseconds("forward", 0));
+    ASSERT_THROWS(ArgumentOutOfRangeException, executor.MeasureGpuMicroseconds("forward", 1025));
+    ASSERT_THROWS(ArgumentException, executor.MeasureGpuMicroseconds("missing", 1));
+}
+
+TEST(gpu, SpanUploadExecutesWithoutOwnedSourceArray)
+{
+    // [[1, 2], [3, 4], [5, 6]] . [2, 3] = [8, 18, 28], as one Q8_0 block per row (d = 1)
+    HipVmExecutor executor(MatVecProgram(SI_HIP_Q8_0, 3, 32));
+    uint8_t matrix[3 * 34] = {};
+    for (int r = 0; r < 3; r++) {
+        matrix[34 * r + 1] = 0x3c;
+        matrix[34 * r + 2] = static_cast<uint8_t>(2 * r + 1);
+        matrix[34 * r + 3] = static_cast<uint8_t>(2 * r + 2);
+    }
+    float input[32] = {2, 3};
+    executor.Upload("weight", matrix, sizeof matrix);
+    executor.Upload("input", input, sizeof input);
+    executor.Execute("forward");
+    ASSERT_TRUE(Floats(executor.Readback("output")) == (std::vector<float>{8, 18, 28}));
+}
+
+TEST(gpu, UploadRequiresExactSlotBytesAndKnownNames)
+{
+    HipVmExecutor executor(MatVecProgram(SI_HIP_Q4_0, 5, 64));
+    ASSERT_THROWS(ArgumentException, executor.Upload("weight", std::vector<uint8_t>(5 * 36 - 1)));
+    ASSERT_THROWS(ArgumentException, executor.Upload("weight", std::vector<uint8_t>(5 * 36 + 1)));
+    ASSERT_THROWS(ArgumentException, executor.Upload("missing", std::vector<uint8_t>(4)));
+    ASSERT_THROWS(ArgumentException, executor.Readback("missing"));
+    ASSERT_THROWS(ArgumentException, executor.Execute("missing"));
+    // slots start zeroed: the product of a zero matrix is zero
+    executor.Execute("forward");
+    for (float v : Floats(executor.Readback("output")))
+        ASSERT_TRUE(v == 0.0f);
+}
+
+TEST(gpu, GatherRowDecodesTheIndexedRowExactlyAndNaNOutsideTheTable)
+{
+    for (int fmt : {SI_HIP_Q8_0, SI_HIP_Q4_0, SI_HIP_Q4_K}) {
+        const int64_t rows = 50, columns = 3072;
+        HipVmExecutor executor(GatherProgram(fmt, rows, columns));
+        const auto table = Quant(fmt, 700 + fmt, rows, columns);
+        executor.Upload("table", table);
+        for (int32_t index : {0, 17, 49, 50, -1}) {
+            std::vector<uint8_t> out(4 * columns);
+            executor.ExecuteWithTransfers("forward", "index", Bytes(std::vector<int32_t>{index}), "output", out);
+            const auto y = Floats(out);
+            if (index < 0 || index >= rows) {
+                for (float v : y)
+                    ASSERT_TRUE(std::isnan(v));
+                continue;
+            }
+            std::vector<float> expected(columns);
+            orc_dequant_row(fmt, table.data() + index * RowBytes(fmt, columns), columns, expected.data());
+            ASSERT_TRUE(std::memcmp(y.data(), expected.data(), 4 * columns) == 0);
+        }
+        std::vector<uint8_t> small(4);
+        ASSERT_THROWS(ArgumentException,
+                      executor.ExecuteWithTransfers("forward", "index", Bytes(std::vector<int32_t>{0}), "output", small));
+    }
+}
+
+}  // namespace
+
+int main(int argc, char** argv)
+{
+    const std::string group = argc > 1 ? argv[1] : "cpu";
+    const std::string only = argc > 2 ? argv[2] : "";
+    if (group != "cpu" && group != "gpu") {
+        std::fprintf(stderr, "usage: %s cpu|gpu [test-name]\n", argv[0]);
+        return 2;
+    }
+    int run = 0, failed = 0;
+    for (const auto& t : Registry()) {
+        if (t.group != group || (!only.empty() && only != t.name))
+            continue;
+        std::printf("[ RUN  ] %s\n", t.name);
+        std::fflush(stdout);
+        run++;
+        try {
+            t.body();
+            std::printf("[  OK  ] %s\n", t.name);
+        } catch (const std::exception& e) {
+            failed++;
+            std::printf("[ FAIL ] %s: %s\n", t.name, e.what());
+        }
+        std::fflush(stdout);
+    }
+    std::printf("%d %s tests, %d failed\n", run, group.c_str(), failed);
+    return failed || run == 0 ? 1 : 0;
+}
