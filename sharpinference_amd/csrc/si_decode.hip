@@ -135,13 +135,65 @@ __global__ __launch_bounds__(64) void attention_prep_kernel(AttentionArgs a)
 
 constexpr int MAX_CHUNKS = 256;
 
-// One workgroup per query head: merge the chunk partials (m_c, l_c, o_c)
-// into softmax-weighted values.  (Merging inside the last partial
+// One workgroup per query head merges the chunk partials (m_c, l_c, o_c):
+// out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) with M = max_c m_c.
+// Thread (half, d) takes chunks half, half + 2, ... in batches of
+// COMBINE_BATCH, every load of a batch issued together, and merges the
+// batches online; the two halves merge through LDS.  The first batch is
+// requested before the position is read (slots past the position hold
+// stale partials and are masked), so a cache of up to 2 * COMBINE_BATCH
+// chunks costs one memory round trip.  (Merging inside the last partial
 // workgroup instead needs a device-scope release per workgroup, which
 // writes back the XCD's L2 and costs far more than this launch.)
+constexpr int COMBINE_BATCH = 16;
+
+struct CombineBatch {
+    float m[COMBINE_BATCH], l[COMBINE_BATCH], o[COMBINE_BATCH];
+};
+
+__device__ __forceinline__ void load_combine_batch(const float* src, int base, int max_chunks, int d, CombineBatch& b)
+{
+#pragma unroll
+    for (int i = 0; i < COMBINE_BATCH; i++) {
+        const int c = base + 2 * i;
+        const float* p = src + static_cast<int64_t>(c < max_chunks ? c : 0) * PART;
+        b.m[i] = p[0];
+        b.l[i] = p[1];
+        b.o[i] = p[2 + d];
+    }
+}
+
+// Folds the batch's chunks below `chunks` into (m, l, acc).
+__device__ __forceinline__ void merge_combine_batch(const CombineBatch& b, int base, int chunks, float& m, float& l,
+                                                    float& acc)
+{
+    float bm = m;
+#pragma unroll
+    for (int i = 0; i < COMBINE_BATCH; i++)
+        if (base + 2 * i < chunks)
+            bm = fmaxf(bm, b.m[i]);
+    const float r = expf(m - bm);   // m = -inf before the first batch: r = 0
+    float bl = 0.0f, bo = 0.0f;
+#pragma unroll
+    for (int i = 0; i < COMBINE_BATCH; i++) {
+        if (base + 2 * i < chunks) {
+            const float w = expf(b.m[i] - bm);
+            bl = fmaf(b.l[i], w, bl);
+            bo = fmaf(b.o[i], w, bo);
+        }
+    }
+    l = fmaf(l, r, bl);
+    acc = fmaf(acc, r, bo);
+    m = bm;
+}
+
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
 {
     const int h = blockIdx.x, t = threadIdx.x;
+    const int d = t & (HEAD_DIM - 1), half = t >> 7;
+    const float* src = a.workspace + static_cast<int64_t>(h) * a.max_chunks * PART;
+    CombineBatch b;
+    load_combine_batch(src, half, a.max_chunks, d, b);
     const int P = *a.position;
     if (P < 0 || P >= a.capacity) {
         if (t < HEAD_DIM)
@@ -149,111 +201,114 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
         return;
     }
     const int chunks = P / CHUNK + 1;
-    const float* src = a.workspace + static_cast<int64_t>(h) * a.max_chunks * PART;
-    __shared__ float wts[MAX_CHUNKS];
-    __shared__ float lw[MAX_CHUNKS];
-    __shared__ float half_acc[2][HEAD_DIM];
-    __shared__ float stat[2];
-    for (int c = t; c < chunks; c += 256)
-        wts[c] = src[c * PART];
-    __syncthreads();
-    if (t < 64) {
-        float m = -INFINITY;
-        for (int c = t; c < chunks; c += 64)
-            m = fmaxf(m, wts[c]);
-        for (int off = 32; off > 0; off >>= 1)
-            m = fmaxf(m, __shfl_xor(m, off));
-        if (t == 0)
-            stat[0] = m;
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    if (half < chunks)
+        merge_combine_batch(b, half, chunks, m, l, acc);
+    for (int base = half + 2 * COMBINE_BATCH; base < chunks; base += 2 * COMBINE_BATCH) {
+        load_combine_batch(src, base, a.max_chunks, d, b);
+        merge_combine_batch(b, base, chunks, m, l, acc);
+    }
+    __shared__ float other[HEAD_DIM + 2];
+    if (half == 1) {
+        other[d] = acc;
+        if (d == 0) {
+            other[HEAD_DIM] = m;
+            other[HEAD_DIM + 1] = l;
+        }
     }
     __syncthreads();
-    const float M = stat[0];
-    for (int c = t; c < chunks; c += 256) {
-        const float w = expf(wts[c] - M);
-        wts[c] = w;
-        lw[c] = src[c * PART + 1] * w;
+    if (half == 0) {
+        const float m1 = other[HEAD_DIM];
+        const float M = fmaxf(m, m1);
+        const float e0 = expf(m - M), e1 = expf(m1 - M);   // half 1 without chunks: m1 = -inf, e1 = 0
+        a.out[h * HEAD_DIM + d] = fmaf(acc, e0, other[d] * e1) / fmaf(l, e0, other[HEAD_DIM + 1] * e1);
     }
-    __syncthreads();
-    if (t < 64) {
-        float l = 0.0f;
-        for (int c = t; c < chunks; c += 64)
-            l += lw[c];
-        for (int off = 32; off > 0; off >>= 1)
-            l += __shfl_xor(l, off);
-        if (t == 0)
-            stat[1] = l;
-    }
-    const int d = t & (HEAD_DIM - 1), half = t >> 7;
-    float acc = 0.0f;
-#pragma unroll 4
-    for (int c = half; c < chunks; c += 2)
-        acc = fmaf(src[c * PART + 2 + d], wts[c], acc);
-    half_acc[half][d] = acc;
-    __syncthreads();
-    if (t < HEAD_DIM)
-        a.out[h * HEAD_DIM + t] = (half_acc[0][t] + half_acc[1][t]) / stat[1];
 }
 
 // One workgroup = one KV head x one chunk of 64 cache positions.  Writes
 // per query head of the group: (max score, sum of exp, sum of exp * v).
-// Every K and V row of the chunk is requested (16-byte loads, one 8-value
-// slice per lane) before q is staged, so the cache reads overlap the setup.
+// The inputs that do not depend on the position (the group's queries, the
+// new K / V rows, the step's rotary table) are requested together with the
+// position; then every K and V row of the chunk is requested (16-byte
+// loads, one 8-value slice per lane), and the queries are staged and
+// rotated while those loads are in flight.
 template <int GROUP>
 __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(AttentionArgs a)
 {
+    constexpr int QPT = (GROUP * HEAD_DIM + ATT_THREADS - 1) / ATT_THREADS;   // query values per thread
     const int g = blockIdx.x;                 // KV head
     const int chunk = blockIdx.y;
-    const int P = *a.position;                // index of the new token
     const int start = chunk * CHUNK;
+    const int koff = a.heads * HEAD_DIM, voff = koff + a.kv_heads * HEAD_DIM;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int dg = t & 15;                    // 8-value slice of a head row
+
+    // 1. position-independent inputs, into registers
+    float qr[QPT];
+#pragma unroll
+    for (int e = 0; e < QPT; e++) {
+        const int i = t + e * ATT_THREADS;
+        qr[e] = a.qkv[g * GROUP * HEAD_DIM + (i < GROUP * HEAD_DIM ? i : 0)];
+    }
+    const float* rope = a.workspace + att_rope(a.heads, a.max_chunks);
+    const int ti = t & (HEAD_DIM - 1);
+    const float kn = a.qkv[koff + g * HEAD_DIM + ti];
+    const float vn = a.qkv[voff + g * HEAD_DIM + ti];
+    const float rp = rope[ti];                // cos at [0, 64), sin at [64, 128)
+
+    const int P = *a.position;                // index of the new token
     if (P < 0 || P >= a.capacity || start > P)
         return;                               // whole workgroup leaves together
     const int count = min(CHUNK, P + 1 - start);
     const int newp = P - start;               // the new token's slot in this chunk (< CHUNK when owned)
     const bool owns_new = newp < CHUNK;
-    const int koff = a.heads * HEAD_DIM, voff = koff + a.kv_heads * HEAD_DIM;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int dg = t & 15;                    // 8-value slice of a head row
 
     __half* kc = a.k_cache + static_cast<int64_t>(g) * a.capacity * HEAD_DIM;
     __half* vc = a.v_cache + static_cast<int64_t>(g) * a.capacity * HEAD_DIM;
 
-    // 1. K rows for the scores (wave w: positions 16w..16w+15) and V rows
-    //    for the weighted sum (position slot t/16 + 16j)
+    // 2. K rows for the scores (wave w: positions 16w..16w+15) and V rows
+    //    for the weighted sum (position slot t/16 + 16j).  The loads are
+    //    unconditional (rows clamped into the cache) so that all eight are
+    //    in flight at once; rows past the chunk's count and the new token's
+    //    slot are masked afterwards (V to zero, K through the score mask).
     uint4 kr[4], vr[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int pk = wave * 16 + (lane >> 4) + 4 * j;
         const int pv = (t >> 4) + 16 * j;
-        kr[j] = (pk < count && pk != newp)
-                    ? *reinterpret_cast<const uint4*>(kc + static_cast<int64_t>(start + pk) * HEAD_DIM + 8 * dg)
-                    : make_uint4(0, 0, 0, 0);
-        vr[j] = (pv < count && pv != newp)
-                    ? *reinterpret_cast<const uint4*>(vc + static_cast<int64_t>(start + pv) * HEAD_DIM + 8 * dg)
-                    : make_uint4(0, 0, 0, 0);
+        kr[j] = *reinterpret_cast<const uint4*>(kc + static_cast<int64_t>(min(start + pk, a.capacity - 1)) * HEAD_DIM +
+                                                8 * dg);
+        vr[j] = *reinterpret_cast<const uint4*>(vc + static_cast<int64_t>(min(start + pv, a.capacity - 1)) * HEAD_DIM +
+                                                8 * dg);
     }
 
     __shared__ float q[GROUP][HEAD_DIM];
     __shared__ float knew[HEAD_DIM];
     __shared__ float vnew[HEAD_DIM];
+    __shared__ float rope_s[HEAD_DIM];
     __shared__ float prob[GROUP][CHUNK];
     __shared__ float mx[GROUP];
     __shared__ float lsum[GROUP];
     __shared__ float red[4][GROUP][HEAD_DIM];
 
-    // 2. rotated queries of the group; the new row, rotated, rounded, appended
-    const float* rope = a.workspace + att_rope(a.heads, a.max_chunks);
-    for (int i = t; i < GROUP * HEAD_DIM; i += ATT_THREADS)
-        q[i / HEAD_DIM][i % HEAD_DIM] = a.qkv[(g * GROUP + i / HEAD_DIM) * HEAD_DIM + i % HEAD_DIM];
-    if (owns_new && t < HEAD_DIM) {
-        knew[t] = a.qkv[koff + g * HEAD_DIM + t];
-        vnew[t] = a.qkv[voff + g * HEAD_DIM + t];
+    // 3. rotated queries of the group; the new row, rotated, rounded, appended
+#pragma unroll
+    for (int e = 0; e < QPT; e++) {
+        const int i = t + e * ATT_THREADS;
+        if (i < GROUP * HEAD_DIM)
+            q[i / HEAD_DIM][i % HEAD_DIM] = qr[e];
+    }
+    if (t < HEAD_DIM) {
+        knew[t] = kn;
+        vnew[t] = vn;
+        rope_s[t] = rp;
     }
     __syncthreads();
     const int half_rot = a.rotary_dim / 2;
     for (int i = t; i < GROUP * half_rot; i += ATT_THREADS)
-        rotate_pair(q[i / half_rot], i % half_rot, a.rotary_dim, rope);
+        rotate_pair(q[i / half_rot], i % half_rot, a.rotary_dim, rope_s);
     if (owns_new && t < half_rot)
-        rotate_pair(knew, t, a.rotary_dim, rope);
+        rotate_pair(knew, t, a.rotary_dim, rope_s);
     __syncthreads();
     if (owns_new && t < HEAD_DIM) {
         const __half kh = __float2half_rn(knew[t]), vh = __float2half_rn(vnew[t]);
@@ -331,7 +386,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(Attentio
             for (int e = 0; e < 8; e++)
                 v8[e] = vnew[8 * dg + e];
         } else {
-            unpack8(vr[j], v8);
+            unpack8(p < count ? vr[j] : make_uint4(0, 0, 0, 0), v8);   // rows past the count may hold anything
         }
 #pragma unroll
         for (int h = 0; h < GROUP; h++) {
