@@ -130,6 +130,7 @@ int si_hip_gemv(si_hip_context* ctx, int format, const void* w, const float* x, 
  * rows of bf16 activations (16-byte aligned) against a block-quantized W,
  * FP32 output (one row of `rows` values per token), FP32 accumulation on
  * MFMA; W is decoded exactly and rounded to bf16 for the matrix cores.
+ * W and X must each be smaller than 4 GiB (UNSUPPORTED otherwise).
  * Replaces: the transpose_right matrix multiply of the CpuVm path
  * (CpuInstructionNumerics.MatrixMultiply, CpuInstructionNumerics.cs:66-77)
  * and the batched prefill matvec of the D3D12 transformer program

@@ -314,6 +314,8 @@ int si_hip_gemm_prefill(si_hip_context* ctx, int format, const void* w, const vo
     const uint64_t xbytes = static_cast<uint64_t>(m) * static_cast<uint64_t>(cols) * 2;
     if (overlaps(y, ybytes, w, wbytes) || overlaps(y, ybytes, x_bf16, xbytes))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: output overlaps an input");
+    if (wbytes > UINT32_MAX || xbytes > UINT32_MAX)
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "gemm_prefill: W and X must each be smaller than 4 GiB");
     const hipError_t e = si::launch_prefill(format, w, x_bf16, y, m, rows, cols, ctx->stream);
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemm_prefill launch");
 }

@@ -33,52 +33,96 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16 raw bytes
 
 constexpr int PF_THREADS = 256;
 constexpr int WS_STRIDE = 40;       // bf16 per LDS tile row: 32 values + 8 pad
+constexpr int PF_DEPTH = 2;         // steps of loads in flight (even: LDS buffer = step parity)
 
-// Raw bytes of one group of 4 values, loaded a step ahead of their decode.
-struct Raw4 {
-    uint32_t a, b, c;
+// Raw words of one item of 16 values (half a 32-value block of one W row),
+// loaded steps ahead of their decode.  The loads are plain word loads and
+// every bit extraction happens at decode time, so a word in flight is never
+// touched before its decode.
+struct Raw16 {
+    uint32_t w[8];
 };
+
+typedef uint32_t u32_a2 __attribute__((aligned(2)));   // 4 bytes at a 2-byte aligned address
 
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p)
 {
     return *reinterpret_cast<const unsigned short*>(p);
 }
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) { return *reinterpret_cast<const u32_a2*>(p); }
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
+// Hides a value from the optimiser: keeps a 32-bit lane offset from being
+// widened to 64 bits outside the loop (so loads keep the scalar-base
+// addressing form), and keeps the known-zero bits of a masked word hidden
+// (so each byte converts with one v_cvt_f32_ubyteN).
+__device__ __forceinline__ uint32_t opaque(uint32_t v)
+{
+    asm("" : "+v"(v));
+    return v;
+}
+
+// Loads address a block through a workgroup-uniform base (W plus the
+// block's offset in a row) and a 32-bit lane offset (the row's offset), so
+// they use the scalar-base addressing form and need no 64-bit vector
+// address arithmetic.  Item h of a block:
+//   Q4_0 {fp16 d; u8 qs[16]}: d and bytes 8h..8h+7 (elements 8h..8h+7 in the
+//        low nibbles, 16+8h..16+8h+7 in the high nibbles);
+//   Q8_0 {fp16 d; int8 q[32]}: d and q[16h..16h+15];
+//   Q4_K {fp16 d, dmin; u8 scales[12]; u8 qs[128]} (16-byte aligned
+//        super-blocks), sub-block j = blk % 8: d | dmin << 16, the three
+//        scale words and the 16 quant bytes of elements 16h..16h+15 (nibble
+//        j % 2 of qs[32 (j / 2) + 16h ..]).
 template <int FMT>
-__device__ __forceinline__ Raw4 load_raw(const uint8_t* row, int blk, int p);
+__device__ __forceinline__ Raw16 load_raw(const uint8_t* W, uint32_t row_off, int blk, int h);
 
-// Q8_0 {fp16 d; int8 q[32]}: d, q[4p..4p+1], q[4p+2..4p+3] (2-byte aligned)
 template <>
-__device__ __forceinline__ Raw4 load_raw<FMT_Q8_0>(const uint8_t* row, int blk, int p)
+__device__ __forceinline__ Raw16 load_raw<FMT_Q4_0>(const uint8_t* W, uint32_t row_off, int blk, int h)
 {
-    const uint8_t* b = row + blk * 34;
-    return Raw4{ld_u16(b), ld_u16(b + 2 + 4 * p), ld_u16(b + 4 + 4 * p)};
+    const uint8_t* b = W + blk * 18;
+    row_off = opaque(row_off);
+    Raw16 r;
+    r.w[0] = ld_u16(b + row_off);
+    r.w[1] = ld_u32_a2(b + (row_off + 2 + 8 * h));
+    r.w[2] = ld_u32_a2(b + (row_off + 6 + 8 * h));
+    return r;
 }
 
-// Q4_0 {fp16 d; u8 qs[16]}: d and the 4 bytes holding elements 4p..4p+3
 template <>
-__device__ __forceinline__ Raw4 load_raw<FMT_Q4_0>(const uint8_t* row, int blk, int p)
+__device__ __forceinline__ Raw16 load_raw<FMT_Q8_0>(const uint8_t* W, uint32_t row_off, int blk, int h)
 {
-    const uint8_t* b = row + blk * 18;
-    const uint8_t* q = b + 2 + 4 * (p & 3);
-    return Raw4{ld_u16(b), ld_u16(q), ld_u16(q + 2)};
+    const uint8_t* b = W + blk * 34;
+    row_off = opaque(row_off);
+    Raw16 r;
+    r.w[0] = ld_u16(b + row_off);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        r.w[1 + k] = ld_u32_a2(b + (row_off + 2 + 16 * h + 4 * k));
+    return r;
 }
 
-// Q4_K: d | dmin << 16, the 3 scale bytes of sub-block j, 4 quant bytes
-// (16-byte aligned super-blocks, so the quant word is dword aligned)
 template <>
-__device__ __forceinline__ Raw4 load_raw<FMT_Q4_K>(const uint8_t* row, int blk, int p)
+__device__ __forceinline__ Raw16 load_raw<FMT_Q4_K>(const uint8_t* W, uint32_t row_off, int blk, int h)
 {
-    const uint8_t* b = row + (blk >> 3) * 144;
+    const uint8_t* b = W + (blk >> 3) * 144;
     const int j = blk & 7;
-    const uint8_t* s = b + 4;
-    const uint32_t sb = j < 4 ? (s[j] | (s[j + 4] << 8)) : (s[j + 4] | (s[j - 4] << 8) | (s[j] << 16));
-    return Raw4{ld_u16(b) | (ld_u16(b + 2) << 16), sb,
-                *reinterpret_cast<const uint32_t*>(b + 16 + 32 * (j >> 1) + 4 * p)};
+    row_off = opaque(row_off);
+    Raw16 r;
+    r.w[0] = ld_u32(b + row_off);
+    r.w[1] = ld_u32(b + (row_off + 4));
+    r.w[2] = ld_u32(b + (row_off + 8));
+    r.w[3] = ld_u32(b + (row_off + 12));
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        r.w[4 + k] = ld_u32(b + 16 + 32 * (j >> 1) + (row_off + 16 * h + 4 * k));
+    return r;
 }
 
 __device__ __forceinline__ float half_bits(uint32_t h)
@@ -86,98 +130,178 @@ __device__ __forceinline__ float half_bits(uint32_t h)
     return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xffffu)));
 }
 
-// The 4 values in FP32, bit-identical to the block decoder (one rounding
-// per operation).
+// Byte i of q as a float (v_cvt_f32_ubyteN).
+__device__ __forceinline__ float ubyte(uint32_t q, int i) { return static_cast<float>((q >> (8 * i)) & 0xffu); }
+
+// 8 values fma(a, byte, c) of two words, rounded to bf16 (RNE).
+__device__ __forceinline__ bf16x8 decode8(uint32_t q0, uint32_t q1, float a, float c)
+{
+    f32x8 v;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[i] = fmaf(a, ubyte(q0, i), c);
+        v[4 + i] = fmaf(a, ubyte(q1, i), c);
+    }
+    return __builtin_convertvector(v, bf16x8);
+}
+
+// The 16 values of an item in FP32 are bit-identical to the block decoder,
+// each one fused multiply-add whose exact result needs no rounding or
+// equals the decoder's single rounding:
+//   Q8_0: d * q = fma(d, q + 128, -128 d)   (d * (q + 128) and 128 d exact)
+//   Q4_0: d * (q - 8) = fma(d, q, -8 d)      (every term exact)
+//   Q4_K: (d sc) q - dmin m = fma(d1, q, -m1) with d1 = d sc and m1 = dmin m
+//         exact (11-bit by 6-bit products), d1 q exact, one rounding.
+// High nibbles are masked in place (16 q per byte) and the factor 1/16 goes
+// into the scale, which stays exact (a power of two).  The two halves of
+// 8 values go to columns c0 and c1 of the block.
 template <int FMT>
-__device__ __forceinline__ void decode_raw(const Raw4& r, int blk, int p, float out[4]);
+__device__ __forceinline__ void decode_raw(const Raw16& r, int blk, int h, bf16x8& v0, bf16x8& v1, int& c0,
+                                           int& c1);
 
 template <>
-__device__ __forceinline__ void decode_raw<FMT_Q8_0>(const Raw4& r, int, int, float out[4])
+__device__ __forceinline__ void decode_raw<FMT_Q4_0>(const Raw16& r, int, int h, bf16x8& v0, bf16x8& v1, int& c0,
+                                                     int& c1)
 {
-    const float d = half_bits(r.a);
-    const uint32_t q = r.b | (r.c << 16);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        out[i] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(q >> (8 * i))));
+    const float d = half_bits(r.w[0]);
+    const float c = -8.0f * d;
+    v0 = decode8(opaque(r.w[1] & 0x0f0f0f0fu), opaque(r.w[2] & 0x0f0f0f0fu), d, c);
+    v1 = decode8(opaque(r.w[1] & 0xf0f0f0f0u), opaque(r.w[2] & 0xf0f0f0f0u), d * 0.0625f, c);
+    c0 = 8 * h;
+    c1 = 16 + 8 * h;
 }
 
 template <>
-__device__ __forceinline__ void decode_raw<FMT_Q4_0>(const Raw4& r, int, int p, float out[4])
+__device__ __forceinline__ void decode_raw<FMT_Q8_0>(const Raw16& r, int, int h, bf16x8& v0, bf16x8& v1, int& c0,
+                                                     int& c1)
 {
-    const float d = half_bits(r.a);
-    const uint32_t q = r.b | (r.c << 16);
-    const int shift = p < 4 ? 0 : 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        out[i] = __fmul_rn(d, static_cast<float>(static_cast<int>((q >> (8 * i + shift)) & 15) - 8));
+    const float d = half_bits(r.w[0]);
+    const float c = -128.0f * d;
+    v0 = decode8(opaque(r.w[1] ^ 0x80808080u), opaque(r.w[2] ^ 0x80808080u), d, c);   // q + 128 as unsigned bytes
+    v1 = decode8(opaque(r.w[3] ^ 0x80808080u), opaque(r.w[4] ^ 0x80808080u), d, c);
+    c0 = 16 * h;
+    c1 = 16 * h + 8;
 }
 
+// 6-bit scale and min of sub-block j (GGML get_scale_min_k4) from the
+// scale words lo = scales[0..3], mid = scales[4..7], hi = scales[8..11].
 template <>
-__device__ __forceinline__ void decode_raw<FMT_Q4_K>(const Raw4& r, int blk, int, float out[4])
+__device__ __forceinline__ void decode_raw<FMT_Q4_K>(const Raw16& r, int blk, int h, bf16x8& v0, bf16x8& v1, int& c0,
+                                                     int& c1)
 {
     const int j = blk & 7;
-    const float d = half_bits(r.a), dmin = half_bits(r.a >> 16);
+    const float d = half_bits(r.w[0]), dmin = half_bits(r.w[0] >> 16);
+    const int sh = 8 * (j & 3);
+    const uint32_t lo = (r.w[1] >> sh) & 0xffu, mid = (r.w[2] >> sh) & 0xffu, hi = (r.w[3] >> sh) & 0xffu;
     int sc, m;
     if (j < 4) {
-        sc = r.b & 63;
-        m = (r.b >> 8) & 63;
-    } else {   // bytes s[j+4], s[j-4], s[j]
-        sc = (r.b & 15) | (((r.b >> 8) >> 6 & 3) << 4);
-        m = ((r.b >> 4) & 15) | (((r.b >> 16) >> 6 & 3) << 4);
+        sc = static_cast<int>(lo & 63u);
+        m = static_cast<int>(mid & 63u);
+    } else {
+        sc = static_cast<int>((hi & 15u) | ((lo >> 6) << 4));
+        m = static_cast<int>((hi >> 4) | ((mid >> 6) << 4));
     }
     const float d1 = __fmul_rn(d, static_cast<float>(sc));
     const float m1 = __fmul_rn(dmin, static_cast<float>(m));
-    const int shift = 4 * (j & 1);
+    const bool high = (j & 1) != 0;
+    const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+    const float a = high ? d1 * 0.0625f : d1;
+    v0 = decode8(opaque(r.w[4] & mask), opaque(r.w[5] & mask), a, -m1);
+    v1 = decode8(opaque(r.w[6] & mask), opaque(r.w[7] & mask), a, -m1);
+    c0 = 16 * h;
+    c1 = 16 * h + 8;
+}
+
+// Scheduling hint for one steady-state step: the step's matrix-core
+// instructions are spread over the step, with the LDS fragment reads, the
+// decode of the next step (vector ALU), its LDS stores and the loads of a
+// later step placed between them, so a single wave keeps the matrix core
+// busy while it decodes (the work of a step is independent of the next
+// step's decode and stores, which go to the other LDS buffer).
+template <int NMFMA>
+__device__ __forceinline__ void interleave_step()
+{
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        out[i] = __fsub_rn(__fmul_rn(d1, static_cast<float>((r.c >> (8 * i + shift)) & 15)), m1);
+    for (int i = 0; i < NMFMA; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // vector ALU
+    }
 }
 
 // MW token rows per wave (32 or 64: MW / 32 accumulator tiles along M),
-// 32 * NT rows of W per workgroup, two 32-column blocks per step.  The raw
-// W bytes of step s + 1 and the X fragments of step s + 1 are requested
-// before the matrix-core work of step s, and decoded into the other LDS
-// buffer after it, so memory latency hides behind the MFMAs; one barrier
-// per step.
-template <int FMT, int MW, int NT>
-__global__ __launch_bounds__(PF_THREADS) void prefill_mfma_kernel(const uint8_t* __restrict__ W,
-                                                                   const __bf16* __restrict__ X,
-                                                                   float* __restrict__ Y, int M, int N, int K,
-                                                                   int64_t row_bytes)
+// 4 * MW token rows and 32 * NT rows of W per workgroup tile, two
+// 32-column blocks (64 columns) per step; KS groups of 4 waves split the
+// steps of the tile (KS = 2: two waves per SIMD, whose LDS, decode and
+// matrix-core phases overlap) and add their sums through LDS at the end.
+//
+//   * X: a group's 4 * MW x 64 bf16 tile of a step is loaded with
+//     coalesced 16-byte loads (8 lanes per 128-byte token row) and stored
+//     to LDS with its 16-byte chunks swizzled (chunk c of row r at
+//     c ^ ((r >> 1) & 7)), so the MFMA fragment reads (32 rows, one chunk)
+//     are free of bank conflicts;
+//   * W: each lane loads the raw words of 16 values (half a block of one
+//     row) and decodes them exactly into the group's bf16 LDS tile;
+//   * both are loaded D steps ahead into a ring of register sets (the loop
+//     is unrolled by D so each slot is one fixed register set) and written
+//     to the other LDS buffer after the step's matrix-core work; one
+//     barrier per step.
+template <int FMT, int MW, int NT, int D, int KS>
+__global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uint8_t* __restrict__ W,
+                                                                        const __bf16* __restrict__ X,
+                                                                        float* __restrict__ Y, int M, int N, int K,
+                                                                        int64_t row_bytes)
 {
     constexpr int MT = MW / 32;                           // accumulator tiles along M per wave
     constexpr int NROWS = 32 * NT;                        // W rows per workgroup
+    constexpr int TROWS = 4 * MW;                         // token rows per workgroup
     constexpr int BPS = 2;                                // 32-column blocks per step
-    constexpr int GROUPS = NROWS * 8 * BPS / PF_THREADS;  // 4-value groups per thread per step
-    static_assert(GROUPS * PF_THREADS == NROWS * 8 * BPS, "whole groups per thread");
-    __shared__ __attribute__((aligned(16))) __bf16 ws[2][BPS][NROWS * WS_STRIDE];
+    constexpr int WI = NROWS * BPS * 2 / PF_THREADS;      // 16-value W items per thread per step
+    constexpr int XL = TROWS * 8 / PF_THREADS;            // 16-byte X chunks per thread per step
+    static_assert(WI >= 1 && WI * PF_THREADS == NROWS * BPS * 2, "whole W items per thread");
+    static_assert(D % 2 == 0, "ring groups start on even steps, so a slot's LDS buffer is fixed");
+    static_assert(XL * PF_THREADS == TROWS * 8, "whole X chunks per thread");
+    static_assert(KS == 1 || KS * 2 * TROWS * 8 * 16 >= PF_THREADS * (KS - 1) * MT * NT * 16 * 4,
+                  "the X buffers hold the partial sums of the other step groups");
+    __shared__ __attribute__((aligned(16))) __bf16 ws[KS][2][BPS][NROWS * WS_STRIDE];
+    __shared__ __attribute__((aligned(16))) u32x4 xs[KS][2][TROWS * 8];
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int t = threadIdx.x % PF_THREADS;              // thread within the step group
+    const int kh = threadIdx.x / PF_THREADS;             // step group
+    const int lane = t & 63;
+    const int wave = t >> 6;
     const int n0 = blockIdx.x * NROWS;
-    const int m0 = blockIdx.y * (4 * MW) + wave * MW;
+    const int mw0 = blockIdx.y * TROWS;                  // first token row of the workgroup
+    const int m0 = mw0 + wave * MW;                       // first token row of this wave
     const int g = lane >> 5;          // K group of the fragment (0, 1)
     const int li = lane & 31;
     const int nblk = K / 32;
-    const int nsteps = (nblk + BPS - 1) / BPS;
+    const int nsteps_all = (nblk + BPS - 1) / BPS;
+    const int nsteps = (nsteps_all + KS - 1) / KS;       // steps of each group (the launcher makes KS divide)
+    const int step0 = kh * nsteps;
 
-    // token rows of this lane's A fragments (clamped for loads)
-    const __bf16* xrow[MT];
+    // this thread's X chunks: token row, 16-byte chunk
+    uint32_t xoff[XL];                                    // byte offset of the token row
+    int xdst[XL];
+    const int xcol = 8 * (t & 7);                         // the same chunk column for every e
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-        xrow[mt] = X + static_cast<int64_t>(min(m0 + 32 * mt + li, M - 1)) * K + 8 * g;
-
-    // this thread's decode groups: (block of the step, W row, part)
-    int gb[GROUPS], gp[GROUPS];
-    const uint8_t* grow[GROUPS];
-#pragma unroll
-    for (int e = 0; e < GROUPS; e++) {
-        const int item = threadIdx.x + e * PF_THREADS;
-        gb[e] = item / (NROWS * 8);
-        const int rem = item % (NROWS * 8);
-        gp[e] = rem & 7;
-        grow[e] = W + static_cast<int64_t>(min(n0 + (rem >> 3), N - 1)) * row_bytes;
+    for (int e = 0; e < XL; e++) {
+        const int item = t + e * PF_THREADS;
+        const int r = item >> 3, c = item & 7;
+        xoff[e] = static_cast<uint32_t>(min(mw0 + r, M - 1)) * static_cast<uint32_t>(2 * K);
+        xdst[e] = r * 8 + (c ^ ((r >> 1) & 7));
     }
+    const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
+
+    // W item i of this thread: idx = t + 256 i -> half h = idx % 2, block
+    // bo = (idx / 2) % 2 of the step, tile row idx / 4 (4 consecutive lanes
+    // cover one row's two blocks)
+    uint32_t wrow[WI];                                    // byte offset of the W row
+#pragma unroll
+    for (int i = 0; i < WI; i++) {
+        const int r = (t + i * PF_THREADS) >> 2;
+        wrow[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * static_cast<uint32_t>(row_bytes);
+    }
+    const int wh = t & 1, wbo = (t >> 1) & 1;
 
     f32x16 acc[MT][NT];
 #pragma unroll
@@ -186,80 +310,131 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_mfma_kernel(const uint8_t*
         for (int nt = 0; nt < NT; nt++)
             acc[mt][nt] = f32x16{};
 
-    Raw4 raw[GROUPS];
-    auto load_step = [&](int step) {
+    // ring slot s % D holds the W words and X chunks of local step s
+    Raw16 raw[D][WI];
+    u32x4 xr[D][XL];
+    auto load_step = [&](int ls, Raw16 (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
+        const int step = step0 + ls;
+        const int blk = min(BPS * step + wbo, nblk - 1);
 #pragma unroll
-        for (int e = 0; e < GROUPS; e++) {
-            const int blk = min(BPS * step + gb[e], nblk - 1);
-            raw[e] = load_raw<FMT>(grow[e], blk, gp[e]);
-        }
-    };
-    auto store_step = [&](int step, int buf) {
+        for (int i = 0; i < WI; i++)
+            wdst[i] = load_raw<FMT>(W, wrow[i], blk, wh);
+        // columns past K (the second block of a partial last step) re-read
+        // the row's last chunk; their MFMAs are skipped
+        const int col = min(BPS * 32 * step + xcol, K - 8);
 #pragma unroll
-        for (int e = 0; e < GROUPS; e++) {
-            const int blk = min(BPS * step + gb[e], nblk - 1);
-            float v[4];
-            decode_raw<FMT>(raw[e], blk, gp[e], v);
-            bf16x4 h;
-            h[0] = static_cast<__bf16>(v[0]);
-            h[1] = static_cast<__bf16>(v[1]);
-            h[2] = static_cast<__bf16>(v[2]);
-            h[3] = static_cast<__bf16>(v[3]);
-            const int r = (threadIdx.x + e * PF_THREADS) % (NROWS * 8) >> 3;
-            *reinterpret_cast<bf16x4*>(&ws[buf][gb[e]][r * WS_STRIDE + 4 * gp[e]]) = h;
-        }
+        for (int e = 0; e < XL; e++)
+            xdst_regs[e] = *reinterpret_cast<const u32x4*>(xbytes + (xoff[e] + static_cast<uint32_t>(2 * col)));
     };
-    bf16x8 a[BPS][MT][2], an[BPS][MT][2];
-    auto load_a = [&](int step, bf16x8 (&dst)[BPS][MT][2]) {
+    auto store_step = [&](int ls, const Raw16 (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
+        const int blk = min(BPS * (step0 + ls) + wbo, nblk - 1);
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            bf16x8 v0, v1;
+            int c0, c1;
+            decode_raw<FMT>(wsrc[i], blk, wh, v0, v1, c0, c1);
+            const int r = (t + i * PF_THREADS) >> 2;
+            *reinterpret_cast<bf16x8*>(&ws[kh][buf][wbo][r * WS_STRIDE + c0]) = v0;
+            *reinterpret_cast<bf16x8*>(&ws[kh][buf][wbo][r * WS_STRIDE + c1]) = v1;
+        }
+#pragma unroll
+        for (int e = 0; e < XL; e++)
+            xs[kh][buf][xdst[e]] = xsrc_regs[e];
+    };
+    // matrix-core work of one local step from LDS buffer buf (= ls & 1);
+    // only the last step of all can hold a block past K (guarded)
+    auto mfma_step = [&](int ls, int buf, bool guarded) {
+        const int step = step0 + ls;
 #pragma unroll
         for (int bo = 0; bo < BPS; bo++) {
-            const int blk = min(BPS * step + bo, nblk - 1);
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int h = 0; h < 2; h++)
-                    dst[bo][mt][h] = *reinterpret_cast<const bf16x8*>(xrow[mt] + blk * 32 + 16 * h);
-        }
-    };
-
-    load_step(0);
-    load_a(0, a);
-    store_step(0, 0);
-    __syncthreads();
-    for (int step = 0; step < nsteps; step++) {
-        const int buf = step & 1;
-        const bool more = step + 1 < nsteps;
-        if (more) {
-            load_step(step + 1);
-            load_a(step + 1, an);
-        }
-#pragma unroll
-        for (int bo = 0; bo < BPS; bo++) {
-            if (BPS * step + bo < nblk) {
+            if (!guarded || BPS * step + bo < nblk) {
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
+                    const int c = 4 * bo + 2 * h + g;   // 16-byte chunk of the fragment
+                    bf16x8 a[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        const int r = wave * MW + 32 * mt + li;
+                        a[mt] = *reinterpret_cast<const bf16x8*>(&xs[kh][buf][r * 8 + (c ^ ((r >> 1) & 7))]);
+                    }
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
-                        const bf16x8 b =
-                            *reinterpret_cast<const bf16x8*>(&ws[buf][bo][(32 * nt + li) * WS_STRIDE + 16 * h + 8 * g]);
+                        const bf16x8 b = *reinterpret_cast<const bf16x8*>(
+                            &ws[kh][buf][bo][(32 * nt + li) * WS_STRIDE + 16 * h + 8 * g]);
 #pragma unroll
                         for (int mt = 0; mt < MT; mt++)
-                            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[bo][mt][h], b, acc[mt][nt], 0, 0, 0);
+                            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], b, acc[mt][nt], 0, 0, 0);
                     }
                 }
             }
         }
-        if (more) {
-            store_step(step + 1, buf ^ 1);
+    };
+
+    // prologue: local step 0 in LDS; steps 1..D in flight
+    {
+        Raw16 w0[WI];
+        u32x4 x0[XL];
+        load_step(0, w0, x0);
 #pragma unroll
-            for (int bo = 0; bo < BPS; bo++)
+        for (int u = 0; u < D; u++)
+            load_step(min(u + 1, nsteps - 1), raw[(u + 1) % D], xr[(u + 1) % D]);
+        store_step(0, w0, x0, 0);
+    }
+    __syncthreads();
+    // Steady state: every step of a group has a successor and the loads are
+    // unconditional (clamped step indexes), so each ring slot stays one
+    // register set across the loop and no load is waited for early.
+    int base = 0;
+    for (; base + D < nsteps; base += D) {
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++)
+        for (int u = 0; u < D; u++) {
+            const int ls = base + u;
+            const int next = (u + 1) % D;   // constant after unrolling
+            mfma_step(ls, u & 1, false);                 // D is even: the buffers are constants
+            store_step(ls + 1, raw[next], xr[next], (u + 1) & 1);
+            load_step(min(ls + 1 + D, nsteps - 1), raw[next], xr[next]);
+            interleave_step<BPS * 2 * MT * NT>();
+            __syncthreads();
+        }
+    }
+    // the last (at most D) steps: their loads are already in flight
 #pragma unroll
-                    for (int h = 0; h < 2; h++)
-                        a[bo][mt][h] = an[bo][mt][h];
+    for (int u = 0; u < D; u++) {
+        const int ls = base + u;
+        if (ls < nsteps) {
+            mfma_step(ls, u & 1, true);
+            if (ls + 1 < nsteps)
+                store_step(ls + 1, raw[(u + 1) % D], xr[(u + 1) % D], (u + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // the other step groups add their sums into group 0 through LDS (the X
+    // buffers are free after the last barrier)
+    if constexpr (KS > 1) {
+        float* red = reinterpret_cast<float*>(&xs[0][0][0]);
+        constexpr int PER = MT * NT * 16;
+        if (kh > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        red[((kh - 1) * PER + (mt * NT + nt) * 16 + r) * PF_THREADS + t] = acc[mt][nt][r];
         }
         __syncthreads();
+        if (kh > 0)
+            return;
+#pragma unroll
+        for (int o = 1; o < KS; o++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        acc[mt][nt][r] += red[((o - 1) * PER + (mt * NT + nt) * 16 + r) * PF_THREADS + t];
     }
 
 #pragma unroll
@@ -277,27 +452,32 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_mfma_kernel(const uint8_t*
     }
 }
 
-template <int FMT, int MW, int NT>
+template <int FMT, int MW, int NT, int KS, int D = PF_DEPTH>
 hipError_t launch_prefill_shape(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
 {
     const int64_t rb = row_bytes(FMT, k);
     const dim3 grid(static_cast<unsigned>((n + 32 * NT - 1) / (32 * NT)), static_cast<unsigned>((m + 4 * MW - 1) / (4 * MW)));
-    hipLaunchKernelGGL((prefill_mfma_kernel<FMT, MW, NT>), grid, dim3(PF_THREADS), 0, s, static_cast<const uint8_t*>(w),
-                       static_cast<const __bf16*>(x), y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), rb);
+    hipLaunchKernelGGL((prefill_mfma_kernel<FMT, MW, NT, D, KS>), grid, dim3(PF_THREADS * KS), 0, s,
+                       static_cast<const uint8_t*>(w), static_cast<const __bf16*>(x), y, static_cast<int>(m),
+                       static_cast<int>(n), static_cast<int>(k), rb);
     return hipGetLastError();
 }
 
-// The largest tile whose grid still covers the 256 CUs: 256 tokens x 64
-// rows, else 128 x 64, else 128 x 32.
+// Tile choice (measured on the Phi-4-mini projections at 512 tokens):
+// 256 tokens x 64 rows when that grid has at least 128 workgroups (its
+// 64 x 64 wave tiles reuse each fragment twice); otherwise 128 tokens x
+// 64 rows with the steps split between two groups of 4 waves when they
+// divide evenly (two waves per SIMD overlap their phases).
 template <int FMT>
 hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
 {
     auto wgs = [&](int mt, int nt) { return ((n + nt - 1) / nt) * ((m + mt - 1) / mt); };
-    if (wgs(256, 64) >= 256)
-        return launch_prefill_shape<FMT, 64, 2>(w, x, y, m, n, k, s);
-    if (wgs(128, 64) >= 256)
-        return launch_prefill_shape<FMT, 32, 2>(w, x, y, m, n, k, s);
-    return launch_prefill_shape<FMT, 32, 1>(w, x, y, m, n, k, s);
+    if (wgs(256, 64) >= 128)
+        return launch_prefill_shape<FMT, 64, 2, 1>(w, x, y, m, n, k, s);
+    const int64_t steps = (k / 32 + 1) / 2;
+    if (steps % 2 == 0)
+        return launch_prefill_shape<FMT, 32, 2, 2>(w, x, y, m, n, k, s);
+    return launch_prefill_shape<FMT, 32, 2, 1>(w, x, y, m, n, k, s);
 }
 
 }  // namespace
