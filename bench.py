@@ -451,22 +451,28 @@ def cpu_baseline(fmt, shapes, host_w, xs, ys, hip, bytes_per_step, budget_s):
         parity[name] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
     log(f"cpu/gpu L2-relative difference per shape: {parity}")
 
-    t0 = time.perf_counter()
-    step(threads)
-    one = time.perf_counter() - t0
-    reps = max(1, int(budget_s / 13 / max(one, 1e-6)))   # 4 warm-up + 9 samples
-    for _ in range(4):
-        for _ in range(reps):
-            step(threads)
-    samples = []
-    for _ in range(9):
+    def median_step(n_threads, budget):
+        """MatVecProfiler protocol: 4 warm-up batches, 9 timed batches, median."""
         t0 = time.perf_counter()
-        for _ in range(reps):
-            step(threads)
-        samples.append((time.perf_counter() - t0) / reps)
-    med = sorted(samples)[4]
+        step(n_threads)
+        one = time.perf_counter() - t0
+        reps = max(1, int(budget / 13 / max(one, 1e-6)))
+        for _ in range(4):
+            for _ in range(reps):
+                step(n_threads)
+        samples = []
+        for _ in range(9):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                step(n_threads)
+            samples.append((time.perf_counter() - t0) / reps)
+        return sorted(samples)[4], reps
+
+    med, reps = median_step(threads, budget_s)
     gbs = bytes_per_step / med / 1e9
     log(f"cpu baseline: {med * 1e3:.2f} ms/step on {threads} threads -> {gbs:.2f} GB/s")
+    med1, reps1 = median_step(1, budget_s / 2)
+    log(f"cpu baseline: {med1 * 1e3:.2f} ms/step on 1 thread -> {bytes_per_step / med1 / 1e9:.2f} GB/s")
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -484,6 +490,9 @@ def cpu_baseline(fmt, shapes, host_w, xs, ys, hip, bytes_per_step, budget_s):
         "sample": f"{reps} steps x 9 samples (median) of the same layer set, one weight copy, "
                   f"oracle CpuVm restatement (-O3 x86-64-v3, OpenMP rows); host {cpu_model}",
         "ms_per_step": round(med * 1e3, 3),
+        "value_1thread": round(bytes_per_step / med1 / 1e9, 3),
+        "ms_per_step_1thread": round(med1 * 1e3, 3),
+        "host_cpus": os.cpu_count(),
         "gpu_vs_cpu_l2_rel": parity,
     }
 

@@ -39,7 +39,19 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16 raw bytes
 
 constexpr int PF_THREADS = 256;
-constexpr int WS_STRIDE = 40;       // bf16 per LDS tile row: 32 values + 8 pad
+// LDS W tile rows of 32 bf16 (four 16-byte chunks).  Padded: a row takes
+// 40 bf16.  Compact (used when two workgroups share a CU, to fit two in
+// 160 KiB): a row takes 32 bf16 and chunk c sits at c ^ ((r / 4) % 4).
+// Both keep the fragment reads (32 consecutive rows, one chunk) and the
+// decode stores free of bank conflicts; the padded form measured faster
+// when a workgroup has its CU to itself.
+template <bool COMPACT>
+constexpr int ws_stride() { return COMPACT ? 32 : 40; }
+template <bool COMPACT>
+__device__ __forceinline__ int ws_off(int r, int c)
+{
+    return COMPACT ? r * 32 + 8 * (c ^ ((r >> 2) & 3)) : r * 40 + 8 * c;
+}
 constexpr int PF_DEPTH = 2;         // steps of loads in flight (even: LDS buffer = step parity)
 
 // Raw words of one item of 16 values (half a 32-value block of one W row),
@@ -245,7 +257,7 @@ __device__ __forceinline__ void interleave_step()
 //     is unrolled by D so each slot is one fixed register set) and written
 //     to the other LDS buffer after the step's matrix-core work; one
 //     barrier per step.
-template <int FMT, int MW, int NT, int D, int KS>
+template <int FMT, int MW, int NT, int D, int KS, bool COMPACT>
 __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uint8_t* __restrict__ W,
                                                                         const __bf16* __restrict__ X,
                                                                         float* __restrict__ Y, int M, int N, int K,
@@ -262,7 +274,7 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
     static_assert(XL * PF_THREADS == TROWS * 8, "whole X chunks per thread");
     static_assert(KS == 1 || KS * 2 * TROWS * 8 * 16 >= PF_THREADS * (KS - 1) * MT * NT * 16 * 4,
                   "the X buffers hold the partial sums of the other step groups");
-    __shared__ __attribute__((aligned(16))) __bf16 ws[KS][2][BPS][NROWS * WS_STRIDE];
+    __shared__ __attribute__((aligned(16))) __bf16 ws[KS][2][BPS][NROWS * ws_stride<COMPACT>()];
     __shared__ __attribute__((aligned(16))) u32x4 xs[KS][2][TROWS * 8];
 
     const int t = threadIdx.x % PF_THREADS;              // thread within the step group
@@ -334,8 +346,8 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
             int c0, c1;
             decode_raw<FMT>(wsrc[i], blk, wh, v0, v1, c0, c1);
             const int r = (t + i * PF_THREADS) >> 2;
-            *reinterpret_cast<bf16x8*>(&ws[kh][buf][wbo][r * WS_STRIDE + c0]) = v0;
-            *reinterpret_cast<bf16x8*>(&ws[kh][buf][wbo][r * WS_STRIDE + c1]) = v1;
+            *reinterpret_cast<bf16x8*>(&ws[kh][buf][wbo][ws_off<COMPACT>(r, c0 >> 3)]) = v0;
+            *reinterpret_cast<bf16x8*>(&ws[kh][buf][wbo][ws_off<COMPACT>(r, c1 >> 3)]) = v1;
         }
 #pragma unroll
         for (int e = 0; e < XL; e++)
@@ -360,7 +372,7 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
                         const bf16x8 b = *reinterpret_cast<const bf16x8*>(
-                            &ws[kh][buf][bo][(32 * nt + li) * WS_STRIDE + 16 * h + 8 * g]);
+                            &ws[kh][buf][bo][ws_off<COMPACT>(32 * nt + li, 2 * h + g)]);
 #pragma unroll
                         for (int mt = 0; mt < MT; mt++)
                             acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], b, acc[mt][nt], 0, 0, 0);
@@ -452,32 +464,40 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
     }
 }
 
-template <int FMT, int MW, int NT, int KS, int D = PF_DEPTH>
+constexpr int NUM_CUS = 256;
+
+template <int FMT, int MW, int NT, int KS, bool COMPACT, int D = PF_DEPTH>
 hipError_t launch_prefill_shape(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
 {
     const int64_t rb = row_bytes(FMT, k);
     const dim3 grid(static_cast<unsigned>((n + 32 * NT - 1) / (32 * NT)), static_cast<unsigned>((m + 4 * MW - 1) / (4 * MW)));
-    hipLaunchKernelGGL((prefill_mfma_kernel<FMT, MW, NT, D, KS>), grid, dim3(PF_THREADS * KS), 0, s,
+    hipLaunchKernelGGL((prefill_mfma_kernel<FMT, MW, NT, D, KS, COMPACT>), grid, dim3(PF_THREADS * KS), 0, s,
                        static_cast<const uint8_t*>(w), static_cast<const __bf16*>(x), y, static_cast<int>(m),
                        static_cast<int>(n), static_cast<int>(k), rb);
     return hipGetLastError();
 }
 
 // Tile choice (measured on the Phi-4-mini projections at 512 tokens):
-// 256 tokens x 64 rows when that grid has at least 128 workgroups (its
-// 64 x 64 wave tiles reuse each fragment twice); otherwise 128 tokens x
-// 64 rows with the steps split between two groups of 4 waves when they
-// divide evenly (two waves per SIMD overlap their phases).
+//   * 256 tokens x 64 rows (64 x 64 wave tiles, each fragment used twice)
+//     when that grid has at least 128 workgroups: padded W tile (84 KiB,
+//     one workgroup per CU) up to one workgroup per CU, compact (80 KiB,
+//     two per CU) above;
+//   * otherwise 128 tokens x 64 rows with the steps split between two
+//     groups of 4 waves when they divide evenly (two waves per SIMD
+//     overlap their phases).
 template <int FMT>
 hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
 {
     auto wgs = [&](int mt, int nt) { return ((n + nt - 1) / nt) * ((m + mt - 1) / mt); };
-    if (wgs(256, 64) >= 128)
-        return launch_prefill_shape<FMT, 64, 2, 1>(w, x, y, m, n, k, s);
+    const int64_t big = wgs(256, 64);
+    if (big > NUM_CUS)
+        return launch_prefill_shape<FMT, 64, 2, 1, true>(w, x, y, m, n, k, s);
+    if (big >= NUM_CUS / 2)
+        return launch_prefill_shape<FMT, 64, 2, 1, false>(w, x, y, m, n, k, s);
     const int64_t steps = (k / 32 + 1) / 2;
     if (steps % 2 == 0)
-        return launch_prefill_shape<FMT, 32, 2, 2>(w, x, y, m, n, k, s);
-    return launch_prefill_shape<FMT, 32, 2, 1>(w, x, y, m, n, k, s);
+        return launch_prefill_shape<FMT, 32, 2, 2, false>(w, x, y, m, n, k, s);
+    return launch_prefill_shape<FMT, 32, 2, 1, false>(w, x, y, m, n, k, s);
 }
 
 }  // namespace
