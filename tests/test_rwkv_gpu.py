@@ -123,9 +123,10 @@ def test_wkv_rejects_bad_arguments(hip):
     s.free()
 
 
-def small_cfg(layers=3):
-    return rwkv7.Rwkv7Config(layers=layers, hidden=1024, heads=16, ffn=2048, vocab=300, rank_w=32, rank_a=32,
-                             rank_v=32, rank_g=64)
+def small_cfg(layers=3, ranks=(32, 32, 32, 64)):
+    rw, ra, rv, rg = ranks
+    return rwkv7.Rwkv7Config(layers=layers, hidden=1024, heads=16, ffn=2048, vocab=300, rank_w=rw, rank_a=ra,
+                             rank_v=rv, rank_g=rg)
 
 
 def oracle_cfg(cfg):
@@ -176,10 +177,14 @@ def test_routed_step_matches_fp64(hip, route):
         sess.close()
 
 
-def test_small_step_sequence_matches_oracle(hip):
+@pytest.mark.parametrize("ranks", [(32, 32, 32, 64), (256, 256, 256, 256), (32, 32, 32, 288)],
+                         ids=["ranks-32-64", "ranks-256", "rank-g-288"])
+def test_small_step_sequence_matches_oracle(hip, ranks):
     """Three layers, random weights and mid-sequence state, four tokens fed
-    back greedily: every step's logits and every layer's state."""
-    cfg = small_cfg(layers=3)
+    back greedily: every step's logits and every layer's state, at small
+    LoRA ranks, at rank 256 for all four LoRAs and at a g rank of 288
+    (LoRA output rows of 1 to 9 blocks)."""
+    cfg = small_cfg(layers=3, ranks=ranks)
     weights = rwkv7.synth_weights(cfg, seed=5)
     st = rwkv7.synth_state(cfg, seed=6)
     sess = rwkv7.Rwkv7DecodeSession(hip, cfg, weights, st)
