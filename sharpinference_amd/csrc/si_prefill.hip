@@ -479,9 +479,10 @@ hipError_t launch_prefill_shape(const void* w, const void* x, float* y, int64_t 
 
 // Tile choice (measured on the Phi-4-mini projections at 512 tokens):
 //   * 256 tokens x 64 rows (64 x 64 wave tiles, each fragment used twice)
-//     when that grid has at least 128 workgroups: padded W tile (84 KiB,
-//     one workgroup per CU) up to one workgroup per CU, compact (80 KiB,
-//     two per CU) above;
+//     when that grid has at least 128 workgroups: above one workgroup per
+//     CU the compact W tile (80 KiB, two workgroups per CU); up to one per
+//     CU two step groups of 4 waves with compact tiles (160 KiB, two waves
+//     per SIMD) when they divide the steps, else the padded tile (84 KiB);
 //   * otherwise 128 tokens x 64 rows with the steps split between two
 //     groups of 4 waves when they divide evenly (two waves per SIMD
 //     overlap their phases).
@@ -490,11 +491,12 @@ hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m,
 {
     auto wgs = [&](int mt, int nt) { return ((n + nt - 1) / nt) * ((m + mt - 1) / mt); };
     const int64_t big = wgs(256, 64);
+    const int64_t steps = (k / 32 + 1) / 2;
     if (big > NUM_CUS)
         return launch_prefill_shape<FMT, 64, 2, 1, true>(w, x, y, m, n, k, s);
     if (big >= NUM_CUS / 2)
-        return launch_prefill_shape<FMT, 64, 2, 1, false>(w, x, y, m, n, k, s);
-    const int64_t steps = (k / 32 + 1) / 2;
+        return steps % 2 == 0 ? launch_prefill_shape<FMT, 64, 2, 2, true>(w, x, y, m, n, k, s)
+                              : launch_prefill_shape<FMT, 64, 2, 1, false>(w, x, y, m, n, k, s);
     if (steps % 2 == 0)
         return launch_prefill_shape<FMT, 32, 2, 2, false>(w, x, y, m, n, k, s);
     return launch_prefill_shape<FMT, 32, 2, 1, false>(w, x, y, m, n, k, s);
