@@ -75,10 +75,10 @@ int ElementSize(GraphElementType type)
 
 bool Satisfies(GraphElementType provided, GraphElementType required)
 {
-    auto rank = [](GraphElementType t) { return t == GraphElementType::Float16 ? 1 : t == GraphElementType::Float32 ? 2 : 0; };
-    if (rank(provided) == 0 || rank(required) == 0)
-        return provided == required;
-    return rank(provided) >= rank(required);
+    for (GraphElementType t : {provided, required})
+        if (t != GraphElementType::Float16 && t != GraphElementType::Float32)
+            throw ArgumentException("'" + TypeName(t) + "' is not a supported floating-point precision.");
+    return provided == required || (provided == GraphElementType::Float32 && required == GraphElementType::Float16);
 }
 
 uint64_t TensorDescriptor::ElementCount() const

@@ -79,8 +79,9 @@ enum class GraphElementType { Float32, Float16, UInt8, Int32 };
 enum class GraphResourceAccess { Read, ReadWrite };
 
 int ElementSize(GraphElementType type);
-// Width order used by precision checks: Float16 < Float32 (integers compare
-// only with themselves).
+// Precision check (NumericTypeCompatibility.Satisfies, OperatorBackend.cs:106-112):
+// equal types, or Float32 where Float16 is required; a type other than
+// Float16 / Float32 is an ArgumentException.
 bool Satisfies(GraphElementType provided, GraphElementType required);
 
 struct InstructionTarget {

@@ -300,8 +300,10 @@ TEST(cpu, AdaptationSelectsTheSignatureAndRejectsMismatches)
                   mv->Adapt(with([](P& p) { p[2].access = GraphResourceAccess::Read; }), kFp32));
     ASSERT_THROWS(InstructionAdaptationException,
                   mv->Adapt(with([](P& p) { p[0].name = "matrix2"; }), kFp32));
-    ASSERT_THROWS(InstructionAdaptationException,
-                  mv->Adapt(ok, {GraphElementType::Int32, GraphElementType::Float32}));
+    // a requirement that is not a floating-point type (OperatorBackend.cs:143-149)
+    ASSERT_THROWS(ArgumentException, mv->Adapt(ok, {GraphElementType::Int32, GraphElementType::Float32}));
+    ASSERT_TRUE(Satisfies(GraphElementType::Float32, GraphElementType::Float16));
+    ASSERT_TRUE(!Satisfies(GraphElementType::Float16, GraphElementType::Float32));
     // Validate: format, columns, and tensor shapes
     ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p[3].value = "q5_0"; }), kFp32));
     ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(with([](P& p) { p[4].value = "500"; }), kFp32));
@@ -319,6 +321,33 @@ TEST(cpu, AdaptationSelectsTheSignatureAndRejectsMismatches)
     } catch (const InstructionAdaptationException& e) {
         const std::string m = e.what();
         ASSERT_TRUE(m.find("Instruction '" + HipInstructionCollectionIds::QuantizedFloat32 + "/quant.mat-vec'") == 0);
+    }
+}
+
+// An FP16-precision instruction: an FP32 requirement cannot be met.
+struct HalfPrecisionMatVec : QuantizedMatVecInstruction {
+    std::vector<InstructionSignature> Signatures() const override
+    {
+        auto s = QuantizedMatVecInstruction::Signatures();
+        for (auto& sig : s)
+            sig.precision = {GraphElementType::Float16, GraphElementType::Float16};
+        return s;
+    }
+};
+
+TEST(cpu, PrecisionRequirementsAboveTheSignatureAreRejectedWithTheProvidedProfiles)
+{
+    HalfPrecisionMatVec half;
+    const auto p = MatVecParameters(SI_HIP_Q8_0, 3, 64, 0);
+    ASSERT_TRUE(half.Adapt(p, {GraphElementType::Float16, GraphElementType::Float16}).precision.arithmetic_type ==
+                GraphElementType::Float16);
+    try {
+        half.Adapt(p, kFp32);
+        throw Failure("an FP32 requirement adapted to an FP16 signature");
+    } catch (const InstructionAdaptationException& e) {
+        const std::string m = e.what();
+        ASSERT_TRUE(m.find("On hip.gfx950, required arithmetic=Float32, accumulator=Float32; provided "
+                           "arithmetic=Float16, accumulator=Float16") != std::string::npos);
     }
 }
 
