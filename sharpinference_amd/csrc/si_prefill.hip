@@ -464,6 +464,184 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
     }
 }
 
+// Warp-specialised form: 4 consumer waves issue only LDS fragment reads and
+// MFMAs (wave w owns MW tokens x all 32 * NT rows of the tile), while 4
+// producer waves load the raw W words and X chunks D steps ahead and decode
+// / store the next step into the other LDS buffer, so a SIMD runs one
+// wave's matrix-core work and another wave's decode at the same time.  One
+// barrier per step; the same exact W decode and swizzled layouts as the
+// kernel above.
+template <int FMT, int MW, int NT, int D>
+__global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_t* __restrict__ W,
+                                                                    const __bf16* __restrict__ X,
+                                                                    float* __restrict__ Y, int M, int N, int K,
+                                                                    int64_t row_bytes)
+{
+    constexpr int MT = MW / 32;
+    constexpr int NROWS = 32 * NT;
+    constexpr int TROWS = 4 * MW;
+    constexpr int BPS = 2;
+    constexpr int WI = NROWS * BPS * 2 / PF_THREADS;      // W items per producer thread per step
+    constexpr int XL = TROWS * 8 / PF_THREADS;            // X chunks per producer thread per step
+    static_assert(WI >= 1 && WI * PF_THREADS == NROWS * BPS * 2, "whole W items per thread");
+    static_assert(XL * PF_THREADS == TROWS * 8, "whole X chunks per thread");
+    static_assert(D % 2 == 0, "ring groups start on even steps, so a slot's LDS buffer is fixed");
+    __shared__ __attribute__((aligned(16))) __bf16 ws[2][BPS][NROWS * ws_stride<true>()];
+    __shared__ __attribute__((aligned(16))) u32x4 xs[2][TROWS * 8];
+
+    // the role is the same for a whole wave; readfirstlane makes that
+    // visible, so each wave runs one branch and both branches execute the
+    // same sequence of barriers (1 + one per step)
+    const bool consumer = __builtin_amdgcn_readfirstlane(threadIdx.x) < PF_THREADS;
+    const int t = threadIdx.x % PF_THREADS;
+    const int lane = t & 63, wave = t >> 6;
+    const int n0 = blockIdx.x * NROWS;
+    const int mw0 = blockIdx.y * TROWS;
+    const int g = lane >> 5, li = lane & 31;
+    const int nblk = K / 32;
+    const int nsteps = (nblk + BPS - 1) / BPS;
+
+    if (consumer) {
+        f32x16 acc[MT][NT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                acc[mt][nt] = f32x16{};
+        auto mfma_step = [&](int step, int buf, bool guarded) {
+#pragma unroll
+            for (int bo = 0; bo < BPS; bo++) {
+                if (!guarded || BPS * step + bo < nblk) {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const int c = 4 * bo + 2 * h + g;
+                        bf16x8 a[MT], b[NT];
+#pragma unroll
+                        for (int mt = 0; mt < MT; mt++) {
+                            const int r = wave * MW + 32 * mt + li;
+                            a[mt] = *reinterpret_cast<const bf16x8*>(&xs[buf][r * 8 + (c ^ ((r >> 1) & 7))]);
+                        }
+#pragma unroll
+                        for (int nt = 0; nt < NT; nt++)
+                            b[nt] = *reinterpret_cast<const bf16x8*>(
+                                &ws[buf][bo][ws_off<true>(32 * nt + li, 2 * h + g)]);
+#pragma unroll
+                        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                            for (int mt = 0; mt < MT; mt++)
+                                acc[mt][nt] =
+                                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
+                    }
+                }
+            }
+        };
+        __syncthreads();                                  // step 0 stored
+        int base = 0;
+        for (; base + D < nsteps; base += D) {
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                mfma_step(base + u, u & 1, false);
+                __syncthreads();
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            if (base + u < nsteps) {
+                mfma_step(base + u, u & 1, true);
+                __syncthreads();
+            }
+        }
+        const int m0 = mw0 + wave * MW;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int n = n0 + 32 * nt + li;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = m0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < M && n < N)
+                        Y[static_cast<int64_t>(m) * N + n] = acc[mt][nt][r];
+                }
+            }
+        }
+    } else {
+        uint32_t xoff[XL];
+        int xdst[XL];
+        const int xcol = 8 * (t & 7);
+#pragma unroll
+        for (int e = 0; e < XL; e++) {
+            const int item = t + e * PF_THREADS;
+            const int r = item >> 3, c = item & 7;
+            xoff[e] = static_cast<uint32_t>(min(mw0 + r, M - 1)) * static_cast<uint32_t>(2 * K);
+            xdst[e] = r * 8 + (c ^ ((r >> 1) & 7));
+        }
+        const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
+        uint32_t wrow[WI];
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            const int r = (t + i * PF_THREADS) >> 2;
+            wrow[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * static_cast<uint32_t>(row_bytes);
+        }
+        const int wh = t & 1, wbo = (t >> 1) & 1;
+        Raw16 raw[D][WI];
+        u32x4 xr[D][XL];
+        auto load_step = [&](int step, Raw16 (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
+            const int blk = min(BPS * step + wbo, nblk - 1);
+#pragma unroll
+            for (int i = 0; i < WI; i++)
+                wdst[i] = load_raw<FMT>(W, wrow[i], blk, wh);
+            const int col = min(BPS * 32 * step + xcol, K - 8);
+#pragma unroll
+            for (int e = 0; e < XL; e++)
+                xdst_regs[e] = *reinterpret_cast<const u32x4*>(xbytes + (xoff[e] + static_cast<uint32_t>(2 * col)));
+        };
+        auto store_step = [&](int step, const Raw16 (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
+            const int blk = min(BPS * step + wbo, nblk - 1);
+#pragma unroll
+            for (int i = 0; i < WI; i++) {
+                bf16x8 v0, v1;
+                int c0, c1;
+                decode_raw<FMT>(wsrc[i], blk, wh, v0, v1, c0, c1);
+                const int r = (t + i * PF_THREADS) >> 2;
+                *reinterpret_cast<bf16x8*>(&ws[buf][wbo][ws_off<true>(r, c0 >> 3)]) = v0;
+                *reinterpret_cast<bf16x8*>(&ws[buf][wbo][ws_off<true>(r, c1 >> 3)]) = v1;
+            }
+#pragma unroll
+            for (int e = 0; e < XL; e++)
+                xs[buf][xdst[e]] = xsrc_regs[e];
+        };
+        {
+            Raw16 w0[WI];
+            u32x4 x0[XL];
+            load_step(0, w0, x0);
+#pragma unroll
+            for (int u = 0; u < D; u++)
+                load_step(min(u + 1, nsteps - 1), raw[(u + 1) % D], xr[(u + 1) % D]);
+            store_step(0, w0, x0, 0);
+        }
+        __syncthreads();                                  // step 0 stored
+        int base = 0;
+        for (; base + D < nsteps; base += D) {
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                const int next = (u + 1) % D;
+                store_step(base + u + 1, raw[next], xr[next], (u + 1) & 1);
+                load_step(min(base + u + 1 + D, nsteps - 1), raw[next], xr[next]);
+                __syncthreads();
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            if (base + u < nsteps) {
+                if (base + u + 1 < nsteps)
+                    store_step(base + u + 1, raw[(u + 1) % D], xr[(u + 1) % D], (u + 1) & 1);
+                __syncthreads();
+            }
+        }
+    }
+}
+
 constexpr int NUM_CUS = 256;
 
 template <int FMT, int MW, int NT, int KS, bool COMPACT, int D = PF_DEPTH>
@@ -477,10 +655,23 @@ hipError_t launch_prefill_shape(const void* w, const void* x, float* y, int64_t 
     return hipGetLastError();
 }
 
+template <int FMT, int MW, int NT, int D = PF_DEPTH>
+hipError_t launch_prefill_ws(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
+{
+    const int64_t rb = row_bytes(FMT, k);
+    const dim3 grid(static_cast<unsigned>((n + 32 * NT - 1) / (32 * NT)), static_cast<unsigned>((m + 4 * MW - 1) / (4 * MW)));
+    hipLaunchKernelGGL((prefill_ws_kernel<FMT, MW, NT, D>), grid, dim3(2 * PF_THREADS), 0, s,
+                       static_cast<const uint8_t*>(w), static_cast<const __bf16*>(x), y, static_cast<int>(m),
+                       static_cast<int>(n), static_cast<int>(k), rb);
+    return hipGetLastError();
+}
+
 // Tile choice (measured on the Phi-4-mini projections at 512 tokens):
+//   * grids of more than 256 workgroups of 256 tokens x 64 rows: the
+//     warp-specialised kernel with 256 x 128 tiles (64 x 128 consumer wave
+//     tiles; gate_up 76 -> 67 us);
 //   * 256 tokens x 64 rows (64 x 64 wave tiles, each fragment used twice)
-//     when that grid has at least 128 workgroups: above one workgroup per
-//     CU the compact W tile (80 KiB, two workgroups per CU); up to one per
+//     when that grid has at least 128 workgroups: up to one per
 //     CU two step groups of 4 waves with compact tiles (160 KiB, two waves
 //     per SIMD) when they divide the steps, else the padded tile (84 KiB);
 //   * otherwise 128 tokens x 64 rows with the steps split between two
@@ -493,7 +684,7 @@ hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m,
     const int64_t big = wgs(256, 64);
     const int64_t steps = (k / 32 + 1) / 2;
     if (big > NUM_CUS)
-        return launch_prefill_shape<FMT, 64, 2, 1, true>(w, x, y, m, n, k, s);
+        return launch_prefill_ws<FMT, 64, 4>(w, x, y, m, n, k, s);
     if (big >= NUM_CUS / 2)
         return steps % 2 == 0 ? launch_prefill_shape<FMT, 64, 2, 2, true>(w, x, y, m, n, k, s)
                               : launch_prefill_shape<FMT, 64, 2, 1, false>(w, x, y, m, n, k, s);

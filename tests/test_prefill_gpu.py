@@ -51,10 +51,11 @@ SMALL = [(1, 32, 256), (7, 64, 256), (256, 96, 512), (300, 100, 768), (513, 33, 
 CASES = [(f, m, n, k) for f in FORMATS for (m, n, k) in SMALL]
 # 64-column steps: an odd count (one group of waves), a partial last step
 # split between two groups, a partial last step on the 256-token tile with
-# two groups and (odd count) with one, and a 256-token tile grid of more
-# than one workgroup per CU with a token tail
+# two groups and (odd count) with one, and the warp-specialised kernel
+# (grids past one 256 x 64 workgroup per CU) with token, row and step tails
 CASES += [(f, m, n, k) for f in (native.Q8_0, native.Q4_0)
-          for (m, n, k) in [(5, 40, 160), (130, 64, 224), (512, 8192, 96), (512, 8192, 160), (600, 16384, 64)]]
+          for (m, n, k) in [(5, 40, 160), (130, 64, 224), (512, 8192, 96), (512, 8192, 160), (600, 16384, 64),
+                            (300, 32768, 96), (520, 16448, 544)]]
 
 
 @pytest.mark.parametrize("fmt,m,rows,cols", CASES, ids=[f"{NAMES[f]}-m{m}-{n}x{k}" for f, m, n, k in CASES])
