@@ -400,7 +400,17 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
     const int local_row0 = group * ROWS_PER_GROUP + lr * RL;
     const int unit0 = slice * UPS + lk;
 
-    // 1. issue every weight load of this lane (rows past the end are
+    // 1. x first: it is small and mostly an L2 hit, and a lane's loads
+    //    complete in issue order, so loading it ahead of the weights lets
+    //    it be staged into LDS while the weights are still in flight
+    constexpr int XPT = K / 4 / THREADS;
+    const float4* x4 = reinterpret_cast<const float4*>(sg.x);
+    float4 xr[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; j++)
+        xr[j] = x4[threadIdx.x + j * THREADS];
+
+    // 2. issue every weight load of this lane (rows past the end are
     //    clamped into the matrix; their results are dropped)
     QUnit<FMT> w[UPL][RL];
 #pragma unroll
@@ -421,14 +431,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
     if constexpr (FULL)
         side_copy(sg, b, THREADS);
 
-    // 2. stage x into LDS (padded per unit); all of this thread's x loads
-    //    are issued before the first LDS write
-    constexpr int XPT = K / 4 / THREADS;
-    const float4* x4 = reinterpret_cast<const float4*>(sg.x);
-    float4 xr[XPT];
-#pragma unroll
-    for (int j = 0; j < XPT; j++)
-        xr[j] = x4[threadIdx.x + j * THREADS];
+    // 3. stage x into LDS (padded per unit), with its transform
     if (in_kind == XF_SWIGLU) {
         // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
 #pragma unroll
@@ -523,7 +526,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
         __syncthreads();
     }
 
-    // 3. per-unit dot products, x read once per unit and reused for RL rows
+    // 4. per-unit dot products, x read once per unit and reused for RL rows
     float acc[RL];
 #pragma unroll
     for (int t = 0; t < RL; t++)
@@ -556,7 +559,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
         }
     }
 
-    // 4. reduce across the LK lanes of a row slot, then across K slices
+    // 5. reduce across the LK lanes of a row slot, then across K slices
 #pragma unroll
     for (int t = 0; t < RL; t++) {
         if constexpr (LK <= 16) {
