@@ -53,6 +53,10 @@ def common_flags() -> list[str]:
         "-fPIC",
         "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # leading scalar kernel arguments arrive in SGPRs at wave launch
+        # (gfx950 kernarg preload), so a kernel's first loads do not wait
+        # for a kernel-argument fetch
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         "-Wall",
         "-Wno-unused-result",
         f"-I{os.path.join(ROOT, 'include')}",

@@ -362,8 +362,16 @@ __device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4
 // FULL = false compiles the plain product (no input transform, plain
 // output with an optional residual, no side copy): the hot decode GEMV keeps
 // the registers and the instruction stream it had before the fused forms.
+//
+// A one-op launch (NS = 1) also receives the weight base, x, the row count
+// and the output kind as leading scalar arguments.  Those are preloaded into
+// SGPRs at wave launch, so the weight and x loads are issued without first
+// waiting for the descriptor's kernel-argument fetch, which then completes
+// under the weight stream.
 template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL>
-__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
+__global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __restrict__ w0,
+                                                           const float* __restrict__ x0, int rows0, int out0,
+                                                           Segs<NS> segs)
 {
     static_assert(NW % KS == 0, "waves must cover whole row groups");
     constexpr int THREADS = 64 * NW;
@@ -385,9 +393,10 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
     __shared__ float red[NW], red2[NW];
 
     const Seg& sg = seg_of(segs);
-    const int b = static_cast<int>(blockIdx.x) - sg.wg0;
-    const int rows = sg.rows;
-    const bool swiglu = FULL && sg.out == OUT_SWIGLU_ROWS;
+    const int b = NS == 1 ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - sg.wg0;
+    const int rows = NS == 1 ? rows0 : sg.rows;
+    const uint8_t* wbase = NS == 1 ? w0 : sg.w;
+    const bool swiglu = FULL && (NS == 1 ? out0 : sg.out) == OUT_SWIGLU_ROWS;
     const int in_kind = FULL ? sg.in : static_cast<int>(XF_PLAIN);
     const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
 
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
     //    complete in issue order, so loading it ahead of the weights lets
     //    it be staged into LDS while the weights are still in flight
     constexpr int XPT = K / 4 / THREADS;
-    const float4* x4 = reinterpret_cast<const float4*>(sg.x);
+    const float4* x4 = reinterpret_cast<const float4*>(NS == 1 ? x0 : sg.x);
     float4 xr[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; j++)
@@ -423,7 +432,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(Segs<NS> segs)
         } else {
             r = min(rb + l, rows - 1);
         }
-        const uint8_t* rp = sg.w + static_cast<int64_t>(r) * ROW_BYTES;
+        const uint8_t* rp = wbase + static_cast<int64_t>(r) * ROW_BYTES;
 #pragma unroll
         for (int i = 0; i < UPL; i++)
             w[i][t].load(rp, unit0 + i * LK);
@@ -852,20 +861,22 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
     // an OUT_SWIGLU_ROWS op puts half as many output rows in a workgroup
     // (its gate and up rows share the tile)
     auto per = [](const GemvOp& op) { return op.out == OUT_SWIGLU_ROWS ? R / 2 : R; };
+    const uint8_t* w0 = static_cast<const uint8_t*>(ops[0].w);
+    const int rows0 = static_cast<int>(ops[0].rows);
     if (n == 1) {
         Segs<1> t;
         const unsigned grid = fill_segs(t, ops, n, per);
         if (is_plain(ops[0]))
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), dim3(grid), dim3(64 * NW), 0,
-                               s, t);
+                               s, w0, ops[0].x, rows0, ops[0].out, t);
         else
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true>), dim3(grid), dim3(64 * NW), 0,
-                               s, t);
+                               s, w0, ops[0].x, rows0, ops[0].out, t);
     } else {
         Segs<MAX_SEGS> t;
         const unsigned grid = fill_segs(t, ops, n, per);
         hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true>), dim3(grid), dim3(64 * NW),
-                           0, s, t);
+                           0, s, w0, ops[0].x, rows0, ops[0].out, t);
     }
     return hipGetLastError();
 }
