@@ -312,8 +312,9 @@ __device__ __forceinline__ const Seg& seg_of(const Segs<NS>& t)
 }
 
 // Output function of one row (OUT_SWIGLU_ROWS is handled by the callers,
-// which hold both halves).
-__device__ __forceinline__ float finish(const Seg& sg, float v, int r)
+// which hold both halves); res is the row's residual, loaded at the start
+// of the kernel when the op has one.
+__device__ __forceinline__ float finish(const Seg& sg, float v, float res, bool has_res)
 {
     switch (sg.out) {
     case OUT_RELU_SQUARE: {
@@ -322,7 +323,7 @@ __device__ __forceinline__ float finish(const Seg& sg, float v, int r)
     }
     case OUT_TANH: return tanhf(v);
     case OUT_SIGMOID: return 1.0f / (1.0f + expf(-v));
-    default: return sg.residual ? v + sg.residual[r] : v;
+    default: return has_res ? v + res : v;
     }
 }
 
@@ -363,15 +364,18 @@ __device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4
 // output with an optional residual, no side copy): the hot decode GEMV keeps
 // the registers and the instruction stream it had before the fused forms.
 //
-// A one-op launch (NS = 1) also receives the weight base, x, the row count
-// and the output kind as leading scalar arguments.  Those are preloaded into
-// SGPRs at wave launch, so the weight and x loads are issued without first
-// waiting for the descriptor's kernel-argument fetch, which then completes
-// under the weight stream.
+// A one-op launch (NS = 1) also receives the weight base, x, the residual,
+// the row count and the output kind as leading scalar arguments.  Those are
+// preloaded into SGPRs at wave launch, so the weight and x loads are issued
+// without first waiting for the descriptor's kernel-argument fetch, which
+// then completes under the weight stream.  The residual (which may alias y)
+// of the rows a thread stores is loaded before the weights: a lane's loads
+// complete in issue order, so a load issued after them would add a memory
+// round trip to the end of the kernel.
 template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL>
 __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __restrict__ w0,
-                                                           const float* __restrict__ x0, int rows0, int out0,
-                                                           Segs<NS> segs)
+                                                           const float* __restrict__ x0, const float* res0,
+                                                           int rows0, int out0, Segs<NS> segs)
 {
     static_assert(NW % KS == 0, "waves must cover whole row groups");
     constexpr int THREADS = 64 * NW;
@@ -385,7 +389,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     constexpr int UPR = UPS * KS;                 // units per row
     constexpr int K = UPR * 64;
     constexpr int64_t ROW_BYTES = static_cast<int64_t>(UPR) * QUnit<FMT>::UNIT_BYTES;
-    static_assert((K / 4) % THREADS == 0, "x staging assumes whole float4 rounds");
+    static_assert(K % 32 == 0 && THREADS % 8 == 0, "x staging keeps 8-thread groups whole");
 
     __shared__ float4 xs4[UPR * XS_UNIT / 4];
     __shared__ float bs[UPR * 2];
@@ -401,7 +405,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: index math stays scalar
     const int slice = wave % KS;
     const int group = wave / KS;
     const int lk = lane % LK;
@@ -412,12 +416,39 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     // 1. x first: it is small and mostly an L2 hit, and a lane's loads
     //    complete in issue order, so loading it ahead of the weights lets
     //    it be staged into LDS while the weights are still in flight
-    constexpr int XPT = K / 4 / THREADS;
+    //    x is staged in XPT rounds of THREADS float4 values; only the last
+    //    round can be partial, and an aligned group of 8 threads (32
+    //    columns) is either wholly inside x or wholly past its end
+    constexpr int XPT = (K / 4 + THREADS - 1) / THREADS;
+    auto xin = [](int j) { return (K / 4) % THREADS == 0 || j < XPT - 1 || threadIdx.x + j * THREADS < K / 4; };
     const float4* x4 = reinterpret_cast<const float4*>(NS == 1 ? x0 : sg.x);
     float4 xr[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; j++)
-        xr[j] = x4[threadIdx.x + j * THREADS];
+        xr[j] = xin(j) ? x4[threadIdx.x + j * THREADS] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    // residual of the rows this thread stores (step 5 below)
+    const float* resid = NS == 1 ? res0 : sg.residual;
+    const bool has_res = resid != nullptr && !swiglu;
+    constexpr bool LANE_STORES = KS == 1;     // else thread t stores row rb + t
+    float rres[RL];
+#pragma unroll
+    for (int t = 0; t < RL; t++)
+        rres[t] = 0.0f;
+    if (has_res) {
+        if (LANE_STORES) {
+            if (lk == 0) {
+#pragma unroll
+                for (int t = 0; t < RL; t++) {
+                    const int r = rb + local_row0 + t;
+                    if (r < rows)
+                        rres[t] = resid[r];
+                }
+            }
+        } else if (threadIdx.x < ROWS_PER_WG && rb + static_cast<int>(threadIdx.x) < rows) {
+            rres[0] = resid[rb + threadIdx.x];
+        }
+    }
 
     // 2. issue every weight load of this lane (rows past the end are
     //    clamped into the matrix; their results are dropped)
@@ -445,7 +476,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
-            const float4 u = x4[K / 4 + threadIdx.x + j * THREADS];
+            const float4 u = xin(j) ? x4[K / 4 + threadIdx.x + j * THREADS] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             xr[j].x = silu_mul(xr[j].x, u.x);
             xr[j].y = silu_mul(xr[j].y, u.y);
             xr[j].z = silu_mul(xr[j].z, u.z);
@@ -462,6 +493,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         const float4* g4 = reinterpret_cast<const float4*>(sg.nw);
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
+            if (!xin(j))
+                continue;
             const float4 g = g4[threadIdx.x + j * THREADS];
             xr[j].x = xr[j].x * scale * g.x;
             xr[j].y = xr[j].y * scale * g.y;
@@ -479,6 +512,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         float s2 = 0.0f;
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
+            if (!xin(j))
+                continue;   // stays zero
             xr[j] = f4_sub(xr[j], mean);
             s2 += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
         }
@@ -492,6 +527,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         const float4* p4 = reinterpret_cast<const float4*>(sg.prev);
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
+            if (!xin(j))
+                continue;
             const int i = threadIdx.x + j * THREADS;
             const float4 g = g4[i], bb = b4[i];
             float4 v;
@@ -514,26 +551,27 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
 #pragma unroll
     for (int j = 0; j < XPT; j++) {
         const int col = 4 * (threadIdx.x + j * THREADS);
-        xs4[(col >> 6) * (XS_UNIT / 4) + ((col & 63) >> 2)] = xr[j];
+        if (xin(j))
+            xs4[(col >> 6) * (XS_UNIT / 4) + ((col & 63) >> 2)] = xr[j];
     }
-    constexpr bool SUMS = FMT != FMT_Q8_0;   // the factored Q4 forms need sum(x) per 32 columns
-    int any_wide = 0;
+    // The factored Q4 forms need sum(x) per 32 columns.  A block holding a
+    // non-finite or huge (|x| > 2^100) value stores NaN instead (NaN fails
+    // every comparison, so it counts as wide too): its products then take
+    // the per-weight form, which keeps each product's IEEE class.
+    constexpr bool SUMS = FMT != FMT_Q8_0;
     if constexpr (SUMS) {
-        bool wide = false;
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             const int i = threadIdx.x + j * THREADS;
-            // NaN fails every comparison, so it counts as wide too
-            wide |= !(fabsf(xr[j].x) <= 0x1p100f && fabsf(xr[j].y) <= 0x1p100f &&
-                      fabsf(xr[j].z) <= 0x1p100f && fabsf(xr[j].w) <= 0x1p100f);
-            const float sum = group_sum<8>((xr[j].x + xr[j].y) + (xr[j].z + xr[j].w));
-            if ((i & 7) == 0)
+            const bool wide = !(fabsf(xr[j].x) <= 0x1p100f && fabsf(xr[j].y) <= 0x1p100f &&
+                                fabsf(xr[j].z) <= 0x1p100f && fabsf(xr[j].w) <= 0x1p100f);
+            const float v = wide ? __builtin_nanf("") : (xr[j].x + xr[j].y) + (xr[j].z + xr[j].w);
+            const float sum = group_sum<8>(v);
+            if ((i & 7) == 0 && xin(j))
                 bs[i >> 3] = sum;
         }
-        any_wide = __syncthreads_or(wide);
-    } else {
-        __syncthreads();
     }
+    __syncthreads();
 
     // 4. per-unit dot products, x read once per unit and reused for RL rows
     float acc[RL];
@@ -552,13 +590,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
                 xv[k] = src[k];
             if constexpr (SUMS) {
                 const float sx = bs[2 * u + h];
-                if (any_wide) {
-                    for (int t = 0; t < RL; t++)
-                        acc[t] += w[i][t].half_exact(h, xv);
-                } else {
+                if (__builtin_expect(sx == sx, 1)) {
 #pragma unroll
                     for (int t = 0; t < RL; t++)
                         acc[t] += w[i][t].half(h, xv, sx);
+                } else {
+                    for (int t = 0; t < RL; t++)
+                        acc[t] += w[i][t].half_exact(h, xv);
                 }
             } else {
 #pragma unroll
@@ -585,7 +623,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             for (int t = 0; t < RL; t++) {
                 const int r = rb + local_row0 + t;
                 if (r < rows)
-                    sg.y[r] = FULL ? finish(sg, acc[t], r) : (sg.residual ? acc[t] + sg.residual[r] : acc[t]);
+                    sg.y[r] = FULL ? finish(sg, acc[t], rres[t], has_res) : (has_res ? acc[t] + rres[t] : acc[t]);
             }
         }
     } else {
@@ -610,7 +648,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
                 if (r < rows)
                     sg.y[r] = silu_mul(v, u);
             } else if (r < rows) {
-                sg.y[r] = FULL ? finish(sg, v, r) : (sg.residual ? v + sg.residual[r] : v);
+                sg.y[r] = FULL ? finish(sg, v, rres[0], has_res) : (has_res ? v + rres[0] : v);
             }
         }
     }
@@ -705,7 +743,7 @@ __global__ __launch_bounds__(WG) void gemv_generic_kernel(Segs<NS> segs)
         if (lane == 0)
             sg.y[row] = silu_mul(acc, u);
     } else if (lane == 0) {
-        sg.y[row] = finish(sg, acc, row);
+        sg.y[row] = finish(sg, acc, sg.residual ? sg.residual[row] : 0.0f, sg.residual != nullptr);
     }
 }
 
@@ -752,7 +790,7 @@ __global__ __launch_bounds__(WG) void gemv_short_kernel(Segs<NS> segs)
             v += part[0][threadIdx.x + k];
             u += part[1][threadIdx.x + k];
         }
-        sg.y[row] = swiglu ? silu_mul(v, u) : finish(sg, v, row);
+        sg.y[row] = swiglu ? silu_mul(v, u) : finish(sg, v, sg.residual ? sg.residual[row] : 0.0f, sg.residual != nullptr);
     }
 }
 
@@ -868,15 +906,15 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
         const unsigned grid = fill_segs(t, ops, n, per);
         if (is_plain(ops[0]))
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), dim3(grid), dim3(64 * NW), 0,
-                               s, w0, ops[0].x, rows0, ops[0].out, t);
+                               s, w0, ops[0].x, ops[0].residual, rows0, ops[0].out, t);
         else
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true>), dim3(grid), dim3(64 * NW), 0,
-                               s, w0, ops[0].x, rows0, ops[0].out, t);
+                               s, w0, ops[0].x, ops[0].residual, rows0, ops[0].out, t);
     } else {
         Segs<MAX_SEGS> t;
         const unsigned grid = fill_segs(t, ops, n, per);
         hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true>), dim3(grid), dim3(64 * NW),
-                           0, s, w0, ops[0].x, rows0, ops[0].out, t);
+                           0, s, w0, ops[0].x, ops[0].residual, rows0, ops[0].out, t);
     }
     return hipGetLastError();
 }
@@ -898,9 +936,17 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     case 2048: return mid    ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s)
                     : rows64 >= 8192 ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s)
                                      : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
-    case 3072: return tall ? launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s)
-                    : mid  ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s)
-                           : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+    case 3072:
+        if (tall)
+            return launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s);
+        if constexpr (FMT == FMT_Q8_0)
+            return mid ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+        // Q4 formats: wide workgroups (one per CU at 3072 and 5120 rows)
+        // stage x once per CU instead of once per 4 rows
+        return mid              ? launch_tiled<FMT, 16, 3, 1, 1, 8>(ops, n, s)
+               : rows64 >= 5120 ? launch_tiled<FMT, 16, 1, 1, 3, 15>(ops, n, s)
+               : rows64 >= 3072 ? launch_tiled<FMT, 16, 1, 1, 3, 9>(ops, n, s)
+                                : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
     case 4096: return mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
     case 6144: return mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
     case 8192: return mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
