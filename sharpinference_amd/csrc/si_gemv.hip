@@ -333,7 +333,12 @@ __device__ __forceinline__ float silu_mul(float g, float u)
 }
 
 // The op's first workgroup copies copy_n floats (a state store that must
-// happen after every reader of the destination has run).
+// happen after every reader of the destination has run).  The first
+// SIDE_HELD * threads values are loaded at the start of the kernel, ahead
+// of the weights, and stored at its end; the rest (if any) at the end.
+constexpr int SIDE_HELD = 8;
+
+// The whole copy in one pass (kernels whose weight stream is short).
 __device__ __forceinline__ void side_copy(const Seg& sg, int b, int threads)
 {
     if (sg.copy_n > 0 && b == 0)
@@ -365,17 +370,24 @@ __device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4
 // the registers and the instruction stream it had before the fused forms.
 //
 // A one-op launch (NS = 1) also receives the weight base, x, the residual,
-// the row count and the output kind as leading scalar arguments.  Those are
-// preloaded into SGPRs at wave launch, so the weight and x loads are issued
-// without first waiting for the descriptor's kernel-argument fetch, which
-// then completes under the weight stream.  The residual (which may alias y)
-// of the rows a thread stores is loaded before the weights: a lane's loads
-// complete in issue order, so a load issued after them would add a memory
-// round trip to the end of the kernel.
-template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL>
+// the norm weight, the row count, the output kind, the input transform and
+// the side-copy length as leading scalar arguments.  Those are preloaded into SGPRs at wave
+// launch, so the weight and x loads are issued without first waiting for
+// the descriptor's kernel-argument fetch, which then completes under the
+// weight stream.  A lane's loads complete in issue order, so everything
+// the kernel needs before its products (x, the transform's vectors) and
+// the residual of the rows a thread stores (which may alias y) are loaded
+// before the weights: loaded after them, they would wait for the whole
+// weight stream and the x staging and products could not overlap it.
+//
+// NV is the number of transform vectors the fused form loads per x value: 1
+// (SwiGLU's up half or the RMSNorm weight; none needed loads x again) or 4
+// (LayerNorm weight and bias, token-mix and previous-token vectors).
+template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL, int NV = 1>
 __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __restrict__ w0,
                                                            const float* __restrict__ x0, const float* res0,
-                                                           int rows0, int out0, Segs<NS> segs)
+                                                           const float* __restrict__ nw0, int rows0, int out0,
+                                                           int in0, int copy0, Segs<NS> segs)
 {
     static_assert(NW % KS == 0, "waves must cover whole row groups");
     constexpr int THREADS = 64 * NW;
@@ -401,7 +413,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     const int rows = NS == 1 ? rows0 : sg.rows;
     const uint8_t* wbase = NS == 1 ? w0 : sg.w;
     const bool swiglu = FULL && (NS == 1 ? out0 : sg.out) == OUT_SWIGLU_ROWS;
-    const int in_kind = FULL ? sg.in : static_cast<int>(XF_PLAIN);
+    const int in_kind = FULL ? (NS == 1 ? in0 : sg.in) : static_cast<int>(XF_PLAIN);
     const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
 
     const int lane = threadIdx.x & 63;
@@ -420,12 +432,52 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     //    round can be partial, and an aligned group of 8 threads (32
     //    columns) is either wholly inside x or wholly past its end
     constexpr int XPT = (K / 4 + THREADS - 1) / THREADS;
+    //    (loads are unconditional, their index clamped into x, so that no
+    //    value has to be merged before the weight loads are issued; the
+    //    threads past the end zero their values when staging)
     auto xin = [](int j) { return (K / 4) % THREADS == 0 || j < XPT - 1 || threadIdx.x + j * THREADS < K / 4; };
+    auto xidx = [](int j) { return min(static_cast<int>(threadIdx.x) + j * THREADS, K / 4 - 1); };
     const float4* x4 = reinterpret_cast<const float4*>(NS == 1 ? x0 : sg.x);
     float4 xr[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; j++)
-        xr[j] = xin(j) ? x4[threadIdx.x + j * THREADS] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xr[j] = x4[xidx(j)];
+
+    // the input transform's vectors (step 3): SwiGLU's up half, the norm
+    // weight, LayerNorm's bias, mix and previous-token vectors
+    //    (pointers chosen per launch; a vector the transform does not use
+    //    reads x again)
+    float4 ta[XPT], tb[XPT], tc[XPT], td[XPT];
+    if constexpr (FULL) {
+        const bool ln = in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX;
+        const bool mix = in_kind == XF_LAYERNORM_MIX;
+        const float* nw = NS == 1 ? nw0 : sg.nw;
+        const float4* pa = reinterpret_cast<const float4*>(
+            in_kind == XF_SWIGLU ? (NS == 1 ? x0 : sg.x) + K : (in_kind == XF_RMSNORM || ln) ? nw : (NS == 1 ? x0 : sg.x));
+#pragma unroll
+        for (int j = 0; j < XPT; j++)
+            ta[j] = pa[xidx(j)];
+        if constexpr (NV == 4) {
+            const float4* pb = ln ? reinterpret_cast<const float4*>(sg.nb) : x4;
+            const float4* pc = mix ? reinterpret_cast<const float4*>(sg.mix) : x4;
+            const float4* pd = mix ? reinterpret_cast<const float4*>(sg.prev) : x4;
+#pragma unroll
+            for (int j = 0; j < XPT; j++) {
+                tb[j] = pb[xidx(j)];
+                tc[j] = pc[xidx(j)];
+                td[j] = pd[xidx(j)];
+            }
+        }
+    }
+
+    // the side copy's values (stored after the products)
+    float cpv[SIDE_HELD];
+    const bool copying = FULL && b == 0 && (NS == 1 ? copy0 : sg.copy_n) > 0;
+    if (copying) {
+#pragma unroll
+        for (int k = 0; k < SIDE_HELD; k++)
+            cpv[k] = sg.copy_src[min(static_cast<int>(threadIdx.x) + k * THREADS, sg.copy_n - 1)];
+    }
 
     // residual of the rows this thread stores (step 5 below)
     const float* resid = NS == 1 ? res0 : sg.residual;
@@ -468,15 +520,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         for (int i = 0; i < UPL; i++)
             w[i][t].load(rp, unit0 + i * LK);
     }
-    if constexpr (FULL)
-        side_copy(sg, b, THREADS);
-
     // 3. stage x into LDS (padded per unit), with its transform
+#pragma unroll
+    for (int j = 0; j < XPT; j++)
+        if (!xin(j))
+            xr[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (in_kind == XF_SWIGLU) {
         // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
-            const float4 u = xin(j) ? x4[K / 4 + threadIdx.x + j * THREADS] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 u = ta[j];
             xr[j].x = silu_mul(xr[j].x, u.x);
             xr[j].y = silu_mul(xr[j].y, u.y);
             xr[j].z = silu_mul(xr[j].z, u.z);
@@ -490,18 +543,17 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             ss += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
         const float total = block_sum<NW>(ss, red);
         const float scale = 1.0f / sqrtf(total / static_cast<float>(K) + sg.eps);
-        const float4* g4 = reinterpret_cast<const float4*>(sg.nw);
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             if (!xin(j))
                 continue;
-            const float4 g = g4[threadIdx.x + j * THREADS];
+            const float4 g = ta[j];
             xr[j].x = xr[j].x * scale * g.x;
             xr[j].y = xr[j].y * scale * g.y;
             xr[j].z = xr[j].z * scale * g.z;
             xr[j].w = xr[j].w * scale * g.w;
         }
-    } else if (in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX) {
+    } else if (NV == 4 && (in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX)) {
         // mean = sum(x) / K; c = x - mean; var = sum(c^2) / K;
         // ln = (c * (1 / sqrt(var + eps))) * weight + bias
         float s1 = 0.0f;
@@ -519,18 +571,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         }
         const float var = block_sum<NW>(s2, red2) / static_cast<float>(K);
         const float inv = 1.0f / sqrtf(var + sg.eps);
-        const float4* g4 = reinterpret_cast<const float4*>(sg.nw);
-        const float4* b4 = reinterpret_cast<const float4*>(sg.nb);
         const bool store = sg.norm_out != nullptr && b == 0;
         const bool mixing = in_kind == XF_LAYERNORM_MIX;
-        const float4* m4 = reinterpret_cast<const float4*>(sg.mix);
-        const float4* p4 = reinterpret_cast<const float4*>(sg.prev);
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             if (!xin(j))
                 continue;
             const int i = threadIdx.x + j * THREADS;
-            const float4 g = g4[i], bb = b4[i];
+            const float4 g = ta[j], bb = tb[j];
             float4 v;
             v.x = xr[j].x * inv * g.x + bb.x;
             v.y = xr[j].y * inv * g.y + bb.y;
@@ -539,7 +587,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             if (store)
                 reinterpret_cast<float4*>(sg.norm_out)[i] = v;
             if (mixing) {
-                const float4 m = m4[i], p = p4[i];
+                const float4 m = tc[j], p = td[j];
                 v.x = v.x + (p.x - v.x) * m.x;
                 v.y = v.y + (p.y - v.y) * m.y;
                 v.z = v.z + (p.z - v.z) * m.z;
@@ -651,6 +699,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
                 sg.y[r] = FULL ? finish(sg, v, rres[0], has_res) : (has_res ? v + rres[0] : v);
             }
         }
+    }
+    if (copying) {
+#pragma unroll
+        for (int k = 0; k < SIDE_HELD; k++) {
+            const int i = threadIdx.x + k * THREADS;
+            if (i < sg.copy_n)
+                sg.copy_dst[i] = cpv[k];
+        }
+        for (int i = threadIdx.x + SIDE_HELD * THREADS; i < sg.copy_n; i += THREADS)
+            sg.copy_dst[i] = sg.copy_src[i];
     }
 }
 
@@ -901,20 +959,32 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
     auto per = [](const GemvOp& op) { return op.out == OUT_SWIGLU_ROWS ? R / 2 : R; };
     const uint8_t* w0 = static_cast<const uint8_t*>(ops[0].w);
     const int rows0 = static_cast<int>(ops[0].rows);
+    // a LayerNorm input transform loads four vectors per x value
+    bool ln = false;
+    for (int i = 0; i < n; i++)
+        ln |= ops[i].in == XF_LAYERNORM || ops[i].in == XF_LAYERNORM_MIX;
+    const GemvOp& o = ops[0];
     if (n == 1) {
         Segs<1> t;
         const unsigned grid = fill_segs(t, ops, n, per);
-        if (is_plain(ops[0]))
+        if (is_plain(o))
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), dim3(grid), dim3(64 * NW), 0,
-                               s, w0, ops[0].x, ops[0].residual, rows0, ops[0].out, t);
+                               s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
+        else if (ln)
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 4>), dim3(grid), dim3(64 * NW), 0,
+                               s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true>), dim3(grid), dim3(64 * NW), 0,
-                               s, w0, ops[0].x, ops[0].residual, rows0, ops[0].out, t);
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 1>), dim3(grid), dim3(64 * NW), 0,
+                               s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     } else {
         Segs<MAX_SEGS> t;
         const unsigned grid = fill_segs(t, ops, n, per);
-        hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true>), dim3(grid), dim3(64 * NW),
-                           0, s, w0, ops[0].x, ops[0].residual, rows0, ops[0].out, t);
+        if (ln)
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4>), dim3(grid),
+                               dim3(64 * NW), 0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
+        else
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 1>), dim3(grid),
+                               dim3(64 * NW), 0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     }
     return hipGetLastError();
 }
@@ -949,7 +1019,12 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
                                 : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
     case 4096: return mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
     case 6144: return mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
-    case 8192: return mid ? launch_tiled<FMT, 16, 4, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
+    case 8192:
+        if (mid)
+            return launch_tiled<FMT, 16, 4, 2, 2, 4>(ops, n, s);
+        if constexpr (FMT == FMT_Q4_K)   // 12 rows per workgroup, 256 workgroups at 3072 rows
+            return launch_tiled<FMT, 16, 2, 1, 4, 12>(ops, n, s);
+        return launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
     default: return hipErrorNotSupported;
     }
 }
