@@ -426,6 +426,257 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(Attentio
     }
 }
 
+// Swaps between the halves (32 lanes) and the row pairs (16 lanes) of a
+// wave: after both steps every lane holds the combination of the four lanes
+// l, l ^ 16, l ^ 32, l ^ 48 (its column of the wave's four rows).
+__device__ __forceinline__ float rows_sum(float v)
+{
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float rows_max(float v)
+{
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ void load8(const float* p, float* f)
+{
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+// Rotate-half of a thread's 8-value slice dg of one head row (rotary width
+// R, a multiple of 16 so that a slice and its partner slice are whole):
+// for i < R/2, h[i] = h[i] c_i - h[i + R/2] s_i; for R/2 <= i < R,
+// h[i] = h[i] c_{i-R/2} + h[i - R/2] s_{i-R/2}; other values unchanged.
+// `own` holds the slice, `partner` the slice R/2 away, cs / sn the table
+// values of the pair.
+__device__ __forceinline__ void rotate8(float* own, const float* partner, const float* cs, const float* sn, int dg,
+                                        int rotary)
+{
+    const int i0 = 8 * dg;
+    if (i0 < rotary / 2) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            own[e] = own[e] * cs[e] - partner[e] * sn[e];
+    } else if (i0 < rotary) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            own[e] = own[e] * cs[e] + partner[e] * sn[e];
+    }
+}
+
+// One workgroup = one KV head x one chunk of 64 cache positions, the same
+// function as attention_partial_kernel with every intermediate kept in
+// registers.  Thread (wave w, lane l) takes the 8-value slice dg = l % 16
+// of positions w * 16 + l / 16 + 4 j (j < 4) for both the scores and the
+// values, so its softmax weights never leave its registers: each wave keeps
+// its own running maximum and sum, sums across its four rows with lane
+// swaps, and the four waves merge (with rescaling) through LDS at one
+// barrier.  The queries, the new K / V rows and their rotary partners are
+// read straight from the step's qkv vector and rotated in registers; the
+// 16 lanes holding the new token's position round it to fp16 and append it.
+// The pointers a wave needs first arrive as preloaded scalar arguments.
+template <int GROUP>
+__global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const float* __restrict__ qkv,
+                                                                      const int32_t* __restrict__ position,
+                                                                      __half* k_cache, __half* v_cache,
+                                                                      float* __restrict__ workspace, int capacity,
+                                                                      int rotary)
+{
+    const int g = blockIdx.x;                 // KV head
+    const int kv_heads = gridDim.x, max_chunks = gridDim.y;
+    const int heads = GROUP * kv_heads;
+    const int chunk = blockIdx.y;
+    const int start = chunk * CHUNK;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int dg = lane & 15, row = lane >> 4;
+    const int half = rotary / 2;
+    const bool rot = 8 * dg < rotary;
+    // the partner slice of a rotated slice (any valid slice otherwise)
+    const int pdg = !rot ? dg : (8 * dg < half ? dg + half / 8 : dg - half / 8);
+    const int tdg = 8 * dg < half ? dg : (rot ? dg - half / 8 : 0);   // table slice of the pair
+
+    // 1. position-independent inputs: queries, new K / V slices, rotary table
+    const float* qg = qkv + static_cast<int64_t>(g) * GROUP * HEAD_DIM;
+    const float* kn_row = qkv + static_cast<int64_t>(heads) * HEAD_DIM + g * HEAD_DIM;
+    const float* vn_row = kn_row + static_cast<int64_t>(kv_heads) * HEAD_DIM;
+    const float* rope = workspace + att_rope(heads, max_chunks);
+    float q[GROUP][8], qp[GROUP][8], kn[8], knp[8], vn[8], cs[8], sn[8];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        load8(qg + h * HEAD_DIM + 8 * dg, q[h]);
+        load8(qg + h * HEAD_DIM + 8 * pdg, qp[h]);
+    }
+    load8(kn_row + 8 * dg, kn);
+    load8(kn_row + 8 * pdg, knp);
+    load8(vn_row + 8 * dg, vn);
+    load8(rope + 8 * tdg, cs);
+    load8(rope + 64 + 8 * tdg, sn);
+
+    // A chunk past the position (or a position outside the cache) loads no
+    // cache rows and stores nothing, but runs the same straight-line code:
+    // with an early return the compiler would move the loads above (used
+    // only on the valid path) behind the position's round trip.
+    const int P = *position;                  // index of the new token
+    const bool valid = P >= 0 && P < capacity && start <= P;
+    const int count = min(CHUNK, P + 1 - start);
+    const int newp = valid ? P - start : CHUNK;   // the new token's slot in this chunk (< CHUNK when owned)
+
+    // 2. K and V rows of this thread's positions (rows clamped into the
+    //    cache; positions past the count are masked below)
+    __half* kc = k_cache + static_cast<int64_t>(g) * capacity * HEAD_DIM;
+    __half* vc = v_cache + static_cast<int64_t>(g) * capacity * HEAD_DIM;
+    //    (an invalid chunk leaves them unloaded: its results are not stored)
+    uint4 kr[4], vr[4];
+    if (valid) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t r = min(start + wave * 16 + row + 4 * j, capacity - 1);
+            kr[j] = *reinterpret_cast<const uint4*>(kc + r * HEAD_DIM + 8 * dg);
+            vr[j] = *reinterpret_cast<const uint4*>(vc + r * HEAD_DIM + 8 * dg);
+        }
+    }
+
+    // 3. rotate the queries and the new key; the new row in fp16
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+        rotate8(q[h], qp[h], cs, sn, dg, rotary);
+    rotate8(kn, knp, cs, sn, dg, rotary);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        kn[e] = __half2float(__float2half_rn(kn[e]));
+        vn[e] = __half2float(__float2half_rn(vn[e]));
+    }
+
+    // 4. scores of the thread's four positions (a 16-lane row holds one
+    //    position), masked past the count
+    const float inv_scale = sqrtf(static_cast<float>(HEAD_DIM));
+    float sc[GROUP][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int p = wave * 16 + row + 4 * j;
+        float k8[8];
+        if (p == newp) {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                k8[e] = kn[e];
+        } else {
+            unpack8(kr[j], k8);
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            float sdot = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                sdot = fmaf(q[h][e], k8[e], sdot);
+            sdot = row_sum<16>(sdot);
+            sc[h][j] = p < count ? sdot / inv_scale : -INFINITY;
+        }
+    }
+
+    // 5. the wave's maximum and exponentials per head; weighted values
+    float m[GROUP], l[GROUP], acc[GROUP][8];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        float mh = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+        mh = rows_max(mh);
+        m[h] = mh;
+        float lh = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float e = sc[h][j] == -INFINITY ? 0.0f : expf(sc[h][j] - mh);
+            sc[h][j] = e;
+            lh += e;
+        }
+        l[h] = lh;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            acc[h][e] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int p = wave * 16 + row + 4 * j;
+        float v8[8];
+        if (p == newp) {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                v8[e] = vn[e];
+        } else {
+            unpack8(p < count ? vr[j] : make_uint4(0, 0, 0, 0), v8);   // rows past the count may hold anything
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                acc[h][e] = fmaf(sc[h][j], v8[e], acc[h][e]);
+    }
+
+    // the owner's 16 lanes append the new row (positions of a lane are
+    // wave * 16 + row + 4 j, so the new one is in row newp % 4 of wave newp / 16)
+    if (newp < CHUNK && (newp >> 4) == wave && (newp & 3) == row) {   // newp < CHUNK only when valid
+        __half kh[8], vh[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kh[e] = __float2half_rn(kn[e]);
+            vh[e] = __float2half_rn(vn[e]);
+        }
+        *reinterpret_cast<uint4*>(kc + static_cast<int64_t>(P) * HEAD_DIM + 8 * dg) = *reinterpret_cast<const uint4*>(kh);
+        *reinterpret_cast<uint4*>(vc + static_cast<int64_t>(P) * HEAD_DIM + 8 * dg) = *reinterpret_cast<const uint4*>(vh);
+    }
+
+    // 6. sums over the wave's four rows, then the four waves through LDS
+    __shared__ float red[4][GROUP][HEAD_DIM];
+    __shared__ float wm[4][GROUP], wl[4][GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        l[h] = rows_sum(l[h]);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            acc[h][e] = rows_sum(acc[h][e]);
+    }
+    if (row == 0) {
+#pragma unroll
+        for (int h = 0; h < GROUP; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                red[wave][h][8 * dg + e] = acc[h][e];
+        if (dg == 0)
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) {
+                wm[wave][h] = m[h];
+                wl[wave][h] = l[h];
+            }
+    }
+    __syncthreads();
+    if (!valid)
+        return;
+    for (int i = t; i < GROUP * HEAD_DIM; i += ATT_THREADS) {
+        const int h = i / HEAD_DIM, d = i % HEAD_DIM;
+        const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+        float o = 0.0f, lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = wm[w][h] == -INFINITY ? 0.0f : expf(wm[w][h] - M);   // a wave without valid positions adds nothing
+            o = fmaf(red[w][h][d], f, o);
+            lsum = fmaf(wl[w][h], f, lsum);
+        }
+        float* dst = workspace + (static_cast<int64_t>(g * GROUP + h) * max_chunks + chunk) * PART;
+        dst[2 + d] = o;
+        if (d == 0) {
+            dst[0] = M;
+            dst[1] = lsum;
+        }
+    }
+}
+
 // ---- argmax ----------------------------------------------------------------------------
 
 constexpr int AM_BLOCKS = 256;
@@ -521,6 +772,27 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
     }
     const int group = a.heads / a.kv_heads;
     const dim3 grid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>(a.max_chunks));
+    if (a.rotary_dim % 16 == 0) {
+        // slices of 8 values and their rotary partners are whole
+        switch (group) {
+#define SI_CHUNK(G)                                                                                               \
+    case G:                                                                                                       \
+        hipLaunchKernelGGL((attention_chunk_kernel<G>), grid, dim3(ATT_THREADS), 0, s, a.qkv, a.position,         \
+                           a.k_cache, a.v_cache, a.workspace, a.capacity, a.rotary_dim);                         \
+        break;
+        SI_CHUNK(1)
+        SI_CHUNK(2)
+        SI_CHUNK(3)
+        SI_CHUNK(4)
+#undef SI_CHUNK
+        default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return e;
+        hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     switch (group) {
     case 1: hipLaunchKernelGGL((attention_partial_kernel<1>), grid, dim3(ATT_THREADS), 0, s, a); break;
     case 2: hipLaunchKernelGGL((attention_partial_kernel<2>), grid, dim3(ATT_THREADS), 0, s, a); break;

@@ -45,6 +45,10 @@ __device__ __forceinline__ float half_hi(uint32_t v)
     return __half2float(__ushort_as_half(static_cast<unsigned short>(v >> 16)));
 }
 
+// Sum of v over the wave, in every lane: DPP inside each 16-lane row, then
+// swaps between the halves and between row pairs.
+__device__ __forceinline__ float wave_sum(float v);
+
 // 4 signed bytes of q times 4 floats, accumulated.
 __device__ __forceinline__ float dot4_i8(uint32_t q, const float4& x, float a)
 {
@@ -81,6 +85,15 @@ __device__ __forceinline__ float group_sum(float v)
         v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
     static_assert(N <= 16, "groups wider than a DPP row use shuffles");
     return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = group_sum<16>(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // 4 unsigned bytes (each < 256) of q times 4 floats, accumulated.
@@ -536,23 +549,24 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             xr[j].w = silu_mul(xr[j].w, u.w);
         }
     } else if (in_kind == XF_RMSNORM) {
-        // scale = 1 / sqrt(sum(x^2) / K + eps); x_i * scale * weight_i
+        // scale = 1 / sqrt(sum(x^2) / K + eps) is common to every x_i * weight_i,
+        // so x * weight is staged now and the scale multiplies each row's
+        // sum at the end: sum_k W_k (x_k * scale * g_k) = scale * sum_k W_k (x_k * g_k),
+        // equal up to FP32 rounding.  The per-wave sums of x^2 go through
+        // LDS at the staging barrier below.
         float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < XPT; j++)
-            ss += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
-        const float total = block_sum<NW>(ss, red);
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(K) + sg.eps);
-#pragma unroll
         for (int j = 0; j < XPT; j++) {
-            if (!xin(j))
-                continue;
+            ss += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
             const float4 g = ta[j];
-            xr[j].x = xr[j].x * scale * g.x;
-            xr[j].y = xr[j].y * scale * g.y;
-            xr[j].z = xr[j].z * scale * g.z;
-            xr[j].w = xr[j].w * scale * g.w;
+            xr[j].x = xr[j].x * g.x;
+            xr[j].y = xr[j].y * g.y;
+            xr[j].z = xr[j].z * g.z;
+            xr[j].w = xr[j].w * g.w;
         }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0)
+            red[wave] = ss;
     } else if (NV == 4 && (in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX)) {
         // mean = sum(x) / K; c = x - mean; var = sum(c^2) / K;
         // ln = (c * (1 / sqrt(var + eps))) * weight + bias
@@ -622,6 +636,17 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     __syncthreads();
 
     // 4. per-unit dot products, x read once per unit and reused for RL rows
+    // the RMSNorm scale, applied to each row's sum by the threads that
+    // store rows (and computed only there)
+    auto out_scale = [&]() {
+        if (!FULL || in_kind != XF_RMSNORM)
+            return 1.0f;
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; i++)
+            total += red[i];
+        return 1.0f / sqrtf(total / static_cast<float>(K) + sg.eps);
+    };
     float acc[RL];
 #pragma unroll
     for (int t = 0; t < RL; t++)
@@ -667,11 +692,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     }
     if (KS == 1 && !swiglu) {
         if (lk == 0) {
+            const float sc = out_scale();
 #pragma unroll
             for (int t = 0; t < RL; t++) {
                 const int r = rb + local_row0 + t;
                 if (r < rows)
-                    sg.y[r] = FULL ? finish(sg, acc[t], rres[t], has_res) : (has_res ? acc[t] + rres[t] : acc[t]);
+                    sg.y[r] = FULL ? finish(sg, acc[t] * sc, rres[t], has_res) : (has_res ? acc[t] + rres[t] : acc[t]);
             }
         }
     } else {
@@ -683,16 +709,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         __syncthreads();
         const int t = threadIdx.x;
         if (t < (swiglu ? HALF : ROWS_PER_WG)) {
+            const float sc = out_scale();
             float v = part[t * KS];
 #pragma unroll
             for (int s2 = 1; s2 < KS; s2++)
                 v += part[t * KS + s2];
+            v *= sc;
             const int r = rb + t;
             if (swiglu) {
                 float u = part[(t + HALF) * KS];
 #pragma unroll
                 for (int s2 = 1; s2 < KS; s2++)
                     u += part[(t + HALF) * KS + s2];
+                u *= sc;
                 if (r < rows)
                     sg.y[r] = silu_mul(v, u);
             } else if (r < rows) {

@@ -93,7 +93,7 @@ def test_fused_transform_rejects_untiled_shapes(hip):
         b.free()
 
 
-def _attention_case(hip, heads, kv_heads, capacity, position, seed):
+def _attention_case(hip, heads, kv_heads, capacity, position, seed, rotary=96):
     d = 128
     rng = np.random.default_rng(seed)
     qkv = rng.standard_normal(heads * d + 2 * kv_heads * d).astype(np.float32)
@@ -106,15 +106,15 @@ def _attention_case(hip, heads, kv_heads, capacity, position, seed):
     dout = hip.alloc(heads * d * 4)
     dpos = hip.to_device(np.array([position], np.int32))
     ws = hip.alloc(native.attention_workspace_bytes(heads, capacity))
-    args = native.AttentionArgs(dq.ptr, dpos.ptr, dk.ptr, dv.ptr, dout.ptr, ws.ptr, heads, kv_heads, d, 96,
+    args = native.AttentionArgs(dq.ptr, dpos.ptr, dk.ptr, dv.ptr, dout.ptr, ws.ptr, heads, kv_heads, d, rotary,
                                 capacity, 10000.0, 1.0)
     hip.attention(args)
     out = dout.readback(np.float32)
     kg, vg = dk.readback(np.uint16).reshape(k.shape), dv.readback(np.uint16).reshape(v.shape)
     # oracle: rotary on q and k, fp16 append, attention over position + 1 rows
     H = heads * d
-    q = orc.rope(qkv[:H], heads, d, 96, position, 10000.0, 1.0)
-    knew = orc.rope(qkv[H:H + kv_heads * d], kv_heads, d, 96, position, 10000.0, 1.0)
+    q = orc.rope(qkv[:H], heads, d, rotary, position, 10000.0, 1.0)
+    knew = orc.rope(qkv[H:H + kv_heads * d], kv_heads, d, rotary, position, 10000.0, 1.0)
     kk, vv = k.copy(), v.copy()
     kk[:, position] = knew.reshape(kv_heads, d).astype(np.float16).view(np.uint16)
     vv[:, position] = qkv[H + kv_heads * d:].reshape(kv_heads, d).astype(np.float16).view(np.uint16)
@@ -134,11 +134,8 @@ def _attention_case(hip, heads, kv_heads, capacity, position, seed):
     return out, truth, t64.reshape(-1), kg, vg, kk, vv, qkv
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(24, 8), (8, 2), (4, 4)])
-@pytest.mark.parametrize("position", [0, 1, 63, 64, 65, 2048])
-def test_attention_matches_oracle(hip, heads, kv_heads, position):
-    capacity = 2112
-    out, truth, t64, kg, vg, kk, vv, qkv = _attention_case(hip, heads, kv_heads, capacity, position, 100 + position)
+def _check_attention(heads, kv_heads, capacity, position, rotary, case):
+    out, truth, t64, kg, vg, kk, vv, qkv = case
     # against the fp64 evaluation of the same operands: the GEMV gates
     close(out, t64, 1e-3, 5e-5, "attention vs fp64")
     # against the oracle's FP32 sequential softmax: both carry FP32 error
@@ -154,8 +151,9 @@ def test_attention_matches_oracle(hip, heads, kv_heads, position):
     b = kk[:, position].view(np.float16).astype(np.float32)
     raw = qkv[heads * 128: heads * 128 + kv_heads * 128].reshape(kv_heads, 128)
     pair = np.abs(raw).copy()
-    pair[:, :48] += np.abs(raw[:, 48:96])
-    pair[:, 48:96] += np.abs(raw[:, :48])
+    half = rotary // 2
+    pair[:, :half] += np.abs(raw[:, half:rotary])
+    pair[:, half:rotary] += np.abs(raw[:, :half])
     bad = np.argwhere(~(np.abs(a - b) <= 2.0 ** -10 * np.maximum(np.abs(a), np.abs(b)) + 2.0 ** -21 * (position + 1) * pair))
     assert bad.size == 0, [(tuple(i), float(a[tuple(i)]), float(b[tuple(i)])) for i in bad[:8]]
     # nothing else in the cache changed
@@ -163,6 +161,24 @@ def test_attention_matches_oracle(hip, heads, kv_heads, position):
     mask[position] = False
     assert np.array_equal(kg[:, mask], kk[:, mask]), np.argwhere(kg[:, mask] != kk[:, mask])[:8]
     assert np.array_equal(vg[:, mask], vv[:, mask]), np.argwhere(vg[:, mask] != vv[:, mask])[:8]
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(24, 8), (8, 2), (4, 4)])
+@pytest.mark.parametrize("position", [0, 1, 63, 64, 65, 2048])
+def test_attention_matches_oracle(hip, heads, kv_heads, position):
+    capacity = 2112
+    _check_attention(heads, kv_heads, capacity, position, 96,
+                     _attention_case(hip, heads, kv_heads, capacity, position, 100 + position))
+
+
+# rotary widths: a multiple of 16 (whole 8-value slices and partners: the
+# register-resident chunk kernel) and one that is not (the staged kernel)
+@pytest.mark.parametrize("rotary", [128, 64, 40, 2])
+@pytest.mark.parametrize("position", [0, 65, 1000])
+def test_attention_rotary_widths(hip, rotary, position):
+    heads, kv_heads, capacity = 24, 8, 1088
+    _check_attention(heads, kv_heads, capacity, position, rotary,
+                     _attention_case(hip, heads, kv_heads, capacity, position, 300 + position + rotary, rotary))
 
 
 def test_attention_position_outside_cache_yields_nan_and_writes_nothing(hip):
