@@ -172,12 +172,12 @@ __device__ __forceinline__ void merge_combine_batch(const CombineBatch& b, int b
     for (int i = 0; i < COMBINE_BATCH; i++)
         if (base + 2 * i < chunks)
             bm = fmaxf(bm, b.m[i]);
-    const float r = expf(m - bm);   // m = -inf before the first batch: r = 0
+    const float r = __expf(m - bm);   // m = -inf before the first batch: r = 0
     float bl = 0.0f, bo = 0.0f;
 #pragma unroll
     for (int i = 0; i < COMBINE_BATCH; i++) {
         if (base + 2 * i < chunks) {
-            const float w = expf(b.m[i] - bm);
+            const float w = __expf(b.m[i] - bm);
             bl = fmaf(b.l[i], w, bl);
             bo = fmaf(b.o[i], w, bo);
         }
@@ -187,17 +187,22 @@ __device__ __forceinline__ void merge_combine_batch(const CombineBatch& b, int b
     m = bm;
 }
 
-__global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
+// The pointers arrive as preloaded scalar arguments; exponentials use the
+// hardware exp2 (__expf), within a few ulp of expf.
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ workspace,
+                                                                const int32_t* __restrict__ position,
+                                                                float* __restrict__ out, int capacity,
+                                                                int max_chunks)
 {
     const int h = blockIdx.x, t = threadIdx.x;
     const int d = t & (HEAD_DIM - 1), half = t >> 7;
-    const float* src = a.workspace + static_cast<int64_t>(h) * a.max_chunks * PART;
+    const float* src = workspace + static_cast<int64_t>(h) * max_chunks * PART;
     CombineBatch b;
-    load_combine_batch(src, half, a.max_chunks, d, b);
-    const int P = *a.position;
-    if (P < 0 || P >= a.capacity) {
+    load_combine_batch(src, half, max_chunks, d, b);
+    const int P = *position;
+    if (P < 0 || P >= capacity) {
         if (t < HEAD_DIM)
-            a.out[h * HEAD_DIM + t] = __int_as_float(0x7fc00000);   // position outside the cache
+            out[h * HEAD_DIM + t] = __int_as_float(0x7fc00000);   // position outside the cache
         return;
     }
     const int chunks = P / CHUNK + 1;
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
     if (half < chunks)
         merge_combine_batch(b, half, chunks, m, l, acc);
     for (int base = half + 2 * COMBINE_BATCH; base < chunks; base += 2 * COMBINE_BATCH) {
-        load_combine_batch(src, base, a.max_chunks, d, b);
+        load_combine_batch(src, base, max_chunks, d, b);
         merge_combine_batch(b, base, chunks, m, l, acc);
     }
     __shared__ float other[HEAD_DIM + 2];
@@ -220,8 +225,8 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttentionArgs a)
     if (half == 0) {
         const float m1 = other[HEAD_DIM];
         const float M = fmaxf(m, m1);
-        const float e0 = expf(m - M), e1 = expf(m1 - M);   // half 1 without chunks: m1 = -inf, e1 = 0
-        a.out[h * HEAD_DIM + d] = fmaf(acc, e0, other[d] * e1) / fmaf(l, e0, other[HEAD_DIM + 1] * e1);
+        const float e0 = __expf(m - M), e1 = __expf(m1 - M);   // half 1 without chunks: m1 = -inf, e1 = 0
+        out[h * HEAD_DIM + d] = fmaf(acc, e0, other[d] * e1) / fmaf(l, e0, other[HEAD_DIM + 1] * e1);
     }
 }
 
@@ -558,7 +563,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
 
     // 4. scores of the thread's four positions (a 16-lane row holds one
     //    position), masked past the count
-    const float inv_scale = sqrtf(static_cast<float>(HEAD_DIM));
+    // scores q.k / sqrt(head_dim) as q.k * (1 / sqrt(head_dim)), and
+    // exponentials with the hardware exp2 (__expf): both within a few ulp
+    // of the exact forms, far inside the attention tolerance
+    const float rscale = 1.0f / sqrtf(static_cast<float>(HEAD_DIM));
     float sc[GROUP][4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -578,7 +586,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
             for (int e = 0; e < 8; e++)
                 sdot = fmaf(q[h][e], k8[e], sdot);
             sdot = row_sum<16>(sdot);
-            sc[h][j] = p < count ? sdot / inv_scale : -INFINITY;
+            sc[h][j] = p < count ? sdot * rscale : -INFINITY;
         }
     }
 
@@ -592,7 +600,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
         float lh = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const float e = sc[h][j] == -INFINITY ? 0.0f : expf(sc[h][j] - mh);
+            const float e = sc[h][j] == -INFINITY ? 0.0f : __expf(sc[h][j] - mh);
             sc[h][j] = e;
             lh += e;
         }
@@ -664,7 +672,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
         float o = 0.0f, lsum = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const float f = wm[w][h] == -INFINITY ? 0.0f : expf(wm[w][h] - M);   // a wave without valid positions adds nothing
+            const float f = wm[w][h] == -INFINITY ? 0.0f : __expf(wm[w][h] - M);   // a wave without valid positions adds nothing
             o = fmaf(red[w][h][d], f, o);
             lsum = fmaf(wl[w][h], f, lsum);
         }
@@ -790,7 +798,8 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess)
             return e;
-        hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a.workspace,
+                       a.position, a.out, a.capacity, a.max_chunks);
         return hipGetLastError();
     }
     switch (group) {
@@ -803,7 +812,8 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a.workspace,
+                       a.position, a.out, a.capacity, a.max_chunks);
     return hipGetLastError();
 }
 
