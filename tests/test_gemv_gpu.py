@@ -231,6 +231,33 @@ def test_nonfinite_sums_retain_classification(hip, fmt, cols):
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("rows", [5120, 3072])
+def test_wide_and_finite_blocks_mix_in_one_row(hip, fmt, rows):
+    """Blocks holding huge values (|x| > 2^100) take the per-weight form and
+    the others the factored one, inside one row and one workgroup (the
+    one-workgroup-per-CU tiles at 3072 / 5120 rows): the sum stays within the
+    GEMV gate of the fp64 product.  A single +inf or NaN gives each row the
+    IEEE class of the dequantise-then-dot sum (0 * inf = NaN where the weight
+    is zero)."""
+    cols = 3072
+    w = orc.gen_quant(fmt, 77 + rows, rows, cols)
+    x = orc.gen_normal_f32(78 + rows, cols, 0.0, 1.0)
+    x[[5, 700, 701, 2050]] = np.float32([3e33, -2e31, 5e30, -7e32])
+    y, _ = run_gemv(hip, fmt, w, x, rows, cols)
+    assert_gemv_close(y, orc.gemv_f64(fmt, w, x, rows, cols), f"{NAMES[fmt]} huge blocks")
+    wd = orc.dequant(fmt, w, rows, cols).reshape(rows, cols).astype(np.float64)
+    for bad in (np.inf, np.nan):
+        xb = orc.gen_normal_f32(79 + rows, cols, 0.0, 1.0)
+        xb[1234] = bad
+        y, _ = run_gemv(hip, fmt, w, xb, rows, cols)
+        with np.errstate(invalid="ignore", over="ignore"):
+            truth = wd @ xb.astype(np.float64)
+        assert np.array_equal(np.isnan(y), np.isnan(truth)), f"{NAMES[fmt]} {bad}: NaN rows differ"
+        fin = ~np.isnan(truth)
+        assert np.array_equal(y[fin], truth[fin].astype(np.float32)), f"{NAMES[fmt]} {bad}: inf rows differ"
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
 def test_cancellation_stays_within_fp32_accumulation_bound(hip, fmt):
     """GpuMatVecTests.CooperativeMergePreservesCancellationAcrossAndWithinLanes
     (GpuMatVecTests.cs:41-52) expects exactly 4094 from a compensated D3D12
