@@ -359,23 +359,6 @@ __device__ __forceinline__ void side_copy(const Seg& sg, int b, int threads)
             sg.copy_dst[i] = sg.copy_src[i];
 }
 
-// Sum of v over the workgroup, returned to every thread; red holds one
-// float per wave and is not reused before the next barrier.
-template <int NW>
-__device__ __forceinline__ float block_sum(float v, float* red)
-{
-    for (int off = 32; off > 0; off >>= 1)
-        v += __shfl_xor(v, off);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NW; i++)
-        t += red[i];
-    return t;
-}
-
 __device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4(a.x - m, a.y - m, a.z - m, a.w - m); }
 
 // FULL = false compiles the plain product (no input transform, plain
@@ -569,22 +552,55 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             red[wave] = ss;
     } else if (NV == 4 && (in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX)) {
         // mean = sum(x) / K; c = x - mean; var = sum(c^2) / K;
-        // ln = (c * (1 / sqrt(var + eps))) * weight + bias
+        // ln = (c * (1 / sqrt(var + eps))) * weight + bias.
+        // Each wave takes the two-pass mean and sum of squared deviations of
+        // its own values (in registers, DPP / lane-swap sums); the waves'
+        // (count, mean, M2) merge after one barrier (Chan et al.'s pairwise
+        // update: M2 = sum M2_w + n_w (mean_w - mean)^2).
+        auto wave_count = [](int w) {   // values of wave w (the last round may be partial)
+            int n = 0;
+#pragma unroll
+            for (int j = 0; j < XPT; j++)
+                n += 4 * max(0, min(64, K / 4 - (j * THREADS + 64 * w)));
+            return n;
+        };
         float s1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < XPT; j++)
             s1 += (xr[j].x + xr[j].y) + (xr[j].z + xr[j].w);
-        const float mean = block_sum<NW>(s1, red) / static_cast<float>(K);
+        const int nown = wave_count(wave);
+        const float mw = nown > 0 ? wave_sum(s1) / static_cast<float>(nown) : 0.0f;
         float s2 = 0.0f;
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             if (!xin(j))
-                continue;   // stays zero
-            xr[j] = f4_sub(xr[j], mean);
-            s2 += (xr[j].x * xr[j].x + xr[j].y * xr[j].y) + (xr[j].z * xr[j].z + xr[j].w * xr[j].w);
+                continue;
+            const float4 c = f4_sub(xr[j], mw);
+            s2 += (c.x * c.x + c.y * c.y) + (c.z * c.z + c.w * c.w);
         }
-        const float var = block_sum<NW>(s2, red2) / static_cast<float>(K);
+        s2 = wave_sum(s2);
+        if ((threadIdx.x & 63) == 0) {
+            red[wave] = mw;
+            red2[wave] = s2;
+        }
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+            tot += static_cast<float>(wave_count(w)) * red[w];
+        const float mean = tot / static_cast<float>(K);
+        float m2 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float dm = red[w] - mean;
+            m2 += red2[w] + static_cast<float>(wave_count(w)) * dm * dm;
+        }
+        const float var = m2 / static_cast<float>(K);
         const float inv = 1.0f / sqrtf(var + sg.eps);
+#pragma unroll
+        for (int j = 0; j < XPT; j++)
+            if (xin(j))
+                xr[j] = f4_sub(xr[j], mean);
         const bool store = sg.norm_out != nullptr && b == 0;
         const bool mixing = in_kind == XF_LAYERNORM_MIX;
 #pragma unroll
