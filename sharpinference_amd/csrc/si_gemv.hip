@@ -114,6 +114,7 @@ template <>
 struct QUnit<FMT_Q8_0> {
     static constexpr int UNIT_BYTES = 68;
     uint32_t v[17];
+    __device__ __forceinline__ void prepare() {}
 
     __device__ __forceinline__ void load(const uint8_t* row, int u)
     {
@@ -152,6 +153,7 @@ template <>
 struct QUnit<FMT_Q4_0> {
     static constexpr int UNIT_BYTES = 36;
     uint32_t v[9];
+    __device__ __forceinline__ void prepare() {}
 
     __device__ __forceinline__ void load(const uint8_t* row, int u)
     {
@@ -216,17 +218,27 @@ struct QUnit<FMT_Q4_K> {
         qs[4] = b.x; qs[5] = b.y; qs[6] = b.z; qs[7] = b.w;
     }
 
-    // 6-bit scale and min of sub-block j (GGML get_scale_min_k4), written
-    // with selects so lanes of different chunks do not diverge.
-    __device__ __forceinline__ void scale_min(int j, int& sc, int& m) const
+    // d * sc and dmin * m of the unit's sub-blocks 2c (low nibbles) and
+    // 2c + 1 (high nibbles), c = chunk (GGML get_scale_min_k4).  Their scale
+    // bytes are the pair jj, jj + 1 with jj = 2 (c % 2) of each scale word,
+    // so both are extracted at once (byte lanes of a 16-bit field), with
+    // selects so lanes of different chunks do not diverge:
+    //   j < 4:  sc = scales[j] & 63, m = scales[j + 4] & 63
+    //   j >= 4: sc = (scales[j + 4] & 15) | (scales[j - 4] >> 6) << 4,
+    //           m = (scales[j + 4] >> 4) | (scales[j] >> 6) << 4
+    float dsc[2], dmn[2];
+    __device__ __forceinline__ void prepare()
     {
-        const int jj = j & 3;
-        const uint32_t s0 = (hd[1] >> (8 * jj)) & 0xffu;   // scales[jj]
-        const uint32_t s1 = (hd[2] >> (8 * jj)) & 0xffu;   // scales[jj + 4]
-        const uint32_t s2 = (hd[3] >> (8 * jj)) & 0xffu;   // scales[jj + 8]
-        const bool low = j < 4;
-        sc = static_cast<int>(low ? (s0 & 63u) : ((s2 & 15u) | ((s0 >> 6) << 4)));
-        m = static_cast<int>(low ? (s1 & 63u) : ((s2 >> 4) | ((s1 >> 6) << 4)));
+        const int sh = 16 * (chunk & 1);
+        const uint32_t s0 = hd[1] >> sh, s1 = hd[2] >> sh, s2 = hd[3] >> sh;
+        const bool low = chunk < 2;
+        const uint32_t sc = low ? (s0 & 0x3f3fu) : ((s2 & 0x0f0fu) | ((s0 >> 2) & 0x3030u));
+        const uint32_t m = low ? (s1 & 0x3f3fu) : (((s2 >> 4) & 0x0f0fu) | ((s1 >> 2) & 0x3030u));
+        const float d = half_lo(hd[0]), dm = half_hi(hd[0]);
+        dsc[0] = d * static_cast<float>(sc & 0xffu);
+        dsc[1] = d * static_cast<float>((sc >> 8) & 0xffu);
+        dmn[0] = dm * static_cast<float>(m & 0xffu);
+        dmn[1] = dm * static_cast<float>((m >> 8) & 0xffu);
     }
 
     // The high nibbles are masked in place (16 * q per byte); 1/16 goes
@@ -240,11 +252,8 @@ struct QUnit<FMT_Q4_K> {
             a0 = dot4_u8(opaque(qs[k] & mask), x[k], a0);
             a1 = dot4_u8(opaque(qs[k + 1] & mask), x[k + 1], a1);
         }
-        int sc, m;
-        scale_min(2 * chunk + h, sc, m);
-        const float d1 = half_lo(hd[0]) * static_cast<float>(sc) * (h == 0 ? 1.0f : 0.0625f);
-        const float m1 = half_hi(hd[0]) * static_cast<float>(m);
-        return fmaf(d1, a0 + a1, -(m1 * sx));
+        const float d1 = dsc[h] * (h == 0 ? 1.0f : 0.0625f);
+        return fmaf(d1, a0 + a1, -(dmn[h] * sx));
     }
 
     // Same contribution with every weight decoded as the oracle does,
@@ -253,10 +262,7 @@ struct QUnit<FMT_Q4_K> {
     // above could change the IEEE class of the result (inf - inf).
     __device__ float half_exact(int h, const float4* x) const
     {
-        int sc, m;
-        scale_min(2 * chunk + h, sc, m);
-        const float d1 = __fmul_rn(half_lo(hd[0]), static_cast<float>(sc));
-        const float m1 = __fmul_rn(half_hi(hd[0]), static_cast<float>(m));
+        const float d1 = dsc[h], m1 = dmn[h];
         float a = 0.0f;
         for (int k = 0; k < 8; k++) {
             const uint32_t q = h == 0 ? (qs[k] & 0x0f0f0f0fu) : ((qs[k] >> 4) & 0x0f0f0f0fu);
@@ -670,6 +676,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
 #pragma unroll
     for (int i = 0; i < UPL; i++) {
         const int u = unit0 + i * LK;
+#pragma unroll
+        for (int t = 0; t < RL; t++)
+            w[i][t].prepare();
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             float4 xv[8];
