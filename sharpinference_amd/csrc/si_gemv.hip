@@ -286,7 +286,9 @@ struct QUnit<FMT_Q4_K> {
 // ---- launch descriptors -----------------------------------------------------
 
 // Device copy of one GemvOp.  A launch carries up to MAX_SEGS of them by
-// value; op i owns workgroups [wg0_i, wg0_{i+1}).
+// value.  The tiled kernel runs a table launch as a 2D grid (grid row i =
+// op i); the one-wave-per-row kernels run a 1D grid in which op i owns
+// workgroups [wg0_i, wg0_{i+1}).
 struct Seg {
     const uint8_t* w;
     const float* x;
@@ -410,13 +412,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     __shared__ float part[ROWS_PER_WG * KS];
     __shared__ float red[NW], red2[NW];
 
-    const Seg& sg = seg_of(segs);
-    const int b = NS == 1 ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - sg.wg0;
+    // A table launch (NS > 1) runs a 2D grid: blockIdx.y is the op, so the
+    // workgroup reads its descriptor directly (one kernel-argument round
+    // trip, no search over the table); workgroups past the op's rows leave
+    // before any load or barrier.
+    const Seg& sg = segs.s[NS == 1 ? 0 : blockIdx.y];
+    const int b = static_cast<int>(blockIdx.x);
     const int rows = NS == 1 ? rows0 : sg.rows;
     const uint8_t* wbase = NS == 1 ? w0 : sg.w;
     const bool swiglu = FULL && (NS == 1 ? out0 : sg.out) == OUT_SWIGLU_ROWS;
     const int in_kind = FULL ? (NS == 1 ? in0 : sg.in) : static_cast<int>(XF_PLAIN);
     const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
+    if (NS > 1 && rb >= rows)
+        return;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: index math stays scalar
@@ -1032,13 +1040,18 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     } else {
         Segs<MAX_SEGS> t;
-        const unsigned grid = fill_segs(t, ops, n, per);
+        fill_segs(t, ops, n, per);
+        // one grid row per op, as wide as the largest op needs
+        unsigned width = 1;
+        for (int i = 0; i < n; i++)
+            width = std::max(width, static_cast<unsigned>((ops[i].rows + per(ops[i]) - 1) / per(ops[i])));
+        const dim3 grid(width, static_cast<unsigned>(n));
         if (ln)
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4>), dim3(grid),
-                               dim3(64 * NW), 0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4>), grid, dim3(64 * NW),
+                               0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 1>), dim3(grid),
-                               dim3(64 * NW), 0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 1>), grid, dim3(64 * NW),
+                               0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     }
     return hipGetLastError();
 }
@@ -1059,6 +1072,7 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     case 1024: return mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
     case 2048: return mid    ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s)
                     : rows64 >= 8192 ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s)
+                    : rows64 >= 4096 ? launch_tiled<FMT, 16, 1, 1, 2, 8>(ops, n, s)   // the RWKV-7 time-mix table
                                      : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
     case 3072:
         if (tall)
