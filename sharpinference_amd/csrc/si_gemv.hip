@@ -23,6 +23,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
+
 namespace si {
 namespace {
 
@@ -286,9 +288,10 @@ struct QUnit<FMT_Q4_K> {
 // ---- launch descriptors -----------------------------------------------------
 
 // Device copy of one GemvOp.  A launch carries up to MAX_SEGS of them by
-// value.  The tiled kernel runs a table launch as a 2D grid (grid row i =
-// op i); the one-wave-per-row kernels run a 1D grid in which op i owns
-// workgroups [wg0_i, wg0_{i+1}).
+// value and runs a 2D grid: grid row i is op i (as wide as the largest op
+// needs), so a workgroup reads its descriptor directly (one
+// kernel-argument round trip, no search over the table); workgroups past
+// their op's rows leave before any load or barrier.
 struct Seg {
     const uint8_t* w;
     const float* x;
@@ -302,7 +305,6 @@ struct Seg {
     const float* copy_src;
     float* copy_dst;
     int rows;               // output rows
-    int wg0;                // first workgroup of this op
     int in;                 // XformKind
     int out;                // OutKind
     int copy_n;
@@ -317,20 +319,6 @@ struct Segs {
     Seg s[NS];
     int count;
 };
-
-// The op that owns this workgroup (uniform across the workgroup).
-template <int NS>
-__device__ __forceinline__ const Seg& seg_of(const Segs<NS>& t)
-{
-    if constexpr (NS == 1) {
-        return t.s[0];
-    } else {
-        int si = 0;
-        for (int i = 1; i < t.count; i++)
-            si = static_cast<int>(blockIdx.x) >= t.s[i].wg0 ? i : si;
-        return t.s[si];
-    }
-}
 
 // Output function of one row (OUT_SWIGLU_ROWS is handled by the callers,
 // which hold both halves); res is the row's residual, loaded at the start
@@ -412,11 +400,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     __shared__ float part[ROWS_PER_WG * KS];
     __shared__ float red[NW], red2[NW];
 
-    // A table launch (NS > 1) runs a 2D grid: blockIdx.y is the op, so the
-    // workgroup reads its descriptor directly (one kernel-argument round
-    // trip, no search over the table); workgroups past the op's rows leave
-    // before any load or barrier.
-    const Seg& sg = segs.s[NS == 1 ? 0 : blockIdx.y];
+    const Seg& sg = segs.s[NS == 1 ? 0 : blockIdx.y];   // the op of this grid row
     const int b = static_cast<int>(blockIdx.x);
     const int rows = NS == 1 ? rows0 : sg.rows;
     const uint8_t* wbase = NS == 1 ? w0 : sg.w;
@@ -849,8 +833,8 @@ __device__ __forceinline__ float row_dot(const uint8_t* rp, const float* x, int 
 template <int FMT, int NS>
 __global__ __launch_bounds__(WG) void gemv_generic_kernel(Segs<NS> segs)
 {
-    const Seg& sg = seg_of(segs);
-    const int b = static_cast<int>(blockIdx.x) - sg.wg0;
+    const Seg& sg = segs.s[NS == 1 ? 0 : blockIdx.y];   // the op of this grid row
+    const int b = static_cast<int>(blockIdx.x);
     side_copy(sg, b, WG);
     const int row = b * (WG / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -879,11 +863,13 @@ __global__ __launch_bounds__(WG) void gemv_short_kernel(Segs<NS> segs)
 {
     __shared__ float xs[SHORT_MAX_COLS];
     __shared__ float part[2][WG];
-    const Seg& sg = seg_of(segs);
-    const int b = static_cast<int>(blockIdx.x) - sg.wg0;
-    side_copy(sg, b, WG);
+    const Seg& sg = segs.s[NS == 1 ? 0 : blockIdx.y];   // the op of this grid row
+    const int b = static_cast<int>(blockIdx.x);
     const int nb = sg.blocks;
     const int rpw = 64 / nb;                       // row slots per wave
+    if (NS > 1 && b * (WG / 64) * rpw >= sg.rows)
+        return;                                    // past this op's rows: the whole workgroup
+    side_copy(sg, b, WG);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int slot = lane / nb, blk = lane - slot * nb;
     const int row = (b * (WG / 64) + wave) * rpw + slot;
@@ -995,21 +981,21 @@ bool is_plain(const GemvOp& op)
     return op.in == XF_PLAIN && op.out == OUT_PLAIN && op.copy_n == 0;
 }
 
-// Builds the descriptor table of n ops, op i taking ceil(rows / per_wg(op))
-// workgroups.
+// Builds the descriptor table of n ops and returns the launch grid: op i
+// takes ceil(rows / per_wg(op)) workgroups; a table of several ops runs one
+// grid row per op, as wide as the largest op needs.
 template <int NS, typename PerWg>
-unsigned fill_segs(Segs<NS>& t, const GemvOp* ops, int n, PerWg per_wg)
+dim3 fill_segs(Segs<NS>& t, const GemvOp* ops, int n, PerWg per_wg)
 {
-    int wg = 0;
     t = Segs<NS>{};
     t.count = n;
+    unsigned width = 1;
     for (int i = 0; i < n; i++) {
         t.s[i] = to_seg(ops[i]);
-        t.s[i].wg0 = wg;
         const int per = per_wg(ops[i]);
-        wg += static_cast<int>((ops[i].rows + per - 1) / per);
+        width = std::max(width, static_cast<unsigned>((ops[i].rows + per - 1) / per));
     }
-    return static_cast<unsigned>(wg);
+    return dim3(width, static_cast<unsigned>(n));
 }
 
 template <int FMT, int LK, int UPL, int RL, int KS, int NW>
@@ -1028,24 +1014,19 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
     const GemvOp& o = ops[0];
     if (n == 1) {
         Segs<1> t;
-        const unsigned grid = fill_segs(t, ops, n, per);
+        const dim3 grid = fill_segs(t, ops, n, per);
         if (is_plain(o))
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), dim3(grid), dim3(64 * NW), 0,
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), grid, dim3(64 * NW), 0,
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else if (ln)
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 4>), dim3(grid), dim3(64 * NW), 0,
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 4>), grid, dim3(64 * NW), 0,
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 1>), dim3(grid), dim3(64 * NW), 0,
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 1>), grid, dim3(64 * NW), 0,
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     } else {
         Segs<MAX_SEGS> t;
-        fill_segs(t, ops, n, per);
-        // one grid row per op, as wide as the largest op needs
-        unsigned width = 1;
-        for (int i = 0; i < n; i++)
-            width = std::max(width, static_cast<unsigned>((ops[i].rows + per(ops[i]) - 1) / per(ops[i])));
-        const dim3 grid(width, static_cast<unsigned>(n));
+        const dim3 grid = fill_segs(t, ops, n, per);
         if (ln)
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4>), grid, dim3(64 * NW),
                                0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
@@ -1103,12 +1084,12 @@ hipError_t launch_generic(const GemvOp* ops, int n, hipStream_t s)
     auto per = [](const GemvOp&) { return WG / 64; };   // one output row per wave
     if (n == 1) {
         Segs<1> t;
-        const unsigned grid = fill_segs(t, ops, n, per);
-        hipLaunchKernelGGL((gemv_generic_kernel<FMT, 1>), dim3(grid), dim3(WG), 0, s, t);
+        const dim3 grid = fill_segs(t, ops, n, per);
+        hipLaunchKernelGGL((gemv_generic_kernel<FMT, 1>), grid, dim3(WG), 0, s, t);
     } else {
         Segs<MAX_SEGS> t;
-        const unsigned grid = fill_segs(t, ops, n, per);
-        hipLaunchKernelGGL((gemv_generic_kernel<FMT, MAX_SEGS>), dim3(grid), dim3(WG), 0, s, t);
+        const dim3 grid = fill_segs(t, ops, n, per);
+        hipLaunchKernelGGL((gemv_generic_kernel<FMT, MAX_SEGS>), grid, dim3(WG), 0, s, t);
     }
     return hipGetLastError();
 }
@@ -1119,12 +1100,12 @@ hipError_t launch_short(const GemvOp* ops, int n, hipStream_t s)
     auto per = [](const GemvOp& op) { return (WG / 64) * (64 / static_cast<int>(op.cols / block_elems(FMT))); };
     if (n == 1) {
         Segs<1> t;
-        const unsigned grid = fill_segs(t, ops, n, per);
-        hipLaunchKernelGGL((gemv_short_kernel<FMT, 1>), dim3(grid), dim3(WG), 0, s, t);
+        const dim3 grid = fill_segs(t, ops, n, per);
+        hipLaunchKernelGGL((gemv_short_kernel<FMT, 1>), grid, dim3(WG), 0, s, t);
     } else {
         Segs<MAX_SEGS> t;
-        const unsigned grid = fill_segs(t, ops, n, per);
-        hipLaunchKernelGGL((gemv_short_kernel<FMT, MAX_SEGS>), dim3(grid), dim3(WG), 0, s, t);
+        const dim3 grid = fill_segs(t, ops, n, per);
+        hipLaunchKernelGGL((gemv_short_kernel<FMT, MAX_SEGS>), grid, dim3(WG), 0, s, t);
     }
     return hipGetLastError();
 }
