@@ -18,18 +18,26 @@ constexpr int WKV_THREADS = 256;   // 4 threads per state row, 16 columns each
 
 __device__ __forceinline__ float sigm(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-__device__ __forceinline__ float wave_sum(float v)
+// Sums over the 4 lanes of a quad and over the wave, left in every lane:
+// DPP moves inside quads and 16-lane rows, then swaps between the wave's
+// halves and between row pairs (v_permlane32_swap / v_permlane16_swap), so
+// no step waits for an LDS round trip.
+__device__ __forceinline__ float quad_sum(float v)
 {
-    for (int off = 32; off > 0; off >>= 1)
-        v += __shfl_xor(v, off);
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
     return v;
 }
 
-__device__ __forceinline__ float quad_sum(float v)
+__device__ __forceinline__ float wave_sum(float v)
 {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    return v;
+    v = quad_sum(v);
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __global__ __launch_bounds__(WKV_THREADS) void rwkv_wkv_kernel(WkvArgs a)
