@@ -697,44 +697,92 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i)
     }
 }
 
+// better() over the lane that DPP control CTRL reads from.
+template <int CTRL>
+__device__ __forceinline__ void better_dpp(float& bv, int& bi)
+{
+    const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), CTRL, 0xF, 0xF, false));
+    const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xF, 0xF, false);
+    better(bv, bi, ov, oi);
+}
+
+// The wave's best (value, index) in every lane: DPP inside quads and rows,
+// then the swaps between halves and row pairs.  better() is a total order
+// (larger value, then smaller index; NaN never wins), so the result does
+// not depend on the pairing.
+__device__ __forceinline__ void wave_best(float& bv, int& bi)
+{
+    better_dpp<0xB1>(bv, bi);    // quad_perm 1,0,3,2
+    better_dpp<0x4E>(bv, bi);    // quad_perm 2,3,0,1
+    better_dpp<0x141>(bv, bi);   // row_half_mirror
+    better_dpp<0x140>(bv, bi);   // row_mirror
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+    const auto ai = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(bi), static_cast<unsigned>(bi), false, false);
+    bv = __uint_as_float(a[0]);
+    bi = static_cast<int>(ai[0]);
+    better(bv, bi, __uint_as_float(a[1]), static_cast<int>(ai[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+    const auto bi2 = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(bi), static_cast<unsigned>(bi), false, false);
+    bv = __uint_as_float(b[0]);
+    bi = static_cast<int>(bi2[0]);
+    better(bv, bi, __uint_as_float(b[1]), static_cast<int>(bi2[1]));
+}
+
+// The four waves' results through LDS at one barrier; thread 0 returns the
+// workgroup's best.
+__device__ __forceinline__ void block_best(float& bv, int& bi)
+{
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    wave_best(bv, bi);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < 4; w++)
+            better(bv, bi, sv[w], si[w]);
+}
+
+// The first AM_PER values of a thread are requested together (indices
+// clamped into the vector, n >= 1), the rest (vectors longer than
+// AM_PER * AM_BLOCKS * 256) one after another.
+constexpr int AM_PER = 4;
+
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ v, int n,
                                                              float* __restrict__ pv, int* __restrict__ pi)
 {
+    constexpr int STRIDE = AM_BLOCKS * 256;
+    const int i0 = blockIdx.x * 256 + threadIdx.x;
+    float vals[AM_PER];
+#pragma unroll
+    for (int k = 0; k < AM_PER; k++)
+        vals[k] = v[min(i0 + k * STRIDE, n - 1)];
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += AM_BLOCKS * 256)
-        better(bv, bi, v[i], i);
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int step = 128; step > 0; step >>= 1) {
-        if (threadIdx.x < step)
-            better(sv[threadIdx.x], si[threadIdx.x], sv[threadIdx.x + step], si[threadIdx.x + step]);
-        __syncthreads();
-    }
+#pragma unroll
+    for (int k = 0; k < AM_PER; k++)
+        if (i0 + k * STRIDE < n)
+            better(bv, bi, vals[k], i0 + k * STRIDE);
+    for (int64_t i = i0 + AM_PER * STRIDE; i < n; i += STRIDE)
+        better(bv, bi, v[i], static_cast<int>(i));
+    block_best(bv, bi);
     if (threadIdx.x == 0) {
-        pv[blockIdx.x] = sv[0];
-        pi[blockIdx.x] = si[0];
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
     }
 }
 
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
                                                            int32_t* __restrict__ out)
 {
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    sv[threadIdx.x] = pv[threadIdx.x];
-    si[threadIdx.x] = pi[threadIdx.x];
-    __syncthreads();
-    for (int step = 128; step > 0; step >>= 1) {
-        if (threadIdx.x < step)
-            better(sv[threadIdx.x], si[threadIdx.x], sv[threadIdx.x + step], si[threadIdx.x + step]);
-        __syncthreads();
-    }
+    float bv = pv[threadIdx.x];
+    int bi = pi[threadIdx.x];
+    block_best(bv, bi);
     if (threadIdx.x == 0)
-        *out = si[0] == 0x7fffffff ? 0 : si[0];
+        *out = bi == 0x7fffffff ? 0 : bi;
 }
 
 }  // namespace
@@ -819,6 +867,8 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
 
 hipError_t launch_argmax(const float* values, int64_t n, void* workspace, int32_t* out, hipStream_t s)
 {
+    if (n <= 0 || n > INT32_MAX)
+        return hipErrorInvalidValue;
     float* pv = static_cast<float*>(workspace);
     int* pi = reinterpret_cast<int*>(pv + AM_BLOCKS);
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(AM_BLOCKS), dim3(256), 0, s, values, static_cast<int>(n), pv, pi);

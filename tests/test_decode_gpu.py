@@ -207,6 +207,9 @@ def test_argmax_matches_first_index_rule(hip):
     big = rng.standard_normal(200064).astype(np.float32)
     big[150000] = big[190000] = 99.0
     cases.append(big)
+    long = rng.standard_normal(300001).astype(np.float32)   # past the values each thread requests together
+    long[299999] = 50.0
+    cases += [long, np.array([7.0], np.float32)]
     for v in cases:
         dv = hip.to_device(v)
         hip.argmax(dv.ptr, v.size, ws.ptr, out.ptr)
