@@ -52,34 +52,52 @@ __global__ __launch_bounds__(WKV_THREADS) void rwkv_wkv_kernel(WkvArgs a)
     const int i = t >> 2;              // state row
     const int j0 = (t & 3) * 16;       // first of this thread's 16 columns
 
-    // the state tile first, so its latency overlaps the vector prep
+    // Every global load is issued here, before any result is waited for:
+    // the state tile, then (wave 0, one element per lane) the head vectors,
+    // the GroupNorm affine and gate, and the side copy's value.  Loads are
+    // unconditional (the first layer's value inputs read v instead of the
+    // v_lora / v0 / v_first it does not use), so no branch holds them back
+    // behind an earlier round trip; the side copy is stored at the end.
     float4 sv[4];
 #pragma unroll
     for (int q = 0; q < 4; q++)
         sv[q] = *reinterpret_cast<const float4*>(S + i * N + j0 + 4 * q);
-    if (a.copy_src && t < N)
-        a.copy_dst[o + t] = a.copy_src[o + t];
+    const int e = o + (t & (N - 1));
+    const bool first = a.first_layer != 0;
+    float kk = 0.0f, wl = 0.0f, w0 = 0.0f, al = 0.0f, a0 = 0.0f, kkk = 0.0f, kka = 0.0f, vv = 0.0f, vf = 0.0f,
+          vl = 0.0f, v0 = 0.0f, rr = 0.0f, rk = 0.0f, lw = 0.0f, lb = 0.0f, gt = 0.0f, cp = 0.0f;
+    if (t < N) {
+        kk = a.k[e];
+        wl = a.w_lora[e];
+        w0 = a.w0[e];
+        al = a.a_lora[e];
+        a0 = a.a0[e];
+        kkk = a.k_k[e];
+        kka = a.k_a[e];
+        vv = a.v[e];
+        vf = (first ? a.v : a.v_first)[e];
+        vl = (first ? a.v : a.v_lora)[e];
+        v0 = (first ? a.v : a.v0)[e];
+        rr = a.r[e];
+        rk = a.r_k[e];
+        lw = a.lnx_weight[e];
+        lb = a.lnx_bias[e];
+        gt = a.gate[e];
+        cp = (a.copy_src ? a.copy_src : a.v)[e];
+    }
 
     if (t < N) {   // wave 0: one element of each head vector per lane
-        const int e = o + t;
-        const float kk = a.k[e];
-        const float decay = expf(-0.606531f * sigm(a.w_lora[e] + a.w0[e]));     // :232-234
-        const float ad = sigm(a.a_lora[e] + a.a0[e]);                            // :235-237
-        const float sk = kk * a.k_k[e];                                          // :241-246
+        const float decay = expf(-0.606531f * sigm(wl + w0));                      // :232-234
+        const float ad = sigm(al + a0);                                           // :235-237
+        const float sk = kk * kkk;                                                // :241-246
         const float squares = wave_sum(sk * sk);
         const float kn = sk * (1.0f / sqrtf(squares > 1e-24f ? squares : 1e-24f));
-        const float ka = kk * a.k_a[e];                                          // :247-248
+        const float ka = kk * kka;                                                // :247-248
         const float key = (kk + ad * ka) - ka;
-        float value;
-        if (a.first_layer) {                                                     // :249-257
-            value = a.v[e];
-            a.v_first[e] = value;
-        } else {
-            const float vv = a.v[e];
-            value = vv + (a.v_first[e] - vv) * sigm(a.v_lora[e] + a.v0[e]);
-        }
-        const float rr = a.r[e];
-        const float bonus = wave_sum((key * rr) * a.r_k[e]);                   // :274-275
+        const float value = first ? vv : vv + (vf - vv) * sigm(vl + v0);          // :249-257
+        if (first)
+            a.v_first[e] = vv;
+        const float bonus = wave_sum((key * rr) * rk);                           // :274-275
         s_decay[t] = decay;
         s_key[t] = key;
         s_value[t] = value;
@@ -128,8 +146,10 @@ __global__ __launch_bounds__(WKV_THREADS) void rwkv_wkv_kernel(WkvArgs a)
         const float mean = wave_sum(yv) / static_cast<float>(N);
         const float c = yv - mean;
         const float var = wave_sum(c * c) / static_cast<float>(N);
-        const float ln = c * (1.0f / sqrtf(var + 64e-5f)) * a.lnx_weight[o + t] + a.lnx_bias[o + t];
-        a.out[o + t] = (ln + s_value[t] * s_bonus) * a.gate[o + t];
+        const float ln = c * (1.0f / sqrtf(var + 64e-5f)) * lw + lb;
+        a.out[o + t] = (ln + s_value[t] * s_bonus) * gt;
+        if (a.copy_src)
+            a.copy_dst[o + t] = cp;
     }
 }
 
