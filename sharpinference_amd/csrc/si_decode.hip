@@ -140,11 +140,14 @@ constexpr int MAX_CHUNKS = 256;
 // Thread (half, d) takes chunks half, half + 2, ... in batches of
 // COMBINE_BATCH, every load of a batch issued together, and merges the
 // batches online; the two halves merge through LDS.  The first batch is
-// requested before the position is read (slots past the position hold
-// stale partials and are masked), so a cache of up to 2 * COMBINE_BATCH
-// chunks costs one memory round trip.  (Merging inside the last partial
-// workgroup instead needs a device-scope release per workgroup, which
-// writes back the XCD's L2 and costs far more than this launch.)
+// written ahead of the position read (slots past the position hold stale
+// partials and are masked), but the compiler issues its loads inside the
+// merge's branch, after the position check: a cache of up to
+// 2 * COMBINE_BATCH chunks costs the position's round trip and one more.
+// (A branch-free merge that keeps them ahead of the position measured
+// slower; merging inside the last partial workgroup needs a device-scope
+// release per workgroup, which writes back the XCD's L2 and costs far more
+// than this launch.)
 constexpr int COMBINE_BATCH = 16;
 
 struct CombineBatch {
