@@ -85,7 +85,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the GEMV shards by output rows; see DESIGN.md)", file=sys.stderr)
+              "(the GEMV would shard by output rows, each GPU taking one slice of W's rows; "
+              "this bench measures one GPU's share)", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)

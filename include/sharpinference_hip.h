@@ -4,7 +4,7 @@
  *
  * The managed side of SharpInference binds these entry points by P/Invoke
  * from a HIP executor that mirrors SharpInference.Backends.D3D12Vm's
- * D3D12VmExecutor; the binding stubs are listed in INTEGRATION.md.  The
+ * D3D12VmExecutor, one [DllImport] per entry point below.  The
  * reference has no native layer, so every entry point below names the
  * managed member whose job it takes over.
  *
