@@ -15,10 +15,11 @@ namespace {
 std::string TypeName(GraphElementType t)
 {
     switch (t) {
-    case GraphElementType::Float32: return "Float32";
-    case GraphElementType::Float16: return "Float16";
-    case GraphElementType::UInt8: return "UInt8";
+    case GraphElementType::Byte: return "Byte";
     case GraphElementType::Int32: return "Int32";
+    case GraphElementType::UInt32: return "UInt32";
+    case GraphElementType::Float16: return "Float16";
+    case GraphElementType::Float32: return "Float32";
     }
     return "?";
 }
@@ -65,10 +66,11 @@ void Check(int status, const si_hip_context* context)
 int ElementSize(GraphElementType type)
 {
     switch (type) {
-    case GraphElementType::Float32: return 4;
-    case GraphElementType::Float16: return 2;
-    case GraphElementType::UInt8: return 1;
+    case GraphElementType::Byte: return 1;
     case GraphElementType::Int32: return 4;
+    case GraphElementType::UInt32: return 4;
+    case GraphElementType::Float16: return 2;
+    case GraphElementType::Float32: return 4;
     }
     return 0;
 }
@@ -322,9 +324,9 @@ std::vector<InstructionSignature> QuantizedMatVecInstruction::Signatures() const
 {
     std::vector<InstructionSignature> s;
     for (const char* weight : {"weight", "matrix"})
-        s.push_back({{{weight, GraphElementType::UInt8, GraphResourceAccess::Read},
+        s.push_back({{{weight, GraphElementType::Byte, GraphResourceAccess::Read},
                       {"input", GraphElementType::Float32, GraphResourceAccess::Read},
-                      {"output", GraphElementType::Float32, GraphResourceAccess::ReadWrite}},
+                      {"output", GraphElementType::Float32, GraphResourceAccess::Write}},
                      {"format", "columns"},
                      FP32});
     return s;
@@ -357,9 +359,9 @@ InstructionRecording QuantizedMatVecInstruction::Generate(const std::vector<Inst
 
 std::vector<InstructionSignature> QuantizedGatherRowInstruction::Signatures() const
 {
-    return {{{{"table", GraphElementType::UInt8, GraphResourceAccess::Read},
+    return {{{{"table", GraphElementType::Byte, GraphResourceAccess::Read},
               {"index", GraphElementType::Int32, GraphResourceAccess::Read},
-              {"output", GraphElementType::Float32, GraphResourceAccess::ReadWrite}},
+              {"output", GraphElementType::Float32, GraphResourceAccess::Write}},
              {"format", "columns"},
              FP32}};
 }
@@ -449,7 +451,7 @@ void HipVmProgram::AddDispatch(const std::string& entry, std::shared_ptr<const I
         const uint64_t end = p.byte_offset + p.tensor.ByteLength();
         if (end < p.byte_offset || end > slots_[s].tensor.ByteLength())
             throw InvalidDataException("Parameter '" + p.name + "' does not fit in slot '" + p.source + "'.");
-        if (p.access == GraphResourceAccess::ReadWrite && slots_[s].access != GraphResourceAccess::ReadWrite)
+        if (p.access != GraphResourceAccess::Read && slots_[s].access != VmAccess::ReadWrite)
             throw InvalidDataException("Parameter '" + p.name + "' writes read-only slot '" + p.source + "'.");
         tensors.push_back(&p);
     }
@@ -458,7 +460,7 @@ void HipVmProgram::AddDispatch(const std::string& entry, std::shared_ptr<const I
             const auto* a = tensors[i];
             const auto* b = tensors[j];
             if (a->source == b->source &&
-                (a->access == GraphResourceAccess::ReadWrite || b->access == GraphResourceAccess::ReadWrite) &&
+                (a->access != GraphResourceAccess::Read || b->access != GraphResourceAccess::Read) &&
                 a->byte_offset < b->byte_offset + b->tensor.ByteLength() &&
                 b->byte_offset < a->byte_offset + a->tensor.ByteLength())
                 throw NotSupportedException("Dispatch '" + entry + "' aliases writable kernel parameters.");

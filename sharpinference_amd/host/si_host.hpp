@@ -75,8 +75,11 @@ void Check(int status, const si_hip_context* context = nullptr);
 
 // ---- operator contract (InstructionCollection.cs) ----------------------------------------
 
-enum class GraphElementType { Float32, Float16, UInt8, Int32 };
-enum class GraphResourceAccess { Read, ReadWrite };
+// GraphModel.cs:63-77 (same members, same order).
+enum class GraphElementType { Byte, Int32, UInt32, Float16, Float32 };
+enum class GraphResourceAccess { Read, Write, ReadWrite };
+// Access of a program slot (VmProgram.cs:10).
+enum class VmAccess { ReadOnly, ReadWrite };
 
 int ElementSize(GraphElementType type);
 // Precision check (NumericTypeCompatibility.Satisfies, OperatorBackend.cs:106-112):
@@ -217,7 +220,7 @@ inline const std::string QuantizedFloat32 = "5c2f7b1e-9a4d-4f0e-8e61-3b7f2d9c4a1
 }
 
 // quant.mat-vec: output[rows] = weight[rows, columns] . input[columns]; the
-// weight port is a UInt8 tensor [rows, row_bytes] of GGUF blocks, attributes
+// weight port is a Byte tensor [rows, row_bytes] of GGUF blocks, attributes
 // format (q8_0 | q4_0 | q4_k) and columns; port names as core.mat-vec
 // (weight or matrix, input, output); FP32 arithmetic and accumulation.
 class QuantizedMatVecInstruction : public Instruction {
@@ -262,7 +265,7 @@ int FormatId(const std::string& name);
 struct HipVmSlot {
     std::string id;
     TensorDescriptor tensor;
-    GraphResourceAccess access = GraphResourceAccess::ReadWrite;
+    VmAccess access = VmAccess::ReadWrite;
 };
 
 struct HipVmDispatch {
@@ -278,9 +281,9 @@ public:
     void AddSlot(HipVmSlot slot);
     // Invokes the instruction on the entry's recorder.  Binding rules
     // (D3D12VmSchedule.cs:74-99): every tensor names an existing slot and
-    // fits inside it at its byte offset; a ReadWrite port needs a writable
-    // slot; writable parameters of one dispatch may not overlap others
-    // (NotSupportedException).
+    // fits inside it at its byte offset; a parameter that writes (Write or
+    // ReadWrite) needs a ReadWrite slot; writing parameters of one dispatch
+    // may not overlap others (NotSupportedException).
     void AddDispatch(const std::string& entry, std::shared_ptr<const Instruction> instruction,
                      const std::vector<InstructionParameter>& parameters, const PrecisionRequirement& precision);
 

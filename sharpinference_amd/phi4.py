@@ -19,6 +19,13 @@ from . import native
 from .synth import synth_blocks  # noqa: F401  (re-exported for callers of this module)
 
 
+# Phi4TextModel.cs:18 (RotarySize): the rotary width when a file does not name one.
+REFERENCE_ROTARY_SIZE = 96
+# Norm weights the reference's RmsNorm reads (Float32 or Float16,
+# Phi4TextModel.cs:116-127); BF16 is widened the same way.
+NORM_TYPES = (native.F32, native.F16, native.BF16)
+
+
 @dataclass
 class Phi4Config:
     """Phi-4-mini text shapes (Phi4TextModel.cs:14-21) with the benchmark
@@ -45,25 +52,34 @@ class Phi4Config:
 
     @classmethod
     def from_gguf(cls, g, capacity: int = 4096) -> "Phi4Config":
-        """Shapes and constants from a phi3 GGUF's metadata and tensor types."""
+        """Shapes and constants from a phi3 GGUF's metadata and tensor types.
+
+        As the reference model (Phi4TextModel.cs:40-42, 95-105, 212-229):
+        the epsilon, rope base and rope scale keys are required (GetMetadata
+        throws when one is missing), the rotary width is 96 unless the file
+        names another, and the vocabulary head is token_embd.weight (tied),
+        whether or not the file also holds an output.weight."""
         if g.get("general.architecture") != "phi3":
             raise ValueError("not a phi3-architecture GGUF")
         hidden = int(g.get("phi3.embedding_length"))
         heads = int(g.get("phi3.attention.head_count"))
         emb = g.tensor("token_embd.weight")
-        head = g.tensors.get("output.weight", emb)
-        layer_types = {g.tensor(f"blk.{l}.{n}.weight").type for l in range(int(g.get("phi3.block_count")))
-                       for n in ("attn_qkv", "attn_output", "ffn_up", "ffn_down")}
+        layer_types: Dict[int, str] = {}   # type -> first tensor of that type
+        for l in range(int(g.get("phi3.block_count"))):
+            for n in ("attn_qkv", "attn_output", "ffn_up", "ffn_down"):
+                t = g.tensor(f"blk.{l}.{n}.weight")
+                layer_types.setdefault(t.type, t.name)
         if len(layer_types) != 1:
-            raise ValueError(f"layer projections use several formats {sorted(layer_types)}; one is supported")
+            seen = ", ".join(f"{native.FORMAT_NAMES.get(k, k)}: {v}" for k, v in sorted(layer_types.items()))
+            raise ValueError(f"layer projections use several formats ({seen}); one is supported")
         return cls(layers=int(g.get("phi3.block_count")), hidden=hidden, heads=heads,
                    kv_heads=int(g.get("phi3.attention.head_count_kv")), head_dim=hidden // heads,
-                   rotary_dim=int(g.metadata.get("phi3.rope.dimension_count", hidden // heads)),
+                   rotary_dim=int(g.metadata.get("phi3.rope.dimension_count", REFERENCE_ROTARY_SIZE)),
                    ffn=int(g.get("phi3.feed_forward_length")), vocab=emb.rows, capacity=capacity,
-                   weight_format=layer_types.pop(), embed_format=emb.type, head_format=head.type,
+                   weight_format=next(iter(layer_types)), embed_format=emb.type, head_format=emb.type,
                    rms_eps=float(g.get("phi3.attention.layer_norm_rms_epsilon")),
                    rope_base=float(g.get("phi3.rope.freq_base")),
-                   rope_scale=float(g.metadata.get("phi3.rope.scaling.attn_factor", 1.0)))
+                   rope_scale=float(g.get("phi3.rope.scaling.attn_factor")))
 
     def layer_shapes(self) -> Dict[str, tuple]:
         return {"qkv": (self.qkv_rows, self.hidden), "o": (self.hidden, self.hidden),
@@ -165,16 +181,21 @@ class Phi4DecodeSession:
     def from_gguf(cls, hip: native.HipContext, g, capacity: int = 4096) -> "Phi4DecodeSession":
         """A session over a phi3-architecture GGUF file (the Phi-4-mini text
         backbone, Phi4ModelPackage.cs:108-113, Phi4TextModel.cs:40-42,53,
-        67-99): every tensor is uploaded once, unchanged, from the mapping."""
+        67-99).  Every tensor's type and dimensions are checked against the
+        configuration first (check_gguf_tensors), then the projections and
+        the embedding are uploaded once, unchanged, from the mapping; norm
+        weights stored as Float16 / BF16 are widened to FP32 on the host
+        (they are a few KB) so the kernels read FP32 norms."""
         cfg = Phi4Config.from_gguf(g, capacity)
+        norms = check_gguf_tensors(g, cfg)
         up = lambda name: g.upload(hip, name)
+        norm = lambda name: norms[name] if name in norms else up(name)
         embed = up("token_embd.weight")
-        lm_head = up("output.weight") if "output.weight" in g.tensors else embed   # tied (Phi4TextModel.cs:99)
         L = range(cfg.layers)
         weights = Phi4Weights(
-            embed=embed, lm_head=lm_head, output_norm=up("output_norm.weight"),
-            attn_norm=[up(f"blk.{l}.attn_norm.weight") for l in L], qkv=[up(f"blk.{l}.attn_qkv.weight") for l in L],
-            o=[up(f"blk.{l}.attn_output.weight") for l in L], ffn_norm=[up(f"blk.{l}.ffn_norm.weight") for l in L],
+            embed=embed, lm_head=embed, output_norm=norm("output_norm.weight"),
+            attn_norm=[norm(f"blk.{l}.attn_norm.weight") for l in L], qkv=[up(f"blk.{l}.attn_qkv.weight") for l in L],
+            o=[up(f"blk.{l}.attn_output.weight") for l in L], ffn_norm=[norm(f"blk.{l}.ffn_norm.weight") for l in L],
             up=[up(f"blk.{l}.ffn_up.weight") for l in L], down=[up(f"blk.{l}.ffn_down.weight") for l in L])
         return cls(hip, cfg, weights)
 
@@ -216,6 +237,46 @@ class Phi4DecodeSession:
         for b in self._bufs:
             b.free()
         self._bufs = []
+
+
+# ---- GGUF checks -----------------------------------------------------------------------
+
+def check_gguf_tensors(g, cfg: Phi4Config) -> Dict[str, np.ndarray]:
+    """Checks every tensor the decode step reads against `cfg` before any
+    device work: GGUF dims ([columns, rows], Phi4TextModel.cs:140-141), the
+    projection and embedding types the kernels decode, and the norm types
+    RmsNorm accepts.  Raises ValueError naming the tensor on any mismatch.
+    Returns the norm weights that are not FP32, widened to FP32 host arrays
+    (name -> array)."""
+    H, F = cfg.hidden, cfg.ffn
+    if H % cfg.heads or cfg.head_dim != 128 or cfg.heads % cfg.kv_heads or not 1 <= cfg.heads // cfg.kv_heads <= 4:
+        raise ValueError(f"unsupported head layout: hidden {H}, {cfg.heads} heads, {cfg.kv_heads} KV heads")
+    if cfg.rotary_dim <= 0 or cfg.rotary_dim % 2 or cfg.rotary_dim > cfg.head_dim:
+        raise ValueError(f"rotary width {cfg.rotary_dim} must be even and at most the head size {cfg.head_dim}")
+
+    def want(name, dims, types):
+        t = g.tensor(name)
+        if tuple(t.dims) != tuple(dims):
+            raise ValueError(f"{name}: dims {list(t.dims)}, expected {list(dims)}")
+        if t.type not in types:
+            names = ", ".join(native.FORMAT_NAMES.get(x, str(x)) for x in types)
+            raise ValueError(f"{name}: tensor type {native.FORMAT_NAMES.get(t.type, t.type)} is not one of {names}")
+        return t
+
+    want("token_embd.weight", (H, cfg.vocab), native.MATRIX_FORMATS)
+    for l in range(cfg.layers):
+        for n, dims in (("attn_qkv", (H, cfg.qkv_rows)), ("attn_output", (H, H)), ("ffn_up", (H, 2 * F)),
+                        ("ffn_down", (F, H))):
+            want(f"blk.{l}.{n}.weight", dims, native.MATRIX_FORMATS)
+    widened = {}
+    for name in ["output_norm.weight"] + [f"blk.{l}.{n}.weight" for l in range(cfg.layers)
+                                          for n in ("attn_norm", "ffn_norm")]:
+        t = want(name, (H,), NORM_TYPES)
+        if t.type == native.F16:
+            widened[name] = g.host_bytes(name).view(np.float16).astype(np.float32)
+        elif t.type == native.BF16:
+            widened[name] = (g.host_bytes(name).view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return widened
 
 
 # ---- synthetic weights --------------------------------------------------------------

@@ -108,7 +108,7 @@ uint64_t RowBytes(int fmt, int64_t columns)
     return b;
 }
 
-TensorDescriptor U8(int64_t rows, int64_t bytes) { return {GraphElementType::UInt8, {rows, bytes}}; }
+TensorDescriptor U8(int64_t rows, int64_t bytes) { return {GraphElementType::Byte, {rows, bytes}}; }
 TensorDescriptor F32(int64_t n) { return {GraphElementType::Float32, {n}}; }
 
 // The parameters of one quant.mat-vec dispatch over a view `padding`
@@ -119,7 +119,7 @@ std::vector<InstructionParameter> MatVecParameters(int fmt, int64_t rows, int64_
     return {InstructionParameter::Tensor(weight_port, U8(rows, RowBytes(fmt, columns)), GraphResourceAccess::Read,
                                          "weight", padding),
             InstructionParameter::Tensor("input", F32(columns), GraphResourceAccess::Read, "input", 4 * padding),
-            InstructionParameter::Tensor("output", F32(rows), GraphResourceAccess::ReadWrite, "output", 4 * padding),
+            InstructionParameter::Tensor("output", F32(rows), GraphResourceAccess::Write, "output", 4 * padding),
             InstructionParameter::Attribute("format", Name(fmt)),
             InstructionParameter::Attribute("columns", std::to_string(columns))};
 }
@@ -131,9 +131,9 @@ HipVmProgram MatVecProgram(int fmt, int64_t rows, int64_t columns, int64_t paddi
 {
     HipVmProgram p;
     p.AddSlot({"weight", U8(1, static_cast<int64_t>(rows * RowBytes(fmt, columns)) + 2 * padding),
-               GraphResourceAccess::Read});
-    p.AddSlot({"input", F32(columns + 2 * padding), GraphResourceAccess::Read});
-    p.AddSlot({"output", F32(rows + 2 * padding), GraphResourceAccess::ReadWrite});
+               VmAccess::ReadOnly});
+    p.AddSlot({"input", F32(columns + 2 * padding), VmAccess::ReadOnly});
+    p.AddSlot({"output", F32(rows + 2 * padding), VmAccess::ReadWrite});
     p.AddDispatch("forward", MatVec(), MatVecParameters(fmt, rows, columns, padding, weight_port), kFp32);
     return p;
 }
@@ -141,15 +141,15 @@ HipVmProgram MatVecProgram(int fmt, int64_t rows, int64_t columns, int64_t paddi
 HipVmProgram GatherProgram(int fmt, int64_t rows, int64_t columns)
 {
     HipVmProgram p;
-    p.AddSlot({"table", U8(rows, RowBytes(fmt, columns)), GraphResourceAccess::Read});
-    p.AddSlot({"index", {GraphElementType::Int32, {1}}, GraphResourceAccess::ReadWrite});
-    p.AddSlot({"output", F32(columns), GraphResourceAccess::ReadWrite});
+    p.AddSlot({"table", U8(rows, RowBytes(fmt, columns)), VmAccess::ReadOnly});
+    p.AddSlot({"index", {GraphElementType::Int32, {1}}, VmAccess::ReadWrite});
+    p.AddSlot({"output", F32(columns), VmAccess::ReadWrite});
     p.AddDispatch("forward", GatherRow(),
                   {InstructionParameter::Tensor("table", U8(rows, RowBytes(fmt, columns)), GraphResourceAccess::Read,
                                                 "table"),
                    InstructionParameter::Tensor("index", {GraphElementType::Int32, {1}}, GraphResourceAccess::Read,
                                                 "index"),
-                   InstructionParameter::Tensor("output", F32(columns), GraphResourceAccess::ReadWrite, "output"),
+                   InstructionParameter::Tensor("output", F32(columns), GraphResourceAccess::Write, "output"),
                    InstructionParameter::Attribute("format", Name(fmt)),
                    InstructionParameter::Attribute("columns", std::to_string(columns))},
                   kFp32);
@@ -351,6 +351,88 @@ TEST(cpu, PrecisionRequirementsAboveTheSignatureAreRejectedWithTheProvidedProfil
     }
 }
 
+// The enums carry the reference's members in its order (GraphModel.cs:63-77,
+// VmProgram.cs:10), so values cross a managed binding unchanged.
+TEST(cpu, ElementTypeAndAccessEnumsMatchTheReference)
+{
+    ASSERT_TRUE(static_cast<int>(GraphElementType::Byte) == 0 && static_cast<int>(GraphElementType::Int32) == 1 &&
+                static_cast<int>(GraphElementType::UInt32) == 2 && static_cast<int>(GraphElementType::Float16) == 3 &&
+                static_cast<int>(GraphElementType::Float32) == 4);
+    ASSERT_TRUE(static_cast<int>(GraphResourceAccess::Read) == 0 && static_cast<int>(GraphResourceAccess::Write) == 1 &&
+                static_cast<int>(GraphResourceAccess::ReadWrite) == 2);
+    ASSERT_TRUE(static_cast<int>(VmAccess::ReadOnly) == 0 && static_cast<int>(VmAccess::ReadWrite) == 1);
+    ASSERT_TRUE(ElementSize(GraphElementType::Byte) == 1 && ElementSize(GraphElementType::Int32) == 4 &&
+                ElementSize(GraphElementType::UInt32) == 4 && ElementSize(GraphElementType::Float16) == 2 &&
+                ElementSize(GraphElementType::Float32) == 4);
+    // only floating-point types are precisions (OperatorBackend.cs:143-149)
+    ASSERT_THROWS(ArgumentException, Satisfies(GraphElementType::UInt32, GraphElementType::Float32));
+    ASSERT_THROWS(ArgumentException, Satisfies(GraphElementType::Float32, GraphElementType::Byte));
+}
+
+// A Write port accepts a Write or a ReadWrite parameter and rejects a Read
+// one; a Read port accepts any access (InstructionCollection.cs:163-165).
+TEST(cpu, WritePortsAcceptWriteAndReadWriteParameters)
+{
+    const auto mv = MatVec();
+    ASSERT_TRUE(mv->Signatures()[0].ports[2].access == GraphResourceAccess::Write);
+    auto p = MatVecParameters(SI_HIP_Q8_0, 7, 64, 0);
+    for (GraphResourceAccess a : {GraphResourceAccess::Write, GraphResourceAccess::ReadWrite}) {
+        p[2].access = a;
+        ASSERT_TRUE(mv->Adapt(p, kFp32).ports[2].name == "output");
+    }
+    p[2].access = GraphResourceAccess::Read;
+    ASSERT_THROWS(InstructionAdaptationException, mv->Adapt(p, kFp32));
+    p[2].access = GraphResourceAccess::Write;
+    p[1].access = GraphResourceAccess::ReadWrite;    // more access than a Read port asks for
+    ASSERT_TRUE(mv->Adapt(p, kFp32).ports[1].name == "input");
+}
+
+// An instruction with UInt32 ports: a UInt32 tensor adapts, an Int32 tensor
+// of the same shape does not (the element type is matched exactly).
+struct UInt32CopyInstruction : Instruction {
+    std::string CollectionId() const override { return HipInstructionCollectionIds::QuantizedFloat32; }
+    std::string Name() const override { return "test.copy-u32"; }
+    InstructionTarget Target() const override { return InstructionTarget::Hip(); }
+    std::vector<InstructionSignature> Signatures() const override
+    {
+        return {{{{"input", GraphElementType::UInt32, GraphResourceAccess::Read},
+                  {"output", GraphElementType::UInt32, GraphResourceAccess::Write}},
+                 {},
+                 {GraphElementType::Float32, GraphElementType::Float32}}};
+    }
+
+protected:
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override
+    {
+        return {"copy", parameters};
+    }
+};
+
+TEST(cpu, UInt32TensorsAdaptByExactElementType)
+{
+    UInt32CopyInstruction copy;
+    const TensorDescriptor u32{GraphElementType::UInt32, {5, 3}};
+    ASSERT_TRUE(u32.ByteLength() == 60);
+    std::vector<InstructionParameter> p{
+        InstructionParameter::Tensor("input", u32, GraphResourceAccess::Read, "a"),
+        InstructionParameter::Tensor("output", u32, GraphResourceAccess::Write, "b")};
+    ASSERT_TRUE(copy.Adapt(p, kFp32).ports[0].element_type == GraphElementType::UInt32);
+    p[0].tensor.element_type = GraphElementType::Int32;
+    ASSERT_THROWS(InstructionAdaptationException, copy.Adapt(p, kFp32));
+    // bound into a program: the UInt32 view must fit its slot, and a write
+    // into a read-only slot is rejected
+    HipVmProgram program;
+    program.AddSlot({"a", u32, VmAccess::ReadOnly});
+    program.AddSlot({"b", {GraphElementType::UInt32, {15}}, VmAccess::ReadOnly});
+    auto q = p;
+    q[0].tensor.element_type = GraphElementType::UInt32;
+    ASSERT_THROWS(InvalidDataException, program.AddDispatch("forward", std::make_shared<UInt32CopyInstruction>(), q, kFp32));
+    program.AddSlot({"c", {GraphElementType::UInt32, {15}}, VmAccess::ReadWrite});
+    q[1].source = "c";
+    program.AddDispatch("forward", std::make_shared<UInt32CopyInstruction>(), q, kFp32);
+    ASSERT_TRUE(program.Entries().at("forward").size() == 1);
+}
+
 struct OtherTargetRecorder : IInstructionRecorder {
     InstructionTarget Target() const override { return {"direct3d12"}; }
     void Record(InstructionRecording) override { throw Failure("recorded on a foreign target"); }
@@ -367,8 +449,8 @@ TEST(cpu, ProgramRejectsUnknownSlotsOversizedViewsWritesToReadSlotsAndAliasing)
     auto program = MatVecProgram(SI_HIP_Q8_0, 7, 65 * 32, 3);
     ASSERT_TRUE(program.Entries().at("forward").size() == 1);
     ASSERT_TRUE(program.Entries().at("forward")[0].recording.operation == "si_hip_gemv");
-    ASSERT_THROWS(InvalidDataException, program.AddSlot({"input", F32(4), GraphResourceAccess::Read}));
-    ASSERT_THROWS(InvalidDataException, program.AddSlot({"empty", F32(0), GraphResourceAccess::Read}));
+    ASSERT_THROWS(InvalidDataException, program.AddSlot({"input", F32(4), VmAccess::ReadOnly}));
+    ASSERT_THROWS(InvalidDataException, program.AddSlot({"empty", F32(0), VmAccess::ReadOnly}));
     auto p = MatVecParameters(SI_HIP_Q8_0, 7, 65 * 32, 3);
     auto unknown = p;
     unknown[1].source = "missing";
@@ -381,8 +463,8 @@ TEST(cpu, ProgramRejectsUnknownSlotsOversizedViewsWritesToReadSlotsAndAliasing)
     ASSERT_THROWS(InvalidDataException, program.AddDispatch("second", MatVec(), readonly, kFp32));
     // the output aliasing the input inside one writable slot
     HipVmProgram shared;
-    shared.AddSlot({"weight", U8(7, RowBytes(SI_HIP_Q8_0, 64)), GraphResourceAccess::Read});
-    shared.AddSlot({"buffer", F32(64), GraphResourceAccess::ReadWrite});
+    shared.AddSlot({"weight", U8(7, RowBytes(SI_HIP_Q8_0, 64)), VmAccess::ReadOnly});
+    shared.AddSlot({"buffer", F32(64), VmAccess::ReadWrite});
     auto aliased = MatVecParameters(SI_HIP_Q8_0, 7, 64, 0);
     aliased[1].source = aliased[2].source = "buffer";
     aliased[2].byte_offset = 4 * 32;

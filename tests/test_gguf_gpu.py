@@ -14,34 +14,9 @@ import pytest
 import oracle as orc
 from sharpinference_amd import gguf, native, phi4
 from sharpinference_amd.synth import synth_blocks
+from tests.phi3_files import write_phi3
 
 pytestmark = pytest.mark.gpu
-
-
-def write_phi3(path, cfg, rng, tied=False):
-    """A phi3-architecture GGUF with the tensor names of Phi4TextModel.cs."""
-    meta = {"general.architecture": (gguf.STRING, "phi3"),
-            "phi3.block_count": (gguf.U32, cfg.layers), "phi3.embedding_length": (gguf.U32, cfg.hidden),
-            "phi3.attention.head_count": (gguf.U32, cfg.heads),
-            "phi3.attention.head_count_kv": (gguf.U32, cfg.kv_heads),
-            "phi3.feed_forward_length": (gguf.U32, cfg.ffn), "phi3.rope.dimension_count": (gguf.U32, cfg.rotary_dim),
-            "phi3.attention.layer_norm_rms_epsilon": (gguf.F32, cfg.rms_eps),
-            "phi3.rope.freq_base": (gguf.F32, cfg.rope_base), "phi3.rope.scaling.attn_factor": (gguf.F32, 1.0)}
-    H, F = cfg.hidden, cfg.ffn
-    norm = lambda: (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
-    t = [("token_embd.weight", cfg.embed_format, [H, cfg.vocab], synth_blocks(cfg.embed_format, cfg.vocab, H, rng)),
-         ("output_norm.weight", native.F32, [H], norm())]
-    if not tied:
-        t.append(("output.weight", cfg.head_format, [H, cfg.vocab], synth_blocks(cfg.head_format, cfg.vocab, H, rng)))
-    wf = cfg.weight_format
-    for l in range(cfg.layers):
-        t += [(f"blk.{l}.attn_norm.weight", native.F32, [H], norm()),
-              (f"blk.{l}.attn_qkv.weight", wf, [H, cfg.qkv_rows], synth_blocks(wf, cfg.qkv_rows, H, rng)),
-              (f"blk.{l}.attn_output.weight", wf, [H, H], synth_blocks(wf, H, H, rng)),
-              (f"blk.{l}.ffn_norm.weight", native.F32, [H], norm()),
-              (f"blk.{l}.ffn_up.weight", wf, [H, 2 * F], synth_blocks(wf, 2 * F, H, rng)),
-              (f"blk.{l}.ffn_down.weight", wf, [F, H], synth_blocks(wf, H, F, rng))]
-    gguf.write_gguf(str(path), meta, t)
 
 
 def small_cfg():
@@ -49,20 +24,23 @@ def small_cfg():
                            vocab=500, capacity=64)
 
 
-@pytest.mark.parametrize("tied", [False, True])
-def test_phi3_gguf_decode_matches_oracle(hip, tmp_path, tied):
+@pytest.mark.parametrize("tied,norm_type", [(False, native.F32), (True, native.F32), (True, native.F16)],
+                         ids=["untied", "tied", "f16-norms"])
+def test_phi3_gguf_decode_matches_oracle(hip, tmp_path, tied, norm_type):
     cfg = small_cfg()
     path = tmp_path / "phi3.gguf"
-    write_phi3(path, cfg, np.random.default_rng(3 + tied), tied)
+    write_phi3(path, cfg, np.random.default_rng(3 + tied), tied, norm_type=norm_type)
     with gguf.GgufFile(str(path)) as g:
         loaded = phi4.Phi4Config.from_gguf(g, capacity=64)
         assert (loaded.layers, loaded.hidden, loaded.ffn, loaded.vocab, loaded.weight_format) == \
             (cfg.layers, cfg.hidden, cfg.ffn, cfg.vocab, cfg.weight_format)
         sess = phi4.Phi4DecodeSession.from_gguf(hip, g, capacity=64)
-        hb, f32 = g.host_bytes, (lambda n: g.host_bytes(n).view(np.float32))
+        hb = g.host_bytes
+        f32 = lambda n: g.host_bytes(n).view(np.float16 if norm_type == native.F16 else np.float32).astype(np.float32)
         L = range(cfg.layers)
-        w = SimpleNamespace(embed=hb("token_embd.weight"),
-                            lm_head=hb("token_embd.weight" if tied else "output.weight"),
+        # the head is token_embd.weight even when the file also holds an
+        # output.weight (GetLogits, Phi4TextModel.cs:95-105)
+        w = SimpleNamespace(embed=hb("token_embd.weight"), lm_head=hb("token_embd.weight"),
                             output_norm=f32("output_norm.weight"),
                             attn_norm=[f32(f"blk.{l}.attn_norm.weight") for l in L],
                             qkv=[hb(f"blk.{l}.attn_qkv.weight") for l in L],

@@ -76,18 +76,21 @@ CONFIG4 = [("qkv", 5120, 3072), ("o_proj", 3072, 3072), ("gate_up", 16384, 3072)
 
 @pytest.mark.parametrize("name,rows,cols", CONFIG4, ids=[c[0] for c in CONFIG4])
 def test_prefill_512_tokens_at_layer_shapes(hip, name, rows, cols):
-    """M = 512 tokens x the Phi-4-mini projections, Q4_0 weights, bf16 X; the
-    oracle checks a sample of 24 token rows spread over all 512."""
+    """M = 512 tokens x the Phi-4-mini projections, Q4_0 weights, bf16 X: all
+    512 token rows against the float64 product over the exactly dequantised
+    weights (equal to orc_gemm_prefill_f64, which a sample of 24 rows also
+    checks directly) and against the bf16-operand float64 product."""
     m = 512
     w = orc.gen_quant(native.Q4_0, 7 + rows, rows, cols)
     x = orc.gen_normal_bf16(8 + cols, m * cols)
     y = run_prefill(hip, native.Q4_0, w, x, m, rows, cols)
+    xd = orc.bf16_to_f32(x).reshape(m, cols).astype(np.float64)
+    wd = orc.dequant(native.Q4_0, w, rows, cols)
+    check(y, xd @ wd.astype(np.float64).T, 2e-2, name)
+    check(y, xd @ bf16_round(wd).astype(np.float64).T, 1e-5, name + " bf16 operands")
     sample = np.linspace(0, m - 1, 24).astype(int)
     xs = np.ascontiguousarray(x.reshape(m, cols)[sample])
-    truth = orc.gemm_prefill_f64(native.Q4_0, w, xs, len(sample), rows, cols)
-    check(y[sample], truth, 2e-2, name)
-    wb = bf16_round(orc.dequant(native.Q4_0, w, rows, cols)).astype(np.float64)
-    check(y[sample], orc.bf16_to_f32(xs).astype(np.float64) @ wb.T, 1e-5, name + " bf16 operands")
+    check(y[sample], orc.gemm_prefill_f64(native.Q4_0, w, xs, len(sample), rows, cols), 2e-2, name + " oracle rows")
 
 
 def test_prefill_rejects_bad_requests(hip):
