@@ -246,6 +246,19 @@ int si_hip_attention_workspace_bytes(int heads, int capacity, uint64_t* bytes);
  * (Phi4D3D12TextSession.cs:873-890). */
 int si_hip_attention_decode(si_hip_context* ctx, const si_hip_attention* args);
 
+/* si_hip_attention_decode without a workspace: args->workspace must be
+ * NULL, and the chunk partials and rotary table go to a device array of the
+ * library (2 MiB per GPU, held until the process ends), so the call
+ * allocates nothing (no hipMalloc, no allocating library routine).  Requests
+ * whose workspace (si_hip_attention_workspace_bytes) exceeds 2 MiB, i.e.
+ * heads * ceil(capacity / 64) > 4032, fail with SI_HIP_ERR_UNSUPPORTED.
+ * Every context on one GPU shares the array: calls that overlap on one GPU
+ * (other contexts' streams, or this one's with another thread's work) race.
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, hosts that
+ * forbid allocation after start-up). */
+int si_hip_attention_decode_noalloc(si_hip_context* ctx, const si_hip_attention* args);
+
 int si_hip_argmax_workspace_bytes(uint64_t* bytes);
 
 /* *index = first index of the maximum of values[0..n).  Replaces:

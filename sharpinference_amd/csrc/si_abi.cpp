@@ -2,6 +2,7 @@
 // contexts, device memory, the quantized matrix-vector entry points,
 // recorded plans (HIP graphs) and event timing.
 #include "si_context.hpp"
+#include "si_decode.hpp"
 
 #include <vector>
 
@@ -104,6 +105,12 @@ int si_hip_init(int device, si_hip_context** out)
         return hip_fail(nullptr, e, "hipSetDevice");
     auto* ctx = new si_hip_context();
     ctx->device = device;
+    // the device address of the library's attention scratch on this GPU
+    // (looked up once per device, with the device current)
+    if ((e = si::attention_scratch(device, &ctx->attention_scratch)) != hipSuccess) {
+        delete ctx;
+        return hip_fail(nullptr, e, "hipGetSymbolAddress (attention scratch)");
+    }
     if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&ctx->t0)) != hipSuccess || (e = hipEventCreate(&ctx->t1)) != hipSuccess) {
         hip_fail(nullptr, e, "init");

@@ -17,6 +17,7 @@ struct si_hip_context {
     hipEvent_t t1 = nullptr;
     bool timer_open = false;
     bool recording = false;
+    float* attention_scratch = nullptr;   // device address of the library's attention scratch on `device`
     std::string error;
     std::recursive_mutex gate;
 };

@@ -18,8 +18,19 @@
 
 #include <hip/hip_fp16.h>
 
+#include <map>
+#include <mutex>
+
 namespace si {
 namespace {
+
+// Attention workspace of the allocation-free entry point: chunk partials
+// and the rotary table, as a caller-provided workspace holds them.  Every
+// context on one GPU shares this array; it keeps the last call's contents,
+// and nothing in it has to start at zero (each call writes every partial
+// and table entry it reads).  Host code never passes `scratch` itself to a
+// kernel: it passes the address attention_scratch() looked up.
+static __device__ __align__(256) float scratch[ATTENTION_SCRATCH_FLOATS];
 
 constexpr int HEAD_DIM = 128;
 constexpr int CHUNK = 64;          // cache positions per attention workgroup
@@ -796,6 +807,25 @@ int64_t attention_workspace_floats(int heads, int capacity)
 }
 
 int64_t argmax_workspace_bytes() { return AM_BLOCKS * 8; }
+
+hipError_t attention_scratch(int device, float** out)
+{
+    static std::mutex lock;
+    static std::map<int, float*> address;   // one copy of the array per GPU
+    std::lock_guard<std::mutex> hold(lock);
+    const auto it = address.find(device);
+    if (it != address.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+        return e != hipSuccess ? e : hipErrorInvalidSymbol;
+    address[device] = static_cast<float*>(p);
+    *out = static_cast<float*>(p);
+    return hipSuccess;
+}
 
 hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index, float* out,
                              hipStream_t s)

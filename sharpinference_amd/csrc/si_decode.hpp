@@ -29,6 +29,15 @@ struct AttentionArgs {
 };
 
 int64_t attention_workspace_floats(int heads, int capacity);
+
+// Largest attention workspace the library's own device scratch holds (the
+// allocation-free entry point): 524288 floats = 2 MiB per GPU, enough for
+// heads * ceil(capacity / 64) <= 4032 (e.g. 24 heads up to 10752 cached
+// positions, 32 heads up to 8064).
+constexpr int64_t ATTENTION_SCRATCH_FLOATS = 524288;
+// Device address of that scratch on `device` (looked up once per device,
+// with the device current; the caller makes it current).
+hipError_t attention_scratch(int device, float** out);
 int64_t argmax_workspace_bytes();
 hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index, float* out,
                              hipStream_t s);

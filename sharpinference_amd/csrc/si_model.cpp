@@ -386,6 +386,32 @@ int si_hip_attention_decode(si_hip_context* ctx, const si_hip_attention* args)
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "attention launch");
 }
 
+int si_hip_attention_decode_noalloc(si_hip_context* ctx, const si_hip_attention* args)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "attention_noalloc: null context");
+    Enter g(ctx);
+    if (!args)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "attention_noalloc: null arguments");
+    if (args->workspace)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT,
+                    "attention_noalloc: workspace must be NULL (the library's device scratch is used)");
+    if (args->heads > 0 && args->capacity > 0 &&
+        si::attention_workspace_floats(args->heads, args->capacity) > si::ATTENTION_SCRATCH_FLOATS)
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                    "attention_noalloc: %d heads at capacity %d need %lld workspace bytes; the library's scratch "
+                    "holds %lld (use si_hip_attention_decode with a workspace)",
+                    args->heads, args->capacity,
+                    static_cast<long long>(si::attention_workspace_floats(args->heads, args->capacity) * 4),
+                    static_cast<long long>(si::ATTENTION_SCRATCH_FLOATS * 4));
+    si_hip_attention a = *args;
+    a.workspace = ctx->attention_scratch;
+    if (const int rc = attention_check(ctx, &a))
+        return rc;
+    const hipError_t e = si::launch_attention(attention_args(&a), ctx->stream);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "attention_noalloc launch");
+}
+
 int si_hip_argmax_workspace_bytes(uint64_t* bytes)
 {
     if (!bytes)

@@ -169,6 +169,7 @@ SIGNATURES.update({
     "si_hip_gather_row": ([_vp, _i32, _vp, _i64, _i64, _vp, _vp], _i32),
     "si_hip_attention_workspace_bytes": ([_i32, _i32, ctypes.POINTER(_u64)], _i32),
     "si_hip_attention_decode": ([_vp, ctypes.POINTER(AttentionArgs)], _i32),
+    "si_hip_attention_decode_noalloc": ([_vp, ctypes.POINTER(AttentionArgs)], _i32),
     "si_hip_argmax_workspace_bytes": ([ctypes.POINTER(_u64)], _i32),
     "si_hip_argmax": ([_vp, _vp, _i64, _vp, _vp], _i32),
     "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
@@ -365,6 +366,10 @@ class HipContext:
 
     def attention(self, args: AttentionArgs) -> None:
         self._call(lib().si_hip_attention_decode, ctypes.byref(args))
+
+    def attention_noalloc(self, args: AttentionArgs) -> None:
+        """si_hip_attention_decode_noalloc: args.workspace must be NULL (0)."""
+        self._call(lib().si_hip_attention_decode_noalloc, ctypes.byref(args))
 
     def argmax(self, values: int, n: int, workspace: int, index: int) -> None:
         self._call(lib().si_hip_argmax, ctypes.c_void_p(int(values)), n, ctypes.c_void_p(int(workspace)),
