@@ -33,7 +33,7 @@ int hip_fail(si_hip_context* ctx, hipError_t e, const char* what)
                 what, hipGetErrorString(e), static_cast<int>(e));
 }
 
-bool is_quant(int fmt) { return fmt == si::FMT_Q8_0 || fmt == si::FMT_Q4_0 || fmt == si::FMT_Q4_K; }
+bool is_quant(int fmt) { return si::is_block_quant(fmt); }
 
 const char* fmt_name(int fmt)
 {
@@ -48,13 +48,15 @@ const char* fmt_name(int fmt)
     }
 }
 
-// Shared validation of a quantized [rows, cols] operand; returns 0 or a status.
+// Shared validation of a [rows, cols] weight operand (Q8_0, Q4_0, Q4_K, F16
+// or F32); returns 0 or a status.
 int check_matrix(si_hip_context* ctx, const char* op, int fmt, const void* w, int64_t rows, int64_t cols,
                  uint64_t* wbytes)
 {
-    if (!is_quant(fmt))
-        return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "%s: tensor type %s (%d) is not a block-quantized type", op,
-                    fmt_name(fmt), fmt);
+    if (!si::is_matrix_format(fmt))
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                    "%s: tensor type %s (%d) is not a weight format of the matrix kernels (Q8_0, Q4_0, Q4_K, F16, F32)",
+                    op, fmt_name(fmt), fmt);
     if (rows <= 0 || rows > INT32_MAX)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: rows %lld out of range 1..%d", op, static_cast<long long>(rows),
                     INT32_MAX);
@@ -313,6 +315,9 @@ int si_hip_gemm_prefill(si_hip_context* ctx, int format, const void* w, const vo
         return rc;
     if (m <= 0 || m > INT32_MAX)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: token count %lld out of range", static_cast<long long>(m));
+    if (!is_quant(format) && cols % 32 != 0)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: %s weights need a multiple of 32 columns, got %lld",
+                    fmt_name(format), static_cast<long long>(cols));
     if (!x_bf16 || !y)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: null input or output");
     if ((reinterpret_cast<uintptr_t>(x_bf16) & 15u) || (reinterpret_cast<uintptr_t>(y) & 3u))

@@ -61,7 +61,12 @@ __global__ __launch_bounds__(256) void gather_row_kernel(const uint8_t* __restri
         } else {
             const uint8_t* b = rp + (c / BE) * BB;
             const int e = c % BE;
-            if constexpr (FMT == FMT_Q8_0) {
+            if constexpr (FMT == FMT_F16) {
+                v = ld_half_u(b);
+            } else if constexpr (FMT == FMT_F32) {
+                v = __uint_as_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8) |
+                                    (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24));
+            } else if constexpr (FMT == FMT_Q8_0) {
                 v = __fmul_rn(ld_half_u(b), static_cast<float>(static_cast<int8_t>(b[2 + e])));
             } else if constexpr (FMT == FMT_Q4_0) {
                 const int q = e < 16 ? (b[2 + e] & 15) : (b[2 + e - 16] >> 4);
@@ -838,6 +843,8 @@ hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t c
     case FMT_Q8_0: hipLaunchKernelGGL((gather_row_kernel<FMT_Q8_0>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
     case FMT_Q4_0: hipLaunchKernelGGL((gather_row_kernel<FMT_Q4_0>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
     case FMT_Q4_K: hipLaunchKernelGGL((gather_row_kernel<FMT_Q4_K>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
+    case FMT_F16: hipLaunchKernelGGL((gather_row_kernel<FMT_F16>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
+    case FMT_F32: hipLaunchKernelGGL((gather_row_kernel<FMT_F32>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

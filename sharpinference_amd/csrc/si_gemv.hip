@@ -1,6 +1,6 @@
-// Quantized matrix-vector product y = W . x for GGUF Q8_0 / Q4_0 / Q4_K
-// weights kept in their native block layout, plus the bit-exact block
-// decoder used to check that layout.
+// Matrix-vector product y = W . x for GGUF Q8_0 / Q4_0 / Q4_K weights kept
+// in their native block layout and for dense F16 / F32 weights, plus the
+// bit-exact decoder used to check those layouts.
 //
 // Semantics follow the core.mat-vec contract
 // (SharpInference.Graphs/TierZeroOperationContracts.cs:113-115,152,161):
@@ -15,6 +15,7 @@
 //   Q4_0  two 18-byte blocks, 36 bytes =  9 dwords, dword aligned
 //   Q4_K  one 32-byte quant chunk of a 144-byte super-block plus the
 //         super-block's 16-byte header (d, dmin, 12 scale bytes)
+//   F16   128 bytes = 32 dwords;  F32  256 bytes = 64 dwords
 // A wave holds 64 / LK row slots of LK lanes; lane k of a slot takes units
 // k, k + LK, ... of RL consecutive rows, so every unit's x values are read
 // from LDS once and reused for RL rows.  All weight loads of a lane are
@@ -275,6 +276,72 @@ struct QUnit<FMT_Q4_K> {
             }
         }
         return a;
+    }
+};
+
+// 64 F16 weights (128 bytes, 32 words): each weight converted exactly to
+// FP32 and multiplied into the sum in one fused op (v_fma_mix_f32), the
+// reference's ConvertToSingle + Dot (CpuHalfMatrixOperators.cs:29-41).
+template <>
+struct QUnit<FMT_F16> {
+    static constexpr int UNIT_BYTES = 128;
+    uint32_t v[32];
+    __device__ __forceinline__ void prepare() {}
+
+    __device__ __forceinline__ void load(const uint8_t* row, int u)
+    {
+        const uint8_t* p = row + u * UNIT_BYTES;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const u32x4 a = ld4(p + 16 * i);
+            v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+        }
+    }
+
+    __device__ __forceinline__ float half(int h, const float4* x, float /*sx*/) const
+    {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t w0 = v[16 * h + 2 * k], w1 = v[16 * h + 2 * k + 1];
+            a0 = fmaf(half_lo(w0), x[k].x, a0);
+            a1 = fmaf(half_hi(w0), x[k].y, a1);
+            a0 = fmaf(half_lo(w1), x[k].z, a0);
+            a1 = fmaf(half_hi(w1), x[k].w, a1);
+        }
+        return a0 + a1;
+    }
+};
+
+// 64 F32 weights (256 bytes), one FMA each (CpuPrimitiveOperatorBackend.cs:222-227).
+template <>
+struct QUnit<FMT_F32> {
+    static constexpr int UNIT_BYTES = 256;
+    uint32_t v[64];
+    __device__ __forceinline__ void prepare() {}
+
+    __device__ __forceinline__ void load(const uint8_t* row, int u)
+    {
+        const uint8_t* p = row + u * UNIT_BYTES;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const u32x4 a = ld4(p + 16 * i);
+            v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+        }
+    }
+
+    __device__ __forceinline__ float half(int h, const float4* x, float /*sx*/) const
+    {
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t* w = v + 32 * h + 4 * k;
+            a0 = fmaf(__uint_as_float(w[0]), x[k].x, a0);
+            a1 = fmaf(__uint_as_float(w[1]), x[k].y, a1);
+            a0 = fmaf(__uint_as_float(w[2]), x[k].z, a0);
+            a1 = fmaf(__uint_as_float(w[3]), x[k].w, a1);
+        }
+        return a0 + a1;
     }
 };
 
@@ -634,7 +701,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     // non-finite or huge (|x| > 2^100) value stores NaN instead (NaN fails
     // every comparison, so it counts as wide too): its products then take
     // the per-weight form, which keeps each product's IEEE class.
-    constexpr bool SUMS = FMT != FMT_Q8_0;
+    constexpr bool SUMS = FMT == FMT_Q4_0 || FMT == FMT_Q4_K;
     if constexpr (SUMS) {
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
@@ -817,12 +884,40 @@ __device__ float block_dot<FMT_Q4_K>(const uint8_t* b, const float* x)
     return a;
 }
 
+// One F16 / F32 weight from its bytes (byte loads: no alignment needs).
+template <int FMT>
+__device__ __forceinline__ float elem(const uint8_t* p)
+{
+    if constexpr (FMT == FMT_F16)
+        return ld_half(p);
+    return __uint_as_float(static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) |
+                           (static_cast<uint32_t>(p[2]) << 16) | (static_cast<uint32_t>(p[3]) << 24));
+}
+
+template <>
+__device__ float block_dot<FMT_F16>(const uint8_t* b, const float* x)
+{
+    return elem<FMT_F16>(b) * x[0];
+}
+
+template <>
+__device__ float block_dot<FMT_F32>(const uint8_t* b, const float* x)
+{
+    return elem<FMT_F32>(b) * x[0];
+}
+
 template <int FMT>
 __device__ __forceinline__ float row_dot(const uint8_t* rp, const float* x, int blocks, int lane)
 {
     float acc = 0.0f;
-    for (int k = lane; k < blocks; k += 64)
-        acc += block_dot<FMT>(rp + static_cast<int64_t>(k) * block_bytes(FMT), x + static_cast<int64_t>(k) * block_elems(FMT));
+    if constexpr (block_elems(FMT) == 1) {   // F16 / F32: one fused multiply-add per weight
+        for (int k = lane; k < blocks; k += 64)
+            acc = fmaf(elem<FMT>(rp + static_cast<int64_t>(k) * block_bytes(FMT)), x[k], acc);
+    } else {
+        for (int k = lane; k < blocks; k += 64)
+            acc += block_dot<FMT>(rp + static_cast<int64_t>(k) * block_bytes(FMT),
+                                  x + static_cast<int64_t>(k) * block_elems(FMT));
+    }
     for (int off = 32; off > 0; off >>= 1)
         acc += __shfl_xor(acc, off);
     return acc;
@@ -911,7 +1006,9 @@ __global__ __launch_bounds__(WG) void dequant_kernel(const uint8_t* __restrict__
         return;
     const uint8_t* b = W + blk * block_bytes(FMT);
     float* o = out + blk * block_elems(FMT);
-    if constexpr (FMT == FMT_Q8_0) {
+    if constexpr (FMT == FMT_F16 || FMT == FMT_F32) {
+        o[0] = elem<FMT>(b);
+    } else if constexpr (FMT == FMT_Q8_0) {
         const float d = ld_half(b);
         for (int i = 0; i < 32; i++)
             o[i] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(b[2 + i])));
@@ -1078,6 +1175,36 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     }
 }
 
+// Shape table of the F16 / F32 weights (2 and 4 bytes per weight: the
+// streams are 2-4x a Q8_0 row's, so fewer units per lane keep the registers
+// of a wave's loads in bounds: F16 units are 32 words, F32 units 64).
+template <int FMT>
+hipError_t launch_fast_dense(const GemvOp* ops, int n, int64_t rows64, int64_t cols, hipStream_t s)
+{
+    const bool mid = rows64 >= 12288;
+    if constexpr (FMT == FMT_F32) {
+        switch (cols) {
+        case 1024: return launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
+        case 2048: return launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
+        case 3072: return launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+        case 4096: return launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
+        case 6144: return launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
+        case 8192: return launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
+        default: return hipErrorNotSupported;
+        }
+    } else {
+        switch (cols) {
+        case 1024: return launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
+        case 2048: return mid ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
+        case 3072: return mid ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+        case 4096: return mid ? launch_tiled<FMT, 16, 2, 1, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
+        case 6144: return mid ? launch_tiled<FMT, 16, 3, 1, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
+        case 8192: return mid ? launch_tiled<FMT, 16, 2, 1, 4, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
+        default: return hipErrorNotSupported;
+        }
+    }
+}
+
 template <int FMT>
 hipError_t launch_generic(const GemvOp* ops, int n, hipStream_t s)
 {
@@ -1138,6 +1265,8 @@ hipError_t launch_group(const GemvOp* ops, int n, int kind, hipStream_t s)
         case FMT_Q8_0: return sh ? launch_short<FMT_Q8_0>(ops, n, s) : launch_generic<FMT_Q8_0>(ops, n, s);
         case FMT_Q4_0: return sh ? launch_short<FMT_Q4_0>(ops, n, s) : launch_generic<FMT_Q4_0>(ops, n, s);
         case FMT_Q4_K: return sh ? launch_short<FMT_Q4_K>(ops, n, s) : launch_generic<FMT_Q4_K>(ops, n, s);
+        case FMT_F16: return sh ? launch_short<FMT_F16>(ops, n, s) : launch_generic<FMT_F16>(ops, n, s);
+        case FMT_F32: return sh ? launch_short<FMT_F32>(ops, n, s) : launch_generic<FMT_F32>(ops, n, s);
         default: return hipErrorInvalidValue;
         }
     }
@@ -1148,6 +1277,8 @@ hipError_t launch_group(const GemvOp* ops, int n, int kind, hipStream_t s)
     case FMT_Q8_0: return launch_fast<FMT_Q8_0>(ops, n, wrows, ops[0].cols, s);
     case FMT_Q4_0: return launch_fast<FMT_Q4_0>(ops, n, wrows, ops[0].cols, s);
     case FMT_Q4_K: return launch_fast<FMT_Q4_K>(ops, n, wrows, ops[0].cols, s);
+    case FMT_F16: return launch_fast_dense<FMT_F16>(ops, n, wrows, ops[0].cols, s);
+    case FMT_F32: return launch_fast_dense<FMT_F32>(ops, n, wrows, ops[0].cols, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -1207,6 +1338,8 @@ hipError_t launch_dequant(int fmt, const void* wv, float* out, int64_t rows, int
     case FMT_Q8_0: hipLaunchKernelGGL((dequant_kernel<FMT_Q8_0>), grid, dim3(WG), 0, s, w, out, nblocks); break;
     case FMT_Q4_0: hipLaunchKernelGGL((dequant_kernel<FMT_Q4_0>), grid, dim3(WG), 0, s, w, out, nblocks); break;
     case FMT_Q4_K: hipLaunchKernelGGL((dequant_kernel<FMT_Q4_K>), grid, dim3(WG), 0, s, w, out, nblocks); break;
+    case FMT_F16: hipLaunchKernelGGL((dequant_kernel<FMT_F16>), grid, dim3(WG), 0, s, w, out, nblocks); break;
+    case FMT_F32: hipLaunchKernelGGL((dequant_kernel<FMT_F32>), grid, dim3(WG), 0, s, w, out, nblocks); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -16,15 +16,21 @@ enum Format : int {
     FMT_Q4_K = 12,
 };
 
-// Elements and bytes per block; 0 for formats the quantized path does not take.
+// Elements and bytes per block (an F16 / F32 "block" is one element); 0 for
+// formats the matrix kernels do not take.
 constexpr int block_elems(int fmt)
 {
-    return fmt == FMT_Q4_0 || fmt == FMT_Q8_0 ? 32 : fmt == FMT_Q4_K ? 256 : 0;
+    return fmt == FMT_Q4_0 || fmt == FMT_Q8_0 ? 32 : fmt == FMT_Q4_K ? 256 : fmt == FMT_F16 || fmt == FMT_F32 ? 1 : 0;
 }
 constexpr int block_bytes(int fmt)
 {
-    return fmt == FMT_Q4_0 ? 18 : fmt == FMT_Q8_0 ? 34 : fmt == FMT_Q4_K ? 144 : 0;
+    return fmt == FMT_Q4_0 ? 18 : fmt == FMT_Q8_0 ? 34 : fmt == FMT_Q4_K ? 144 : fmt == FMT_F16 ? 2 : fmt == FMT_F32 ? 4 : 0;
 }
+constexpr bool is_block_quant(int fmt) { return fmt == FMT_Q4_0 || fmt == FMT_Q8_0 || fmt == FMT_Q4_K; }
+// Weight formats of the matrix-vector kernels: the block-quantized ones and
+// the dense F16 / F32 of the reference's own core.mat-vec
+// (TierZeroOperationContracts.cs:161).
+constexpr bool is_matrix_format(int fmt) { return is_block_quant(fmt) || fmt == FMT_F16 || fmt == FMT_F32; }
 
 // Bytes of one row of `cols` elements, or -1 when cols is not a whole number
 // of blocks (GgufModelFile.cs:323-329 rejects such tensors the same way).

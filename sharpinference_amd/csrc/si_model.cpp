@@ -88,8 +88,10 @@ int phi4_check(si_hip_context* ctx, const si_hip_phi4_model* m)
                     "phi4: hidden %d and ffn %d must be tiled column counts (1024/2048/3072/4096/6144/8192) "
                     "for the fused norms", m->hidden, m->ffn);
     for (int fmt : {m->weight_format, m->embed_format, m->head_format})
-        if (!is_quant(fmt))
-            return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "phi4: tensor type %d is not block-quantized", fmt);
+        if (!si::is_matrix_format(fmt))
+            return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                        "phi4: tensor type %d is not a weight format of the matrix kernels (Q8_0, Q4_0, Q4_K, F16, F32)",
+                        fmt);
     if (si::row_bytes(m->weight_format, m->hidden) < 0 || si::row_bytes(m->weight_format, m->ffn) < 0 ||
         si::row_bytes(m->embed_format, m->hidden) < 0 || si::row_bytes(m->head_format, m->hidden) < 0)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4: hidden/ffn are not whole blocks of the weight formats");

@@ -1,6 +1,7 @@
 // Batched prefill product Y[m, n] = sum_k X[m, k] * W[n, k] on MFMA.
 //
-// W is a GGUF block-quantized matrix [N, K] (Q4_0, Q8_0 or Q4_K), X holds M
+// W is a GGUF matrix [N, K] (Q4_0, Q8_0, Q4_K, or F16 / F32 with K a
+// multiple of 32), X holds M
 // token rows of bf16 activations [M, K], Y is FP32 [M, N] (one output row per
 // token), FP32 accumulation.  Reference semantics: the transpose_right branch
 // of CpuInstructionNumerics.MatrixMultiply
@@ -57,9 +58,11 @@ constexpr int PF_DEPTH = 2;         // steps of loads in flight (even: LDS buffe
 // Raw words of one item of 16 values (half a 32-value block of one W row),
 // loaded steps ahead of their decode.  The loads are plain word loads and
 // every bit extraction happens at decode time, so a word in flight is never
-// touched before its decode.
-struct Raw16 {
-    uint32_t w[8];
+// touched before its decode.  An F32 item is 16 words, every other format's
+// at most 8.
+template <int FMT>
+struct RawW {
+    uint32_t w[FMT == FMT_F32 ? 16 : 8];
 };
 
 typedef uint32_t u32_a2 __attribute__((aligned(2)));   // 4 bytes at a 2-byte aligned address
@@ -93,14 +96,14 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v)
 //        scale words and the 16 quant bytes of elements 16h..16h+15 (nibble
 //        j % 2 of qs[32 (j / 2) + 16h ..]).
 template <int FMT>
-__device__ __forceinline__ Raw16 load_raw(const uint8_t* W, uint32_t row_off, int blk, int h);
+__device__ __forceinline__ RawW<FMT> load_raw(const uint8_t* W, uint32_t row_off, int blk, int h);
 
 template <>
-__device__ __forceinline__ Raw16 load_raw<FMT_Q4_0>(const uint8_t* W, uint32_t row_off, int blk, int h)
+__device__ __forceinline__ RawW<FMT_Q4_0> load_raw<FMT_Q4_0>(const uint8_t* W, uint32_t row_off, int blk, int h)
 {
     const uint8_t* b = W + blk * 18;
     row_off = opaque(row_off);
-    Raw16 r;
+    RawW<FMT_Q4_0> r;
     r.w[0] = ld_u16(b + row_off);
     r.w[1] = ld_u32_a2(b + (row_off + 2 + 8 * h));
     r.w[2] = ld_u32_a2(b + (row_off + 6 + 8 * h));
@@ -108,11 +111,11 @@ __device__ __forceinline__ Raw16 load_raw<FMT_Q4_0>(const uint8_t* W, uint32_t r
 }
 
 template <>
-__device__ __forceinline__ Raw16 load_raw<FMT_Q8_0>(const uint8_t* W, uint32_t row_off, int blk, int h)
+__device__ __forceinline__ RawW<FMT_Q8_0> load_raw<FMT_Q8_0>(const uint8_t* W, uint32_t row_off, int blk, int h)
 {
     const uint8_t* b = W + blk * 34;
     row_off = opaque(row_off);
-    Raw16 r;
+    RawW<FMT_Q8_0> r;
     r.w[0] = ld_u16(b + row_off);
 #pragma unroll
     for (int k = 0; k < 4; k++)
@@ -121,12 +124,12 @@ __device__ __forceinline__ Raw16 load_raw<FMT_Q8_0>(const uint8_t* W, uint32_t r
 }
 
 template <>
-__device__ __forceinline__ Raw16 load_raw<FMT_Q4_K>(const uint8_t* W, uint32_t row_off, int blk, int h)
+__device__ __forceinline__ RawW<FMT_Q4_K> load_raw<FMT_Q4_K>(const uint8_t* W, uint32_t row_off, int blk, int h)
 {
     const uint8_t* b = W + (blk >> 3) * 144;
     const int j = blk & 7;
     row_off = opaque(row_off);
-    Raw16 r;
+    RawW<FMT_Q4_K> r;
     r.w[0] = ld_u32(b + row_off);
     r.w[1] = ld_u32(b + (row_off + 4));
     r.w[2] = ld_u32(b + (row_off + 8));
@@ -134,6 +137,32 @@ __device__ __forceinline__ Raw16 load_raw<FMT_Q4_K>(const uint8_t* W, uint32_t r
 #pragma unroll
     for (int k = 0; k < 4; k++)
         r.w[4 + k] = ld_u32(b + 16 + 32 * (j >> 1) + (row_off + 16 * h + 4 * k));
+    return r;
+}
+
+// F16 / F32 (dense rows, a "block" is 32 consecutive elements): item h is
+// elements 16h..16h+15, 8 words (F16) or 16 words (F32).
+template <>
+__device__ __forceinline__ RawW<FMT_F16> load_raw<FMT_F16>(const uint8_t* W, uint32_t row_off, int blk, int h)
+{
+    const uint8_t* b = W + blk * 64 + 32 * h;
+    row_off = opaque(row_off);
+    RawW<FMT_F16> r;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        r.w[k] = ld_u32(b + (row_off + 4 * k));
+    return r;
+}
+
+template <>
+__device__ __forceinline__ RawW<FMT_F32> load_raw<FMT_F32>(const uint8_t* W, uint32_t row_off, int blk, int h)
+{
+    const uint8_t* b = W + blk * 128 + 64 * h;
+    row_off = opaque(row_off);
+    RawW<FMT_F32> r;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        r.w[k] = ld_u32(b + (row_off + 4 * k));
     return r;
 }
 
@@ -168,11 +197,11 @@ __device__ __forceinline__ bf16x8 decode8(uint32_t q0, uint32_t q1, float a, flo
 // into the scale, which stays exact (a power of two).  The two halves of
 // 8 values go to columns c0 and c1 of the block.
 template <int FMT>
-__device__ __forceinline__ void decode_raw(const Raw16& r, int blk, int h, bf16x8& v0, bf16x8& v1, int& c0,
+__device__ __forceinline__ void decode_raw(const RawW<FMT>& r, int blk, int h, bf16x8& v0, bf16x8& v1, int& c0,
                                            int& c1);
 
 template <>
-__device__ __forceinline__ void decode_raw<FMT_Q4_0>(const Raw16& r, int, int h, bf16x8& v0, bf16x8& v1, int& c0,
+__device__ __forceinline__ void decode_raw<FMT_Q4_0>(const RawW<FMT_Q4_0>& r, int, int h, bf16x8& v0, bf16x8& v1, int& c0,
                                                      int& c1)
 {
     const float d = half_bits(r.w[0]);
@@ -184,7 +213,7 @@ __device__ __forceinline__ void decode_raw<FMT_Q4_0>(const Raw16& r, int, int h,
 }
 
 template <>
-__device__ __forceinline__ void decode_raw<FMT_Q8_0>(const Raw16& r, int, int h, bf16x8& v0, bf16x8& v1, int& c0,
+__device__ __forceinline__ void decode_raw<FMT_Q8_0>(const RawW<FMT_Q8_0>& r, int, int h, bf16x8& v0, bf16x8& v1, int& c0,
                                                      int& c1)
 {
     const float d = half_bits(r.w[0]);
@@ -198,7 +227,7 @@ __device__ __forceinline__ void decode_raw<FMT_Q8_0>(const Raw16& r, int, int h,
 // 6-bit scale and min of sub-block j (GGML get_scale_min_k4) from the
 // scale words lo = scales[0..3], mid = scales[4..7], hi = scales[8..11].
 template <>
-__device__ __forceinline__ void decode_raw<FMT_Q4_K>(const Raw16& r, int blk, int h, bf16x8& v0, bf16x8& v1, int& c0,
+__device__ __forceinline__ void decode_raw<FMT_Q4_K>(const RawW<FMT_Q4_K>& r, int blk, int h, bf16x8& v0, bf16x8& v1, int& c0,
                                                      int& c1)
 {
     const int j = blk & 7;
@@ -220,6 +249,42 @@ __device__ __forceinline__ void decode_raw<FMT_Q4_K>(const Raw16& r, int blk, in
     const float a = high ? d1 * 0.0625f : d1;
     v0 = decode8(opaque(r.w[4] & mask), opaque(r.w[5] & mask), a, -m1);
     v1 = decode8(opaque(r.w[6] & mask), opaque(r.w[7] & mask), a, -m1);
+    c0 = 16 * h;
+    c1 = 16 * h + 8;
+}
+
+// F16: each value converted exactly to FP32, then rounded to bf16 (one
+// rounding from the exact value).  F32: rounded to bf16.
+template <>
+__device__ __forceinline__ void decode_raw<FMT_F16>(const RawW<FMT_F16>& r, int, int h, bf16x8& v0, bf16x8& v1,
+                                                    int& c0, int& c1)
+{
+    f32x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        a[2 * i] = half_bits(r.w[i]);
+        a[2 * i + 1] = half_bits(r.w[i] >> 16);
+        b[2 * i] = half_bits(r.w[4 + i]);
+        b[2 * i + 1] = half_bits(r.w[4 + i] >> 16);
+    }
+    v0 = __builtin_convertvector(a, bf16x8);
+    v1 = __builtin_convertvector(b, bf16x8);
+    c0 = 16 * h;
+    c1 = 16 * h + 8;
+}
+
+template <>
+__device__ __forceinline__ void decode_raw<FMT_F32>(const RawW<FMT_F32>& r, int, int h, bf16x8& v0, bf16x8& v1,
+                                                    int& c0, int& c1)
+{
+    f32x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = __uint_as_float(r.w[i]);
+        b[i] = __uint_as_float(r.w[8 + i]);
+    }
+    v0 = __builtin_convertvector(a, bf16x8);
+    v1 = __builtin_convertvector(b, bf16x8);
     c0 = 16 * h;
     c1 = 16 * h + 8;
 }
@@ -323,9 +388,9 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
             acc[mt][nt] = f32x16{};
 
     // ring slot s % D holds the W words and X chunks of local step s
-    Raw16 raw[D][WI];
+    RawW<FMT> raw[D][WI];
     u32x4 xr[D][XL];
-    auto load_step = [&](int ls, Raw16 (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
+    auto load_step = [&](int ls, RawW<FMT> (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
         const int step = step0 + ls;
         const int blk = min(BPS * step + wbo, nblk - 1);
 #pragma unroll
@@ -338,7 +403,7 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
         for (int e = 0; e < XL; e++)
             xdst_regs[e] = *reinterpret_cast<const u32x4*>(xbytes + (xoff[e] + static_cast<uint32_t>(2 * col)));
     };
-    auto store_step = [&](int ls, const Raw16 (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
+    auto store_step = [&](int ls, const RawW<FMT> (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
         const int blk = min(BPS * (step0 + ls) + wbo, nblk - 1);
 #pragma unroll
         for (int i = 0; i < WI; i++) {
@@ -384,7 +449,7 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
 
     // prologue: local step 0 in LDS; steps 1..D in flight
     {
-        Raw16 w0[WI];
+        RawW<FMT> w0[WI];
         u32x4 x0[XL];
         load_step(0, w0, x0);
 #pragma unroll
@@ -584,9 +649,9 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
             wrow[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * static_cast<uint32_t>(row_bytes);
         }
         const int wh = t & 1, wbo = (t >> 1) & 1;
-        Raw16 raw[D][WI];
+        RawW<FMT> raw[D][WI];
         u32x4 xr[D][XL];
-        auto load_step = [&](int step, Raw16 (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
+        auto load_step = [&](int step, RawW<FMT> (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
             const int blk = min(BPS * step + wbo, nblk - 1);
 #pragma unroll
             for (int i = 0; i < WI; i++)
@@ -596,7 +661,7 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
             for (int e = 0; e < XL; e++)
                 xdst_regs[e] = *reinterpret_cast<const u32x4*>(xbytes + (xoff[e] + static_cast<uint32_t>(2 * col)));
         };
-        auto store_step = [&](int step, const Raw16 (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
+        auto store_step = [&](int step, const RawW<FMT> (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
             const int blk = min(BPS * step + wbo, nblk - 1);
 #pragma unroll
             for (int i = 0; i < WI; i++) {
@@ -612,7 +677,7 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
                 xs[buf][xdst[e]] = xsrc_regs[e];
         };
         {
-            Raw16 w0[WI];
+            RawW<FMT> w0[WI];
             u32x4 x0[XL];
             load_step(0, w0, x0);
 #pragma unroll
@@ -702,6 +767,10 @@ hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, 
     case FMT_Q8_0: return launch_prefill_fmt<FMT_Q8_0>(w, x_bf16, y, m, rows, cols, stream);
     case FMT_Q4_0: return launch_prefill_fmt<FMT_Q4_0>(w, x_bf16, y, m, rows, cols, stream);
     case FMT_Q4_K: return launch_prefill_fmt<FMT_Q4_K>(w, x_bf16, y, m, rows, cols, stream);
+    case FMT_F16: return cols % 32 == 0 ? launch_prefill_fmt<FMT_F16>(w, x_bf16, y, m, rows, cols, stream)
+                                        : hipErrorInvalidValue;
+    case FMT_F32: return cols % 32 == 0 ? launch_prefill_fmt<FMT_F32>(w, x_bf16, y, m, rows, cols, stream)
+                                        : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 }

@@ -74,8 +74,9 @@ int rwkv7_check(si_hip_context* ctx, const si_hip_rwkv7_model* m)
         return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
                     "rwkv7: hidden %d and ffn %d must be tiled column counts (1024/2048/3072/4096/6144/8192) for the "
                     "fused LayerNorm", m->hidden, m->ffn);
-    if (!is_quant(m->weight_format) || !is_quant(m->embed_format) || !is_quant(m->head_format))
-        return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "rwkv7: formats must be Q8_0, Q4_0 or Q4_K");
+    if (!si::is_matrix_format(m->weight_format) || !si::is_matrix_format(m->embed_format) ||
+        !si::is_matrix_format(m->head_format))
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "rwkv7: formats must be Q8_0, Q4_0, Q4_K, F16 or F32");
     const int be = si::block_elems(m->weight_format);
     for (int rank : {m->rank_w, m->rank_a, m->rank_g, m->rank_v})
         if (rank < 1 || rank % be != 0)

@@ -21,7 +21,7 @@ F32, F16, Q4_0, Q8_0, Q4_K, BF16 = 0, 1, 2, 8, 12, 30
 FORMAT_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", BF16: "bf16"}
 BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
 # Weight formats the matrix-vector kernels decode.
-MATRIX_FORMATS = (Q8_0, Q4_0, Q4_K)
+MATRIX_FORMATS = (Q8_0, Q4_0, Q4_K, F16, F32)
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
 
 OK, ERR_ARGUMENT, ERR_UNSUPPORTED, ERR_ADAPTATION, ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_STATE, ERR_FORMAT, ERR_IO = range(9)

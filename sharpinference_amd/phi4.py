@@ -281,10 +281,12 @@ def check_gguf_tensors(g, cfg: Phi4Config) -> Dict[str, np.ndarray]:
 
 # ---- synthetic weights --------------------------------------------------------------
 
-def synth_weights(cfg: Phi4Config, seed: int = 0, distinct_layers: int = 0) -> Phi4Weights:
+def synth_weights(cfg: Phi4Config, seed: int = 0, distinct_layers: int = 0, tied: bool = False) -> Phi4Weights:
     """Random Phi-4-shaped weights.  distinct_layers = 0 gives every layer
     its own tensors; n > 0 generates n layers and reuses them cyclically
-    (each layer still gets its own device copy when uploaded)."""
+    (each layer still gets its own device copy when uploaded).  tied = True
+    projects onto the embedding table, as the reference model does
+    (Phi4TextModel.cs:95-105)."""
     rng = np.random.default_rng(seed)
     n = cfg.layers if distinct_layers <= 0 else min(distinct_layers, cfg.layers)
     shapes = cfg.layer_shapes()
@@ -293,9 +295,11 @@ def synth_weights(cfg: Phi4Config, seed: int = 0, distinct_layers: int = 0) -> P
     attn_norm = [norm() for _ in range(n)]
     ffn_norm = [norm() for _ in range(n)]
     pick = lambda lst: [lst[i % n] for i in range(cfg.layers)]
+    embed = synth_blocks(cfg.embed_format, cfg.vocab, cfg.hidden, rng)
+    if tied and cfg.head_format != cfg.embed_format:
+        raise ValueError("a tied head has the embedding's format")
     return Phi4Weights(
-        embed=synth_blocks(cfg.embed_format, cfg.vocab, cfg.hidden, rng),
-        lm_head=synth_blocks(cfg.head_format, cfg.vocab, cfg.hidden, rng),
+        embed=embed, lm_head=embed if tied else synth_blocks(cfg.head_format, cfg.vocab, cfg.hidden, rng),
         output_norm=norm(), attn_norm=pick(attn_norm), qkv=pick(gen["qkv"]), o=pick(gen["o"]),
         ffn_norm=pick(ffn_norm), up=pick(gen["up"]), down=pick(gen["down"]))
 

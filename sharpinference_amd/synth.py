@@ -15,7 +15,15 @@ def synth_blocks(fmt: int, rows: int, cols: int, rng: np.random.Generator, sigma
     """GGUF blocks with the benchmark distributions: Q8_0 q ~ U{-127..127},
     d = |N(0, sigma)| / 127; Q4_0 nibbles ~ U{0..15}, d = |N(0, sigma)| / 8;
     Q4_K q ~ U{0..15}, 6-bit sc, m ~ U{0..63}, d = |N(0, sigma)| / 504,
-    dmin = |N(0, sigma)| / 63."""
+    dmin = |N(0, sigma)| / 63; F16 / F32 weights N(0, sigma)."""
+    if fmt in (native.F16, native.F32):
+        dt = np.float16 if fmt == native.F16 else np.float32
+        out = np.empty(rows * cols, dt)
+        step = 1 << 24   # generated in slices so a large table needs no float64 copy of itself
+        for i in range(0, out.size, step):
+            n = min(step, out.size - i)
+            out[i:i + n] = rng.standard_normal(n, dtype=np.float32) * np.float32(sigma)
+        return out.view(np.uint8)
     if fmt == native.Q8_0:
         nb = rows * cols // 32
         out = np.empty((nb, 34), np.uint8)

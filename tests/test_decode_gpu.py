@@ -264,6 +264,19 @@ def test_small_phi4_decode_steps_match_oracle(hip):
             assert np.allclose(a, b, rtol=2e-3, atol=2e-3), (l, which)
 
 
+@pytest.mark.parametrize("fmt", [native.F16, native.F32], ids=["f16", "f32"])
+def test_small_dense_phi4_decode_steps_match_oracle(hip, fmt):
+    """The reference's own storage (Phi4TextModel.cs:140-209, 95-105): dense
+    layer weights and a tied dense embedding / vocabulary head."""
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=3000, capacity=128,
+                          weight_format=fmt, embed_format=fmt, head_format=fmt)
+    weights = phi4.synth_weights(cfg, seed=23, tied=True)
+    kv = phi4.synth_kv(cfg, length=40, seed=24)
+    results, _, _ = _run_steps(hip, cfg, weights, kv, [(7, 40), (2999, 41), (12, 42)])
+    for i, (g, gl, o, ol) in enumerate(results):
+        _check_logits(g, gl, o, ol, f"{native.FORMAT_NAMES[fmt]} step {i}")
+
+
 def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
     """The full decode workload: 32 layers, Phi-4-mini shapes, Q4_K layers, Q8_0
     embedding and head (200064 x 3072), fp16 KV cache with 2048 tokens of

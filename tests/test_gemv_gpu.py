@@ -328,7 +328,7 @@ def test_invalid_requests_are_rejected_without_fallback(hip):
             fn()
         return e.value.status
 
-    assert status(lambda: hip.gemv(native.F32, w.ptr, x.ptr, y.ptr, 4, 32)) == native.ERR_UNSUPPORTED
+    assert status(lambda: hip.gemv(native.BF16, w.ptr, x.ptr, y.ptr, 4, 32)) == native.ERR_UNSUPPORTED
     assert status(lambda: hip.gemv(native.Q8_0, w.ptr, x.ptr, y.ptr, 4, 48)) == native.ERR_ARGUMENT
     assert status(lambda: hip.gemv(native.Q4_K, w.ptr, x.ptr, y.ptr, 4, 128)) == native.ERR_ARGUMENT
     assert status(lambda: hip.gemv(native.Q8_0, w.ptr, x.ptr, y.ptr, 0, 32)) == native.ERR_ARGUMENT

@@ -98,7 +98,7 @@ def test_prefill_rejects_bad_requests(hip):
     x = hip.alloc(1 << 16)
     y = hip.alloc(1 << 16)
     for args, status in [
-        ((native.F16, w.ptr, x.ptr, y.ptr, 4, 32, 32), native.ERR_UNSUPPORTED),
+        ((native.BF16, w.ptr, x.ptr, y.ptr, 4, 32, 32), native.ERR_UNSUPPORTED),
         ((native.Q4_0, w.ptr, x.ptr, y.ptr, 0, 32, 32), native.ERR_ARGUMENT),
         ((native.Q4_0, w.ptr, x.ptr + 8, y.ptr, 4, 32, 32), native.ERR_ARGUMENT),   # X not 16-byte aligned
         ((native.Q4_K, w.ptr, x.ptr, y.ptr, 4, 32, 128), native.ERR_ARGUMENT),      # partial super-block
