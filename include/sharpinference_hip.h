@@ -265,6 +265,74 @@ int si_hip_argmax_workspace_bytes(uint64_t* bytes);
  * transformer.argmax (GpuTransformerInstructionCollection.cs:697-748). */
 int si_hip_argmax(si_hip_context* ctx, const float* values, int64_t n, void* workspace, int32_t* index);
 
+/* ---- transformer operators, one launch each ------------------------------------ */
+
+/* The operators of the reference's D3D12 decode program as separate
+ * launches, for VM programs that dispatch them one by one (the fused
+ * si_hip_phi4_decode step keeps its own layout).  KV caches here are
+ * [context][kv_heads][head_size] rows, FP32 as in the reference or fp16. */
+
+/* output[j] = input[j] * (1 / sqrt(sum(input^2) / n + eps)) * weight[j], n in
+ * 1..1048576, eps finite and >= 0.  Replaces: transformer.rms-norm
+ * (GpuTransformerInstructionCollection.cs:323-368). */
+int si_hip_rms_norm(si_hip_context* ctx, const float* input, const float* weight, float* output, int64_t n,
+                    float eps);
+
+/* updated = hidden + residual, output = updated * (1 / sqrt(sum(updated^2) / n
+ * + eps)) * weight; outputs may not overlap any input.  Replaces:
+ * transformer.residual-rms-norm (GpuTransformerInstructionCollection.cs:370-417). */
+int si_hip_residual_rms_norm(si_hip_context* ctx, const float* hidden, const float* residual, const float* weight,
+                             float* updated, float* output, int64_t n, float eps);
+
+/* output[i] = g_i / (1 + exp(-g_i)) * u_i for gate_up = [g (n values) | u (n
+ * values)].  Replaces: transformer.swiglu (GpuTransformerInstructionCollection.cs:419-443). */
+int si_hip_swiglu(si_hip_context* ctx, const float* gate_up, float* output, int64_t n);
+
+typedef struct si_hip_rope_kv_write_args {
+    const float* qkv;          /* [query_size | kv_size | kv_size] of one token */
+    const int32_t* position;   /* device scalar: the cache row written */
+    const float* frequencies;  /* [rotary_size / 2]: angle of pair i = position * frequencies[i] */
+    float* query;              /* [query_size] rotated queries */
+    void* key_cache;           /* [context][kv_size], cache_format */
+    void* value_cache;
+    int32_t cache_format;      /* SI_HIP_F32 or SI_HIP_F16 (rounded to nearest even) */
+    int32_t query_size;        /* a multiple of head_size */
+    int32_t kv_size;           /* kv_heads * head_size */
+    int32_t head_size;
+    int32_t rotary_size;       /* even, <= head_size */
+    int32_t context;
+    float rope_scale;          /* multiplies cos and sin */
+} si_hip_rope_kv_write_args;
+
+/* Rotate-half rotary embedding of the first rotary_size values of every q
+ * and k head, q to `query`, k and v to row *position of the caches; a
+ * position outside 0..context-1 writes nothing.  Replaces:
+ * transformer.rope-kv-write (GpuTransformerInstructionCollection.cs:445-543). */
+int si_hip_rope_kv_write(si_hip_context* ctx, const si_hip_rope_kv_write_args* args);
+
+typedef struct si_hip_gqa_args {
+    const float* query;        /* [query_heads * head_size], 16-byte aligned */
+    const void* key_cache;     /* [context][kv_heads][head_size], 16-byte aligned */
+    const void* value_cache;
+    const int32_t* position;   /* device scalar */
+    float* output;             /* [query_heads * head_size] */
+    int32_t cache_format;      /* SI_HIP_F32 or SI_HIP_F16 */
+    int32_t query_heads;       /* a multiple of kv_heads */
+    int32_t kv_heads;
+    int32_t head_size;         /* 64, 128 or 256 */
+    int32_t context;           /* 1..16384 */
+    float* workspace;          /* si_hip_gqa_workspace_bytes: per-chunk partials; any contents on entry;
+                                  calls sharing one workspace must not overlap on the GPU */
+} si_hip_gqa_args;
+
+int si_hip_gqa_workspace_bytes(int query_heads, int head_size, int context, uint64_t* bytes);
+
+/* output_h = softmax(q_h . K^T / sqrt(head_size)) . V over cache rows
+ * 0..min(max(*position, 0), context - 1) of KV head h / (query_heads /
+ * kv_heads), in 64-row chunks merged by a second launch.  Replaces: transformer.grouped-query-attention
+ * (GpuTransformerInstructionCollection.cs:46-143). */
+int si_hip_grouped_query_attention(si_hip_context* ctx, const si_hip_gqa_args* args);
+
 /* ---- Phi-4 decode step ------------------------------------------------------------ */
 
 typedef struct si_hip_phi4_layer {

@@ -35,6 +35,8 @@ SOURCES = [
     "si_rwkv.hip",
     "si_rwkv_program.cpp",
     "si_gguf.cpp",
+    "si_transformer.hip",
+    "si_ops.cpp",
 ]
 
 
@@ -103,7 +105,8 @@ def build_host() -> str:
     same directory (found through an $ORIGIN run path)."""
     tmp = HOST_LIB_PATH + ".tmp"
     cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
-           f"-I{os.path.join(ROOT, 'include')}", os.path.join(HOST_DIR, "si_host.cpp"),
+           f"-I{os.path.join(ROOT, 'include')}",
+           *[os.path.join(HOST_DIR, f) for f in sorted(os.listdir(HOST_DIR)) if f.endswith(".cpp")],
            f"-L{PKG}", "-lsharpinference_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:

@@ -279,6 +279,8 @@ int FormatId(const std::string& name)
     if (name == "q8_0") return SI_HIP_Q8_0;
     if (name == "q4_0") return SI_HIP_Q4_0;
     if (name == "q4_k") return SI_HIP_Q4_K;
+    if (name == "f16") return SI_HIP_F16;
+    if (name == "f32") return SI_HIP_F32;
     return -1;
 }
 
@@ -302,7 +304,7 @@ QuantShape ReadQuantShape(const Instruction& self, const std::vector<Instruction
     const auto* c = Find(parameters, "columns");
     const int format = FormatId(f->value);
     if (format < 0)
-        return fail("format '" + f->value + "' is not q8_0, q4_0 or q4_k.");
+        return fail("format '" + f->value + "' is not q8_0, q4_0, q4_k, f16 or f32.");
     int64_t columns = 0;
     try {
         size_t used = 0;
@@ -484,10 +486,25 @@ HipVmExecutor::HipVmExecutor(HipVmProgram program, int device) : program_(std::m
             buffers_.push_back(p);
             Check(si_hip_fill_u32(context_, p, 0, (bytes + 3) / 4), context_);
         }
+        // the executor's own scratch: argmax partials, attention chunk partials
+        uint64_t scratch = 0;
+        Check(si_hip_argmax_workspace_bytes(&scratch));
+        for (const auto& entry : program_.Entries())
+            for (const auto& d : entry.second)
+                if (d.recording.operation == "si_hip_grouped_query_attention") {
+                    const auto& k = Find(d.recording.parameters, "key_cache")->tensor.dimensions;
+                    const int heads = static_cast<int>(Find(d.recording.parameters, "query")->tensor.ElementCount() / k[2]);
+                    uint64_t b = 0;
+                    Check(si_hip_gqa_workspace_bytes(heads, static_cast<int>(k[2]), static_cast<int>(k[0]), &b));
+                    scratch = std::max(scratch, b);
+                }
+        Check(si_hip_alloc(context_, scratch, &scratch_), context_);
         Check(si_hip_sync(context_), context_);
     } catch (...) {
         for (void* p : buffers_)
             si_hip_free(context_, p);
+        if (scratch_)
+            si_hip_free(context_, scratch_);
         si_hip_destroy(context_);
         throw;
     }
@@ -499,6 +516,8 @@ HipVmExecutor::~HipVmExecutor()
         si_hip_plan_destroy(kv.second);
     for (void* p : buffers_)
         si_hip_free(context_, p);
+    if (scratch_)
+        si_hip_free(context_, scratch_);
     si_hip_destroy(context_);
 }
 
@@ -534,6 +553,12 @@ void* HipVmExecutor::Address(const InstructionParameter& p) const
 void HipVmExecutor::Launch(const InstructionRecording& r)
 {
     const auto attr = [&](const char* n) { return Find(r.parameters, n)->value; };
+    const auto F = [&](const InstructionRecording& rec, const char* n) {
+        return static_cast<const float*>(Address(*Find(rec.parameters, n)));
+    };
+    const auto Fw = [&](const InstructionRecording& rec, const char* n) {
+        return static_cast<float*>(Address(*Find(rec.parameters, n)));
+    };
     if (r.operation == "si_hip_gemv") {
         const auto* w = Find(r.parameters, "weight");
         if (!w)
@@ -551,6 +576,77 @@ void HipVmExecutor::Launch(const InstructionRecording& r)
         Check(si_hip_gather_row(context_, FormatId(attr("format")), Address(*t), t->tensor.dimensions[0],
                                 std::stoll(attr("columns")), static_cast<const int32_t*>(Address(*i)),
                                 static_cast<float*>(Address(*y))),
+              context_);
+    } else if (r.operation == "si_hip_gemv.dense") {
+        const auto* w = Find(r.parameters, "weight");
+        if (!w)
+            w = Find(r.parameters, "matrix");
+        const int fmt = w->tensor.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+        Check(si_hip_gemv(context_, fmt, Address(*w), F(r, "input"), Fw(r, "output"), w->tensor.dimensions[0],
+                          w->tensor.dimensions[1], nullptr, nullptr),
+              context_);
+    } else if (r.operation == "si_hip_gather_row.dense") {
+        const auto* t = Find(r.parameters, "table");
+        const int fmt = t->tensor.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+        Check(si_hip_gather_row(context_, fmt, Address(*t), t->tensor.dimensions[0], t->tensor.dimensions[1],
+                                static_cast<const int32_t*>(Address(*Find(r.parameters, "index"))), Fw(r, "output")),
+              context_);
+    } else if (r.operation == "si_hip_batched_matvec") {
+        const auto& d = Find(r.parameters, "matrix")->tensor.dimensions;
+        Check(si_hip_batched_matvec(context_, F(r, "matrix"), F(r, "vector"), Fw(r, "output"), static_cast<int>(d[0]),
+                                    static_cast<int>(d[1]), static_cast<int>(d[2])),
+              context_);
+    } else if (r.operation == "si_hip_rms_norm") {
+        Check(si_hip_rms_norm(context_, F(r, "input"), F(r, "weight"), Fw(r, "output"),
+                              static_cast<int64_t>(Find(r.parameters, "output")->tensor.ElementCount()),
+                              std::stof(attr("epsilon"))),
+              context_);
+    } else if (r.operation == "si_hip_residual_rms_norm") {
+        Check(si_hip_residual_rms_norm(context_, F(r, "hidden"), F(r, "residual"), F(r, "weight"), Fw(r, "updated"),
+                                       Fw(r, "output"),
+                                       static_cast<int64_t>(Find(r.parameters, "output")->tensor.ElementCount()),
+                                       std::stof(attr("epsilon"))),
+              context_);
+    } else if (r.operation == "si_hip_swiglu") {
+        Check(si_hip_swiglu(context_, F(r, "gate_up"), Fw(r, "output"),
+                            static_cast<int64_t>(Find(r.parameters, "output")->tensor.ElementCount())),
+              context_);
+    } else if (r.operation == "si_hip_rope_kv_write") {
+        const auto& k = Find(r.parameters, "key_cache")->tensor;
+        si_hip_rope_kv_write_args a{};
+        a.qkv = F(r, "qkv");
+        a.position = static_cast<const int32_t*>(Address(*Find(r.parameters, "position")));
+        a.frequencies = F(r, "frequencies");
+        a.query = Fw(r, "query");
+        a.key_cache = Address(*Find(r.parameters, "key_cache"));
+        a.value_cache = Address(*Find(r.parameters, "value_cache"));
+        a.cache_format = k.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+        a.query_size = static_cast<int32_t>(Find(r.parameters, "query")->tensor.ElementCount());
+        a.kv_size = static_cast<int32_t>(k.dimensions[1] * k.dimensions[2]);
+        a.head_size = std::stoi(attr("head_size"));
+        a.rotary_size = std::stoi(attr("rotary_size"));
+        a.context = static_cast<int32_t>(k.dimensions[0]);
+        a.rope_scale = std::stof(attr("rope_scale"));
+        Check(si_hip_rope_kv_write(context_, &a), context_);
+    } else if (r.operation == "si_hip_grouped_query_attention") {
+        const auto& k = Find(r.parameters, "key_cache")->tensor;
+        si_hip_gqa_args a{};
+        a.query = F(r, "query");
+        a.key_cache = Address(*Find(r.parameters, "key_cache"));
+        a.value_cache = Address(*Find(r.parameters, "value_cache"));
+        a.position = static_cast<const int32_t*>(Address(*Find(r.parameters, "position")));
+        a.output = Fw(r, "output");
+        a.cache_format = k.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+        a.kv_heads = static_cast<int32_t>(k.dimensions[1]);
+        a.head_size = static_cast<int32_t>(k.dimensions[2]);
+        a.query_heads = static_cast<int32_t>(Find(r.parameters, "query")->tensor.ElementCount() / k.dimensions[2]);
+        a.context = static_cast<int32_t>(k.dimensions[0]);
+        a.workspace = static_cast<float*>(scratch_);
+        Check(si_hip_grouped_query_attention(context_, &a), context_);
+    } else if (r.operation == "si_hip_argmax") {
+        Check(si_hip_argmax(context_, F(r, "input"),
+                            static_cast<int64_t>(Find(r.parameters, "input")->tensor.ElementCount()), scratch_,
+                            static_cast<int32_t*>(Address(*Find(r.parameters, "output")))),
               context_);
     } else {
         throw NotSupportedException("No HIP launch for recording '" + r.operation + "'.");

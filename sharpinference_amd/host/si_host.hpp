@@ -260,6 +260,99 @@ public:
 // GGUF format name of the quant attribute -> GGUF type id (-1 if unknown).
 int FormatId(const std::string& name);
 
+// ---- the reference's collections on the HIP target ----------------------------------------
+
+namespace InstructionCollectionIds {
+// The reference's collection GUIDs (InstructionCollection.cs:6-12): the HIP
+// target implements instructions of these collections under the same
+// identity, so a program names them exactly as it does for D3D12.
+inline const std::string TierZeroFloat32 = "00000000-0000-0000-0000-000000000000";
+inline const std::string TransformerFloat32 = "824d0f9c-16c7-46d8-b49d-0f91d6a4ec83";
+}  // namespace InstructionCollectionIds
+
+// An instruction of one fixed identity whose signatures are given as port
+// lists (FP32 arithmetic and accumulation, one attribute set); Validate and
+// Generate come from the concrete instruction.
+class HipFixedInstruction : public Instruction {
+public:
+    HipFixedInstruction(std::string collection, std::string name, std::vector<std::vector<InstructionPort>> signatures,
+                        std::vector<std::string> attributes);
+    std::string CollectionId() const override { return collection_; }
+    std::string Name() const override { return name_; }
+    InstructionTarget Target() const override { return InstructionTarget::Hip(); }
+    std::vector<InstructionSignature> Signatures() const override;
+
+protected:
+    const InstructionParameter& TensorOf(const std::vector<InstructionParameter>& parameters,
+                                         const std::string& name) const;
+    // Attribute parsers with the reference's rules (PositiveInteger: digits
+    // only and > 0; PositiveFloat: finite and > 0; GpuTransformerInstructionCollection.cs:300-311,530-540).
+    int PositiveInteger(const std::vector<InstructionParameter>& parameters, const std::string& name) const;
+    float PositiveFloat(const std::vector<InstructionParameter>& parameters, const std::string& name) const;
+
+private:
+    std::string collection_, name_;
+    std::vector<std::vector<InstructionPort>> signatures_;
+    std::vector<std::string> attributes_;
+};
+
+// T0 core.mat-vec on HIP: matrix|weight [rows, columns] Float32 or Float16,
+// input Float32 [columns], output Float32 [rows] (TierZeroOperationContracts.cs:113-115,152,161;
+// TierZeroInstruction.cs:100-106 adds the weight alias).
+class TierZeroMatVecInstruction : public HipFixedInstruction {
+public:
+    TierZeroMatVecInstruction();
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& parameters) const override;
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
+};
+
+// T0 core.gather-row: table [rows, columns] Float32 or Float16, index Int32
+// [1], output Float32 [columns] (TierZeroOperationContracts.cs:132-134,151,159).
+class TierZeroGatherRowInstruction : public HipFixedInstruction {
+public:
+    TierZeroGatherRowInstruction();
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& parameters) const override;
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
+};
+
+// T0 core.tensor.batched-mat-vec: matrix [B, R, C], vector [B, C] -> output
+// [B, R], Float32 (PortableTensorOperationContracts.cs:61-62,74-75).
+class TierZeroBatchedMatVecInstruction : public HipFixedInstruction {
+public:
+    TierZeroBatchedMatVecInstruction();
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& parameters) const override;
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
+};
+
+class HipTierZeroInstructions : public IInstructionCollectionProvider {
+public:
+    std::vector<InstructionCollectionDescription> QueryInstructionCollection() const override;
+    std::vector<std::shared_ptr<const Instruction>> QueryInstruction(const std::string& collection_id,
+                                                                    const std::string& name) const override;
+};
+
+// The transformer collection (GpuTransformerInstructionCollection.cs:11-33)
+// on HIP: transformer.rms-norm, residual-rms-norm, swiglu, rope-kv-write,
+// grouped-query-attention and argmax, with the reference's port names,
+// accesses and attributes.  rope-kv-write and grouped-query-attention take
+// Float32 caches (the reference's signature) or Float16 caches (a second
+// signature of this target).
+class HipTransformerInstructions : public IInstructionCollectionProvider {
+public:
+    std::vector<InstructionCollectionDescription> QueryInstructionCollection() const override;
+    std::vector<std::shared_ptr<const Instruction>> QueryInstruction(const std::string& collection_id,
+                                                                    const std::string& name) const override;
+};
+
+// Every HIP collection of this library behind one registry.
+std::shared_ptr<const InstructionRegistry> DefaultHipRegistry();
+
 // ---- program and executor (VmProgram, D3D12VmExecutor) ------------------------------------
 
 struct HipVmSlot {
@@ -328,7 +421,40 @@ private:
     HipVmProgram program_;
     si_hip_context* context_ = nullptr;
     std::vector<void*> buffers_;
+    void* scratch_ = nullptr;   // the executor's own device scratch (argmax partials)
     std::map<std::string, si_hip_plan*> plans_;
 };
+
+// ---- the Phi-4 decode program, dispatch by dispatch --------------------------------------
+
+// Shapes and storage of a Phi-4 decode program.  Formats are GGUF type ids
+// (Q8_0 / Q4_0 / Q4_K weights are Byte rows dispatched to quant.mat-vec,
+// F16 / F32 weights typed tensors dispatched to core.mat-vec); the cache is
+// Float32 (the reference's) or Float16.
+struct Phi4ProgramShape {
+    int layers = 32, hidden = 3072, heads = 24, kv_heads = 8, head_dim = 128, rotary_dim = 96, ffn = 8192;
+    int vocab = 200064, context = 4096;
+    int weight_format = SI_HIP_Q4_K, embed_format = SI_HIP_Q8_0, head_format = SI_HIP_Q8_0;
+    bool tied = false;        // project onto token_embedding (the reference model) instead of output_weight
+    GraphElementType cache_type = GraphElementType::Float16;
+    float rms_eps = 1e-5f, rope_base = 10000.0f, rope_scale = 1.0f;
+};
+
+// The decode program of Phi4D3D12TextSession.Build (Phi4D3D12TextSession.cs:
+// 391-426, 866-919) as a HipVmProgram: slots token_embedding, output_weight
+// (untied), output_norm, rope_frequencies, attn_norm_{l}, ffn_norm_{l},
+// qkv_weight_{l}, attn_output_weight_{l}, ffn_up_weight_{l},
+// ffn_down_weight_{l}, key_cache_{l}, value_cache_{l}, control ([token,
+// position]), hidden, hidden_after_attention, normalized, qkv, query,
+// attention, projected, gate_up, activated, down, logits, next_token; entry
+// "decode" = embedding gather, rms-norm, per layer qkv mat-vec, rope-kv-write,
+// grouped-query-attention, output mat-vec, residual-rms-norm, up mat-vec,
+// swiglu, down mat-vec, residual-rms-norm (onto the next layer's attention
+// norm, the output norm after the last), then the vocabulary mat-vec and
+// argmax: 2 + 9 * layers + 2 dispatches.
+HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& shape);
+// rope_frequencies contents: 1 / base^(2i / rotary) for i < rotary / 2
+// (Phi4D3D12TextSession.cs:395-397).
+std::vector<float> Phi4RopeFrequencies(const Phi4ProgramShape& shape);
 
 }  // namespace sharpinference

@@ -1,0 +1,160 @@
+// C entry points of the host library (si_host_c.h) over HipVmProgram /
+// HipVmExecutor and BuildPhi4DecodeProgram.
+#include "si_host_c.h"
+
+#include "si_host.hpp"
+
+#include <memory>
+#include <string>
+
+using namespace sharpinference;
+
+struct sih_program {
+    HipVmProgram program;
+    std::unique_ptr<HipVmExecutor> executor;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+// Runs f, mapping the host layer's exceptions to library status codes.
+template <typename Fn>
+int Guard(Fn&& f)
+{
+    try {
+        f();
+        return SI_HIP_OK;
+    } catch (const InstructionAdaptationException& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_ADAPTATION;
+    } catch (const NotSupportedException& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_UNSUPPORTED;
+    } catch (const InvalidDataException& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_FORMAT;
+    } catch (const OutOfMemoryException& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_OUT_OF_MEMORY;
+    } catch (const InvalidOperationException& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_STATE;
+    } catch (const ArgumentException& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_ARGUMENT;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return SI_HIP_ERR_DEVICE;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int sih_phi4_program_create(const sih_phi4_shape* s, int device, sih_program** out)
+{
+    return Guard([&] {
+        if (!s || !out)
+            throw ArgumentException("sih_phi4_program_create: null argument");
+        *out = nullptr;
+        Phi4ProgramShape shape;
+        shape.layers = s->layers;
+        shape.hidden = s->hidden;
+        shape.heads = s->heads;
+        shape.kv_heads = s->kv_heads;
+        shape.head_dim = s->head_dim;
+        shape.rotary_dim = s->rotary_dim;
+        shape.ffn = s->ffn;
+        shape.vocab = s->vocab;
+        shape.context = s->context;
+        shape.weight_format = s->weight_format;
+        shape.embed_format = s->embed_format;
+        shape.head_format = s->head_format;
+        shape.tied = s->tied != 0;
+        shape.cache_type = s->cache_fp16 ? GraphElementType::Float16 : GraphElementType::Float32;
+        shape.rms_eps = s->rms_eps;
+        shape.rope_base = s->rope_base;
+        shape.rope_scale = s->rope_scale;
+        auto p = std::make_unique<sih_program>();
+        p->program = BuildPhi4DecodeProgram(shape);
+        p->executor = std::make_unique<HipVmExecutor>(p->program, device);
+        const auto f = Phi4RopeFrequencies(shape);
+        p->executor->Upload("rope_frequencies", f.data(), f.size() * sizeof(float));
+        *out = p.release();
+    });
+}
+
+int sih_program_destroy(sih_program* program)
+{
+    delete program;
+    return SI_HIP_OK;
+}
+
+int sih_program_slot_bytes(const sih_program* program, const char* slot, uint64_t* bytes)
+{
+    return Guard([&] {
+        if (!program || !slot || !bytes)
+            throw ArgumentException("sih_program_slot_bytes: null argument");
+        const int i = program->program.SlotIndex(slot);
+        if (i < 0)
+            throw ArgumentException(std::string("Unknown slot '") + slot + "'.");
+        *bytes = program->program.Slots()[i].tensor.ByteLength();
+    });
+}
+
+int sih_program_upload(sih_program* program, const char* slot, const void* bytes, uint64_t length)
+{
+    return Guard([&] {
+        if (!program || !slot)
+            throw ArgumentException("sih_program_upload: null argument");
+        program->executor->Upload(slot, bytes, length);
+    });
+}
+
+int sih_program_readback(sih_program* program, const char* slot, void* bytes, uint64_t length)
+{
+    return Guard([&] {
+        if (!program || !slot || !bytes)
+            throw ArgumentException("sih_program_readback: null argument");
+        const auto v = program->executor->Readback(slot);
+        if (v.size() != length)
+            throw ArgumentException("Expected a " + std::to_string(v.size()) + "-byte buffer for slot '" + slot + "'.");
+        std::copy(v.begin(), v.end(), static_cast<uint8_t*>(bytes));
+    });
+}
+
+int sih_program_execute(sih_program* program, const char* entry)
+{
+    return Guard([&] {
+        if (!program || !entry)
+            throw ArgumentException("sih_program_execute: null argument");
+        program->executor->Execute(entry);
+    });
+}
+
+int sih_program_measure_us(sih_program* program, const char* entry, int repetitions, double* microseconds)
+{
+    return Guard([&] {
+        if (!program || !entry || !microseconds)
+            throw ArgumentException("sih_program_measure_us: null argument");
+        *microseconds = program->executor->MeasureGpuMicroseconds(entry, repetitions);
+    });
+}
+
+int sih_program_dispatch_count(const sih_program* program, const char* entry, int* count)
+{
+    return Guard([&] {
+        if (!program || !entry || !count)
+            throw ArgumentException("sih_program_dispatch_count: null argument");
+        const auto it = program->program.Entries().find(entry);
+        if (it == program->program.Entries().end())
+            throw ArgumentException(std::string("Unknown entry '") + entry + "'.");
+        *count = static_cast<int>(it->second.size());
+    });
+}
+
+const char* sih_last_error(void) { return g_error.c_str(); }
+
+}  // extern "C"

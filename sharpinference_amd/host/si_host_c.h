@@ -1,0 +1,43 @@
+/*
+ * C entry points of libsharpinference_hip_host.so for callers that cannot
+ * bind C++ (the Python package): a Phi-4 decode program built dispatch by
+ * dispatch (BuildPhi4DecodeProgram) and run by its HipVmExecutor.  Status
+ * codes are si_hip_status values; the message of the calling thread's last
+ * failure is sih_last_error().
+ */
+#ifndef SI_HOST_C_H
+#define SI_HOST_C_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sih_program sih_program;
+
+typedef struct sih_phi4_shape {
+    int32_t layers, hidden, heads, kv_heads, head_dim, rotary_dim, ffn, vocab, context;
+    int32_t weight_format, embed_format, head_format;   /* GGUF type ids */
+    int32_t tied;                                       /* vocabulary projection onto token_embedding */
+    int32_t cache_fp16;                                 /* 1: Float16 KV cache, 0: Float32 */
+    float rms_eps, rope_base, rope_scale;
+} sih_phi4_shape;
+
+/* Builds the program, creates its executor on `device` (every slot zeroed)
+ * and uploads rope_frequencies. */
+int sih_phi4_program_create(const sih_phi4_shape* shape, int device, sih_program** out);
+int sih_program_destroy(sih_program* program);
+int sih_program_slot_bytes(const sih_program* program, const char* slot, uint64_t* bytes);
+int sih_program_upload(sih_program* program, const char* slot, const void* bytes, uint64_t length);
+int sih_program_readback(sih_program* program, const char* slot, void* bytes, uint64_t length);
+/* Executes an entry (recorded once as a plan, replayed, waited for). */
+int sih_program_execute(sih_program* program, const char* entry);
+int sih_program_measure_us(sih_program* program, const char* entry, int repetitions, double* microseconds);
+int sih_program_dispatch_count(const sih_program* program, const char* entry, int* count);
+const char* sih_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

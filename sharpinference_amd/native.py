@@ -86,6 +86,20 @@ class AttentionArgs(ctypes.Structure):
                 ("rope_scale", ctypes.c_float)]
 
 
+class RopeKvWriteArgs(ctypes.Structure):
+    """si_hip_rope_kv_write_args."""
+    _fields_ = [("qkv", _vp), ("position", _vp), ("frequencies", _vp), ("query", _vp), ("key_cache", _vp),
+                ("value_cache", _vp), ("cache_format", _i32), ("query_size", _i32), ("kv_size", _i32),
+                ("head_size", _i32), ("rotary_size", _i32), ("context", _i32), ("rope_scale", ctypes.c_float)]
+
+
+class GqaArgs(ctypes.Structure):
+    """si_hip_gqa_args."""
+    _fields_ = [("query", _vp), ("key_cache", _vp), ("value_cache", _vp), ("position", _vp), ("output", _vp),
+                ("cache_format", _i32), ("query_heads", _i32), ("kv_heads", _i32), ("head_size", _i32),
+                ("context", _i32), ("workspace", _vp)]
+
+
 class Phi4Layer(ctypes.Structure):
     """si_hip_phi4_layer."""
     _fields_ = [("attn_norm", _vp), ("qkv", _vp), ("o", _vp), ("ffn_norm", _vp), ("up", _vp), ("down", _vp),
@@ -171,6 +185,12 @@ SIGNATURES.update({
     "si_hip_attention_decode": ([_vp, ctypes.POINTER(AttentionArgs)], _i32),
     "si_hip_attention_decode_noalloc": ([_vp, ctypes.POINTER(AttentionArgs)], _i32),
     "si_hip_argmax_workspace_bytes": ([ctypes.POINTER(_u64)], _i32),
+    "si_hip_rms_norm": ([_vp, _vp, _vp, _vp, _i64, ctypes.c_float], _i32),
+    "si_hip_residual_rms_norm": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, ctypes.c_float], _i32),
+    "si_hip_swiglu": ([_vp, _vp, _vp, _i64], _i32),
+    "si_hip_rope_kv_write": ([_vp, ctypes.POINTER(RopeKvWriteArgs)], _i32),
+    "si_hip_grouped_query_attention": ([_vp, ctypes.POINTER(GqaArgs)], _i32),
+    "si_hip_gqa_workspace_bytes": ([_i32, _i32, _i32, ctypes.POINTER(_u64)], _i32),
     "si_hip_argmax": ([_vp, _vp, _i64, _vp, _vp], _i32),
     "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
     "si_hip_phi4_decode": ([_vp, ctypes.POINTER(Phi4Model)], _i32),
@@ -371,6 +391,24 @@ class HipContext:
         """si_hip_attention_decode_noalloc: args.workspace must be NULL (0)."""
         self._call(lib().si_hip_attention_decode_noalloc, ctypes.byref(args))
 
+    def rms_norm(self, x: int, w: int, out: int, n: int, eps: float) -> None:
+        self._call(lib().si_hip_rms_norm, ctypes.c_void_p(int(x)), ctypes.c_void_p(int(w)), ctypes.c_void_p(int(out)),
+                   n, ctypes.c_float(eps))
+
+    def residual_rms_norm(self, hidden: int, residual: int, w: int, updated: int, out: int, n: int,
+                          eps: float) -> None:
+        self._call(lib().si_hip_residual_rms_norm, *[ctypes.c_void_p(int(p)) for p in (hidden, residual, w, updated, out)],
+                   n, ctypes.c_float(eps))
+
+    def swiglu(self, gate_up: int, out: int, n: int) -> None:
+        self._call(lib().si_hip_swiglu, ctypes.c_void_p(int(gate_up)), ctypes.c_void_p(int(out)), n)
+
+    def rope_kv_write(self, args: RopeKvWriteArgs) -> None:
+        self._call(lib().si_hip_rope_kv_write, ctypes.byref(args))
+
+    def grouped_query_attention(self, args: GqaArgs) -> None:
+        self._call(lib().si_hip_grouped_query_attention, ctypes.byref(args))
+
     def argmax(self, values: int, n: int, workspace: int, index: int) -> None:
         self._call(lib().si_hip_argmax, ctypes.c_void_p(int(values)), n, ctypes.c_void_p(int(workspace)),
                    ctypes.c_void_p(int(index)))
@@ -434,6 +472,12 @@ def attention_workspace_bytes(heads: int, capacity: int) -> int:
     out = ctypes.c_uint64(0)
     _check(lib().si_hip_attention_workspace_bytes(heads, capacity, ctypes.byref(out)))
     return out.value
+
+
+def gqa_workspace_bytes(query_heads: int, head_size: int, context: int) -> int:
+    n = ctypes.c_uint64(0)
+    _check(lib().si_hip_gqa_workspace_bytes(query_heads, head_size, context, ctypes.byref(n)))
+    return n.value
 
 
 def argmax_workspace_bytes() -> int:

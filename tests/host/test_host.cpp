@@ -477,6 +477,129 @@ TEST(cpu, ProgramRejectsUnknownSlotsOversizedViewsWritesToReadSlotsAndAliasing)
     ASSERT_TRUE(shared.Entries().empty());
 }
 
+// The reference's collections resolve on the HIP target under their own
+// identities (InstructionCollection.cs:6-12, GpuTransformerInstructionCollection.cs:11-44).
+TEST(cpu, ReferenceCollectionsResolveOnTheHipTarget)
+{
+    const auto reg = DefaultHipRegistry();
+    const auto& T = InstructionCollectionIds::TransformerFloat32;
+    for (const char* n : {"transformer.rms-norm", "transformer.residual-rms-norm", "transformer.swiglu",
+                          "transformer.rope-kv-write", "transformer.grouped-query-attention", "transformer.argmax"})
+        ASSERT_TRUE(reg->Resolve(T, n, InstructionTarget::Hip())->Name() == n);
+    for (const char* n : {"core.mat-vec", "core.gather-row", "core.tensor.batched-mat-vec"})
+        ASSERT_TRUE(reg->Resolve(InstructionCollectionIds::TierZeroFloat32, n, InstructionTarget::Hip())->Name() == n);
+    ASSERT_THROWS(NotSupportedException, reg->Resolve(T, "transformer.rms-norm", {"direct3d12"}));
+    ASSERT_TRUE(reg->QueryInstruction(T, "transformer.gqa-scores").empty());
+    // the transformer ports carry the reference's names, types and accesses
+    const auto rope = reg->Resolve(T, "transformer.rope-kv-write", InstructionTarget::Hip());
+    const auto sig = rope->Signatures()[0];
+    ASSERT_TRUE(sig.ports.size() == 6 && sig.ports[1].name == "position" &&
+                sig.ports[1].element_type == GraphElementType::Int32 && sig.ports[4].name == "key_cache" &&
+                sig.ports[4].access == GraphResourceAccess::Write);
+    ASSERT_TRUE((sig.attributes == std::vector<std::string>{"head_size", "rotary_size", "rope_scale"}));
+}
+
+TEST(cpu, TransformerInstructionsAdaptWithTheReferenceRules)
+{
+    const auto reg = DefaultHipRegistry();
+    const auto& T = InstructionCollectionIds::TransformerFloat32;
+    using P = InstructionParameter;
+    const auto f32 = [](std::vector<int64_t> d) { return TensorDescriptor{GraphElementType::Float32, std::move(d)}; };
+    const auto rms = reg->Resolve(T, "transformer.rms-norm", InstructionTarget::Hip());
+    std::vector<P> p{P::Tensor("input", f32({64}), GraphResourceAccess::Read, "a"),
+                     P::Tensor("weight", f32({64}), GraphResourceAccess::Read, "b"),
+                     P::Tensor("output", f32({64}), GraphResourceAccess::Write, "c"), P::Attribute("epsilon", "1e-05")};
+    rms->Adapt(p, kFp32);
+    for (const char* bad : {"0", "-1", "nan", "inf", "1e-5x", ""}) {
+        auto q = p;
+        q[3].value = bad;
+        ASSERT_THROWS(InstructionAdaptationException, rms->Adapt(q, kFp32));
+    }
+    const auto gqa = reg->Resolve(T, "transformer.grouped-query-attention", InstructionTarget::Hip());
+    const auto cache = [](GraphElementType t) { return TensorDescriptor{t, {16, 2, 128}}; };
+    for (GraphElementType t : {GraphElementType::Float32, GraphElementType::Float16}) {
+        std::vector<P> g{P::Tensor("query", f32({8 * 128}), GraphResourceAccess::Read, "q"),
+                         P::Tensor("key_cache", cache(t), GraphResourceAccess::Read, "k"),
+                         P::Tensor("value_cache", cache(t), GraphResourceAccess::Read, "v"),
+                         P::Tensor("position", {GraphElementType::Int32, {1}}, GraphResourceAccess::Read, "p"),
+                         P::Tensor("output", f32({8 * 128}), GraphResourceAccess::Write, "o")};
+        ASSERT_TRUE(gqa->Adapt(g, kFp32).ports[1].element_type == t);
+        auto bad = g;
+        bad[0].tensor = f32({6 * 128});   // query and output heads differ
+        ASSERT_THROWS(InstructionAdaptationException, gqa->Adapt(bad, kFp32));
+        bad[4].tensor = f32({6 * 128});   // 6 query heads over 2 KV heads
+        gqa->Adapt(bad, kFp32);
+        bad[1].tensor = bad[2].tensor = TensorDescriptor{t, {16, 4, 128}};
+        ASSERT_THROWS(InstructionAdaptationException, gqa->Adapt(bad, kFp32));   // 6 heads over 4 KV heads
+        bad = g;
+        bad[2].tensor = TensorDescriptor{t, {16, 2, 64}};
+        ASSERT_THROWS(InstructionAdaptationException, gqa->Adapt(bad, kFp32));   // mismatched caches
+    }
+}
+
+TEST(cpu, Phi4ProgramFollowsTheReferenceDispatchOrder)
+{
+    Phi4ProgramShape s;
+    s.layers = 2;
+    s.hidden = 1024;
+    s.heads = 8;
+    s.kv_heads = 2;
+    s.ffn = 2048;
+    s.vocab = 100;
+    s.context = 32;
+    const auto p = BuildPhi4DecodeProgram(s);
+    const auto& d = p.Entries().at("decode");
+    ASSERT_TRUE(d.size() == 2 + 9 * 2 + 2);
+    std::vector<std::string> names;
+    for (const auto& x : d)
+        names.push_back(x.instruction->Name());
+    const std::vector<std::string> layer{"quant.mat-vec",    "transformer.rope-kv-write",
+                                         "transformer.grouped-query-attention", "quant.mat-vec",
+                                         "transformer.residual-rms-norm",       "quant.mat-vec",
+                                         "transformer.swiglu",                  "quant.mat-vec",
+                                         "transformer.residual-rms-norm"};
+    std::vector<std::string> want{"quant.gather-row", "transformer.rms-norm"};
+    for (int l = 0; l < 2; l++)
+        want.insert(want.end(), layer.begin(), layer.end());
+    want.push_back("quant.mat-vec");
+    want.push_back("transformer.argmax");
+    ASSERT_TRUE(names == want);
+    // the second residual-rms-norm of layer 0 normalises onto layer 1's attention norm
+    const auto& r = d[2 + 8].recording.parameters;
+    bool onto_next = false;
+    for (const auto& q : r)
+        onto_next |= q.name == "weight" && q.source == "attn_norm_1";
+    ASSERT_TRUE(onto_next);
+    // dense weights dispatch the T0 mat-vec and gather over typed slots; the
+    // tied head projects onto the embedding table
+    s.weight_format = s.embed_format = s.head_format = SI_HIP_F16;
+    s.tied = true;
+    s.cache_type = GraphElementType::Float32;
+    const auto dense = BuildPhi4DecodeProgram(s);
+    const auto& dd = dense.Entries().at("decode");
+    ASSERT_TRUE(dd.front().instruction->Name() == "core.gather-row" &&
+                dd.front().instruction->CollectionId() == InstructionCollectionIds::TierZeroFloat32);
+    ASSERT_TRUE(dd[2].instruction->Name() == "core.mat-vec");
+    ASSERT_TRUE(dense.SlotIndex("output_weight") < 0 &&
+                dense.Slots()[dense.SlotIndex("qkv_weight_0")].tensor.element_type == GraphElementType::Float16 &&
+                dense.Slots()[dense.SlotIndex("key_cache_1")].tensor.element_type == GraphElementType::Float32);
+    bool head_on_embedding = false;
+    for (const auto& q : dd[dd.size() - 2].recording.parameters)
+        head_on_embedding |= q.name == "weight" && q.source == "token_embedding";
+    ASSERT_TRUE(head_on_embedding);
+    auto bad = s;
+    bad.hidden = 1000;
+    ASSERT_THROWS(ArgumentException, BuildPhi4DecodeProgram(bad));
+    bad = s;
+    bad.rotary_dim = 97;
+    ASSERT_THROWS(ArgumentException, BuildPhi4DecodeProgram(bad));
+    bad = s;
+    bad.head_format = SI_HIP_Q8_0;   // tied head in another format
+    ASSERT_THROWS(ArgumentException, BuildPhi4DecodeProgram(bad));
+    const auto f = Phi4RopeFrequencies(Phi4ProgramShape{});
+    ASSERT_TRUE(f.size() == 48 && f[0] == 1.0f && std::fabs(f[47] - 1.0f / std::pow(10000.0f, 94.0f / 96.0f)) < 1e-12f);
+}
+
 TEST(cpu, ExecutorWithoutADeviceFailsLoudly)
 {
     int n = 0;

@@ -41,34 +41,33 @@ def _weights(cfg):
         down=[q(40 + l, H, F, 0.03) for l in range(L)])
 
 
-def _dq(w, rows, cols):
-    return orc.dequant(orc.Q8_0, w, rows, cols).astype(np.float64)
-
-
-def _f16(a):
-    return np.asarray(a, np.float64).astype(np.float16)
+def _dq(w, rows, cols, fmt=orc.Q8_0):
+    return orc.dequant(fmt, w, rows, cols).astype(np.float64)
 
 
 class Float64Phi4:
-    """Phi4TextModel.cs:59-105 in float64 (fp16 KV cache as in the workload).
+    """Phi4TextModel.cs:59-105 in float64, with the KV cache rounded to
+    `cache_dtype` (fp16 as in the workload; float64 keeps it exact).
     `mutation` names one deliberate composition mistake (None = faithful)."""
 
-    def __init__(self, cfg, w, k_init, v_init, mutation=None):
+    def __init__(self, cfg, w, k_init, v_init, mutation=None, cache_dtype=np.float16):
         self.cfg, self.mut = cfg, mutation
         H, F, D, KVH = cfg.hidden, cfg.ffn, cfg.head_dim, cfg.kv_heads
-        self.embed = _dq(w.embed, cfg.vocab, H)
-        self.head = _dq(w.lm_head, cfg.vocab, H)
+        wf = getattr(cfg, "weight_format", orc.Q8_0)
+        self.embed = _dq(w.embed, cfg.vocab, H, cfg.embed_format)
+        self.head = _dq(w.lm_head, cfg.vocab, H, cfg.head_format)
         self.onorm = w.output_norm.astype(np.float64)
         self.an = [a.astype(np.float64) for a in w.attn_norm]
         self.fn = [a.astype(np.float64) for a in w.ffn_norm]
         if mutation == "norms_swapped":
             self.an, self.fn = self.fn, self.an
-        self.qkv = [_dq(a, H + 2 * KVH * D, H) for a in w.qkv]
-        self.o = [_dq(a, H, H) for a in w.o]
-        self.up = [_dq(a, 2 * F, H) for a in w.up]
-        self.down = [_dq(a, H, F) for a in w.down]
-        self.k = [a.view(np.float16).copy() for a in k_init]
-        self.v = [a.view(np.float16).copy() for a in v_init]
+        self.qkv = [_dq(a, H + 2 * KVH * D, H, wf) for a in w.qkv]
+        self.o = [_dq(a, H, H, wf) for a in w.o]
+        self.up = [_dq(a, 2 * F, H, wf) for a in w.up]
+        self.down = [_dq(a, H, F, wf) for a in w.down]
+        self.cache_dtype = cache_dtype
+        self.k = [a.view(np.float16).astype(cache_dtype) for a in k_init]
+        self.v = [a.view(np.float16).astype(cache_dtype) for a in v_init]
 
     def rms(self, x, g):
         return x / np.sqrt(np.mean(x * x) + self.cfg.rms_eps) * g
@@ -98,8 +97,8 @@ class Float64Phi4:
                 k = self.rope(k, KVH, pos)
             if self.mut == "v_rotated":
                 v = self.rope(v, KVH, pos)
-            self.k[l][:, pos] = _f16(k.reshape(KVH, D))
-            self.v[l][:, pos] = _f16(v.reshape(KVH, D))
+            self.k[l][:, pos] = k.reshape(KVH, D).astype(self.cache_dtype)
+            self.v[l][:, pos] = v.reshape(KVH, D).astype(self.cache_dtype)
             attn = np.empty(H)
             for hd in range(NH):
                 g = hd % KVH if self.mut == "heads_interleaved" else hd // (NH // KVH)
