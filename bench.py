@@ -73,6 +73,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill (MFMA) measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the Phi-4-mini decode-step measurement")
     ap.add_argument("--no-rwkv", action="store_true", help="skip the RWKV-7 token-step measurement")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the single-matrix legs (Q8_0 and F16 3072x3072, F16 head) and the F16 decode step")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the Phi-4 and RWKV-7 token loops (one token at a time, no back-to-back "
                          "replays, no CPU leg); prints their JSON; for kernel-trace profiles")
@@ -147,13 +149,20 @@ def main() -> int:
     # plan-launch gap to every step, reported as `one_plan_per_step`.
     round_plan = record_steps(0, copies)
     plans = [record_steps(c, 1) for c in range(copies)]
+    rest_plans = {}
 
     def run_steps(n: int) -> None:
+        """n steps = whole rounds of `copies` steps plus one plan holding the
+        remaining steps (recorded once per remainder, before any timing)."""
         full, rest = divmod(n, copies)
         if full:
             hip.launch_sequence([round_plan], full)
         if rest:
-            hip.launch_sequence(plans[:rest], rest)
+            hip.launch_sequence([rest_plans[rest]], 1)
+
+    for n in (max(args.warmup, 1), args.steps):
+        if n % copies and n % copies not in rest_plans:
+            rest_plans[n % copies] = record_steps(0, n % copies)
 
     # per-shape plans (rotation over copies) for the per-kernel breakdown
     shape_plans = {}
@@ -205,8 +214,35 @@ def main() -> int:
                          "GBs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         log(f"  {name:8s} {rows}x{cols}: {us:.3f} us/launch, {b / us / 1e3:.1f} GB/s")
 
+    # plain-read ceiling: the same bytes, read once by a streaming kernel
+    # (si_hip_checksum), in the same plan structure (one launch per weight
+    # tensor, the step's four in order, rotating over the copies)
+    acc = hip.alloc(4 * native.CHECKSUM_PARTS)
+    read_plan = hip.record(lambda: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
+                                    for c in range(copies) for k in range(len(shapes))])
+    read_plan.measure_us(2)
+    read_us = sorted(read_plan.measure_us(8) for _ in range(5))[2] / copies
+    read_w = sum(w.nbytes for w in host_w)
+    read_shapes = {}
+    for k, (name, rows, cols) in enumerate(shapes):
+        plan = hip.record(lambda k=k: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
+                                       for c in range(copies)])
+        plan.measure_us(2)
+        us = sorted(plan.measure_us(8) for _ in range(5))[2] / copies
+        read_shapes[name] = {"bytes": host_w[k].nbytes, "us_per_launch": round(us, 3),
+                             "GBs": round(host_w[k].nbytes / us / 1e3, 1)}
+        plan.destroy()
+    read_plan.destroy()
+    acc.free()
+    ceiling = {"kernel": "checksum_kernel (streaming 16-byte reads, one partial per workgroup)", "us_per_step": round(read_us, 3),
+               "GBs": round(read_w / read_us / 1e3, 1), "frac": round(read_w / read_us / 1e3 / HBM_PEAK_GBS, 4),
+               "shapes": read_shapes}
+    log(f"plain-read ceiling of the same weights: {read_us:.2f} us/step, {read_w / read_us / 1e3:.0f} GB/s")
+
+    legs = None if args.no_legs else bench_matvec_legs(hip, rng)
     prefill = None if args.no_prefill else bench_prefill(hip, rng)
     decode = None if args.no_decode else bench_decode(hip, cpu=not args.no_cpu)
+    decode_f16 = None if args.no_decode or args.no_legs else bench_decode_dense(hip)
     rwkv = None if args.no_rwkv else bench_rwkv_decode(hip, cpu=not args.no_cpu)
 
     # dispatch floor: the same graph mechanism with 64 one-wave fill kernels
@@ -244,8 +280,11 @@ def main() -> int:
         "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
         "kernels": kernels,
         "dispatch_floor_us": round(floor_us, 3),
+        "plain_read_ceiling": ceiling,
+        "matvec_legs": legs,
         "prefill": prefill,
         "decode": decode,
+        "decode_f16": decode_f16,
         "decode_rwkv7": rwkv,
         "roofline": {
             "bound": "hbm",
@@ -267,11 +306,83 @@ def main() -> int:
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(fmt, shapes, host_w, xs, ys, hip, bytes_per_step, args.cpu_seconds)
 
-    for plan in plans + [round_plan] + list(shape_plans.values()):
+    for plan in plans + [round_plan] + list(shape_plans.values()) + list(rest_plans.values()):
         plan.destroy()
     hip.close()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def time_rotated_gemv(hip, fmt, host, rows, cols, copies, rng):
+    """Median event-timed microseconds per launch of one GEMV shape: a plan
+    of `copies` dependent launches over distinct weight copies."""
+    from sharpinference_amd import native
+    dev = []
+    for _ in range(copies):
+        b = hip.alloc(host.nbytes)
+        b.upload(host)
+        dev.append(b)
+    x = hip.to_device(rng.standard_normal(cols).astype(np.float32))
+    y = hip.alloc(4 * rows)
+    plan = hip.record(lambda: [hip.gemv(fmt, b.ptr, x.ptr, y.ptr, rows, cols) for b in dev])
+    plan.measure_us(2)
+    us = sorted(plan.measure_us(8) for _ in range(7))[3] / copies
+    plan.destroy()
+    for b in dev + [x, y]:
+        b.free()
+    nbytes = host.nbytes + 4 * (rows + cols)
+    return {"format": native.FORMAT_NAMES[fmt], "rows": rows, "cols": cols, "bytes": nbytes,
+            "weight_copies_rotated": copies, "us_per_launch": round(us, 3), "GBs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def bench_matvec_legs(hip, rng):
+    """Single-matrix lines beside the layer set: the minimum slice (Q8_0
+    3072x3072, weights uniform in [-127, 127], d = |N(0, 0.02)| / 127), the
+    reference's own F16 weights at the same shape, and the F16 200064 x 3072
+    tied vocabulary head of the reference's Phi-4 model.  Copies rotate
+    through > 512 MB so every launch reads HBM."""
+    from sharpinference_amd import native
+    from sharpinference_amd.synth import synth_blocks
+    out = {}
+    for key, fmt, rows, cols in (("q8_0_3072x3072", native.Q8_0, 3072, 3072),
+                                 ("f16_3072x3072", native.F16, 3072, 3072),
+                                 ("f16_head_200064x3072", native.F16, 200064, 3072)):
+        host = synth_blocks(fmt, rows, cols, rng)
+        copies = max(1, -(-640 * 2 ** 20 // host.nbytes))
+        out[key] = time_rotated_gemv(hip, fmt, host, rows, cols, copies, rng)
+        log(f"  {key}: {out[key]['us_per_launch']:.3f} us/launch, {out[key]['GBs']:.1f} GB/s "
+            f"({100 * out[key]['frac']:.1f}% of HBM)")
+    return out
+
+
+def bench_decode_dense(hip, context: int = 2048):
+    """The Phi-4-mini decode step in the reference model's own storage: F16
+    layer weights and the tied F16 token_embd table as embedding and head
+    (Phi4TextModel.cs:53,95-105), fp16 KV cache with `context` tokens."""
+    from sharpinference_amd import native, phi4
+    cfg = phi4.Phi4Config(weight_format=native.F16, embed_format=native.F16, head_format=native.F16)
+    t0 = time.time()
+    weights = phi4.synth_weights(cfg, seed=11, distinct_layers=4, tied=True)
+    sess = phi4.Phi4DecodeSession(hip, cfg, weights)
+    kv = phi4.synth_kv(phi4.Phi4Config(layers=1, capacity=cfg.capacity), context, seed=12)[0]
+    for l in range(cfg.layers):
+        sess.load_kv(l, *kv)
+    log(f"decode f16: model on device in {time.time() - t0:.1f} s")
+    sess.set_control(1, context)
+    sess.plan.launch()
+    hip.sync()
+    us = sorted(sess.plan.measure_us(16) for _ in range(5))[2]
+    sess.close()
+    del weights
+    step_bytes = cfg.weight_bytes_per_token() + cfg.kv_bytes(context + 1)
+    gbs = step_bytes / us / 1e3
+    log(f"decode f16: {us:.1f} us/token ({1e6 / us:.0f} tok/s, {gbs:.0f} GB/s)")
+    return {"workload": "Phi-4-mini decode step, 32 layers, F16 layers, tied F16 embedding/head 200064x3072, "
+                        f"fp16 KV cache with {context} tokens, batch 1",
+            "us_per_token": r1(us), "tok_s": r1(1e6 / us), "bytes_per_token": step_bytes, "GBs": r1(gbs),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
+            "layer_weights": "4 distinct layers uploaded as 32 separate device copies"}
 
 
 def bench_prefill(hip, rng, m: int = 512):
@@ -360,13 +471,28 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
     sess.close()
     log(f"decode: {us:.1f} us/token on device ({1e6 / us:.0f} tok/s, {gbs:.0f} GB/s), "
         f"{loop_s * 1e6:.1f} us/token with host round trips")
+    op_program = None
+    if replay_timing:
+        # the same model as the reference's program form: 292 separate
+        # dispatches through the C++ host executor
+        from sharpinference_amd import host_program
+        prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True)
+        for l in range(cfg.layers):
+            prog.load_kv(l, *kv)
+        prog.forward_token(1, context)
+        op_us = sorted(prog.measure_us(8) for _ in range(5))[2]
+        op_program = {"us_per_token": r1(op_us), "tok_s": r1(1e6 / op_us), "dispatches": prog.dispatch_count(),
+                      "form": "transformer.* / quant.mat-vec instructions, one launch each (two for attention)"}
+        prog.close()
+        log(f"decode op-by-op program: {op_us:.1f} us/token ({1e6 / op_us:.0f} tok/s)")
     out = {"workload": "Phi-4-mini decode step, 32 layers, Q4_K layers, Q8_0 embedding/head 200064x3072, "
                        f"fp16 KV cache with {context} tokens, batch 1",
            "us_per_token": r1(us), "tok_s": r1(1e6 / us),
            "bytes_per_token": step_bytes, "GBs": r1(gbs), "hbm_frac": None if gbs != gbs else round(gbs / HBM_PEAK_GBS, 4),
            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
            "loop_us_per_token": round(loop_s * 1e6, 1), "loop_tok_s": round(1.0 / loop_s, 1),
-           "layer_weights": "4 distinct layers uploaded as 32 separate device copies"}
+           "layer_weights": "4 distinct layers uploaded as 32 separate device copies",
+           "op_program": op_program}
     if cpu:
         import oracle as orc
         model = orc.Phi4Oracle(cfg, weights)

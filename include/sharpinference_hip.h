@@ -107,6 +107,16 @@ int si_hip_copy(si_hip_context* ctx, void* device_dst, const void* device_src, u
  * it may be recorded into a plan). */
 int si_hip_fill_u32(si_hip_context* ctx, void* device_dst, uint32_t value, uint64_t count);
 
+/* Checksum of a device buffer: parts[0..SI_HIP_CHECKSUM_PARTS) receive
+ * partial sums (mod 2^32) of the 32-bit words of device_src, whose total is
+ * the buffer's word sum; one streaming read of `bytes` (a non-zero multiple
+ * of 4; src 16-byte aligned), e.g. to check uploaded tensors against a host
+ * checksum without reading them back.  No counterpart in the reference; a
+ * plain read of known size also gives the read bandwidth a kernel of the
+ * same bytes can reach. */
+#define SI_HIP_CHECKSUM_PARTS 1024
+int si_hip_checksum(si_hip_context* ctx, const void* device_src, uint64_t bytes, uint32_t* parts);
+
 /* Waits for all work queued on the context.  Replaces: the executor's fence
  * wait after a submission (Submit / WaitForCompletion, D3D12VmExecutor.cs:875-890). */
 int si_hip_sync(si_hip_context* ctx);

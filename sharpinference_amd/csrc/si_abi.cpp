@@ -265,6 +265,20 @@ int si_hip_fill_u32(si_hip_context* ctx, void* device_dst, uint32_t value, uint6
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "fill");
 }
 
+int si_hip_checksum(si_hip_context* ctx, const void* device_src, uint64_t bytes, uint32_t* parts)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "checksum: null context");
+    Enter g(ctx);
+    if (!device_src || !parts || !aligned(device_src, 16) || !aligned(parts, 4) || bytes % 4 != 0 || bytes == 0)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT,
+                    "checksum: src must be 16-byte aligned with a non-zero multiple of 4 bytes, parts 4-byte aligned");
+    if (overlaps(parts, 4 * SI_HIP_CHECKSUM_PARTS, device_src, bytes))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "checksum: parts overlap src");
+    const hipError_t e = si::launch_checksum(device_src, bytes, parts, ctx->stream);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "checksum");
+}
+
 int si_hip_sync(si_hip_context* ctx)
 {
     if (!ctx)

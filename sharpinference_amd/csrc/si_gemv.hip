@@ -1048,6 +1048,48 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, uint
         dst[i] = value;
 }
 
+// Partial sums (mod 2^32) of the 32-bit words of src: workgroup b of the
+// grid (at most CHECKSUM_PARTS) writes parts[b]; the first workgroup also
+// zeroes parts[grid..CHECKSUM_PARTS).  A streaming read of the whole
+// buffer, 64 bytes in flight per thread per step (four 16-byte loads), no
+// atomics.
+constexpr int CHECKSUM_PARTS = 1024;
+
+__global__ __launch_bounds__(WG) void checksum_kernel(const uint32_t* __restrict__ src, uint64_t words,
+                                                     uint32_t* __restrict__ parts)
+{
+    __shared__ uint32_t red[WG / 64];
+    const uint4* v = reinterpret_cast<const uint4*>(src);
+    const uint64_t n16 = words / 4;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * WG;
+    uint32_t sum = 0;
+    uint64_t i = static_cast<uint64_t>(blockIdx.x) * WG + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = v[i], b = v[i + stride], c = v[i + 2 * stride], d = v[i + 3 * stride];
+        sum += (a.x + a.y + a.z + a.w) + (b.x + b.y + b.z + b.w) + (c.x + c.y + c.z + c.w) + (d.x + d.y + d.z + d.w);
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = v[i];
+        sum += a.x + a.y + a.z + a.w;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < words % 4)
+        sum += src[n16 * 4 + threadIdx.x];
+    for (int off = 32; off > 0; off >>= 1)
+        sum += __shfl_xor(sum, off);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < WG / 64; w++)
+            t += red[w];
+        parts[blockIdx.x] = t;
+    }
+    if (blockIdx.x == 0)
+        for (int j = static_cast<int>(gridDim.x) + threadIdx.x; j < CHECKSUM_PARTS; j += WG)
+            parts[j] = 0;
+}
+
 // ---- dispatch --------------------------------------------------------------
 
 Seg to_seg(const GemvOp& op)
@@ -1342,6 +1384,15 @@ hipError_t launch_dequant(int fmt, const void* wv, float* out, int64_t rows, int
     case FMT_F32: hipLaunchKernelGGL((dequant_kernel<FMT_F32>), grid, dim3(WG), 0, s, w, out, nblocks); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_checksum(const void* src, uint64_t bytes, uint32_t* parts, hipStream_t s)
+{
+    const uint64_t chunks = (bytes / 16 + 4 * WG - 1) / (4 * WG);   // four 16-byte loads per thread
+    const unsigned grid = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(chunks, CHECKSUM_PARTS)));
+    hipLaunchKernelGGL(checksum_kernel, dim3(grid), dim3(WG), 0, s, static_cast<const uint32_t*>(src), bytes / 4,
+                       parts);
     return hipGetLastError();
 }
 

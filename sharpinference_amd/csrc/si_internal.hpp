@@ -101,5 +101,7 @@ hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, 
 hipError_t launch_dequant(int fmt, const void* w, float* out, int64_t rows, int64_t cols,
                           hipStream_t stream);
 hipError_t launch_fill_u32(void* dst, uint32_t value, uint64_t count, hipStream_t stream);
+// parts: SI_HIP_CHECKSUM_PARTS (1024) words whose sum is the checksum.
+hipError_t launch_checksum(const void* src, uint64_t bytes, uint32_t* parts, hipStream_t stream);
 
 }  // namespace si

@@ -26,6 +26,7 @@ BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
 
 OK, ERR_ARGUMENT, ERR_UNSUPPORTED, ERR_ADAPTATION, ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_STATE, ERR_FORMAT, ERR_IO = range(9)
 PATH_FAST, PATH_GENERIC, PATH_SHORT = 1, 2, 3
+CHECKSUM_PARTS = 1024
 
 # Every symbol include/sharpinference_hip.h declares, with its ctypes signature.
 _vp, _i32, _i64, _u32, _u64, _dbl = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32,
@@ -43,6 +44,7 @@ SIGNATURES = {
     "si_hip_readback": ([_vp, _vp, _vp, _u64], _i32),
     "si_hip_copy": ([_vp, _vp, _vp, _u64], _i32),
     "si_hip_fill_u32": ([_vp, _vp, _u32, _u64], _i32),
+    "si_hip_checksum": ([_vp, _vp, _u64, _vp], _i32),
     "si_hip_sync": ([_vp], _i32),
     "si_hip_gemv": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_i32)], _i32),
     "si_hip_dequant": ([_vp, _i32, _vp, _vp, _i64, _i64], _i32),
@@ -348,6 +350,11 @@ class HipContext:
 
     def fill_u32(self, dst: int, value: int, count: int) -> None:
         self._call(lib().si_hip_fill_u32, ctypes.c_void_p(int(dst)), ctypes.c_uint32(value), ctypes.c_uint64(count))
+
+    def checksum(self, src: int, nbytes: int, parts: int) -> None:
+        """parts[0..CHECKSUM_PARTS) = partial word sums of src (their total
+        mod 2^32 is the checksum)."""
+        self._call(lib().si_hip_checksum, ctypes.c_void_p(int(src)), nbytes, ctypes.c_void_p(int(parts)))
 
     def sync(self) -> None:
         self._call(lib().si_hip_sync)

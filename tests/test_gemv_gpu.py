@@ -339,3 +339,24 @@ def test_invalid_requests_are_rejected_without_fallback(hip):
     assert "overlaps" in native.lib().si_hip_last_error(hip.handle).decode()
     for b in (w, x, y):
         b.free()
+
+
+def test_checksum_sums_every_word(hip):
+    """si_hip_checksum: the partial sums cover every 32-bit word once (total
+    = word sum mod 2^32), for sizes with and without a tail past the 16-byte
+    chunks and for grids below and at the partial count; stale partials from
+    a larger buffer are zeroed."""
+    rng = np.random.default_rng(9)
+    parts = hip.to_device(np.full(native.CHECKSUM_PARTS, 0xDEADBEEF, np.uint32))
+    for words in (7 * 2 ** 20 + 3, 1, 7, 4096, 1000003, 3):
+        a = rng.integers(0, 2 ** 32, size=words, dtype=np.uint64).astype(np.uint32)
+        d = hip.to_device(a)
+        hip.checksum(d.ptr, a.nbytes, parts.ptr)
+        got = int(parts.readback(np.uint32).astype(np.uint64).sum() % 2 ** 32)
+        assert got == int(a.astype(np.uint64).sum() % 2 ** 32), words
+        d.free()
+    with pytest.raises(native.HipError):
+        hip.checksum(parts.ptr + 4, 16, parts.ptr + 8192)       # not 16-byte aligned
+    with pytest.raises(native.HipError):
+        hip.checksum(parts.ptr, 6, parts.ptr + 8192)            # not whole words
+    parts.free()
