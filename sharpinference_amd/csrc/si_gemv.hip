@@ -90,6 +90,50 @@ __device__ __forceinline__ float group_sum(float v)
     return v;
 }
 
+// Maximum and sum of unsigned / signed integers over aligned groups of 8
+// lanes (same DPP lane moves as group_sum).
+__device__ __forceinline__ uint32_t group8_max_u32(uint32_t v)
+{
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
+    return max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x141, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ int group8_sum_i32(int v)
+{
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
+}
+
+// ---- x as integer digit planes ----------------------------------------------
+// Each 32-column block of the staged x is scaled by a power of two 2^s
+// chosen from the block's largest magnitude M (M * 2^s < 2^21) and rounded
+// to integers X (|X| <= 2^21; the rounding is below 2^-22 M per value,
+// finer than the FP32 rounding of a sum that holds M).  X + 0x808080 has
+// bytes b0, b1, b2 in [0, 255]; the signed bytes d_p = b_p - 128 are its
+// balanced base-256 digits, X = d0 + 256 d1 + 65536 d2 (|d2| <= 32).  Plane p
+// packs d_p of 4 consecutive values into one word, so a 4-bit weight word
+// (nibbles masked into bytes 0..15) is multiplied with 4 values in one
+// v_dot4_i32_i8, exactly.  Per block and row, the three planes combine in
+// INT32 (Horner in 256: |sum q X| <= 32 * 15 * 2^21 < 2^31) and the block
+// enters the FP32 row sum once: d * 2^-s * sum((q - offset) * X).
+//
+// LDS per 64-column unit (PLANE_UNIT words): block h's planes at 24h +
+// 8p + w (word w = values 4w..4w+3 of the block), then inv_0, inv_1
+// (2^-s, or NaN when the block holds a non-finite value or a magnitude
+// outside [2^-100, 2^100], whose products then take the per-weight FP32
+// form with x read from global memory), then aux_0, aux_1 (Q4_0: 8 sum(X)
+// as INT32; Q4_K: sum(X) 2^-s as FP32).  52 words: 16 lanes reading
+// consecutive units with 16-byte reads touch distinct banks.
+constexpr int PLANE_UNIT = 52;
+constexpr uint32_t BIG_BITS = 0x71800000u;    // 2^100
+constexpr uint32_t TINY_BITS = 0x0D800000u;   // 2^-100
+
+__device__ __forceinline__ int dot4_planes(uint32_t q, uint32_t p, int a)
+{
+    return __builtin_amdgcn_sdot4(static_cast<int>(q), static_cast<int>(p), a, false);
+}
+
 __device__ __forceinline__ float wave_sum(float v)
 {
     v = group_sum<16>(v);
@@ -185,6 +229,37 @@ struct QUnit<FMT_Q4_0> {
         return scale(h) * fmaf(-8.0f, sx, fmaf(a_hi, 0.0625f, a_lo));
     }
 
+    // Block h against x's digit planes P (24 words, plane p word w at
+    // 8p + w); inv = 2^-s, sum8 = 8 sum(X).  Low nibbles are values 4k..4k+3
+    // (plane word k), high nibbles values 16+4k.. (word 4+k).
+    __device__ __forceinline__ float planes(int h, const uint32_t* P, float inv, int sum8, float acc) const
+    {
+        constexpr uint32_t M = 0x0f0f0f0fu;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (h == 0) {
+                lo[k] = __builtin_amdgcn_alignbit(v[k + 1], v[k], 16) & M;
+                hi[k] = __builtin_amdgcn_alignbit(v[k + 1], v[k], 20) & M;
+            } else {
+                lo[k] = v[5 + k] & M;
+                hi[k] = (v[5 + k] >> 4) & M;
+            }
+        }
+        int s = 0;
+#pragma unroll
+        for (int p = 2; p >= 0; p--) {
+            if (p < 2)
+                s <<= 8;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s = dot4_planes(lo[k], P[8 * p + k], s);
+                s = dot4_planes(hi[k], P[8 * p + 4 + k], s);
+            }
+        }
+        return fmaf(scale(h) * inv, static_cast<float>(s - sum8), acc);
+    }
+
     // Classification-exact form for non-finite or huge x: (nibble ^ 8) is
     // (nibble - 8) as a signed 4-bit number; moved to the top of a byte it
     // reads as the signed byte 16 * (nibble - 8), so every product carries
@@ -257,6 +332,27 @@ struct QUnit<FMT_Q4_K> {
         }
         const float d1 = dsc[h] * (h == 0 ? 1.0f : 0.0625f);
         return fmaf(d1, a0 + a1, -(dmn[h] * sx));
+    }
+
+    // Sub-block 2c + h against x's digit planes P (nibble word k holds
+    // values 4k..4k+3, plane word k); inv = 2^-s, sxq = sum(X) 2^-s.
+    __device__ __forceinline__ float planes(int h, const uint32_t* P, float inv, float sxq, float acc) const
+    {
+        constexpr uint32_t M = 0x0f0f0f0fu;
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            q[k] = (h == 0 ? qs[k] : qs[k] >> 4) & M;
+        int s = 0;
+#pragma unroll
+        for (int p = 2; p >= 0; p--) {
+            if (p < 2)
+                s <<= 8;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                s = dot4_planes(q[k], P[8 * p + k], s);
+        }
+        return fmaf(dsc[h] * inv, static_cast<float>(s), fmaf(-dmn[h], sxq, acc));
     }
 
     // Same contribution with every weight decoded as the oracle does,
@@ -442,7 +538,7 @@ __device__ __forceinline__ float4 f4_sub(float4 a, float m) { return make_float4
 // NV is the number of transform vectors the fused form loads per x value: 1
 // (SwiGLU's up half or the RMSNorm weight; none needed loads x again) or 4
 // (LayerNorm weight and bias, token-mix and previous-token vectors).
-template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL, int NV = 1>
+template <int FMT, int LK, int UPL, int RL, int KS, int NW, int NS, bool FULL, int NV = 1, int XM = 0>
 __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __restrict__ w0,
                                                            const float* __restrict__ x0, const float* res0,
                                                            const float* __restrict__ nw0, int rows0, int out0,
@@ -462,8 +558,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     constexpr int64_t ROW_BYTES = static_cast<int64_t>(UPR) * QUnit<FMT>::UNIT_BYTES;
     static_assert(K % 32 == 0 && THREADS % 8 == 0, "x staging keeps 8-thread groups whole");
 
-    __shared__ float4 xs4[UPR * XS_UNIT / 4];
-    __shared__ float bs[UPR * 2];
+    constexpr bool PLANES = XM == 1;
+    static_assert(!PLANES || FMT == FMT_Q4_0 || FMT == FMT_Q4_K, "digit planes serve the 4-bit formats");
+    __shared__ float4 xs4[PLANES ? 1 : UPR * XS_UNIT / 4];
+    __shared__ float bs[PLANES ? 1 : UPR * 2];
+    __shared__ uint4 xp4[PLANES ? UPR * PLANE_UNIT / 4 : 1];
     __shared__ float part[ROWS_PER_WG * KS];
     __shared__ float red[NW], red2[NW];
 
@@ -586,6 +685,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     for (int j = 0; j < XPT; j++)
         if (!xin(j))
             xr[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float ln_mean = 0.0f, ln_inv = 0.0f;   // LayerNorm statistics (the per-weight form recomputes x)
     if (in_kind == XF_SWIGLU) {
         // x = [gate | up]; reference order: gate / (1 + exp(-gate)) * up
 #pragma unroll
@@ -662,6 +762,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
         }
         const float var = m2 / static_cast<float>(K);
         const float inv = 1.0f / sqrtf(var + sg.eps);
+        ln_mean = mean;
+        ln_inv = inv;
 #pragma unroll
         for (int j = 0; j < XPT; j++)
             if (xin(j))
@@ -691,17 +793,65 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             xr[j] = v;
         }
     }
+    if constexpr (PLANES) {
+        // digit planes of each 32-column block (8 threads of 4 values)
+        uint32_t* xp = reinterpret_cast<uint32_t*>(xp4);
 #pragma unroll
-    for (int j = 0; j < XPT; j++) {
-        const int col = 4 * (threadIdx.x + j * THREADS);
-        if (xin(j))
-            xs4[(col >> 6) * (XS_UNIT / 4) + ((col & 63) >> 2)] = xr[j];
+        for (int j = 0; j < XPT; j++) {
+            const int i = threadIdx.x + j * THREADS;
+            const float4 v = xr[j];
+            // largest magnitude as bits (integer order = magnitude order;
+            // NaN sorts above inf), over the block's 8 threads
+            uint32_t mb = max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                              max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu));
+            mb = group8_max_u32(mb);
+            const bool exact = mb > BIG_BITS || (mb != 0u && mb < TINY_BITS);
+            const uint32_t e = max(mb >> 23, 27u);                  // biased exponent of M (zero blocks: 27)
+            // M < 2^(e - 126), so s = 147 - e gives M 2^s < 2^21
+            const float scale = __uint_as_float((274u - e) << 23);  // 2^s
+            const float inv = __uint_as_float((e - 20u) << 23);     // 2^-s
+            // X + 0x808080 from the FP32 bits of X + 1.5 * 2^23 (round to nearest even)
+            const uint32_t y0 = __float_as_uint(fmaf(v.x, scale, 0x1.8p23f)) - 0x4ABF7F80u;
+            const uint32_t y1 = __float_as_uint(fmaf(v.y, scale, 0x1.8p23f)) - 0x4ABF7F80u;
+            const uint32_t y2 = __float_as_uint(fmaf(v.z, scale, 0x1.8p23f)) - 0x4ABF7F80u;
+            const uint32_t y3 = __float_as_uint(fmaf(v.w, scale, 0x1.8p23f)) - 0x4ABF7F80u;
+            // byte transpose: plane p = byte p of y0..y3, then b - 128 as a signed byte
+            const uint32_t t01 = __builtin_amdgcn_perm(y1, y0, 0x06020400u);   // y0.b0 y1.b0 y0.b2 y1.b2
+            const uint32_t t23 = __builtin_amdgcn_perm(y3, y2, 0x06020400u);
+            const uint32_t u01 = __builtin_amdgcn_perm(y1, y0, 0x0c0c0501u);   // y0.b1 y1.b1
+            const uint32_t u23 = __builtin_amdgcn_perm(y3, y2, 0x0c0c0501u);
+            const uint32_t p0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+            const uint32_t p1 = __builtin_amdgcn_perm(u23, u01, 0x05040100u) ^ 0x80808080u;
+            const uint32_t p2 = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+            const int sx = group8_sum_i32(static_cast<int>((y0 + y1) + (y2 + y3)) - 4 * 0x808080);
+            if (xin(j)) {
+                const int col = 4 * i;
+                const int h = (col >> 5) & 1;
+                uint32_t* ub = xp + (col >> 6) * PLANE_UNIT;
+                uint32_t* pw = ub + 24 * h + ((col >> 2) & 7);
+                pw[0] = p0;
+                pw[8] = p1;
+                pw[16] = p2;
+                if ((i & 7) == 0) {
+                    ub[48 + h] = exact ? 0x7fc00000u : __float_as_uint(inv);
+                    ub[50 + h] = FMT == FMT_Q4_0 ? static_cast<uint32_t>(8 * sx)
+                                                 : __float_as_uint(static_cast<float>(sx) * inv);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < XPT; j++) {
+            const int col = 4 * (threadIdx.x + j * THREADS);
+            if (xin(j))
+                xs4[(col >> 6) * (XS_UNIT / 4) + ((col & 63) >> 2)] = xr[j];
+        }
     }
     // The factored Q4 forms need sum(x) per 32 columns.  A block holding a
     // non-finite or huge (|x| > 2^100) value stores NaN instead (NaN fails
     // every comparison, so it counts as wide too): its products then take
     // the per-weight form, which keeps each product's IEEE class.
-    constexpr bool SUMS = FMT == FMT_Q4_0 || FMT == FMT_Q4_K;
+    constexpr bool SUMS = (FMT == FMT_Q4_0 || FMT == FMT_Q4_K) && !PLANES;
     if constexpr (SUMS) {
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
@@ -728,6 +878,34 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
             total += red[i];
         return 1.0f / sqrtf(total / static_cast<float>(K) + sg.eps);
     };
+    // the staged values of float4 q recomputed from global memory (the
+    // per-weight form of a block whose digit planes are not valid)
+    auto xval4 = [&](int q) -> float4 {
+        float4 v = x4[q];
+        if constexpr (FULL) {
+            const float* nw = NS == 1 ? nw0 : sg.nw;
+            if (in_kind == XF_SWIGLU) {
+                const float4 up = x4[K / 4 + q];
+                v = make_float4(silu_mul(v.x, up.x), silu_mul(v.y, up.y), silu_mul(v.z, up.z), silu_mul(v.w, up.w));
+            } else if (in_kind == XF_RMSNORM) {
+                const float4 g = reinterpret_cast<const float4*>(nw)[q];
+                v = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
+            } else if (NV == 4 && (in_kind == XF_LAYERNORM || in_kind == XF_LAYERNORM_MIX)) {
+                const float4 g = reinterpret_cast<const float4*>(nw)[q];
+                const float4 bb = reinterpret_cast<const float4*>(sg.nb)[q];
+                v = f4_sub(v, ln_mean);
+                v = make_float4(v.x * ln_inv * g.x + bb.x, v.y * ln_inv * g.y + bb.y, v.z * ln_inv * g.z + bb.z,
+                                v.w * ln_inv * g.w + bb.w);
+                if (in_kind == XF_LAYERNORM_MIX) {
+                    const float4 m = reinterpret_cast<const float4*>(sg.mix)[q];
+                    const float4 pv = reinterpret_cast<const float4*>(sg.prev)[q];
+                    v = make_float4(v.x + (pv.x - v.x) * m.x, v.y + (pv.y - v.y) * m.y, v.z + (pv.z - v.z) * m.z,
+                                    v.w + (pv.w - v.w) * m.w);
+                }
+            }
+        }
+        return v;
+    };
     float acc[RL];
 #pragma unroll
     for (int t = 0; t < RL; t++)
@@ -738,6 +916,37 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
 #pragma unroll
         for (int t = 0; t < RL; t++)
             w[i][t].prepare();
+        if constexpr (PLANES) {
+            const uint4* ub = xp4 + u * (PLANE_UNIT / 4);
+            const uint4 info = ub[12];   // inv_0, inv_1, aux_0, aux_1
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t P[24];
+#pragma unroll
+                for (int k = 0; k < 6; k++) {
+                    const uint4 q = ub[6 * h + k];
+                    P[4 * k] = q.x; P[4 * k + 1] = q.y; P[4 * k + 2] = q.z; P[4 * k + 3] = q.w;
+                }
+                const float inv = __uint_as_float(h == 0 ? info.x : info.y);
+                const uint32_t aux = h == 0 ? info.z : info.w;
+                if (__builtin_expect(inv == inv, 1)) {
+#pragma unroll
+                    for (int t = 0; t < RL; t++) {
+                        if constexpr (FMT == FMT_Q4_0)
+                            acc[t] = w[i][t].planes(h, P, inv, static_cast<int>(aux), acc[t]);
+                        else
+                            acc[t] = w[i][t].planes(h, P, inv, __uint_as_float(aux), acc[t]);
+                    }
+                } else {
+                    float4 xv[8];
+                    for (int k = 0; k < 8; k++)
+                        xv[k] = xval4(u * 16 + h * 8 + k);
+                    for (int t = 0; t < RL; t++)
+                        acc[t] += w[i][t].half_exact(h, xv);
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             float4 xv[8];
@@ -1137,7 +1346,7 @@ dim3 fill_segs(Segs<NS>& t, const GemvOp* ops, int n, PerWg per_wg)
     return dim3(width, static_cast<unsigned>(n));
 }
 
-template <int FMT, int LK, int UPL, int RL, int KS, int NW>
+template <int FMT, int LK, int UPL, int RL, int KS, int NW, int XM = 0>
 hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
 {
     constexpr int R = (64 / LK) * RL * (NW / KS);
@@ -1155,22 +1364,22 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
         Segs<1> t;
         const dim3 grid = fill_segs(t, ops, n, per);
         if (is_plain(o))
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false>), grid, dim3(64 * NW), 0,
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, false, 1, XM>), grid, dim3(64 * NW), 0,
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else if (ln)
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 4>), grid, dim3(64 * NW), 0,
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 4, XM>), grid, dim3(64 * NW), 0,
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 1>), grid, dim3(64 * NW), 0,
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, 1, true, 1, XM>), grid, dim3(64 * NW), 0,
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     } else {
         Segs<MAX_SEGS> t;
         const dim3 grid = fill_segs(t, ops, n, per);
         if (ln)
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4>), grid, dim3(64 * NW),
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4, XM>), grid, dim3(64 * NW),
                                0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
         else
-            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 1>), grid, dim3(64 * NW),
+            hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 1, XM>), grid, dim3(64 * NW),
                                0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     }
     return hipGetLastError();
@@ -1199,19 +1408,22 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
             return launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s);
         if constexpr (FMT == FMT_Q8_0)
             return mid ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
-        // Q4 formats: wide workgroups (one per CU at 3072 and 5120 rows)
-        // stage x once per CU instead of once per 4 rows
-        return mid              ? launch_tiled<FMT, 16, 3, 1, 1, 8>(ops, n, s)
-               : rows64 >= 5120 ? launch_tiled<FMT, 16, 1, 1, 3, 15>(ops, n, s)
-               : rows64 >= 3072 ? launch_tiled<FMT, 16, 1, 1, 3, 9>(ops, n, s)
-                                : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+        else   // Q4 formats: wide workgroups (one per CU at 3072 and 5120 rows)
+            // stage x once per CU instead of once per 4 rows, as digit planes
+            // for the integer dot products
+            return mid              ? launch_tiled<FMT, 16, 3, 1, 1, 4, 1>(ops, n, s)
+                   : rows64 >= 5120 ? launch_tiled<FMT, 16, 1, 1, 3, 15, 1>(ops, n, s)
+                   : rows64 >= 3072 ? launch_tiled<FMT, 16, 1, 1, 3, 12, 1>(ops, n, s)
+                                    : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
     case 4096: return mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
     case 6144: return mid ? launch_tiled<FMT, 16, 3, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
     case 8192:
         if (mid)
             return launch_tiled<FMT, 16, 4, 2, 2, 4>(ops, n, s);
         if constexpr (FMT == FMT_Q4_K)   // 12 rows per workgroup, 256 workgroups at 3072 rows
-            return launch_tiled<FMT, 16, 2, 1, 4, 12>(ops, n, s);
+            return launch_tiled<FMT, 16, 2, 1, 4, 12, 1>(ops, n, s);
+        // 4 rows per workgroup: deriving digit planes of 8192 values would
+        // cost more than the integer products save
         return launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
     default: return hipErrorNotSupported;
     }

@@ -257,6 +257,41 @@ def test_wide_and_finite_blocks_mix_in_one_row(hip, fmt, rows):
         assert np.array_equal(y[fin], truth[fin].astype(np.float32)), f"{NAMES[fmt]} {bad}: inf rows differ"
 
 
+@pytest.mark.parametrize("fmt", [native.Q4_0, native.Q4_K])
+@pytest.mark.parametrize("rows", [16384, 5120, 3072])
+def test_digit_plane_block_scales(hip, fmt, rows):
+    """The 4-bit tiles at 3072 columns stage x as integer digit planes under
+    a power-of-two scale per 32 columns (the block's largest magnitude M
+    maps below 2^21).  Edge blocks: M exactly 2^100 (planes) and one ulp
+    above (per-weight form), M exactly 2^-100 (planes) and below it
+    (per-weight form, subnormals included), an all-zero block, and one
+    large value next to 31 small ones; every row within the GEMV gate of
+    the fp64 product."""
+    cols = 3072
+    w = orc.gen_quant(fmt, 91 + rows, rows, cols)
+    rng = np.random.default_rng(rows)
+    big = orc.gen_normal_f32(92 + rows, cols, 0.0, 1.0)
+    big[96] = np.float32(2.0 ** 100)
+    big[160] = np.nextafter(np.float32(2.0 ** 100), np.float32(np.inf))
+    small = orc.gen_normal_f32(93 + rows, cols, 0.0, 1.0)
+    small[224:256] = (rng.uniform(0.5, 1.0, 32) * 2.0 ** -100).astype(np.float32)
+    small[230] = np.float32(2.0 ** -100)                               # M = 2^-100: planes
+    small[288:320] = (rng.uniform(0.5, 1.0, 32) * 2.0 ** -101).astype(np.float32)
+    small[300:304] = np.float32([1e-40, -3e-42, 1e-45, 0.0])          # subnormals: per-weight form
+    small[320:352] = 0.0
+    small[384:416] = rng.uniform(-1e-3, 1e-3, 32).astype(np.float32)
+    small[400] = np.float32(1000.0)
+    for name, x in (("huge", big), ("small", small)):
+        y, _ = run_gemv(hip, fmt, w, x, rows, cols)
+        assert_gemv_close(y, orc.gemv_f64(fmt, w, x, rows, cols), f"{NAMES[fmt]} {rows} {name}")
+    # scale-free blocks alone: a row sum made only of 2^-100-scale values
+    tiny = np.zeros(cols, np.float32)
+    tiny[224:256] = small[224:256]
+    tiny[288:320] = small[288:320]
+    y, _ = run_gemv(hip, fmt, w, tiny, rows, cols)
+    assert_gemv_close(y, orc.gemv_f64(fmt, w, tiny, rows, cols), f"{NAMES[fmt]} {rows} tiny")
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_cancellation_stays_within_fp32_accumulation_bound(hip, fmt):
     """GpuMatVecTests.CooperativeMergePreservesCancellationAcrossAndWithinLanes
