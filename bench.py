@@ -73,6 +73,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill (MFMA) measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the Phi-4-mini decode-step measurement")
     ap.add_argument("--no-rwkv", action="store_true", help="skip the RWKV-7 token-step measurement")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the plain-read ceiling leg")
     ap.add_argument("--no-legs", action="store_true",
                     help="skip the single-matrix legs (Q8_0 and F16 3072x3072, F16 head) and the F16 decode step")
     ap.add_argument("--decode-only", action="store_true",
@@ -214,30 +215,7 @@ def main() -> int:
                          "GBs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         log(f"  {name:8s} {rows}x{cols}: {us:.3f} us/launch, {b / us / 1e3:.1f} GB/s")
 
-    # plain-read ceiling: the same bytes, read once by a streaming kernel
-    # (si_hip_checksum), in the same plan structure (one launch per weight
-    # tensor, the step's four in order, rotating over the copies)
-    acc = hip.alloc(4 * native.CHECKSUM_PARTS)
-    read_plan = hip.record(lambda: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
-                                    for c in range(copies) for k in range(len(shapes))])
-    read_plan.measure_us(2)
-    read_us = sorted(read_plan.measure_us(8) for _ in range(5))[2] / copies
-    read_w = sum(w.nbytes for w in host_w)
-    read_shapes = {}
-    for k, (name, rows, cols) in enumerate(shapes):
-        plan = hip.record(lambda k=k: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
-                                       for c in range(copies)])
-        plan.measure_us(2)
-        us = sorted(plan.measure_us(8) for _ in range(5))[2] / copies
-        read_shapes[name] = {"bytes": host_w[k].nbytes, "us_per_launch": round(us, 3),
-                             "GBs": round(host_w[k].nbytes / us / 1e3, 1)}
-        plan.destroy()
-    read_plan.destroy()
-    acc.free()
-    ceiling = {"kernel": "checksum_kernel (streaming 16-byte reads, one partial per workgroup)", "us_per_step": round(read_us, 3),
-               "GBs": round(read_w / read_us / 1e3, 1), "frac": round(read_w / read_us / 1e3 / HBM_PEAK_GBS, 4),
-               "shapes": read_shapes}
-    log(f"plain-read ceiling of the same weights: {read_us:.2f} us/step, {read_w / read_us / 1e3:.0f} GB/s")
+    ceiling = None if args.no_ceiling else bench_read_ceiling(hip, shapes, copies, dev_w, host_w)
 
     legs = None if args.no_legs else bench_matvec_legs(hip, rng)
     prefill = None if args.no_prefill else bench_prefill(hip, rng)
@@ -334,6 +312,34 @@ def time_rotated_gemv(hip, fmt, host, rows, cols, copies, rng):
     return {"format": native.FORMAT_NAMES[fmt], "rows": rows, "cols": cols, "bytes": nbytes,
             "weight_copies_rotated": copies, "us_per_launch": round(us, 3), "GBs": round(nbytes / us / 1e3, 1),
             "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def bench_read_ceiling(hip, shapes, copies, dev_w, host_w):
+    """Plain-read ceiling: the same bytes, read once by a streaming kernel
+    (si_hip_checksum), in the same plan structure (one launch per weight
+    tensor, the step's four in order, rotating over the copies)."""
+    acc = hip.alloc(4 * native.CHECKSUM_PARTS)
+    read_plan = hip.record(lambda: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
+                                    for c in range(copies) for k in range(len(shapes))])
+    read_plan.measure_us(2)
+    read_us = sorted(read_plan.measure_us(8) for _ in range(5))[2] / copies
+    read_w = sum(w.nbytes for w in host_w)
+    read_shapes = {}
+    for k, (name, rows, cols) in enumerate(shapes):
+        plan = hip.record(lambda k=k: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
+                                       for c in range(copies)])
+        plan.measure_us(2)
+        us = sorted(plan.measure_us(8) for _ in range(5))[2] / copies
+        read_shapes[name] = {"bytes": host_w[k].nbytes, "us_per_launch": round(us, 3),
+                             "GBs": round(host_w[k].nbytes / us / 1e3, 1)}
+        plan.destroy()
+    read_plan.destroy()
+    acc.free()
+    ceiling = {"kernel": "checksum_kernel (streaming 16-byte reads, one partial per workgroup)", "us_per_step": round(read_us, 3),
+               "GBs": round(read_w / read_us / 1e3, 1), "frac": round(read_w / read_us / 1e3 / HBM_PEAK_GBS, 4),
+               "shapes": read_shapes}
+    log(f"plain-read ceiling of the same weights: {read_us:.2f} us/step, {read_w / read_us / 1e3:.0f} GB/s")
+    return ceiling
 
 
 def bench_matvec_legs(hip, rng):

@@ -1259,27 +1259,33 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, uint
 
 // Partial sums (mod 2^32) of the 32-bit words of src: workgroup b of the
 // grid (at most CHECKSUM_PARTS) writes parts[b]; the first workgroup also
-// zeroes parts[grid..CHECKSUM_PARTS).  A streaming read of the whole
-// buffer, 64 bytes in flight per thread per step (four 16-byte loads), no
-// atomics.
+// zeroes parts[grid..CHECKSUM_PARTS).  A plain streaming read, no atomics:
+// each pass issues every 16-byte load of a thread (LOADS of them, a
+// workgroup's 4 KB apart) before the first is used, so a pass costs one
+// memory round trip; LOADS is the smallest of 2, 4, 8, 16 that covers the
+// buffer in one pass of CHECKSUM_PARTS workgroups.
 constexpr int CHECKSUM_PARTS = 1024;
 
+template <int CHECKSUM_LOADS>
 __global__ __launch_bounds__(WG) void checksum_kernel(const uint32_t* __restrict__ src, uint64_t words,
                                                      uint32_t* __restrict__ parts)
 {
     __shared__ uint32_t red[WG / 64];
     const uint4* v = reinterpret_cast<const uint4*>(src);
     const uint64_t n16 = words / 4;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * WG;
+    const uint64_t span = static_cast<uint64_t>(WG) * CHECKSUM_LOADS;
     uint32_t sum = 0;
-    uint64_t i = static_cast<uint64_t>(blockIdx.x) * WG + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const uint4 a = v[i], b = v[i + stride], c = v[i + 2 * stride], d = v[i + 3 * stride];
-        sum += (a.x + a.y + a.z + a.w) + (b.x + b.y + b.z + b.w) + (c.x + c.y + c.z + c.w) + (d.x + d.y + d.z + d.w);
-    }
-    for (; i < n16; i += stride) {
-        const uint4 a = v[i];
-        sum += a.x + a.y + a.z + a.w;
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * span + threadIdx.x; base < n16;
+         base += static_cast<uint64_t>(gridDim.x) * span) {
+        uint4 a[CHECKSUM_LOADS];
+#pragma unroll
+        for (int k = 0; k < CHECKSUM_LOADS; k++) {
+            const uint64_t i = base + static_cast<uint64_t>(k) * WG;
+            a[k] = i < n16 ? v[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < CHECKSUM_LOADS; k++)
+            sum += (a[k].x + a[k].y) + (a[k].z + a[k].w);
     }
     if (blockIdx.x == 0 && threadIdx.x < words % 4)
         sum += src[n16 * 4 + threadIdx.x];
@@ -1601,10 +1607,18 @@ hipError_t launch_dequant(int fmt, const void* wv, float* out, int64_t rows, int
 
 hipError_t launch_checksum(const void* src, uint64_t bytes, uint32_t* parts, hipStream_t s)
 {
-    const uint64_t chunks = (bytes / 16 + 4 * WG - 1) / (4 * WG);   // four 16-byte loads per thread
-    const unsigned grid = static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(chunks, CHECKSUM_PARTS)));
-    hipLaunchKernelGGL(checksum_kernel, dim3(grid), dim3(WG), 0, s, static_cast<const uint32_t*>(src), bytes / 4,
-                       parts);
+    const uint64_t n16 = bytes / 16;
+    const uint64_t cover = static_cast<uint64_t>(CHECKSUM_PARTS) * WG;   // 16-byte loads per load slot
+    const int loads = n16 <= 2 * cover ? 2 : n16 <= 4 * cover ? 4 : n16 <= 8 * cover ? 8 : 16;
+    const uint64_t chunks = (n16 + static_cast<uint64_t>(loads) * WG - 1) / (static_cast<uint64_t>(loads) * WG);
+    const dim3 grid(static_cast<unsigned>(std::max<uint64_t>(1, std::min<uint64_t>(chunks, CHECKSUM_PARTS))));
+    const uint32_t* w = static_cast<const uint32_t*>(src);
+    switch (loads) {
+    case 2: hipLaunchKernelGGL(checksum_kernel<2>, grid, dim3(WG), 0, s, w, bytes / 4, parts); break;
+    case 4: hipLaunchKernelGGL(checksum_kernel<4>, grid, dim3(WG), 0, s, w, bytes / 4, parts); break;
+    case 8: hipLaunchKernelGGL(checksum_kernel<8>, grid, dim3(WG), 0, s, w, bytes / 4, parts); break;
+    default: hipLaunchKernelGGL(checksum_kernel<16>, grid, dim3(WG), 0, s, w, bytes / 4, parts); break;
+    }
     return hipGetLastError();
 }
 
