@@ -343,6 +343,107 @@ int si_hip_gqa_workspace_bytes(int query_heads, int head_size, int context, uint
  * (GpuTransformerInstructionCollection.cs:46-143). */
 int si_hip_grouped_query_attention(si_hip_context* ctx, const si_hip_gqa_args* args);
 
+/* ---- batched (prefill) transformer operators -------------------------------------- */
+
+/* The operators of the reference's D3D12 prefill program
+ * (GpuBatchTransformerInstructions.cs), one launch each (batch-gqa-values:
+ * two).  Every one takes control = device int32[2] {start, valid}: the
+ * batch's buffers hold `batch` rows (1..16), row r < valid is the token at
+ * position start + r, rows r >= valid are neither read nor written.
+ * Matrices are row-major [batch][width]; KV caches [context][kv_heads][128]
+ * (FP32 as in the reference, or fp16). */
+
+/* output[r] = table[start + r] for r < valid and 0 <= start + r < table_rows.
+ * Replaces: transformer.batch-gather-rows (GpuBatchTransformerInstructions.cs:646-679). */
+int si_hip_batch_gather_rows(si_hip_context* ctx, const float* table, int64_t table_rows, int64_t width,
+                             const int32_t* control, float* output, int batch);
+
+/* Per live row: output = input * (1 / sqrt(sum(input^2) / width + eps)) * weight.
+ * Replaces: transformer.batch-rms-norm (GpuBatchTransformerInstructions.cs:101-156). */
+int si_hip_batch_rms_norm(si_hip_context* ctx, const float* input, const float* weight, const int32_t* control,
+                          float* output, int batch, int64_t width, float eps);
+
+/* Per live row: updated = hidden + residual, output = rms-norm(updated).
+ * Replaces: transformer.batch-residual-rms-norm (GpuBatchTransformerInstructions.cs:158-222). */
+int si_hip_batch_residual_rms_norm(si_hip_context* ctx, const float* hidden, const float* residual,
+                                   const float* weight, const int32_t* control, float* updated, float* output,
+                                   int batch, int64_t width, float eps);
+
+/* output[r] = W . input[r] for live rows, W [rows, columns] in any matrix
+ * format (Q8_0, Q4_0, Q4_K, F16, F32; columns % 32 == 0, Q4_K % 256), FP32
+ * products and sums on the matrix cores (v_mfma_f32_16x16x4_f32).  Replaces:
+ * transformer.batch-shared-matvec (GpuBatchTransformerInstructions.cs:224-279),
+ * whose weight is F16. */
+int si_hip_batch_matvec(si_hip_context* ctx, int format, const void* weight, const float* input,
+                        const int32_t* control, float* output, int batch, int64_t rows, int64_t columns);
+
+/* Per live row: output[i] = g_i / (1 + exp(-g_i)) * u_i over gate_up[r] = [g | u].
+ * Replaces: transformer.batch-swiglu (GpuBatchTransformerInstructions.cs:281-316). */
+int si_hip_batch_swiglu(si_hip_context* ctx, const float* gate_up, const int32_t* control, float* output,
+                        int batch, int64_t width);
+
+typedef struct si_hip_batch_rope_args {
+    const float* qkv;          /* [batch][query_size | kv_size | kv_size] */
+    const int32_t* control;
+    const float* frequencies;  /* [rotary_size / 2] */
+    float* query;              /* [batch][query_size] rotated queries */
+    void* key_cache;           /* [context][kv_size], cache_format */
+    void* value_cache;
+    int32_t cache_format;      /* SI_HIP_F32 or SI_HIP_F16 (rounded to nearest even) */
+    int32_t batch;
+    int32_t query_size;        /* a multiple of head_size */
+    int32_t kv_size;           /* kv_heads * head_size */
+    int32_t head_size;
+    int32_t rotary_size;       /* even, <= head_size */
+    int32_t context;
+    float rope_scale;
+} si_hip_batch_rope_args;
+
+/* Per live row r at position p = start + r inside the cache: rotate-half
+ * rotary embedding of q and k (angle p * frequencies[i], cos and sin times
+ * rope_scale), q to query[r], k and v to cache row p.  Replaces:
+ * transformer.batch-rope-kv-write (GpuBatchTransformerInstructions.cs:318-413). */
+int si_hip_batch_rope_kv_write(si_hip_context* ctx, const si_hip_batch_rope_args* args);
+
+typedef struct si_hip_batch_attention_args {
+    const float* query;          /* scores: [batch][query_heads * 128], 16-byte aligned */
+    const float* probabilities;  /* values: [batch][query_heads][context] */
+    const void* cache;           /* scores: key cache; values: value cache ([context][kv_heads][128]) */
+    const int32_t* control;
+    float* output;               /* scores: [batch][query_heads][context]; values: [batch][query_heads * 128] */
+    float* workspace;            /* values: si_hip_batch_values_workspace_bytes; any contents on entry;
+                                    calls sharing one workspace must not overlap on the GPU */
+    int32_t cache_format;        /* SI_HIP_F32 or SI_HIP_F16 */
+    int32_t batch;
+    int32_t query_heads;         /* a multiple of kv_heads, at most 8 per KV head */
+    int32_t kv_heads;
+    int32_t head_size;           /* 128 */
+    int32_t context;             /* 1..16384 */
+} si_hip_batch_attention_args;
+
+/* scores[r][h][j] = q[r][h] . k[j][h / group] / sqrt(128) for j <= start + r,
+ * -FLT_MAX for every other column.  Replaces: transformer.batch-gqa-scores
+ * (GpuBatchTransformerInstructions.cs:415-470). */
+int si_hip_batch_gqa_scores(si_hip_context* ctx, const si_hip_batch_attention_args* args);
+
+/* probabilities[r][h][j] = exp(s_j - max) / sum over j <= start + r, 0 for
+ * the other columns.  Replaces: transformer.batch-causal-softmax
+ * (GpuBatchTransformerInstructions.cs:472-542). */
+int si_hip_batch_causal_softmax(si_hip_context* ctx, const float* scores, const int32_t* control,
+                                float* probabilities, int batch, int heads, int64_t context);
+
+/* output[r][h][d] = sum over j <= start + r of p[r][h][j] v[j][h / group][d],
+ * in 64-column chunks added by a second launch.  Replaces:
+ * transformer.batch-gqa-values (GpuBatchTransformerInstructions.cs:544-598). */
+int si_hip_batch_gqa_values(si_hip_context* ctx, const si_hip_batch_attention_args* args);
+
+int si_hip_batch_values_workspace_bytes(int batch, int query_heads, int context, uint64_t* bytes);
+
+/* output = input[valid - 1] when 0 < valid <= batch.  Replaces:
+ * transformer.batch-select-last (GpuBatchTransformerInstructions.cs:600-625). */
+int si_hip_batch_select_last(si_hip_context* ctx, const float* input, const int32_t* control, float* output,
+                             int batch, int64_t width);
+
 /* ---- Phi-4 decode step ------------------------------------------------------------ */
 
 typedef struct si_hip_phi4_layer {

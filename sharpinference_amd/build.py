@@ -37,6 +37,8 @@ SOURCES = [
     "si_gguf.cpp",
     "si_transformer.hip",
     "si_ops.cpp",
+    "si_batch.hip",
+    "si_batch_abi.cpp",
 ]
 
 

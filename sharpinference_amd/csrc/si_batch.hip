@@ -1,0 +1,631 @@
+// The batched (prefill) transformer operators of the reference's D3D12
+// prefill program as separate launches, with the reference's semantics and
+// layouts (SharpInference.Instructions.D3D12/GpuBatchTransformerInstructions.cs).
+// control = device int32[2] {start, valid}; batch row r is the token at
+// position start + r and only rows r < valid are read or written.
+//
+//   batch-gather-rows        :646-679  out[r] = table[start + r] (rows inside the table)
+//   batch-rms-norm           :101-156  per row: x * (1 / sqrt(sum(x^2) / H + eps)) * w
+//   batch-residual-rms-norm  :158-222  updated = hidden + residual; out = rms-norm(updated)
+//   batch-shared-matvec      :224-279  y[r] = W x[r], FP32 products and sums
+//   batch-swiglu             :281-316  out[r][i] = g / (1 + exp(-g)) * u over [g | u]
+//   batch-rope-kv-write      :318-413  rotate q and k of row r at position start + r,
+//                                      q to `query`, k / v to that cache row
+//   batch-gqa-scores         :415-470  q . k / sqrt(head) for cache rows <= start + r,
+//                                      -FLT_MAX elsewhere, every context column
+//   batch-causal-softmax     :472-542  softmax over columns <= start + r, 0 elsewhere
+//   batch-gqa-values         :544-598  sum over columns <= start + r of p * v
+//   batch-select-last        :600-625  out = in[valid - 1]
+//
+// Caches are [context][kv_heads][head] (FP32 as in the reference, or fp16).
+// The attention launches are built for 128-value heads.
+#include "si_batch.hpp"
+#include "si_internal.hpp"
+
+#include <hip/hip_fp16.h>
+
+#include <cfloat>
+
+namespace si {
+namespace {
+
+constexpr int NORM_THREADS = 1024;
+constexpr int THREADS = 256;
+
+__device__ __forceinline__ float half_bits(uint32_t h)
+{
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xffffu)));
+}
+
+template <int THREADS_>
+__device__ __forceinline__ float block_sum(float v, float* red)
+{
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < THREADS_ / 64; w++)
+        t += red[w];
+    __syncthreads();
+    return t;
+}
+
+template <int THREADS_>
+__device__ __forceinline__ float block_max(float v, float* red)
+{
+    for (int off = 32; off > 0; off >>= 1)
+        v = fmaxf(v, __shfl_xor(v, off));
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int w = 1; w < THREADS_ / 64; w++)
+        t = fmaxf(t, red[w]);
+    __syncthreads();
+    return t;
+}
+
+// Sum over the 16 lanes of a DPP row (every lane of the row gets it).
+__device__ __forceinline__ float row_sum16(float v)
+{
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ void load8(const float* p, float* f)
+{
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ void load8(const __half* p, float* f)
+{
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        f[2 * k] = half_bits(w[k]);
+        f[2 * k + 1] = half_bits(w[k] >> 16);
+    }
+}
+__device__ __forceinline__ float2 load2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+__device__ __forceinline__ float2 load2(const __half* p)
+{
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+    return make_float2(half_bits(w), half_bits(w >> 16));
+}
+
+template <typename T>
+__device__ __forceinline__ void store_cache(T* cache, int64_t i, float v);
+template <>
+__device__ __forceinline__ void store_cache<float>(float* cache, int64_t i, float v) { cache[i] = v; }
+template <>
+__device__ __forceinline__ void store_cache<__half>(__half* cache, int64_t i, float v) { cache[i] = __float2half_rn(v); }
+
+// ---- row-wise operators ----------------------------------------------------------------
+
+__global__ __launch_bounds__(THREADS) void batch_gather_rows_kernel(const float* __restrict__ table,
+                                                                    int64_t table_rows, int width,
+                                                                    const int32_t* __restrict__ control,
+                                                                    float* __restrict__ out, int64_t total)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    if (e >= total)
+        return;
+    const int row = static_cast<int>(e / width);
+    const int64_t src = static_cast<int64_t>(control[0]) + row;
+    if (row < control[1] && src >= 0 && src < table_rows)
+        out[e] = table[src * width + (e - static_cast<int64_t>(row) * width)];
+}
+
+// One workgroup per live row (the decode form's operation order).
+template <bool RESIDUAL>
+__global__ __launch_bounds__(NORM_THREADS) void batch_rms_norm_kernel(const float* __restrict__ hidden,
+                                                                      const float* __restrict__ residual,
+                                                                      const float* __restrict__ weight,
+                                                                      float* __restrict__ updated,
+                                                                      float* __restrict__ out, int width, float eps,
+                                                                      const int32_t* __restrict__ control)
+{
+    __shared__ float red[NORM_THREADS / 64];
+    const int row = blockIdx.x;
+    if (row >= control[1])
+        return;   // the whole workgroup, before any barrier
+    const int64_t base = static_cast<int64_t>(row) * width;
+    float ss = 0.0f;
+    for (int j = threadIdx.x; j < width; j += NORM_THREADS) {
+        float v = hidden[base + j];
+        if (RESIDUAL) {
+            v = v + residual[base + j];
+            updated[base + j] = v;
+        }
+        ss = fmaf(v, v, ss);
+    }
+    const float total = block_sum<NORM_THREADS>(ss, red);
+    const float scale = 1.0f / sqrtf(total / static_cast<float>(width) + eps);
+    for (int j = threadIdx.x; j < width; j += NORM_THREADS) {
+        const float v = RESIDUAL ? updated[base + j] : hidden[base + j];   // written by this thread above
+        out[base + j] = v * scale * weight[j];
+    }
+}
+
+__global__ __launch_bounds__(THREADS) void batch_swiglu_kernel(const float* __restrict__ gate_up,
+                                                               float* __restrict__ out, int width, int64_t total,
+                                                               const int32_t* __restrict__ control)
+{
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    if (e >= total)
+        return;
+    const int row = static_cast<int>(e / width);
+    if (row >= control[1])
+        return;
+    const int64_t src = e + static_cast<int64_t>(row) * width;   // row * 2 * width + column
+    const float g = gate_up[src];
+    out[e] = g / (1.0f + expf(-g)) * gate_up[src + width];
+}
+
+// One thread per value of the batch's qkv rows.
+template <typename T>
+__global__ __launch_bounds__(THREADS) void batch_rope_kv_write_kernel(BatchRopeArgs a, T* __restrict__ kc,
+                                                                      T* __restrict__ vc)
+{
+    const int width = a.query_size + 2 * a.kv_size;
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    if (e >= static_cast<int64_t>(a.batch) * width)
+        return;
+    const int row = static_cast<int>(e / width);
+    const int64_t position = static_cast<int64_t>(a.control[0]) + row;
+    if (row >= a.control[1] || position < 0 || position >= a.context)
+        return;
+    const int local = static_cast<int>(e - static_cast<int64_t>(row) * width);
+    const int half = a.rotary_size / 2;
+    auto rotate = [&](int in_head, float value) {
+        const int d = in_head % a.head_size;
+        if (d >= a.rotary_size)
+            return value;
+        const int ri = d < half ? d : d - half;
+        const int64_t pair = d < half ? e + half : e - half;
+        const float angle = static_cast<float>(position) * a.frequencies[ri];
+        const float c = cosf(angle) * a.rope_scale, s = sinf(angle) * a.rope_scale;
+        const float other = a.qkv[pair];
+        return d < half ? value * c - other * s : value * c + other * s;
+    };
+    const float value = a.qkv[e];
+    if (local < a.query_size) {
+        a.query[static_cast<int64_t>(row) * a.query_size + local] = rotate(local, value);
+    } else if (local < a.query_size + a.kv_size) {
+        const int c = local - a.query_size;
+        store_cache<T>(kc, position * a.kv_size + c, rotate(c, value));
+    } else {
+        const int c = local - a.query_size - a.kv_size;
+        store_cache<T>(vc, position * a.kv_size + c, value);
+    }
+}
+
+// ---- attention ---------------------------------------------------------------------------
+
+// One workgroup per (KV head, 64 cache positions): each lane holds an
+// 8-value slice of four positions' keys (16 lanes per position), the
+// group's queries of every live row are staged in LDS, and each query's four
+// dot products are summed across the 16 lanes with DPP.  Positions past a
+// row's own position get -FLT_MAX; a chunk wholly past the batch's last
+// position writes only those.
+template <typename T>
+__global__ __launch_bounds__(THREADS) void batch_gqa_scores_kernel(BatchAttentionArgs a, const T* __restrict__ kc)
+{
+    __shared__ float4 qs[BATCH_MAX * BATCH_GROUP_MAX * (BATCH_HEAD / 4)];
+    const int g = blockIdx.x, chunk = blockIdx.y;
+    const int group = a.query_heads / a.kv_heads;
+    const int start = a.control[0], valid = min(a.control[1], a.batch);
+    const int nq = max(valid, 0) * group;   // query qi = row * group + head-in-group
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int dg = lane & 15, row = lane >> 4;
+    const int j0 = chunk * BATCH_CHUNK;
+    for (int i = t; i < nq * (BATCH_HEAD / 4); i += THREADS) {
+        const int qi = i / (BATCH_HEAD / 4), c4 = i % (BATCH_HEAD / 4);
+        const int r = qi / group, h = g * group + qi % group;
+        qs[i] = reinterpret_cast<const float4*>(a.query +
+                                                (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD)[c4];
+    }
+    const int64_t last = static_cast<int64_t>(start) + valid - 1;   // the batch's last position
+    const bool any = nq > 0 && last >= 0 && j0 <= last;
+    float k[4][8];
+    if (any) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = min(j0 + wave * 16 + row + 4 * i, a.context - 1);
+            load8(kc + (static_cast<int64_t>(j) * a.kv_heads + g) * BATCH_HEAD + 8 * dg, k[i]);
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(static_cast<float>(BATCH_HEAD));
+    const int j = j0 + wave * 16 + row + 4 * dg;   // the position lane dg < 4 of this row stores
+    for (int qi = 0; qi < nq; qi++) {
+        const int r = qi / group, h = g * group + qi % group;
+        const int64_t active = static_cast<int64_t>(start) + r;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (any) {
+            const float4 q0 = qs[qi * (BATCH_HEAD / 4) + 2 * dg], q1 = qs[qi * (BATCH_HEAD / 4) + 2 * dg + 1];
+            const float q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 8; c++)
+                    d = fmaf(q[c], k[i][c], d);
+                s[i] = row_sum16(d);
+            }
+        }
+        if (dg < 4 && j < a.context) {
+            const float sv = dg == 0 ? s[0] : dg == 1 ? s[1] : dg == 2 ? s[2] : s[3];
+            const float v = active >= 0 && j <= active ? sv * scale : -FLT_MAX;
+            a.out[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j] = v;
+        }
+    }
+}
+
+// One workgroup per (live row, query head).
+__global__ __launch_bounds__(THREADS) void batch_causal_softmax_kernel(const float* __restrict__ scores,
+                                                                       float* __restrict__ probs, int heads,
+                                                                       int context,
+                                                                       const int32_t* __restrict__ control)
+{
+    __shared__ float red[THREADS / 64];
+    const int r = blockIdx.x / heads, h = blockIdx.x % heads;
+    if (r >= control[1])
+        return;   // the whole workgroup
+    const int64_t active = static_cast<int64_t>(control[0]) + r;
+    const int last = active < 0 ? -1 : static_cast<int>(min(active, static_cast<int64_t>(context) - 1));
+    const int64_t base = (static_cast<int64_t>(r) * heads + h) * context;
+    float m = -FLT_MAX;
+    for (int j = threadIdx.x; j <= last; j += THREADS)
+        m = fmaxf(m, scores[base + j]);
+    m = block_max<THREADS>(m, red);
+    float sum = 0.0f;
+    for (int j = threadIdx.x; j <= last; j += THREADS)
+        sum += expf(scores[base + j] - m);
+    sum = block_sum<THREADS>(sum, red);
+    for (int j = threadIdx.x; j < context; j += THREADS)
+        probs[base + j] = j <= last ? expf(scores[base + j] - m) / sum : 0.0f;
+}
+
+// Values, first pass: one workgroup per (KV head, 64 cache positions); lane
+// l holds channels 2l, 2l + 1 and wave w the queries w, w + 4, ... (eight at
+// a time); the chunk's probabilities of every live query are staged in LDS.
+// Partial sums over the chunk's positions up to the batch's last position
+// go to the workspace [chunk][row][head][128]; the second pass adds the
+// chunks up to each row's own position in order.
+constexpr int VQ = 8;   // queries per wave per pass
+
+template <typename T>
+__global__ __launch_bounds__(THREADS) void batch_gqa_values_partial_kernel(BatchAttentionArgs a,
+                                                                           const T* __restrict__ vc)
+{
+    __shared__ float ps[BATCH_MAX * BATCH_GROUP_MAX][BATCH_CHUNK];
+    const int g = blockIdx.x, chunk = blockIdx.y;
+    const int group = a.query_heads / a.kv_heads;
+    const int start = a.control[0], valid = min(a.control[1], a.batch);
+    const int nq = max(valid, 0) * group;
+    const int64_t last = static_cast<int64_t>(start) + valid - 1;
+    const int j0 = chunk * BATCH_CHUNK;
+    if (nq == 0 || last < 0 || j0 > last)
+        return;   // the whole workgroup: no live position in this chunk
+    const int jn = static_cast<int>(min(static_cast<int64_t>(BATCH_CHUNK), min(last, static_cast<int64_t>(a.context) - 1) - j0 + 1));
+    for (int i = threadIdx.x; i < nq * BATCH_CHUNK; i += THREADS) {
+        const int qi = i / BATCH_CHUNK, jj = i % BATCH_CHUNK;
+        const int r = qi / group, h = g * group + qi % group;
+        ps[qi][jj] = jj < jn ? a.probabilities[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j0 + jj]
+                             : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const T* vbase = vc + static_cast<int64_t>(g) * BATCH_HEAD + 2 * lane;
+    const int64_t vstride = static_cast<int64_t>(a.kv_heads) * BATCH_HEAD;
+    for (int q0 = wave; q0 < nq; q0 += 4 * VQ) {
+        float2 acc[VQ];
+#pragma unroll
+        for (int m = 0; m < VQ; m++)
+            acc[m] = make_float2(0.0f, 0.0f);
+        for (int jj = 0; jj < jn; jj++) {
+            const float2 v = load2(vbase + static_cast<int64_t>(j0 + jj) * vstride);
+#pragma unroll
+            for (int m = 0; m < VQ; m++) {
+                const int qi = q0 + 4 * m;
+                if (qi < nq) {
+                    const float p = ps[qi][jj];
+                    acc[m].x = fmaf(p, v.x, acc[m].x);
+                    acc[m].y = fmaf(p, v.y, acc[m].y);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < VQ; m++) {
+            const int qi = q0 + 4 * m;
+            if (qi < nq) {
+                const int r = qi / group, h = g * group + qi % group;
+                float* dst = a.workspace +
+                             ((static_cast<int64_t>(chunk) * a.batch + r) * a.query_heads + h) * BATCH_HEAD + 2 * lane;
+                *reinterpret_cast<float2*>(dst) = acc[m];
+            }
+        }
+    }
+}
+
+// Values, second pass: one workgroup per (live row, query head).
+__global__ __launch_bounds__(BATCH_HEAD) void batch_gqa_values_reduce_kernel(BatchAttentionArgs a)
+{
+    const int r = blockIdx.x / a.query_heads, h = blockIdx.x % a.query_heads;
+    if (r >= min(a.control[1], a.batch))
+        return;
+    const int64_t active = static_cast<int64_t>(a.control[0]) + r;
+    float sum = 0.0f;
+    if (active >= 0) {
+        const int n = static_cast<int>(min(active, static_cast<int64_t>(a.context) - 1) / BATCH_CHUNK) + 1;
+        const float* src = a.workspace + (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + threadIdx.x;
+        const int64_t cstride = static_cast<int64_t>(a.batch) * a.query_heads * BATCH_HEAD;
+        for (int c = 0; c < n; c++)
+            sum += src[c * cstride];
+    }
+    a.out[(static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + threadIdx.x] = sum;
+}
+
+__global__ __launch_bounds__(THREADS) void batch_select_last_kernel(const float* __restrict__ input,
+                                                                    float* __restrict__ out, int batch, int width,
+                                                                    const int32_t* __restrict__ control)
+{
+    const int c = static_cast<int>(blockIdx.x) * THREADS + threadIdx.x;
+    const int valid = control[1];
+    if (c < width && valid > 0 && valid <= batch)
+        out[c] = input[static_cast<int64_t>(valid - 1) * width + c];
+}
+
+// ---- batched matrix-vector product on the FP32 matrix cores ------------------------------
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+// Elements 8g .. 8g + 7 of 32-column block `blk` of a row, dequantised as
+// the CpuVm decode does (one rounding per operation).
+template <int FMT>
+__device__ __forceinline__ void decode8(const uint8_t* row, int blk, int g, float* w);
+
+template <>
+__device__ __forceinline__ void decode8<FMT_F32>(const uint8_t* row, int blk, int g, float* w)
+{
+    load8(reinterpret_cast<const float*>(row) + 32 * blk + 8 * g, w);
+}
+
+template <>
+__device__ __forceinline__ void decode8<FMT_F16>(const uint8_t* row, int blk, int g, float* w)
+{
+    load8(reinterpret_cast<const __half*>(row) + 32 * blk + 8 * g, w);
+}
+
+template <>
+__device__ __forceinline__ void decode8<FMT_Q8_0>(const uint8_t* row, int blk, int g, float* w)
+{
+    const uint8_t* b = row + 34 * static_cast<int64_t>(blk);
+    const float d = half_bits(ld_u16(b));
+    const uint8_t* q = b + 2 + 8 * g;   // 2-byte aligned
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t two = ld_u16(q + 2 * i);
+        w[2 * i] = d * static_cast<float>(static_cast<int8_t>(two & 0xffu));
+        w[2 * i + 1] = d * static_cast<float>(static_cast<int8_t>(two >> 8));
+    }
+}
+
+template <>
+__device__ __forceinline__ void decode8<FMT_Q4_0>(const uint8_t* row, int blk, int g, float* w)
+{
+    const uint8_t* b = row + 18 * static_cast<int64_t>(blk);
+    const float d = half_bits(ld_u16(b));
+    const uint8_t* q = b + 2 + 8 * (g & 1);   // elements 0..15: low nibbles, 16..31: high nibbles
+    const int sh = g < 2 ? 0 : 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t two = ld_u16(q + 2 * i);
+        w[2 * i] = d * static_cast<float>(static_cast<int>((two >> sh) & 15u) - 8);
+        w[2 * i + 1] = d * static_cast<float>(static_cast<int>((two >> (8 + sh)) & 15u) - 8);
+    }
+}
+
+template <>
+__device__ __forceinline__ void decode8<FMT_Q4_K>(const uint8_t* row, int blk, int g, float* w)
+{
+    const uint8_t* sb = row + 144 * static_cast<int64_t>(blk >> 3);
+    const int j = blk & 7;   // sub-block: chunk j / 2, low nibbles for even j
+    const uint4 h = *reinterpret_cast<const uint4*>(sb);
+    const uint32_t sw[3] = {h.y, h.z, h.w};
+    auto sbyte = [&](int i) { return static_cast<int>((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+    int sc, m;
+    if (j < 4) {
+        sc = sbyte(j) & 63;
+        m = sbyte(j + 4) & 63;
+    } else {
+        sc = (sbyte(j + 4) & 15) | ((sbyte(j - 4) >> 6) << 4);
+        m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+    }
+    const float d1 = __fmul_rn(half_bits(h.x), static_cast<float>(sc));
+    const float m1 = __fmul_rn(half_bits(h.x >> 16), static_cast<float>(m));
+    const uint2 q = *reinterpret_cast<const uint2*>(sb + 16 + 32 * (j >> 1) + 8 * g);
+    const int sh = (j & 1) * 4;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t word = i < 4 ? q.x : q.y;
+        const float n = static_cast<float>((word >> (8 * (i & 3) + sh)) & 15u);
+        w[i] = __fsub_rn(__fmul_rn(d1, n), m1);
+    }
+}
+
+// One workgroup = 16 output rows x 16 batch rows, its four waves splitting
+// the 32-column blocks (wave w takes blocks w, w + 4, ...) and adding their
+// 16 x 16 tiles through LDS in a fixed order.  Per block, lane (r, g) = (l %
+// 16, l / 16) dequantises elements 8g..8g+7 of row o0 + r and loads the same
+// columns of batch row t0 + r; eight v_mfma_f32_16x16x4_f32 take k = 8g + s
+// (s < 8) from lane group g: the sum over k is the row's dot product in any
+// order.  D[i][j] of the tile (batch row t0 + i, output row o0 + j) is held
+// by lane j + 16 (i / 4), element i % 4.
+template <int FMT>
+__global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __restrict__ W,
+                                                               const float* __restrict__ X, float* __restrict__ Y,
+                                                               int batch, int rows, int cols, int64_t row_bytes,
+                                                               const int32_t* __restrict__ control)
+{
+    __shared__ floatx4 red[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int o0 = static_cast<int>(blockIdx.x) * 16, t0 = static_cast<int>(blockIdx.y) * 16;
+    const int live = min(control[1], batch) - t0;   // live batch rows of this tile
+    if (live <= 0)
+        return;   // the whole workgroup, before the barrier
+    const uint8_t* wrow = W + static_cast<int64_t>(min(o0 + r, rows - 1)) * row_bytes;
+    const bool tok = r < live;
+    const float* xrow = X + static_cast<int64_t>(t0 + (tok ? r : 0)) * cols + 8 * g;
+    const int nb = cols / 32;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = wave; b < nb; b += 4) {
+        float w[8], x[8];
+        decode8<FMT>(wrow, b, g, w);
+        load8(xrow + 32 * b, x);
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(tok ? x[s] : 0.0f, w[s], acc, 0, 0, 0);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        const floatx4 v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+        const int o = o0 + r;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int i = 4 * g + m;
+            if (i < live && o < rows)
+                Y[static_cast<int64_t>(t0 + i) * rows + o] = v[m];
+        }
+    }
+}
+
+}  // namespace
+
+int64_t batch_values_workspace_floats(int batch, int query_heads, int context)
+{
+    return static_cast<int64_t>((context + BATCH_CHUNK - 1) / BATCH_CHUNK) * batch * query_heads * BATCH_HEAD;
+}
+
+hipError_t launch_batch_gather_rows(const float* table, int64_t table_rows, int width, const int32_t* control,
+                                    float* out, int batch, hipStream_t s)
+{
+    const int64_t total = static_cast<int64_t>(batch) * width;
+    hipLaunchKernelGGL(batch_gather_rows_kernel, dim3(static_cast<unsigned>((total + THREADS - 1) / THREADS)),
+                       dim3(THREADS), 0, s, table, table_rows, width, control, out, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_rms_norm(const float* hidden, const float* residual, const float* weight, float* updated,
+                                 float* out, int batch, int width, float eps, const int32_t* control, hipStream_t s)
+{
+    if (residual)
+        hipLaunchKernelGGL((batch_rms_norm_kernel<true>), dim3(static_cast<unsigned>(batch)), dim3(NORM_THREADS), 0, s,
+                           hidden, residual, weight, updated, out, width, eps, control);
+    else
+        hipLaunchKernelGGL((batch_rms_norm_kernel<false>), dim3(static_cast<unsigned>(batch)), dim3(NORM_THREADS), 0,
+                           s, hidden, nullptr, weight, nullptr, out, width, eps, control);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_swiglu(const float* gate_up, float* out, int batch, int width, const int32_t* control,
+                               hipStream_t s)
+{
+    const int64_t total = static_cast<int64_t>(batch) * width;
+    hipLaunchKernelGGL(batch_swiglu_kernel, dim3(static_cast<unsigned>((total + THREADS - 1) / THREADS)), dim3(THREADS),
+                       0, s, gate_up, out, width, total, control);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_rope_kv_write(const BatchRopeArgs& a, hipStream_t s)
+{
+    const int64_t total = static_cast<int64_t>(a.batch) * (a.query_size + 2 * a.kv_size);
+    const dim3 grid(static_cast<unsigned>((total + THREADS - 1) / THREADS));
+    if (a.cache_fp16)
+        hipLaunchKernelGGL((batch_rope_kv_write_kernel<__half>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<__half*>(a.key_cache), static_cast<__half*>(a.value_cache));
+    else
+        hipLaunchKernelGGL((batch_rope_kv_write_kernel<float>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<float*>(a.key_cache), static_cast<float*>(a.value_cache));
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_gqa_scores(const BatchAttentionArgs& a, hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>(a.kv_heads),
+                    static_cast<unsigned>((a.context + BATCH_CHUNK - 1) / BATCH_CHUNK));
+    if (a.cache_fp16)
+        hipLaunchKernelGGL((batch_gqa_scores_kernel<__half>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<const __half*>(a.cache));
+    else
+        hipLaunchKernelGGL((batch_gqa_scores_kernel<float>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<const float*>(a.cache));
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_causal_softmax(const float* scores, float* probabilities, int batch, int heads, int context,
+                                       const int32_t* control, hipStream_t s)
+{
+    hipLaunchKernelGGL(batch_causal_softmax_kernel, dim3(static_cast<unsigned>(batch * heads)), dim3(THREADS), 0, s,
+                       scores, probabilities, heads, context, control);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_gqa_values(const BatchAttentionArgs& a, hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>(a.kv_heads),
+                    static_cast<unsigned>((a.context + BATCH_CHUNK - 1) / BATCH_CHUNK));
+    if (a.cache_fp16)
+        hipLaunchKernelGGL((batch_gqa_values_partial_kernel<__half>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<const __half*>(a.cache));
+    else
+        hipLaunchKernelGGL((batch_gqa_values_partial_kernel<float>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<const float*>(a.cache));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(batch_gqa_values_reduce_kernel, dim3(static_cast<unsigned>(a.batch * a.query_heads)),
+                       dim3(BATCH_HEAD), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_select_last(const float* input, float* out, int batch, int width, const int32_t* control,
+                                    hipStream_t s)
+{
+    hipLaunchKernelGGL(batch_select_last_kernel, dim3(static_cast<unsigned>((width + THREADS - 1) / THREADS)),
+                       dim3(THREADS), 0, s, input, out, batch, width, control);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_matvec(int fmt, const void* w, const float* x, float* y, int batch, int64_t rows,
+                               int64_t cols, const int32_t* control, hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>((rows + 15) / 16), static_cast<unsigned>((batch + 15) / 16));
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const int64_t rb = row_bytes(fmt, cols);
+    const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    switch (fmt) {
+    case FMT_Q8_0: hipLaunchKernelGGL((batch_matvec_kernel<FMT_Q8_0>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
+    case FMT_Q4_0: hipLaunchKernelGGL((batch_matvec_kernel<FMT_Q4_0>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
+    case FMT_Q4_K: hipLaunchKernelGGL((batch_matvec_kernel<FMT_Q4_K>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
+    case FMT_F16: hipLaunchKernelGGL((batch_matvec_kernel<FMT_F16>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
+    case FMT_F32: hipLaunchKernelGGL((batch_matvec_kernel<FMT_F32>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace si

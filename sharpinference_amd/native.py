@@ -102,6 +102,21 @@ class GqaArgs(ctypes.Structure):
                 ("context", _i32), ("workspace", _vp)]
 
 
+class BatchRopeArgs(ctypes.Structure):
+    """si_hip_batch_rope_args."""
+    _fields_ = [("qkv", _vp), ("control", _vp), ("frequencies", _vp), ("query", _vp), ("key_cache", _vp),
+                ("value_cache", _vp), ("cache_format", _i32), ("batch", _i32), ("query_size", _i32),
+                ("kv_size", _i32), ("head_size", _i32), ("rotary_size", _i32), ("context", _i32),
+                ("rope_scale", ctypes.c_float)]
+
+
+class BatchAttentionArgs(ctypes.Structure):
+    """si_hip_batch_attention_args."""
+    _fields_ = [("query", _vp), ("probabilities", _vp), ("cache", _vp), ("control", _vp), ("output", _vp),
+                ("workspace", _vp), ("cache_format", _i32), ("batch", _i32), ("query_heads", _i32),
+                ("kv_heads", _i32), ("head_size", _i32), ("context", _i32)]
+
+
 class Phi4Layer(ctypes.Structure):
     """si_hip_phi4_layer."""
     _fields_ = [("attn_norm", _vp), ("qkv", _vp), ("o", _vp), ("ffn_norm", _vp), ("up", _vp), ("down", _vp),
@@ -194,6 +209,17 @@ SIGNATURES.update({
     "si_hip_grouped_query_attention": ([_vp, ctypes.POINTER(GqaArgs)], _i32),
     "si_hip_gqa_workspace_bytes": ([_i32, _i32, _i32, ctypes.POINTER(_u64)], _i32),
     "si_hip_argmax": ([_vp, _vp, _i64, _vp, _vp], _i32),
+    "si_hip_batch_gather_rows": ([_vp, _vp, _i64, _i64, _vp, _vp, _i32], _i32),
+    "si_hip_batch_rms_norm": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, ctypes.c_float], _i32),
+    "si_hip_batch_residual_rms_norm": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, ctypes.c_float], _i32),
+    "si_hip_batch_matvec": ([_vp, _i32, _vp, _vp, _vp, _vp, _i32, _i64, _i64], _i32),
+    "si_hip_batch_swiglu": ([_vp, _vp, _vp, _vp, _i32, _i64], _i32),
+    "si_hip_batch_rope_kv_write": ([_vp, ctypes.POINTER(BatchRopeArgs)], _i32),
+    "si_hip_batch_gqa_scores": ([_vp, ctypes.POINTER(BatchAttentionArgs)], _i32),
+    "si_hip_batch_causal_softmax": ([_vp, _vp, _vp, _vp, _i32, _i32, _i64], _i32),
+    "si_hip_batch_gqa_values": ([_vp, ctypes.POINTER(BatchAttentionArgs)], _i32),
+    "si_hip_batch_values_workspace_bytes": ([_i32, _i32, _i32, ctypes.POINTER(_u64)], _i32),
+    "si_hip_batch_select_last": ([_vp, _vp, _vp, _vp, _i32, _i64], _i32),
     "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
     "si_hip_phi4_decode": ([_vp, ctypes.POINTER(Phi4Model)], _i32),
     "si_hip_batched_matvec": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
@@ -229,6 +255,11 @@ def lib() -> ctypes.CDLL:
             fn.restype = res
         _lib = handle
     return _lib
+
+
+def _p(address: int) -> ctypes.c_void_p:
+    """A device address as a pointer argument."""
+    return ctypes.c_void_p(int(address))
 
 
 def _check(rc: int, ctx=None) -> None:
@@ -420,6 +451,39 @@ class HipContext:
         self._call(lib().si_hip_argmax, ctypes.c_void_p(int(values)), n, ctypes.c_void_p(int(workspace)),
                    ctypes.c_void_p(int(index)))
 
+    # batched (prefill) operators; `control` is a device int32[2] {start, valid}
+    def batch_gather_rows(self, table: int, table_rows: int, width: int, control: int, out: int, batch: int) -> None:
+        self._call(lib().si_hip_batch_gather_rows, _p(table), table_rows, width, _p(control), _p(out), batch)
+
+    def batch_rms_norm(self, x: int, w: int, control: int, out: int, batch: int, width: int, eps: float) -> None:
+        self._call(lib().si_hip_batch_rms_norm, _p(x), _p(w), _p(control), _p(out), batch, width, ctypes.c_float(eps))
+
+    def batch_residual_rms_norm(self, hidden: int, residual: int, w: int, control: int, updated: int, out: int,
+                                batch: int, width: int, eps: float) -> None:
+        self._call(lib().si_hip_batch_residual_rms_norm, _p(hidden), _p(residual), _p(w), _p(control), _p(updated),
+                   _p(out), batch, width, ctypes.c_float(eps))
+
+    def batch_matvec(self, fmt: int, w: int, x: int, control: int, y: int, batch: int, rows: int, cols: int) -> None:
+        self._call(lib().si_hip_batch_matvec, fmt, _p(w), _p(x), _p(control), _p(y), batch, rows, cols)
+
+    def batch_swiglu(self, gate_up: int, control: int, out: int, batch: int, width: int) -> None:
+        self._call(lib().si_hip_batch_swiglu, _p(gate_up), _p(control), _p(out), batch, width)
+
+    def batch_rope_kv_write(self, args: "BatchRopeArgs") -> None:
+        self._call(lib().si_hip_batch_rope_kv_write, ctypes.byref(args))
+
+    def batch_gqa_scores(self, args: "BatchAttentionArgs") -> None:
+        self._call(lib().si_hip_batch_gqa_scores, ctypes.byref(args))
+
+    def batch_causal_softmax(self, scores: int, control: int, probs: int, batch: int, heads: int, context: int) -> None:
+        self._call(lib().si_hip_batch_causal_softmax, _p(scores), _p(control), _p(probs), batch, heads, context)
+
+    def batch_gqa_values(self, args: "BatchAttentionArgs") -> None:
+        self._call(lib().si_hip_batch_gqa_values, ctypes.byref(args))
+
+    def batch_select_last(self, x: int, control: int, out: int, batch: int, width: int) -> None:
+        self._call(lib().si_hip_batch_select_last, _p(x), _p(control), _p(out), batch, width)
+
     def phi4_decode(self, model: Phi4Model) -> None:
         self._call(lib().si_hip_phi4_decode, ctypes.byref(model))
 
@@ -484,6 +548,12 @@ def attention_workspace_bytes(heads: int, capacity: int) -> int:
 def gqa_workspace_bytes(query_heads: int, head_size: int, context: int) -> int:
     n = ctypes.c_uint64(0)
     _check(lib().si_hip_gqa_workspace_bytes(query_heads, head_size, context, ctypes.byref(n)))
+    return n.value
+
+
+def batch_values_workspace_bytes(batch: int, query_heads: int, context: int) -> int:
+    n = ctypes.c_uint64(0)
+    _check(lib().si_hip_batch_values_workspace_bytes(batch, query_heads, context, ctypes.byref(n)))
     return n.value
 
 
