@@ -388,6 +388,36 @@ InstructionRecording QuantizedGatherRowInstruction::Generate(const std::vector<I
     return {"si_hip_gather_row", parameters};
 }
 
+std::vector<InstructionSignature> QuantizedBatchMatVecInstruction::Signatures() const
+{
+    return {{{{"weight", GraphElementType::Byte, GraphResourceAccess::Read},
+              {"input", GraphElementType::Float32, GraphResourceAccess::Read},
+              {"control", GraphElementType::Int32, GraphResourceAccess::Read},
+              {"output", GraphElementType::Float32, GraphResourceAccess::Write}},
+             {"format", "columns"},
+             FP32}};
+}
+
+void QuantizedBatchMatVecInstruction::Validate(const std::vector<InstructionParameter>& parameters) const
+{
+    const QuantShape q = ReadQuantShape(*this, parameters);
+    const auto& w = Find(parameters, "weight")->tensor.dimensions;
+    const auto& x = Find(parameters, "input")->tensor.dimensions;
+    const auto& y = Find(parameters, "output")->tensor.dimensions;
+    if (w.size() != 2 || w[1] != static_cast<int64_t>(q.row_bytes) || w[0] < 1)
+        Fail("the weight must be [rows, " + std::to_string(q.row_bytes) + "] bytes for " + std::to_string(q.columns) +
+             " columns.");
+    if (x.size() != 2 || y.size() != 2 || x[1] != q.columns || y[0] != x[0] || y[1] != w[0] || x[0] < 1)
+        Fail("Expected weight [O,I], input [B,I], and output [B,O].");
+    if (Find(parameters, "control")->tensor.ElementCount() != 2)
+        Fail("'control' must have shape [2].");
+}
+
+InstructionRecording QuantizedBatchMatVecInstruction::Generate(const std::vector<InstructionParameter>& parameters) const
+{
+    return {"si_hip_batch_matvec", parameters};
+}
+
 std::vector<InstructionCollectionDescription> HipQuantizedInstructions::QueryInstructionCollection() const
 {
     return {{HipInstructionCollectionIds::QuantizedFloat32, "HIP quantized products", 0, InstructionTarget::Hip()}};
@@ -402,6 +432,8 @@ std::vector<std::shared_ptr<const Instruction>> HipQuantizedInstructions::QueryI
         return {std::make_shared<QuantizedMatVecInstruction>()};
     if (name == "quant.gather-row")
         return {std::make_shared<QuantizedGatherRowInstruction>()};
+    if (name == "quant.batch-mat-vec")
+        return {std::make_shared<QuantizedBatchMatVecInstruction>()};
     return {};
 }
 
@@ -497,6 +529,12 @@ HipVmExecutor::HipVmExecutor(HipVmProgram program, int device) : program_(std::m
                     uint64_t b = 0;
                     Check(si_hip_gqa_workspace_bytes(heads, static_cast<int>(k[2]), static_cast<int>(k[0]), &b));
                     scratch = std::max(scratch, b);
+                } else if (d.recording.operation == "si_hip_batch_gqa_values") {
+                    const auto& pr = Find(d.recording.parameters, "probabilities")->tensor.dimensions;
+                    uint64_t b = 0;
+                    Check(si_hip_batch_values_workspace_bytes(static_cast<int>(pr[0]), static_cast<int>(pr[1]),
+                                                              static_cast<int>(pr[2]), &b));
+                    scratch = std::max(scratch, b);
                 }
         Check(si_hip_alloc(context_, scratch, &scratch_), context_);
         Check(si_hip_sync(context_), context_);
@@ -558,6 +596,9 @@ void HipVmExecutor::Launch(const InstructionRecording& r)
     };
     const auto Fw = [&](const InstructionRecording& rec, const char* n) {
         return static_cast<float*>(Address(*Find(rec.parameters, n)));
+    };
+    const auto I = [&](const InstructionRecording& rec, const char* n) {
+        return static_cast<const int32_t*>(Address(*Find(rec.parameters, n)));
     };
     if (r.operation == "si_hip_gemv") {
         const auto* w = Find(r.parameters, "weight");
@@ -647,6 +688,83 @@ void HipVmExecutor::Launch(const InstructionRecording& r)
         Check(si_hip_argmax(context_, F(r, "input"),
                             static_cast<int64_t>(Find(r.parameters, "input")->tensor.ElementCount()), scratch_,
                             static_cast<int32_t*>(Address(*Find(r.parameters, "output")))),
+              context_);
+    } else if (r.operation == "si_hip_batch_gather_rows") {
+        const auto& t = Find(r.parameters, "table")->tensor.dimensions;
+        Check(si_hip_batch_gather_rows(context_, F(r, "table"), t[0], t[1], I(r, "control"), Fw(r, "output"),
+                                       static_cast<int>(Find(r.parameters, "output")->tensor.dimensions[0])),
+              context_);
+    } else if (r.operation == "si_hip_batch_rms_norm") {
+        const auto& d = Find(r.parameters, "input")->tensor.dimensions;
+        Check(si_hip_batch_rms_norm(context_, F(r, "input"), F(r, "weight"), I(r, "control"), Fw(r, "output"),
+                                    static_cast<int>(d[0]), d[1], std::stof(attr("epsilon"))),
+              context_);
+    } else if (r.operation == "si_hip_batch_residual_rms_norm") {
+        const auto& d = Find(r.parameters, "hidden")->tensor.dimensions;
+        Check(si_hip_batch_residual_rms_norm(context_, F(r, "hidden"), F(r, "residual"), F(r, "weight"),
+                                             I(r, "control"), Fw(r, "updated"), Fw(r, "output"),
+                                             static_cast<int>(d[0]), d[1], std::stof(attr("epsilon"))),
+              context_);
+    } else if (r.operation == "si_hip_batch_matvec" || r.operation == "si_hip_batch_matvec.dense") {
+        const auto* w = Find(r.parameters, "weight");
+        const auto& x = Find(r.parameters, "input")->tensor.dimensions;
+        const int fmt = r.operation == "si_hip_batch_matvec"
+                            ? FormatId(attr("format"))
+                            : (w->tensor.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32);
+        Check(si_hip_batch_matvec(context_, fmt, Address(*w), F(r, "input"), I(r, "control"), Fw(r, "output"),
+                                  static_cast<int>(x[0]), w->tensor.dimensions[0], x[1]),
+              context_);
+    } else if (r.operation == "si_hip_batch_swiglu") {
+        const auto& d = Find(r.parameters, "output")->tensor.dimensions;
+        Check(si_hip_batch_swiglu(context_, F(r, "gate_up"), I(r, "control"), Fw(r, "output"), static_cast<int>(d[0]),
+                                  d[1]),
+              context_);
+    } else if (r.operation == "si_hip_batch_rope_kv_write") {
+        const auto& k = Find(r.parameters, "key_cache")->tensor;
+        const auto& q = Find(r.parameters, "query")->tensor.dimensions;
+        si_hip_batch_rope_args a{};
+        a.qkv = F(r, "qkv");
+        a.control = I(r, "control");
+        a.frequencies = F(r, "frequencies");
+        a.query = Fw(r, "query");
+        a.key_cache = Address(*Find(r.parameters, "key_cache"));
+        a.value_cache = Address(*Find(r.parameters, "value_cache"));
+        a.cache_format = k.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+        a.batch = static_cast<int32_t>(q[0]);
+        a.query_size = static_cast<int32_t>(q[1]);
+        a.kv_size = static_cast<int32_t>(k.dimensions[1] * k.dimensions[2]);
+        a.head_size = std::stoi(attr("head_size"));
+        a.rotary_size = std::stoi(attr("rotary_size"));
+        a.context = static_cast<int32_t>(k.dimensions[0]);
+        a.rope_scale = std::stof(attr("rope_scale"));
+        Check(si_hip_batch_rope_kv_write(context_, &a), context_);
+    } else if (r.operation == "si_hip_batch_gqa_scores" || r.operation == "si_hip_batch_gqa_values") {
+        const bool values = r.operation == "si_hip_batch_gqa_values";
+        const auto& c = Find(r.parameters, values ? "value_cache" : "key_cache")->tensor;
+        const auto& sd = Find(r.parameters, values ? "probabilities" : "scores")->tensor.dimensions;
+        si_hip_batch_attention_args a{};
+        a.query = values ? nullptr : F(r, "query");
+        a.probabilities = values ? F(r, "probabilities") : nullptr;
+        a.cache = Address(*Find(r.parameters, values ? "value_cache" : "key_cache"));
+        a.control = I(r, "control");
+        a.output = Fw(r, values ? "output" : "scores");
+        a.workspace = values ? static_cast<float*>(scratch_) : nullptr;
+        a.cache_format = c.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+        a.batch = static_cast<int32_t>(sd[0]);
+        a.query_heads = static_cast<int32_t>(sd[1]);
+        a.kv_heads = static_cast<int32_t>(c.dimensions[1]);
+        a.head_size = static_cast<int32_t>(c.dimensions[2]);
+        a.context = static_cast<int32_t>(c.dimensions[0]);
+        Check(values ? si_hip_batch_gqa_values(context_, &a) : si_hip_batch_gqa_scores(context_, &a), context_);
+    } else if (r.operation == "si_hip_batch_causal_softmax") {
+        const auto& d = Find(r.parameters, "scores")->tensor.dimensions;
+        Check(si_hip_batch_causal_softmax(context_, F(r, "scores"), I(r, "control"), Fw(r, "probabilities"),
+                                          static_cast<int>(d[0]), static_cast<int>(d[1]), d[2]),
+              context_);
+    } else if (r.operation == "si_hip_batch_select_last") {
+        const auto& d = Find(r.parameters, "input")->tensor.dimensions;
+        Check(si_hip_batch_select_last(context_, F(r, "input"), I(r, "control"), Fw(r, "output"),
+                                       static_cast<int>(d[0]), d[1]),
               context_);
     } else {
         throw NotSupportedException("No HIP launch for recording '" + r.operation + "'.");

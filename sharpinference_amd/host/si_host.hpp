@@ -250,6 +250,23 @@ protected:
     InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
 };
 
+// quant.batch-mat-vec: output[b] = weight . input[b] for the live rows of
+// control {start, valid} (transformer.batch-shared-matvec,
+// GpuBatchTransformerInstructions.cs:224-279, over GGUF block rows): weight
+// Byte [rows, row_bytes], input Float32 [batch, columns], control Int32 [2],
+// output Float32 [batch, rows]; attributes format and columns.
+class QuantizedBatchMatVecInstruction : public Instruction {
+public:
+    std::string CollectionId() const override { return HipInstructionCollectionIds::QuantizedFloat32; }
+    std::string Name() const override { return "quant.batch-mat-vec"; }
+    InstructionTarget Target() const override { return InstructionTarget::Hip(); }
+    std::vector<InstructionSignature> Signatures() const override;
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& parameters) const override;
+    InstructionRecording Generate(const std::vector<InstructionParameter>& parameters) const override;
+};
+
 class HipQuantizedInstructions : public IInstructionCollectionProvider {
 public:
     std::vector<InstructionCollectionDescription> QueryInstructionCollection() const override;
@@ -438,6 +455,7 @@ struct Phi4ProgramShape {
     bool tied = false;        // project onto token_embedding (the reference model) instead of output_weight
     GraphElementType cache_type = GraphElementType::Float16;
     float rms_eps = 1e-5f, rope_base = 10000.0f, rope_scale = 1.0f;
+    int prompt_rows = 0;      // > 0: the prefill entry over fused_embeddings [prompt_rows, hidden]
 };
 
 // The decode program of Phi4D3D12TextSession.Build (Phi4D3D12TextSession.cs:
@@ -452,6 +470,20 @@ struct Phi4ProgramShape {
 // swiglu, down mat-vec, residual-rms-norm (onto the next layer's attention
 // norm, the output norm after the last), then the vocabulary mat-vec and
 // argmax: 2 + 9 * layers + 2 dispatches.
+//
+// With prompt_rows > 0 the program also holds the reference's prefill entry
+// "prefill_fused_16" (Phi4D3D12TextSession.cs:428-504, 952-1168): slot
+// fused_embeddings [prompt_rows, hidden] (FP32 prompt embeddings), control
+// read as [start, valid], batch slots of 16 rows (batch_hidden,
+// batch_normalized, batch_qkv, batch_query, batch_scores and
+// batch_probabilities [16, heads, context], batch_attention,
+// batch_projected, batch_hidden_after_attention, batch_gate_up,
+// batch_activated, batch_down, batch_last [hidden]); dispatches = batch
+// gather, batch rms-norm, per layer the batched qkv product, batch
+// rope-kv-write, gqa-scores, causal-softmax, gqa-values, output product,
+// residual-rms-norm, up product, swiglu, down product, residual-rms-norm,
+// then batch select-last, the vocabulary mat-vec and argmax: 2 + 11 *
+// layers + 3 dispatches.  It writes the same caches as "decode".
 HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& shape);
 // rope_frequencies contents: 1 / base^(2i / rotary) for i < rotary / 2
 // (Phi4D3D12TextSession.cs:395-397).

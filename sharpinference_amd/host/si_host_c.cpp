@@ -77,6 +77,7 @@ int sih_phi4_program_create(const sih_phi4_shape* s, int device, sih_program** o
         shape.rms_eps = s->rms_eps;
         shape.rope_base = s->rope_base;
         shape.rope_scale = s->rope_scale;
+        shape.prompt_rows = s->prompt_rows;
         auto p = std::make_unique<sih_program>();
         p->program = BuildPhi4DecodeProgram(shape);
         p->executor = std::make_unique<HipVmExecutor>(p->program, device);

@@ -22,6 +22,8 @@ typedef struct sih_phi4_shape {
     int32_t tied;                                       /* vocabulary projection onto token_embedding */
     int32_t cache_fp16;                                 /* 1: Float16 KV cache, 0: Float32 */
     float rms_eps, rope_base, rope_scale;
+    int32_t prompt_rows;                                /* > 0: fused_embeddings [prompt_rows, hidden] and
+                                                           the prefill_fused_16 entry */
 } sih_phi4_shape;
 
 /* Builds the program, creates its executor on `device` (every slot zeroed)

@@ -353,6 +353,355 @@ protected:
     }
 };
 
+// ---- batched (prefill) operators: GpuBatchTransformerInstructions.cs ------------------------
+
+// Shape helpers with the reference's rules and messages
+// (GpuBatchTransformerInstructions.cs:12-96).
+class BatchInstruction : public HipFixedInstruction {
+public:
+    using HipFixedInstruction::HipFixedInstruction;
+
+protected:
+    std::pair<int64_t, int64_t> BatchMatrix(const std::vector<InstructionParameter>& p, const std::string& name) const
+    {
+        const auto& d = Rank(p, name, 2);
+        if (d[0] <= 0 || d[1] <= 0)
+            Fail("'" + name + "' dimensions must be positive.");
+        return {d[0], d[1]};
+    }
+    int64_t Vector(const std::vector<InstructionParameter>& p, const std::string& name) const
+    {
+        const auto& d = Rank(p, name, 1);
+        if (d[0] <= 0)
+            Fail("'" + name + "' dimensions must be positive.");
+        return d[0];
+    }
+    std::vector<int64_t> Cache(const std::vector<InstructionParameter>& p, const std::string& name) const
+    {
+        const auto& d = Rank(p, name, 3);
+        for (const int64_t v : d)
+            if (v <= 0)
+                Fail("'" + name + "' dimensions must be positive.");
+        return d;
+    }
+    void RequireControl(const std::vector<InstructionParameter>& p) const
+    {
+        const auto& d = TensorOf(p, "control").tensor.dimensions;
+        if (d.size() != 1 || d[0] != 2)
+            Fail("'control' must have shape [2].");
+    }
+    void RequireSameShape(const std::vector<InstructionParameter>& p, const std::string& a, const std::string& b) const
+    {
+        if (TensorOf(p, a).tensor.dimensions != TensorOf(p, b).tensor.dimensions)
+            Fail("'" + a + "' and '" + b + "' must have matching shapes.");
+    }
+    // The HIP launches hold at most 16 batch rows (the reference's prefill batch).
+    void RequireBatch(int64_t batch) const
+    {
+        if (batch > 16)
+            Fail("the HIP batched operators take at most 16 rows.");
+    }
+
+private:
+    const std::vector<int64_t>& Rank(const std::vector<InstructionParameter>& p, const std::string& name,
+                                     size_t rank) const
+    {
+        const auto& d = TensorOf(p, name).tensor.dimensions;
+        if (d.size() != rank)
+            Fail("'" + name + "' must have rank " + std::to_string(rank) + ".");
+        return d;
+    }
+};
+
+class BatchRmsNormInstruction : public BatchInstruction {
+public:
+    BatchRmsNormInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-rms-norm",
+                           {{{"input", F32, R}, {"weight", F32, R}, {"control", I32, R}, {"output", F32, W}}},
+                           {"epsilon"})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [batch, width] = BatchMatrix(p, "input");
+        RequireSameShape(p, "input", "output");
+        if (Vector(p, "weight") != width)
+            Fail("'weight' must have shape [H].");
+        RequireControl(p);
+        PositiveFloat(p, "epsilon");
+        RequireBatch(batch);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_rms_norm", p};
+    }
+};
+
+class BatchResidualRmsNormInstruction : public BatchInstruction {
+public:
+    BatchResidualRmsNormInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-residual-rms-norm",
+                           {{{"hidden", F32, R},
+                             {"residual", F32, R},
+                             {"weight", F32, R},
+                             {"control", I32, R},
+                             {"updated", F32, W},
+                             {"output", F32, W}}},
+                           {"epsilon"})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [batch, width] = BatchMatrix(p, "hidden");
+        RequireSameShape(p, "hidden", "residual");
+        RequireSameShape(p, "hidden", "updated");
+        RequireSameShape(p, "hidden", "output");
+        if (Vector(p, "weight") != width)
+            Fail("'weight' must have shape [H].");
+        RequireControl(p);
+        PositiveFloat(p, "epsilon");
+        RequireBatch(batch);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_residual_rms_norm", p};
+    }
+};
+
+// The reference's weight is F16; F32 weights are a second signature here.
+class BatchSharedMatVecInstruction : public BatchInstruction {
+public:
+    BatchSharedMatVecInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-shared-matvec",
+                           {{{"weight", F16, R}, {"input", F32, R}, {"control", I32, R}, {"output", F32, W}},
+                            {{"weight", F32, R}, {"input", F32, R}, {"control", I32, R}, {"output", F32, W}}},
+                           {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [out_size, in_size] = BatchMatrix(p, "weight");
+        const auto [batch, in_width] = BatchMatrix(p, "input");
+        const auto [out_batch, out_width] = BatchMatrix(p, "output");
+        if (in_width != in_size || out_batch != batch || out_width != out_size)
+            Fail("Expected weight [O,I], input [B,I], and output [B,O].");
+        RequireControl(p);
+        RequireBatch(batch);
+        if (in_size % 32 != 0)
+            Fail("the HIP batched mat-vec takes a multiple of 32 input columns.");
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_matvec.dense", p};
+    }
+};
+
+class BatchSwiGluInstruction : public BatchInstruction {
+public:
+    BatchSwiGluInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-swiglu",
+                           {{{"gate_up", F32, R}, {"control", I32, R}, {"output", F32, W}}}, {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [batch, combined] = BatchMatrix(p, "gate_up");
+        const auto [out_batch, width] = BatchMatrix(p, "output");
+        if (combined != 2 * width || out_batch != batch)
+            Fail("Expected gate_up [B,2I] and output [B,I].");
+        RequireControl(p);
+        RequireBatch(batch);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_swiglu", p};
+    }
+};
+
+class BatchRopeKvWriteInstruction : public BatchInstruction {
+public:
+    BatchRopeKvWriteInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-rope-kv-write",
+                           CacheSignatures([](GraphElementType c) {
+                               return std::vector<InstructionPort>{{"qkv", F32, R},         {"control", I32, R},
+                                                                   {"frequencies", F32, R}, {"query", F32, W},
+                                                                   {"key_cache", c, W},     {"value_cache", c, W}};
+                           }),
+                           {"head_size", "rotary_size", "rope_scale"})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [batch, qkv_width] = BatchMatrix(p, "qkv");
+        const auto [query_batch, query_size] = BatchMatrix(p, "query");
+        const auto k = Cache(p, "key_cache");
+        const auto v = Cache(p, "value_cache");
+        const int head = PositiveInteger(p, "head_size"), rotary = PositiveInteger(p, "rotary_size");
+        PositiveFloat(p, "rope_scale");
+        const int64_t kv = k[1] * head;
+        if (query_batch != batch || v != k || k[2] != head || query_size % head != 0 || rotary > head ||
+            rotary % 2 != 0 || qkv_width != query_size + 2 * kv)
+            Fail("Invalid qkv, query, cache, head, or rotary dimensions.");
+        if (Vector(p, "frequencies") != rotary / 2)
+            Fail("'frequencies' must have shape [rotary_size/2].");
+        RequireControl(p);
+        RequireBatch(batch);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_rope_kv_write", p};
+    }
+};
+
+class BatchGqaScoresInstruction : public BatchInstruction {
+public:
+    BatchGqaScoresInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-gqa-scores",
+                           CacheSignatures([](GraphElementType c) {
+                               return std::vector<InstructionPort>{
+                                   {"query", F32, R}, {"key_cache", c, R}, {"control", I32, R}, {"scores", F32, W}};
+                           }),
+                           {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [batch, query_size] = BatchMatrix(p, "query");
+        const auto k = Cache(p, "key_cache");
+        const auto& s = TensorOf(p, "scores").tensor.dimensions;
+        if (s.size() != 3 || s[0] != batch || s[2] != k[0])
+            Fail("'scores' must have shape [B,qheads,context].");
+        if (s[1] <= 0 || s[1] % k[1] != 0 || query_size != s[1] * k[2])
+            Fail("Incompatible query, cache, and GQA score shapes.");
+        RequireControl(p);
+        RequireBatch(batch);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_gqa_scores", p};
+    }
+};
+
+class BatchCausalSoftmaxInstruction : public BatchInstruction {
+public:
+    BatchCausalSoftmaxInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-causal-softmax",
+                           {{{"scores", F32, R}, {"control", I32, R}, {"probabilities", F32, W}}}, {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto& s = TensorOf(p, "scores").tensor.dimensions;
+        if (s.size() != 3)
+            Fail("'scores' must have shape [B,heads,context].");
+        RequireSameShape(p, "scores", "probabilities");
+        if (s[0] <= 0 || s[1] <= 0 || s[2] <= 0)
+            Fail("'scores' dimensions must be positive.");
+        RequireControl(p);
+        RequireBatch(s[0]);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_causal_softmax", p};
+    }
+};
+
+class BatchGqaValuesInstruction : public BatchInstruction {
+public:
+    BatchGqaValuesInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-gqa-values",
+                           CacheSignatures([](GraphElementType c) {
+                               return std::vector<InstructionPort>{{"probabilities", F32, R},
+                                                                   {"value_cache", c, R},
+                                                                   {"control", I32, R},
+                                                                   {"output", F32, W}};
+                           }),
+                           {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto& pr = TensorOf(p, "probabilities").tensor.dimensions;
+        if (pr.size() != 3)
+            Fail("'probabilities' must have shape [B,qheads,context].");
+        const auto v = Cache(p, "value_cache");
+        const auto [out_batch, out_width] = BatchMatrix(p, "output");
+        if (pr[0] <= 0 || pr[1] <= 0 || pr[2] != v[0] || pr[1] % v[1] != 0 || out_batch != pr[0] ||
+            out_width != pr[1] * v[2])
+            Fail("Incompatible probability, value cache, and output shapes.");
+        RequireControl(p);
+        RequireBatch(pr[0]);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_gqa_values", p};
+    }
+};
+
+class BatchSelectLastInstruction : public BatchInstruction {
+public:
+    BatchSelectLastInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-select-last",
+                           {{{"input", F32, R}, {"control", I32, R}, {"output", F32, W}}}, {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [batch, width] = BatchMatrix(p, "input");
+        if (Vector(p, "output") != width)
+            Fail("Expected input [B,H] and output [H].");
+        RequireControl(p);
+        RequireBatch(batch);
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_select_last", p};
+    }
+};
+
+class BatchGatherRowsInstruction : public BatchInstruction {
+public:
+    BatchGatherRowsInstruction()
+        : BatchInstruction(InstructionCollectionIds::TransformerFloat32, "transformer.batch-gather-rows",
+                           {{{"table", F32, R}, {"control", I32, R}, {"output", F32, W}}}, {})
+    {
+    }
+
+protected:
+    void Validate(const std::vector<InstructionParameter>& p) const override
+    {
+        const auto [rows, width] = BatchMatrix(p, "table");
+        const auto [batch, out_width] = BatchMatrix(p, "output");
+        if (out_width != width)
+            Fail("Expected table [N,H] and output [B,H].");
+        RequireControl(p);
+        RequireBatch(batch);
+        (void)rows;
+    }
+    InstructionRecording Generate(const std::vector<InstructionParameter>& p) const override
+    {
+        return {"si_hip_batch_gather_rows", p};
+    }
+};
+
 }  // namespace
 
 std::vector<InstructionCollectionDescription> HipTransformerInstructions::QueryInstructionCollection() const
@@ -371,6 +720,16 @@ std::vector<std::shared_ptr<const Instruction>> HipTransformerInstructions::Quer
     if (name == "transformer.rope-kv-write") return {std::make_shared<RopeKvWriteInstruction>()};
     if (name == "transformer.grouped-query-attention") return {std::make_shared<GroupedQueryAttentionInstruction>()};
     if (name == "transformer.argmax") return {std::make_shared<ArgMaxInstruction>()};
+    if (name == "transformer.batch-rms-norm") return {std::make_shared<BatchRmsNormInstruction>()};
+    if (name == "transformer.batch-residual-rms-norm") return {std::make_shared<BatchResidualRmsNormInstruction>()};
+    if (name == "transformer.batch-shared-matvec") return {std::make_shared<BatchSharedMatVecInstruction>()};
+    if (name == "transformer.batch-swiglu") return {std::make_shared<BatchSwiGluInstruction>()};
+    if (name == "transformer.batch-rope-kv-write") return {std::make_shared<BatchRopeKvWriteInstruction>()};
+    if (name == "transformer.batch-gqa-scores") return {std::make_shared<BatchGqaScoresInstruction>()};
+    if (name == "transformer.batch-causal-softmax") return {std::make_shared<BatchCausalSoftmaxInstruction>()};
+    if (name == "transformer.batch-gqa-values") return {std::make_shared<BatchGqaValuesInstruction>()};
+    if (name == "transformer.batch-select-last") return {std::make_shared<BatchSelectLastInstruction>()};
+    if (name == "transformer.batch-gather-rows") return {std::make_shared<BatchGatherRowsInstruction>()};
     return {};
 }
 
@@ -424,11 +783,114 @@ TensorDescriptor Vec(int64_t n, GraphElementType t = F32) { return {t, {n}}; }
 
 }  // namespace
 
+namespace {
+
+// The reference's prefill entry (Phi4D3D12TextSession.cs:952-1168) on the
+// program's slots: 16-row batches of the fused prompt embeddings.
+template <typename TensorFn, typename MatVecFn>
+void AddPhi4Prefill(HipVmProgram& p, const Phi4ProgramShape& s, const std::shared_ptr<const InstructionRegistry>& registry,
+                    const TensorFn& tensor, const MatVecFn& matvec)
+{
+    constexpr int64_t B = 16;
+    const std::string E = "prefill_fused_16";
+    const auto resolve = [&](const std::string& collection, const std::string& name) {
+        return registry->Resolve(collection, name, InstructionTarget::Hip());
+    };
+    const auto& T = InstructionCollectionIds::TransformerFloat32;
+    const auto quant_bmv = resolve(HipInstructionCollectionIds::QuantizedFloat32, "quant.batch-mat-vec");
+    const auto dense_bmv = resolve(T, "transformer.batch-shared-matvec");
+    const auto gather = resolve(T, "transformer.batch-gather-rows"), rms = resolve(T, "transformer.batch-rms-norm");
+    const auto residual_rms = resolve(T, "transformer.batch-residual-rms-norm");
+    const auto swiglu = resolve(T, "transformer.batch-swiglu"), rope = resolve(T, "transformer.batch-rope-kv-write");
+    const auto scores = resolve(T, "transformer.batch-gqa-scores");
+    const auto softmax = resolve(T, "transformer.batch-causal-softmax");
+    const auto values = resolve(T, "transformer.batch-gqa-values");
+    const auto last = resolve(T, "transformer.batch-select-last");
+    const auto argmax = resolve(T, "transformer.argmax");
+    const int64_t H = s.hidden, F = s.ffn, Q = s.hidden, KV = static_cast<int64_t>(s.kv_heads) * s.head_dim;
+    const auto rw = VmAccess::ReadWrite;
+    p.AddSlot({"fused_embeddings", {F32, {s.prompt_rows, H}}, VmAccess::ReadOnly});
+    for (const auto& [name, dims] : std::vector<std::pair<const char*, std::vector<int64_t>>>{
+             {"batch_hidden", {B, H}}, {"batch_normalized", {B, H}}, {"batch_qkv", {B, Q + 2 * KV}},
+             {"batch_query", {B, Q}}, {"batch_scores", {B, s.heads, s.context}},
+             {"batch_probabilities", {B, s.heads, s.context}}, {"batch_attention", {B, H}},
+             {"batch_projected", {B, H}}, {"batch_hidden_after_attention", {B, H}}, {"batch_gate_up", {B, 2 * F}},
+             {"batch_activated", {B, F}}, {"batch_down", {B, H}}, {"batch_last", {H}}})
+        p.AddSlot({name, {F32, dims}, rw});
+
+    using P = InstructionParameter;
+    const PrecisionRequirement fp32{F32, F32};
+    const auto control = tensor("control", "control", R, 0, nullptr);
+    char eps[64], scale[64];
+    std::snprintf(eps, sizeof eps, "%.9g", static_cast<double>(s.rms_eps));
+    std::snprintf(scale, sizeof scale, "%.9g", static_cast<double>(s.rope_scale));
+    const auto batch_matvec = [&](const std::string& weight, const std::string& input, const std::string& output,
+                                  int64_t columns) {
+        std::vector<P> args{tensor("weight", weight, R, 0, nullptr), tensor("input", input, R, 0, nullptr), control,
+                            tensor("output", output, W, 0, nullptr)};
+        if (Dense(s.weight_format)) {
+            p.AddDispatch(E, dense_bmv, args, fp32);
+        } else {
+            args.push_back(P::Attribute("format", FormatName(s.weight_format)));
+            args.push_back(P::Attribute("columns", std::to_string(columns)));
+            p.AddDispatch(E, quant_bmv, args, fp32);
+        }
+    };
+    const auto t = [&](const char* port, const std::string& slot, GraphResourceAccess access) {
+        return tensor(port, slot, access, 0, nullptr);
+    };
+    p.AddDispatch(E, gather, {t("table", "fused_embeddings", R), control, t("output", "batch_hidden", W)}, fp32);
+    p.AddDispatch(E, rms,
+                  {t("input", "batch_hidden", R), t("weight", "attn_norm_0", R), control,
+                   t("output", "batch_normalized", W), P::Attribute("epsilon", eps)},
+                  fp32);
+    for (int l = 0; l < s.layers; l++) {
+        const std::string L = std::to_string(l);
+        batch_matvec("qkv_weight_" + L, "batch_normalized", "batch_qkv", H);
+        p.AddDispatch(E, rope,
+                      {t("qkv", "batch_qkv", R), control, t("frequencies", "rope_frequencies", R),
+                       t("query", "batch_query", W), t("key_cache", "key_cache_" + L, W),
+                       t("value_cache", "value_cache_" + L, W), P::Attribute("head_size", std::to_string(s.head_dim)),
+                       P::Attribute("rotary_size", std::to_string(s.rotary_dim)), P::Attribute("rope_scale", scale)},
+                      fp32);
+        p.AddDispatch(E, scores,
+                      {t("query", "batch_query", R), t("key_cache", "key_cache_" + L, R), control,
+                       t("scores", "batch_scores", W)},
+                      fp32);
+        p.AddDispatch(E, softmax, {t("scores", "batch_scores", R), control, t("probabilities", "batch_probabilities", W)},
+                      fp32);
+        p.AddDispatch(E, values,
+                      {t("probabilities", "batch_probabilities", R), t("value_cache", "value_cache_" + L, R), control,
+                       t("output", "batch_attention", W)},
+                      fp32);
+        batch_matvec("attn_output_weight_" + L, "batch_attention", "batch_projected", H);
+        p.AddDispatch(E, residual_rms,
+                      {t("hidden", "batch_hidden", R), t("residual", "batch_projected", R),
+                       t("weight", "ffn_norm_" + L, R), control, t("updated", "batch_hidden_after_attention", W),
+                       t("output", "batch_normalized", W), P::Attribute("epsilon", eps)},
+                      fp32);
+        batch_matvec("ffn_up_weight_" + L, "batch_normalized", "batch_gate_up", H);
+        p.AddDispatch(E, swiglu, {t("gate_up", "batch_gate_up", R), control, t("output", "batch_activated", W)}, fp32);
+        batch_matvec("ffn_down_weight_" + L, "batch_activated", "batch_down", F);
+        const std::string next_norm = l + 1 < s.layers ? "attn_norm_" + std::to_string(l + 1) : "output_norm";
+        p.AddDispatch(E, residual_rms,
+                      {t("hidden", "batch_hidden_after_attention", R), t("residual", "batch_down", R),
+                       t("weight", next_norm, R), control, t("updated", "batch_hidden", W),
+                       t("output", "batch_normalized", W), P::Attribute("epsilon", eps)},
+                      fp32);
+    }
+    p.AddDispatch(E, last, {t("input", "batch_normalized", R), control, t("output", "batch_last", W)}, fp32);
+    matvec(s.head_format, s.tied ? "token_embedding" : "output_weight", "batch_last", "logits", H, E);
+    p.AddDispatch(E, argmax, {t("input", "logits", R), t("output", "next_token", W)}, fp32);
+}
+
+}  // namespace
+
 HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& s)
 {
     if (s.layers < 1 || s.hidden < 1 || s.heads < 1 || s.kv_heads < 1 || s.heads % s.kv_heads != 0 ||
         s.hidden != s.heads * s.head_dim || s.ffn < 1 || s.vocab < 1 || s.context < 1 || s.rotary_dim < 2 ||
-        s.rotary_dim > s.head_dim || s.rotary_dim % 2 != 0)
+        s.rotary_dim > s.head_dim || s.rotary_dim % 2 != 0 || s.prompt_rows < 0 || s.prompt_rows > s.context)
         throw ArgumentException("Invalid Phi-4 program shape.");
     if (s.cache_type != F32 && s.cache_type != F16)
         throw ArgumentException("The KV cache is Float32 or Float16.");
@@ -492,14 +954,14 @@ HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& s)
         return std::string(b);
     }();
     const auto matvec = [&](int fmt, const std::string& weight, const std::string& input, const std::string& output,
-                            int64_t columns) {
+                            int64_t columns, const std::string& entry = "decode") {
         std::vector<P> args{tensor("weight", weight, R), tensor("input", input, R), tensor("output", output, W)};
         if (Dense(fmt)) {
-            p.AddDispatch("decode", t0_mv, args, fp32);
+            p.AddDispatch(entry, t0_mv, args, fp32);
         } else {
             args.push_back(P::Attribute("format", FormatName(fmt)));
             args.push_back(P::Attribute("columns", std::to_string(columns)));
-            p.AddDispatch("decode", quant_mv, args, fp32);
+            p.AddDispatch(entry, quant_mv, args, fp32);
         }
     };
     // embedding
@@ -551,6 +1013,8 @@ HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& s)
     }
     matvec(s.head_format, s.tied ? "token_embedding" : "output_weight", "normalized", "logits", H);
     p.AddDispatch("decode", argmax, {tensor("input", "logits", R), tensor("output", "next_token", W)}, fp32);
+    if (s.prompt_rows > 0)
+        AddPhi4Prefill(p, s, registry, tensor, matvec);
     return p;
 }
 

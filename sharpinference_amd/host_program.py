@@ -32,7 +32,8 @@ class Phi4Shape(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("layers", "hidden", "heads", "kv_heads", "head_dim", "rotary_dim",
                                               "ffn", "vocab", "context", "weight_format", "embed_format",
                                               "head_format", "tied", "cache_fp16")] + \
-        [("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("rope_scale", ctypes.c_float)]
+        [("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("rope_scale", ctypes.c_float),
+         ("prompt_rows", ctypes.c_int32)]
 
 
 def host_lib() -> ctypes.CDLL:
@@ -72,13 +73,15 @@ def _check(rc: int) -> None:
 class Phi4OpProgram:
     """One model's decode program, uploaded and ready to step."""
 
-    def __init__(self, cfg: Phi4Config, weights: Phi4Weights, cache_fp16: bool = True, device: int = 0):
+    def __init__(self, cfg: Phi4Config, weights: Phi4Weights, cache_fp16: bool = True, device: int = 0,
+                 prompt_rows: int = 0):
         self.cfg = cfg
         self.cache_fp16 = cache_fp16
+        self.prompt_rows = prompt_rows
         tied = weights.lm_head is weights.embed
         shape = Phi4Shape(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.rotary_dim, cfg.ffn,
                           cfg.vocab, cfg.capacity, cfg.weight_format, cfg.embed_format, cfg.head_format, int(tied),
-                          int(cache_fp16), cfg.rms_eps, cfg.rope_base, cfg.rope_scale)
+                          int(cache_fp16), cfg.rms_eps, cfg.rope_base, cfg.rope_scale, prompt_rows)
         h = ctypes.c_void_p()
         _check(host_lib().sih_phi4_program_create(ctypes.byref(shape), device, ctypes.byref(h)))
         self._h = h
@@ -145,12 +148,35 @@ class Phi4OpProgram:
         self.position = position + 1
         return int(self.readback("next_token", np.int32)[0])
 
+    def prefill_embeddings(self, embeddings: np.ndarray) -> int:
+        """PrefillFusedEmbeddings (Phi4D3D12TextSession.cs:267-287): uploads the
+        prompt's FP32 embeddings [prompt_rows, hidden] and runs
+        prefill_fused_16 over batches of up to 16 rows from the current
+        position (control = [start, valid]); returns the next token after the
+        last prompt row."""
+        if self.prompt_rows <= 0:
+            raise RuntimeError("this program was created without a prefill entry (prompt_rows = 0)")
+        emb = np.ascontiguousarray(embeddings, np.float32)
+        if emb.shape != (self.prompt_rows, self.cfg.hidden):
+            raise ValueError(f"expected embeddings of shape {(self.prompt_rows, self.cfg.hidden)}, got {emb.shape}")
+        if self.position >= self.prompt_rows:
+            raise RuntimeError("All fused prompt embeddings have already been consumed.")
+        self.upload("fused_embeddings", emb)
+        token = -1
+        while self.position < self.prompt_rows:
+            count = min(16, self.prompt_rows - self.position)
+            self.upload("control", np.array([self.position, count], np.int32))
+            _check(host_lib().sih_program_execute(self._h, b"prefill_fused_16"))
+            self.position += count
+            token = int(self.readback("next_token", np.int32)[0])
+        return token
+
     def read_logits(self) -> np.ndarray:
         return self.readback("logits", np.float32)
 
-    def measure_us(self, repetitions: int = 8) -> float:
+    def measure_us(self, repetitions: int = 8, entry: str = "decode") -> float:
         us = ctypes.c_double(0.0)
-        _check(host_lib().sih_program_measure_us(self._h, b"decode", repetitions, ctypes.byref(us)))
+        _check(host_lib().sih_program_measure_us(self._h, entry.encode(), repetitions, ctypes.byref(us)))
         return us.value
 
     def close(self) -> None:

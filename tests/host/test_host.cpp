@@ -600,6 +600,139 @@ TEST(cpu, Phi4ProgramFollowsTheReferenceDispatchOrder)
     ASSERT_TRUE(f.size() == 48 && f[0] == 1.0f && std::fabs(f[47] - 1.0f / std::pow(10000.0f, 94.0f / 96.0f)) < 1e-12f);
 }
 
+TEST(cpu, BatchInstructionsAdaptWithTheReferenceRules)
+{
+    // GpuBatchTransformerInstructions.cs:12-96 shape rules, :101-679 per op
+    const auto reg = DefaultHipRegistry();
+    const auto& T = InstructionCollectionIds::TransformerFloat32;
+    using P = InstructionParameter;
+    const auto R = GraphResourceAccess::Read, W = GraphResourceAccess::Write;
+    const auto f32 = [](std::vector<int64_t> d) { return TensorDescriptor{GraphElementType::Float32, std::move(d)}; };
+    const TensorDescriptor ctl{GraphElementType::Int32, {2}};
+    const auto rms = reg->Resolve(T, "transformer.batch-rms-norm", InstructionTarget::Hip());
+    std::vector<P> p{P::Tensor("input", f32({16, 64}), R, "a"), P::Tensor("weight", f32({64}), R, "b"),
+                     P::Tensor("control", ctl, R, "c"), P::Tensor("output", f32({16, 64}), W, "d"),
+                     P::Attribute("epsilon", "1e-05")};
+    rms->Adapt(p, kFp32);
+    auto bad = p;
+    bad[0].tensor = f32({16 * 64});            // 'input' must have rank 2
+    ASSERT_THROWS(InstructionAdaptationException, rms->Adapt(bad, kFp32));
+    bad = p;
+    bad[3].tensor = f32({8, 64});              // input and output shapes differ
+    ASSERT_THROWS(InstructionAdaptationException, rms->Adapt(bad, kFp32));
+    bad = p;
+    bad[2].tensor = TensorDescriptor{GraphElementType::Int32, {3}};   // control [3]
+    ASSERT_THROWS(InstructionAdaptationException, rms->Adapt(bad, kFp32));
+    bad = p;
+    bad[0].tensor = bad[3].tensor = f32({17, 64});   // more rows than the HIP batch
+    ASSERT_THROWS(InstructionAdaptationException, rms->Adapt(bad, kFp32));
+
+    // the shared mat-vec: F16 (the reference) and F32 weights; block formats go to quant.batch-mat-vec
+    const auto bmv = reg->Resolve(T, "transformer.batch-shared-matvec", InstructionTarget::Hip());
+    for (GraphElementType wt : {GraphElementType::Float16, GraphElementType::Float32}) {
+        std::vector<P> m{P::Tensor("weight", TensorDescriptor{wt, {96, 64}}, R, "w"),
+                         P::Tensor("input", f32({16, 64}), R, "x"), P::Tensor("control", ctl, R, "c"),
+                         P::Tensor("output", f32({16, 96}), W, "y")};
+        ASSERT_TRUE(bmv->Adapt(m, kFp32).ports[0].element_type == wt);
+        auto wrong = m;
+        wrong[3].tensor = f32({16, 95});        // output [B,O] mismatch
+        ASSERT_THROWS(InstructionAdaptationException, bmv->Adapt(wrong, kFp32));
+    }
+    const auto qbmv = reg->Resolve(HipInstructionCollectionIds::QuantizedFloat32, "quant.batch-mat-vec",
+                                   InstructionTarget::Hip());
+    std::vector<P> q{P::Tensor("weight", TensorDescriptor{GraphElementType::Byte, {96, 36}}, R, "w"),
+                     P::Tensor("input", f32({16, 64}), R, "x"), P::Tensor("control", ctl, R, "c"),
+                     P::Tensor("output", f32({16, 96}), W, "y"), P::Attribute("format", "q4_0"),
+                     P::Attribute("columns", "64")};
+    qbmv->Adapt(q, kFp32);
+    auto wq = q;
+    wq[5].value = "128";                        // 36-byte rows hold 64 Q4_0 columns
+    ASSERT_THROWS(InstructionAdaptationException, qbmv->Adapt(wq, kFp32));
+
+    // rope-kv-write: qkv width = query + 2 kv, frequencies [rotary/2]
+    const auto rope = reg->Resolve(T, "transformer.batch-rope-kv-write", InstructionTarget::Hip());
+    const auto cache = [](GraphElementType t) { return TensorDescriptor{t, {32, 2, 128}}; };
+    for (GraphElementType t : {GraphElementType::Float32, GraphElementType::Float16}) {
+        std::vector<P> r{P::Tensor("qkv", f32({16, 8 * 128 + 2 * 256}), R, "qkv"), P::Tensor("control", ctl, R, "c"),
+                         P::Tensor("frequencies", f32({48}), R, "f"), P::Tensor("query", f32({16, 8 * 128}), W, "q"),
+                         P::Tensor("key_cache", cache(t), W, "k"), P::Tensor("value_cache", cache(t), W, "v"),
+                         P::Attribute("head_size", "128"), P::Attribute("rotary_size", "96"),
+                         P::Attribute("rope_scale", "1.19")};
+        rope->Adapt(r, kFp32);
+        auto wr = r;
+        wr[2].tensor = f32({47});
+        ASSERT_THROWS(InstructionAdaptationException, rope->Adapt(wr, kFp32));
+        wr = r;
+        wr[0].tensor = f32({16, 8 * 128 + 256});
+        ASSERT_THROWS(InstructionAdaptationException, rope->Adapt(wr, kFp32));
+    }
+    // scores [B, qheads, context] over a matching cache; values output [B, qheads * head]
+    const auto scores = reg->Resolve(T, "transformer.batch-gqa-scores", InstructionTarget::Hip());
+    std::vector<P> sc{P::Tensor("query", f32({16, 8 * 128}), R, "q"),
+                      P::Tensor("key_cache", cache(GraphElementType::Float32), R, "k"),
+                      P::Tensor("control", ctl, R, "c"), P::Tensor("scores", f32({16, 8, 32}), W, "s")};
+    scores->Adapt(sc, kFp32);
+    auto ws = sc;
+    ws[3].tensor = f32({16, 8, 31});            // context column count differs from the cache
+    ASSERT_THROWS(InstructionAdaptationException, scores->Adapt(ws, kFp32));
+    const auto values = reg->Resolve(T, "transformer.batch-gqa-values", InstructionTarget::Hip());
+    std::vector<P> va{P::Tensor("probabilities", f32({16, 8, 32}), R, "p"),
+                      P::Tensor("value_cache", cache(GraphElementType::Float16), R, "v"),
+                      P::Tensor("control", ctl, R, "c"), P::Tensor("output", f32({16, 8 * 128}), W, "o")};
+    values->Adapt(va, kFp32);
+    auto wv = va;
+    wv[0].tensor = f32({16, 6, 32});            // 6 query heads, output holds 8
+    ASSERT_THROWS(InstructionAdaptationException, values->Adapt(wv, kFp32));
+    const auto last = reg->Resolve(T, "transformer.batch-select-last", InstructionTarget::Hip());
+    std::vector<P> sl{P::Tensor("input", f32({16, 64}), R, "x"), P::Tensor("control", ctl, R, "c"),
+                      P::Tensor("output", f32({63}), W, "y")};
+    ASSERT_THROWS(InstructionAdaptationException, last->Adapt(sl, kFp32));
+}
+
+TEST(cpu, Phi4PrefillEntryFollowsTheReferenceDispatchOrder)
+{
+    Phi4ProgramShape s;
+    s.layers = 2;
+    s.hidden = 1024;
+    s.heads = 8;
+    s.kv_heads = 2;
+    s.ffn = 2048;
+    s.vocab = 100;
+    s.context = 64;
+    s.prompt_rows = 40;
+    const auto p = BuildPhi4DecodeProgram(s);
+    ASSERT_TRUE(p.Entries().at("decode").size() == 2 + 9 * 2 + 2);
+    const auto& d = p.Entries().at("prefill_fused_16");
+    ASSERT_TRUE(d.size() == 2 + 11 * 2 + 3);
+    std::vector<std::string> names;
+    for (const auto& x : d)
+        names.push_back(x.instruction->Name());
+    const std::vector<std::string> layer{
+        "quant.batch-mat-vec",         "transformer.batch-rope-kv-write",       "transformer.batch-gqa-scores",
+        "transformer.batch-causal-softmax", "transformer.batch-gqa-values",     "quant.batch-mat-vec",
+        "transformer.batch-residual-rms-norm", "quant.batch-mat-vec",           "transformer.batch-swiglu",
+        "quant.batch-mat-vec",         "transformer.batch-residual-rms-norm"};
+    std::vector<std::string> want{"transformer.batch-gather-rows", "transformer.batch-rms-norm"};
+    for (int l = 0; l < 2; l++)
+        want.insert(want.end(), layer.begin(), layer.end());
+    want.insert(want.end(), {"transformer.batch-select-last", "quant.mat-vec", "transformer.argmax"});
+    ASSERT_TRUE(names == want);
+    // the batch slots and the shared caches / control
+    ASSERT_TRUE(p.Slots()[p.SlotIndex("fused_embeddings")].tensor.dimensions == std::vector<int64_t>({40, 1024}));
+    ASSERT_TRUE(p.Slots()[p.SlotIndex("batch_scores")].tensor.dimensions == std::vector<int64_t>({16, 8, 64}));
+    bool writes_layer_cache = false;
+    for (const auto& q : d[3].recording.parameters)
+        writes_layer_cache |= q.name == "key_cache" && q.source == "key_cache_0";
+    ASSERT_TRUE(writes_layer_cache);
+    // dense weights use the transformer collection's shared mat-vec
+    s.weight_format = s.embed_format = s.head_format = SI_HIP_F16;
+    const auto dense = BuildPhi4DecodeProgram(s);
+    ASSERT_TRUE(dense.Entries().at("prefill_fused_16")[2].instruction->Name() == "transformer.batch-shared-matvec");
+    auto bad = s;
+    bad.prompt_rows = 65;                        // longer than the context
+    ASSERT_THROWS(ArgumentException, BuildPhi4DecodeProgram(bad));
+}
+
 TEST(cpu, ExecutorWithoutADeviceFailsLoudly)
 {
     int n = 0;

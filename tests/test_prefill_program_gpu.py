@@ -1,0 +1,131 @@
+"""The Phi-4 prefill entry (prefill_fused_16, Phi4D3D12TextSession.cs:
+267-287, 952-1168) dispatched operator by operator through the C++ host
+layer: prompt embeddings in 16-row batches masked by control = [start,
+valid], then the decode entry continuing from the prompt's end.
+
+Truth: the float64 restatement of Phi4TextModel.cs:59-105 stepped over the
+same tokens one at a time (a prompt of n tokens is n decode steps of the
+CpuVm model); with FP32 caches (the reference's cache type) the GPU's only
+departure is FP32 rounding.  Gates: logits |d| <= 3e-4 + 3e-4 * |t| after the
+last prompt row and after each following decode step; the same greedy
+token when the top-2 margin exceeds the gate; every cache row the prompt
+wrote within 1e-5 of the float64 row, rows past it untouched (zero).  The
+fp16-cache program is held to the same logits gate against the oracle
+(orc_phi4_decode_step, which rounds its cache rows to fp16 as well).
+"""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from sharpinference_amd import host_program, phi4
+from tests.test_oracle_phi4_step import Float64Phi4
+
+pytestmark = pytest.mark.gpu
+
+
+def _gate(gl, tl, what):
+    d = np.abs(np.asarray(gl, np.float64) - tl)
+    bound = 3e-4 + 3e-4 * np.abs(tl)
+    assert np.all(d <= bound), f"{what}: worst {np.max(d / bound):.2f} of the gate"
+
+
+def _greedy(g, tl, what):
+    top2 = np.sort(tl)[-2:]
+    if top2[1] - top2[0] > 1e-3 * max(1.0, abs(top2[1])):
+        assert g == int(np.argmax(tl)), what
+
+
+def _embeddings(cfg, weights, tokens):
+    table = orc.dequant(cfg.embed_format, weights.embed, cfg.vocab, cfg.hidden).reshape(cfg.vocab, cfg.hidden)
+    return np.ascontiguousarray(table[tokens], np.float32)
+
+
+@pytest.mark.parametrize("prompt", [37, 16, 5])
+def test_prefill_then_decode_matches_float64_model(hip, prompt):
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=3000, capacity=64,
+                          rope_scale=1.19)
+    weights = phi4.synth_weights(cfg, seed=61 + prompt)
+    rng = np.random.default_rng(prompt)
+    tokens = rng.integers(0, cfg.vocab, prompt)
+    prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=False, prompt_rows=prompt)
+    zeros = [np.zeros((cfg.kv_heads, cfg.capacity, cfg.head_dim), np.uint16) for _ in range(cfg.layers)]
+    ref = Float64Phi4(SimpleNamespace(**cfg.__dict__), weights, zeros, zeros, cache_dtype=np.float64)
+    try:
+        assert prog.dispatch_count("prefill_fused_16") == 2 + 11 * cfg.layers + 3
+        g = prog.prefill_embeddings(_embeddings(cfg, weights, tokens))
+        for pos, t in enumerate(tokens):
+            truth = ref.step(int(t), pos)
+        _gate(prog.read_logits(), truth, f"prompt of {prompt}")
+        _greedy(g, truth, "prefill token")
+        assert prog.position == prompt
+        for l in range(cfg.layers):
+            k, v = prog.read_kv(l)
+            for got, want in ((k, ref.k[l]), (v, ref.v[l])):
+                assert np.allclose(got[:, :prompt], want[:, :prompt], rtol=1e-5, atol=1e-5), f"layer {l} cache"
+                assert np.all(got[:, prompt:] == 0), f"layer {l}: rows past the prompt written"
+        # decoding continues on the same caches
+        for i, t in enumerate((7, 2999)):
+            g = prog.forward_token(t)
+            truth = ref.step(t, prompt + i)
+            _gate(prog.read_logits(), truth, f"decode step {i} after the prompt")
+            _greedy(g, truth, f"decode token {i}")
+    finally:
+        prog.close()
+
+
+def test_fp16_cache_prefill_matches_oracle(hip):
+    cfg = phi4.Phi4Config(layers=3, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=4000, capacity=128,
+                          rope_scale=1.19)
+    weights = phi4.synth_weights(cfg, seed=71)
+    tokens = np.random.default_rng(72).integers(0, cfg.vocab, 50)
+    prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True, prompt_rows=len(tokens))
+    ref = orc.Phi4Oracle(cfg, weights)
+    try:
+        g = prog.prefill_embeddings(_embeddings(cfg, weights, tokens))
+        for pos, t in enumerate(tokens):
+            o, ol = ref.step(int(t), pos)
+        _gate(prog.read_logits(), ol, "fp16 prefill")
+        _greedy(g, ol, "fp16 prefill token")
+        o2, ol2 = ref.step(11, len(tokens))
+        prog.forward_token(11)
+        _gate(prog.read_logits(), ol2, "fp16 decode after prefill")
+    finally:
+        prog.close()
+
+
+def test_dense_tied_prefill_matches_float64_model(hip):
+    """F16 layers and the tied head: the reference's own storage, on the
+    transformer collection's batch-shared-matvec."""
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=2000, capacity=48,
+                          weight_format=phi4.native.F16, embed_format=phi4.native.F16, head_format=phi4.native.F16)
+    weights = phi4.synth_weights(cfg, seed=73, tied=True)
+    tokens = np.random.default_rng(74).integers(0, cfg.vocab, 21)
+    prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=False, prompt_rows=len(tokens))
+    zeros = [np.zeros((cfg.kv_heads, cfg.capacity, cfg.head_dim), np.uint16) for _ in range(cfg.layers)]
+    ref = Float64Phi4(SimpleNamespace(**cfg.__dict__), weights, zeros, zeros, cache_dtype=np.float64)
+    try:
+        g = prog.prefill_embeddings(_embeddings(cfg, weights, tokens))
+        for pos, t in enumerate(tokens):
+            truth = ref.step(int(t), pos)
+        _gate(prog.read_logits(), truth, "dense prefill")
+        _greedy(g, truth, "dense prefill token")
+    finally:
+        prog.close()
+
+
+def test_prefill_rejects_a_consumed_prompt_and_bad_shapes(hip):
+    cfg = phi4.Phi4Config(layers=1, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=64, capacity=32)
+    weights = phi4.synth_weights(cfg, seed=75)
+    prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=False, prompt_rows=3)
+    try:
+        with pytest.raises(ValueError):
+            prog.prefill_embeddings(np.zeros((4, cfg.hidden), np.float32))
+        prog.prefill_embeddings(_embeddings(cfg, weights, [1, 2, 3]))
+        with pytest.raises(RuntimeError):
+            prog.prefill_embeddings(_embeddings(cfg, weights, [1, 2, 3]))
+    finally:
+        prog.close()
+    with pytest.raises(phi4.native.HipError):
+        host_program.Phi4OpProgram(cfg, weights, prompt_rows=33)     # longer than the context
