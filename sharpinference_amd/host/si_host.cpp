@@ -501,8 +501,9 @@ void HipVmProgram::AddDispatch(const std::string& entry, std::shared_ptr<const I
         }
     EntryRecorder recorder;
     instruction->Invoke(recorder, parameters, precision);
+    const KernelPrecisionProfile resolved = instruction->Adapt(parameters, precision).precision;
     for (auto& r : recorder.recordings)
-        entries_[entry].push_back({instruction, std::move(r)});
+        entries_[entry].push_back({instruction, std::move(r), precision, resolved});
 }
 
 // ---- HipVmExecutor -------------------------------------------------------------------------

@@ -372,15 +372,29 @@ std::shared_ptr<const InstructionRegistry> DefaultHipRegistry();
 
 // ---- program and executor (VmProgram, D3D12VmExecutor) ------------------------------------
 
+// VmSlotScope (VmProgram.cs:9): model-lifetime, session-lifetime (KV
+// caches) or per-invocation slots.
+enum class VmSlotScope { Global, Session, Local };
+
 struct HipVmSlot {
     std::string id;
     TensorDescriptor tensor;
     VmAccess access = VmAccess::ReadWrite;
+    VmSlotScope scope = VmSlotScope::Global;
+    std::string binding_key;   // empty: none
 };
 
 struct HipVmDispatch {
     std::shared_ptr<const Instruction> instruction;
     InstructionRecording recording;
+    PrecisionRequirement precision{GraphElementType::Float32, GraphElementType::Float32};
+    KernelPrecisionProfile resolved{GraphElementType::Float32, GraphElementType::Float32};   // the adapted signature's
+};
+
+// VmStateEntry (VmProgram.cs:46): a named piece of session state and its slot.
+struct HipVmStateEntry {
+    std::string name;
+    std::string slot;
 };
 
 // Slots and named entries; each entry is a list of dispatches separated by
@@ -401,10 +415,53 @@ public:
     const std::map<std::string, std::vector<HipVmDispatch>>& Entries() const { return entries_; }
     int SlotIndex(const std::string& id) const;   // -1 if absent
 
+    // Program identity and session state (VmProgram name / abi / state).
+    std::string name = "hip-program", abi = "hip.fp32";
+    std::string state_schema = "none";
+    int state_version = 1;
+    std::vector<HipVmStateEntry> state;
+
 private:
     std::vector<HipVmSlot> slots_;
     std::map<std::string, std::vector<HipVmDispatch>> entries_;
 };
+
+// ---- VmProgram XML and artifacts (VmProgramXml.cs, D3D12VmArtifact.cs) ----------------------
+
+// The reference's VmProgram XML (VmProgramXml.cs:13-41) with target "Hip":
+// slots as written; each entry as an Orchestration definition whose
+// parameters are the entry's distinct slot views (the whole slot by its id,
+// a narrower view such as control's position word by its port name), an
+// Operator node per dispatch (collection GUID, name, arguments, precision,
+// resolved precision, execution configuration hip.gfx950 / its C ABI
+// operation, sorted attributes and port accesses) followed by a Barrier
+// node over the parameters it writes, and an Entry binding each parameter to
+// its slot and byte offset.
+std::string SerializeVmProgram(const HipVmProgram& program);
+// The inverse, with the reference's reader rules (VmProgramXml.cs:43-107,
+// 236-296): no DTD, comments and processing instructions ignored, at most
+// 16 Mi characters, 100000 elements and nesting 64, only the schema's
+// elements and attributes, no text content, enums by exact name.  Every
+// operator is resolved on the HIP target through `registry` and re-adapted
+// by AddDispatch.  Malformed input raises InvalidDataException.
+HipVmProgram DeserializeVmProgram(const std::string& xml,
+                                  const std::shared_ptr<const InstructionRegistry>& registry = nullptr);
+
+// HIP program artifact (D3D12VmArtifact.cs:90-148 for this target): a ZIP
+// holding program.xml and manifest.json = {"Manifest": <manifest JSON>,
+// "Sha256": <its hash>}, the manifest naming the format version, the
+// backend ABI (HipVmArtifactAbi), the target "hip.gfx950", the C ABI
+// version of libsharpinference_hip it was exported against and program.xml's
+// SHA-256.  Kernels are the library's code objects, so the archive holds no
+// kernel modules.  Import checks sizes, entry names, both hashes, version,
+// ABI, target and library ABI, then deserializes the program.  Hashes detect
+// corruption; they are not a signature.
+inline const std::string HipVmArtifactAbi = "SharpInference.HipVm.c-abi-launch.ic-precision.v1";
+std::vector<uint8_t> ExportHipVmArtifact(const HipVmProgram& program);
+HipVmProgram ImportHipVmArtifact(const std::vector<uint8_t>& archive,
+                                 const std::shared_ptr<const InstructionRegistry>& registry = nullptr);
+// SHA-256 of bytes as 64 upper-case hex digits (Convert.ToHexString(SHA256.HashData)).
+std::string Sha256Hex(const void* data, size_t length);
 
 // The executor of a HipVmProgram on one device (D3D12VmExecutor.cs): one
 // persistent device buffer per slot, exact-size uploads, entries recorded

@@ -4,8 +4,10 @@
 
 #include "si_host.hpp"
 
+#include <algorithm>
 #include <memory>
 #include <string>
+#include <vector>
 
 using namespace sharpinference;
 
@@ -153,6 +155,63 @@ int sih_program_dispatch_count(const sih_program* program, const char* entry, in
         if (it == program->program.Entries().end())
             throw ArgumentException(std::string("Unknown entry '") + entry + "'.");
         *count = static_cast<int>(it->second.size());
+    });
+}
+
+int sih_program_serialize(const sih_program* program, char* buffer, uint64_t capacity, uint64_t* length)
+{
+    return Guard([&] {
+        if (!program || !length)
+            throw ArgumentException("sih_program_serialize: null argument");
+        const std::string xml = SerializeVmProgram(program->program);
+        *length = xml.size();
+        if (buffer) {
+            if (capacity < xml.size())
+                throw ArgumentException("sih_program_serialize: buffer too small");
+            std::copy(xml.begin(), xml.end(), buffer);
+        }
+    });
+}
+
+int sih_program_create_from_xml(const char* xml, int device, sih_program** out)
+{
+    return Guard([&] {
+        if (!xml || !out)
+            throw ArgumentException("sih_program_create_from_xml: null argument");
+        *out = nullptr;
+        auto p = std::make_unique<sih_program>();
+        p->program = DeserializeVmProgram(xml);
+        p->executor = std::make_unique<HipVmExecutor>(p->program, device);
+        *out = p.release();
+    });
+}
+
+int sih_program_export_artifact(const sih_program* program, void* buffer, uint64_t capacity, uint64_t* length)
+{
+    return Guard([&] {
+        if (!program || !length)
+            throw ArgumentException("sih_program_export_artifact: null argument");
+        const auto a = ExportHipVmArtifact(program->program);
+        *length = a.size();
+        if (buffer) {
+            if (capacity < a.size())
+                throw ArgumentException("sih_program_export_artifact: buffer too small");
+            std::copy(a.begin(), a.end(), static_cast<uint8_t*>(buffer));
+        }
+    });
+}
+
+int sih_program_import_artifact(const void* bytes, uint64_t length, int device, sih_program** out)
+{
+    return Guard([&] {
+        if (!bytes || !out)
+            throw ArgumentException("sih_program_import_artifact: null argument");
+        *out = nullptr;
+        auto p = std::make_unique<sih_program>();
+        const auto* b = static_cast<const uint8_t*>(bytes);
+        p->program = ImportHipVmArtifact(std::vector<uint8_t>(b, b + length));
+        p->executor = std::make_unique<HipVmExecutor>(p->program, device);
+        *out = p.release();
     });
 }
 

@@ -37,6 +37,15 @@ int sih_program_readback(sih_program* program, const char* slot, void* bytes, ui
 int sih_program_execute(sih_program* program, const char* entry);
 int sih_program_measure_us(sih_program* program, const char* entry, int repetitions, double* microseconds);
 int sih_program_dispatch_count(const sih_program* program, const char* entry, int* count);
+/* VmProgram XML of the program (the reference's schema, target "Hip"):
+ * with buffer NULL only *length (bytes, without a terminator) is set. */
+int sih_program_serialize(const sih_program* program, char* buffer, uint64_t capacity, uint64_t* length);
+/* A program from VmProgram XML, every operator re-adapted on the HIP
+ * target, with its executor on `device` (every slot zeroed). */
+int sih_program_create_from_xml(const char* xml, int device, sih_program** out);
+/* The program as a HIP VM artifact (ZIP: program.xml + hashed manifest). */
+int sih_program_export_artifact(const sih_program* program, void* buffer, uint64_t capacity, uint64_t* length);
+int sih_program_import_artifact(const void* bytes, uint64_t length, int device, sih_program** out);
 const char* sih_last_error(void);
 
 #ifdef __cplusplus

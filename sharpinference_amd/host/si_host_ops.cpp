@@ -809,14 +809,14 @@ void AddPhi4Prefill(HipVmProgram& p, const Phi4ProgramShape& s, const std::share
     const auto argmax = resolve(T, "transformer.argmax");
     const int64_t H = s.hidden, F = s.ffn, Q = s.hidden, KV = static_cast<int64_t>(s.kv_heads) * s.head_dim;
     const auto rw = VmAccess::ReadWrite;
-    p.AddSlot({"fused_embeddings", {F32, {s.prompt_rows, H}}, VmAccess::ReadOnly});
+    p.AddSlot({"fused_embeddings", {F32, {s.prompt_rows, H}}, VmAccess::ReadOnly, VmSlotScope::Local});
     for (const auto& [name, dims] : std::vector<std::pair<const char*, std::vector<int64_t>>>{
              {"batch_hidden", {B, H}}, {"batch_normalized", {B, H}}, {"batch_qkv", {B, Q + 2 * KV}},
              {"batch_query", {B, Q}}, {"batch_scores", {B, s.heads, s.context}},
              {"batch_probabilities", {B, s.heads, s.context}}, {"batch_attention", {B, H}},
              {"batch_projected", {B, H}}, {"batch_hidden_after_attention", {B, H}}, {"batch_gate_up", {B, 2 * F}},
              {"batch_activated", {B, F}}, {"batch_down", {B, H}}, {"batch_last", {H}}})
-        p.AddSlot({name, {F32, dims}, rw});
+        p.AddSlot({name, {F32, dims}, rw, VmSlotScope::Local});
 
     using P = InstructionParameter;
     const PrecisionRequirement fp32{F32, F32};
@@ -912,7 +912,11 @@ HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& s)
     const int64_t H = s.hidden, F = s.ffn, Q = s.hidden, KV = static_cast<int64_t>(s.kv_heads) * s.head_dim;
     const int64_t QKV = Q + 2 * KV;
     HipVmProgram p;
+    p.name = "phi4-hip-decode";
+    p.abi = s.cache_type == F16 ? "phi4.decode.fp16" : "phi4.decode.fp32";
+    p.state_schema = "phi4-kv-cache";
     const auto ro = VmAccess::ReadOnly, rw = VmAccess::ReadWrite;
+    const auto session = VmSlotScope::Session, local = VmSlotScope::Local;
     p.AddSlot({"token_embedding", WeightTensor(s.embed_format, s.vocab, H), ro});
     if (!s.tied)
         p.AddSlot({"output_weight", WeightTensor(s.head_format, s.vocab, H), ro});
@@ -927,16 +931,18 @@ HipVmProgram BuildPhi4DecodeProgram(const Phi4ProgramShape& s)
         p.AddSlot({"attn_output_weight_" + L, WeightTensor(s.weight_format, H, H), ro});
         p.AddSlot({"ffn_up_weight_" + L, WeightTensor(s.weight_format, 2 * F, H), ro});
         p.AddSlot({"ffn_down_weight_" + L, WeightTensor(s.weight_format, H, F), ro});
-        p.AddSlot({"key_cache_" + L, cache, rw});
-        p.AddSlot({"value_cache_" + L, cache, rw});
+        p.AddSlot({"key_cache_" + L, cache, rw, session});
+        p.AddSlot({"value_cache_" + L, cache, rw, session});
+        p.state.push_back({"key_cache_" + L, "key_cache_" + L});
+        p.state.push_back({"value_cache_" + L, "value_cache_" + L});
     }
-    p.AddSlot({"control", Vec(2, I32), ro});
+    p.AddSlot({"control", Vec(2, I32), ro, local});
     for (const auto& [name, n] : std::vector<std::pair<const char*, int64_t>>{
              {"hidden", H}, {"hidden_after_attention", H}, {"normalized", H}, {"qkv", QKV}, {"query", Q},
              {"attention", H}, {"projected", H}, {"gate_up", 2 * F}, {"activated", F}, {"down", H},
              {"logits", s.vocab}})
-        p.AddSlot({name, Vec(n), rw});
-    p.AddSlot({"next_token", Vec(1, I32), rw});
+        p.AddSlot({name, Vec(n), rw, local});
+    p.AddSlot({"next_token", Vec(1, I32), rw, local});
 
     using P = InstructionParameter;
     const PrecisionRequirement fp32{F32, F32};

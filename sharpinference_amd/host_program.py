@@ -54,6 +54,10 @@ def host_lib() -> ctypes.CDLL:
             "sih_program_execute": [vp, cp],
             "sih_program_measure_us": [vp, cp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)],
             "sih_program_dispatch_count": [vp, cp, ctypes.POINTER(ctypes.c_int)],
+            "sih_program_serialize": [vp, vp, u64, ctypes.POINTER(u64)],
+            "sih_program_create_from_xml": [cp, ctypes.c_int, ctypes.POINTER(vp)],
+            "sih_program_export_artifact": [vp, vp, u64, ctypes.POINTER(u64)],
+            "sih_program_import_artifact": [vp, u64, ctypes.c_int, ctypes.POINTER(vp)],
         }
         for name, args in sigs.items():
             fn = getattr(l, name)
@@ -74,19 +78,31 @@ class Phi4OpProgram:
     """One model's decode program, uploaded and ready to step."""
 
     def __init__(self, cfg: Phi4Config, weights: Phi4Weights, cache_fp16: bool = True, device: int = 0,
-                 prompt_rows: int = 0):
+                 prompt_rows: int = 0, xml: Optional[str] = None, artifact: Optional[bytes] = None,
+                 rope_frequencies: Optional[np.ndarray] = None):
+        """Builds the program from the configuration (BuildPhi4DecodeProgram),
+        or loads it from VmProgram XML or a HIP VM artifact of such a program
+        (then `rope_frequencies` fills that slot, which loading leaves zero)."""
         self.cfg = cfg
         self.cache_fp16 = cache_fp16
         self.prompt_rows = prompt_rows
         tied = weights.lm_head is weights.embed
-        shape = Phi4Shape(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.rotary_dim, cfg.ffn,
-                          cfg.vocab, cfg.capacity, cfg.weight_format, cfg.embed_format, cfg.head_format, int(tied),
-                          int(cache_fp16), cfg.rms_eps, cfg.rope_base, cfg.rope_scale, prompt_rows)
         h = ctypes.c_void_p()
-        _check(host_lib().sih_phi4_program_create(ctypes.byref(shape), device, ctypes.byref(h)))
+        if xml is not None:
+            _check(host_lib().sih_program_create_from_xml(xml.encode(), device, ctypes.byref(h)))
+        elif artifact is not None:
+            buf = ctypes.create_string_buffer(bytes(artifact), len(artifact))
+            _check(host_lib().sih_program_import_artifact(buf, len(artifact), device, ctypes.byref(h)))
+        else:
+            shape = Phi4Shape(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.rotary_dim, cfg.ffn,
+                              cfg.vocab, cfg.capacity, cfg.weight_format, cfg.embed_format, cfg.head_format,
+                              int(tied), int(cache_fp16), cfg.rms_eps, cfg.rope_base, cfg.rope_scale, prompt_rows)
+            _check(host_lib().sih_phi4_program_create(ctypes.byref(shape), device, ctypes.byref(h)))
         self._h = h
         try:
             up = self.upload
+            if rope_frequencies is not None:
+                up("rope_frequencies", np.ascontiguousarray(rope_frequencies, np.float32))
             up("token_embedding", weights.embed)
             if not tied:
                 up("output_weight", weights.lm_head)
@@ -170,6 +186,22 @@ class Phi4OpProgram:
             self.position += count
             token = int(self.readback("next_token", np.int32)[0])
         return token
+
+    def to_xml(self) -> str:
+        """The program as VmProgram XML (the reference's schema, target "Hip")."""
+        n = ctypes.c_uint64(0)
+        _check(host_lib().sih_program_serialize(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value)
+        _check(host_lib().sih_program_serialize(self._h, buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value].decode()
+
+    def to_artifact(self) -> bytes:
+        """The program as a HIP VM artifact (ZIP: program.xml + hashed manifest)."""
+        n = ctypes.c_uint64(0)
+        _check(host_lib().sih_program_export_artifact(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value)
+        _check(host_lib().sih_program_export_artifact(self._h, buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value]
 
     def read_logits(self) -> np.ndarray:
         return self.readback("logits", np.float32)

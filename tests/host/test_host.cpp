@@ -18,7 +18,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <functional>
+#include <sstream>
 #include <string>
 #include <typeinfo>
 #include <vector>
@@ -731,6 +733,151 @@ TEST(cpu, Phi4PrefillEntryFollowsTheReferenceDispatchOrder)
     auto bad = s;
     bad.prompt_rows = 65;                        // longer than the context
     ASSERT_THROWS(ArgumentException, BuildPhi4DecodeProgram(bad));
+}
+
+// Everything a program's execution depends on, in entry and dispatch order.
+std::string Fingerprint(const HipVmProgram& p)
+{
+    std::ostringstream o;
+    o << p.name << '|' << p.abi << '|' << p.state_schema << '|' << p.state_version << '\n';
+    for (const auto& s : p.state)
+        o << "state " << s.name << '=' << s.slot << '\n';
+    for (const auto& s : p.Slots()) {
+        o << "slot " << s.id << ' ' << static_cast<int>(s.scope) << ' ' << static_cast<int>(s.access) << ' '
+          << static_cast<int>(s.tensor.element_type) << ' ' << s.binding_key;
+        for (auto d : s.tensor.dimensions)
+            o << ',' << d;
+        o << '\n';
+    }
+    for (const auto& [entry, ds] : p.Entries())
+        for (const auto& d : ds) {
+            o << entry << ' ' << d.instruction->CollectionId() << ' ' << d.instruction->Name() << ' '
+              << d.recording.operation << ' ' << static_cast<int>(d.precision.minimum_arithmetic_type)
+              << static_cast<int>(d.resolved.accumulator_type);
+            auto ps = d.recording.parameters;
+            std::sort(ps.begin(), ps.end(), [](const auto& a, const auto& b) { return a.name < b.name; });
+            for (const auto& q : ps) {
+                o << " [" << q.name << ':' << static_cast<int>(q.kind) << ':' << q.value << ':' << q.source << '@'
+                  << q.byte_offset << ':' << static_cast<int>(q.access) << ':'
+                  << static_cast<int>(q.tensor.element_type);
+                for (auto x : q.tensor.dimensions)
+                    o << ',' << x;
+                o << ']';
+            }
+            o << '\n';
+        }
+    return o.str();
+}
+
+TEST(cpu, VmProgramXmlRoundTripsThePhi4Program)
+{
+    Phi4ProgramShape s;
+    s.layers = 2;
+    s.hidden = 1024;
+    s.heads = 8;
+    s.kv_heads = 2;
+    s.ffn = 2048;
+    s.vocab = 100;
+    s.context = 64;
+    s.prompt_rows = 20;
+    const auto p = BuildPhi4DecodeProgram(s);
+    const std::string xml = SerializeVmProgram(p);
+    ASSERT_TRUE(xml.rfind("<VmProgram name=\"phi4-hip-decode\" abi=\"phi4.decode.fp16\" target=\"Hip\">", 0) == 0);
+    // control's token and position words are parameters of their own, bound at byte offsets 0 and 4
+    ASSERT_TRUE(xml.find("<Argument parameter=\"position\" source=\"control\" byteOffset=\"4\" />") != std::string::npos);
+    ASSERT_TRUE(xml.find("<Port name=\"key_cache\" access=\"Write\" />") != std::string::npos);
+    const auto q = DeserializeVmProgram(xml);
+    ASSERT_TRUE(Fingerprint(q) == Fingerprint(p));
+    ASSERT_TRUE(SerializeVmProgram(q) == xml);
+    // dense weights, FP32 caches, no prefill entry
+    s.weight_format = s.embed_format = s.head_format = SI_HIP_F32;
+    s.tied = true;
+    s.cache_type = GraphElementType::Float32;
+    s.prompt_rows = 0;
+    const auto d = BuildPhi4DecodeProgram(s);
+    ASSERT_TRUE(Fingerprint(DeserializeVmProgram(SerializeVmProgram(d))) == Fingerprint(d));
+}
+
+TEST(cpu, VmProgramXmlReaderRejectsWhatTheReferenceRejects)
+{
+    const std::string good = SerializeVmProgram(MatVecProgram(SI_HIP_Q8_0, 3, 32));
+    DeserializeVmProgram(good);
+    const auto edit = [&](const std::string& from, const std::string& to) {
+        std::string x = good;
+        const size_t i = x.find(from);
+        if (i == std::string::npos)
+            throw Failure("fixture text not found: " + from);
+        return x.replace(i, from.size(), to);
+    };
+    const std::vector<std::string> bad{
+        "<!DOCTYPE VmProgram [<!ENTITY x \"y\">]>" + good,       // DTD processing is prohibited
+        edit("<Slots>", "<Slots>text"),                            // text content
+        edit("<Slots>", "<Slots><Extra />"),                      // unknown element
+        edit("<Slots>", "<Slots extra=\"1\">"),                   // unknown attribute
+        edit("target=\"Hip\"", "target=\"Direct3D12\""),         // another target
+        edit("scope=\"Global\"", "scope=\"global\""),             // enum names are exact
+        edit("elementType=\"Byte\"", "elementType=\"Int8\""),
+        edit("kind=\"Orchestration\"", "kind=\"Kernel\""),        // the HIP executor runs orchestrations
+        edit("<Dimension size=\"3\" />", "<Dimension size=\"0\" />"),
+        edit("<Slots>", "<Slots><Slot id=\"a\" scope=\"Global\" access=\"ReadOnly\" access=\"ReadOnly\" /></Slots><Slots>"),
+        edit("<State ", "<State xmlns:z=\"urn:z\" z:a=\"1\" "),   // namespaced attribute
+        edit(" />", " &bogus; />"),                               // undeclared entity
+        good.substr(0, good.size() - 3),                           // truncated
+        edit("5c2f7b1e-9a4d-4f0e-8e61-3b7f2d9c4a10", "5c2f7b1e-9a4d-4f0e-8e61-3b7f2d9c4a11"),   // unknown collection
+        std::string(64 + 2, '<'),
+    };
+    int i = 0;
+    for (const auto& x : bad) {
+        bool threw = false;
+        try {
+            DeserializeVmProgram(x);
+        } catch (const std::exception&) {
+            threw = true;
+        }
+        if (!threw)
+            throw Failure("malformed case " + std::to_string(i) + " was accepted");
+        i++;
+    }
+    // nesting beyond 64 levels
+    std::string deep = "<VmProgram name=\"a\" abi=\"b\" target=\"Hip\">";
+    for (int k = 0; k < 70; k++)
+        deep += "<Slots>";
+    ASSERT_THROWS(InvalidDataException, DeserializeVmProgram(deep));
+    // comments and processing instructions are ignored
+    DeserializeVmProgram("<?xml version=\"1.0\"?><!-- c -->" + good + "<!-- d -->");
+}
+
+TEST(cpu, HipArtifactRoundTripsAndDetectsCorruption)
+{
+    ASSERT_TRUE(Sha256Hex("", 0) == "E3B0C44298FC1C149AFBF4C8996FB92427AE41E4649B934CA495991B7852B855");
+    ASSERT_TRUE(Sha256Hex("abc", 3) == "BA7816BF8F01CFEA414140DE5DAE2223B00361A396177A9CB410FF61F20015AD");
+    const std::string m56 = "abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq";
+    ASSERT_TRUE(Sha256Hex(m56.data(), m56.size()) ==
+                "248D6A61D20638B8E5C026930C3E6039A33CE45964FF2167F6ECEDD419DB06C1");
+    Phi4ProgramShape s;
+    s.layers = 1;
+    s.hidden = 1024;
+    s.heads = 8;
+    s.kv_heads = 2;
+    s.ffn = 2048;
+    s.vocab = 64;
+    s.context = 32;
+    const auto p = BuildPhi4DecodeProgram(s);
+    const auto a = ExportHipVmArtifact(p);
+    ASSERT_TRUE(a.size() > 4 && a[0] == 'P' && a[1] == 'K');
+    ASSERT_TRUE(Fingerprint(ImportHipVmArtifact(a)) == Fingerprint(p));
+    // a flipped byte inside program.xml: the stored entry's CRC or the program hash rejects it
+    auto c = a;
+    c[200] ^= 0x20;
+    ASSERT_THROWS(InvalidDataException, ImportHipVmArtifact(c));
+    // the envelope hash covers the manifest
+    std::string t(a.begin(), a.end());
+    const size_t at = t.find("c-abi-launch");
+    ASSERT_TRUE(at != std::string::npos);
+    auto d = a;
+    d[at] = 'C';
+    ASSERT_THROWS(InvalidDataException, ImportHipVmArtifact(d));
+    ASSERT_THROWS(InvalidDataException, ImportHipVmArtifact(std::vector<uint8_t>(a.begin(), a.begin() + 40)));
 }
 
 TEST(cpu, ExecutorWithoutADeviceFailsLoudly)
