@@ -33,7 +33,9 @@ namespace {
 static __device__ __align__(256) float scratch[ATTENTION_SCRATCH_FLOATS];
 
 constexpr int HEAD_DIM = 128;
-constexpr int CHUNK = 64;          // cache positions per attention workgroup
+constexpr int CHUNK = 64;          // cache positions per workgroup of the staged partial kernel (workspace layout)
+constexpr int FCHUNK = 128;        // cache positions per workgroup of the register-resident chunk kernel
+constexpr int FPPL = FCHUNK / 16;  // positions per lane of the chunk kernel
 constexpr int ATT_THREADS = 256;
 constexpr int PART = HEAD_DIM + 2; // per head and chunk: max, sum, 128 weighted values
 
@@ -211,7 +213,7 @@ __device__ __forceinline__ void merge_combine_batch(const CombineBatch& b, int b
 __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ workspace,
                                                                 const int32_t* __restrict__ position,
                                                                 float* __restrict__ out, int capacity,
-                                                                int max_chunks)
+                                                                int max_chunks, int chunk_size)
 {
     const int h = blockIdx.x, t = threadIdx.x;
     const int d = t & (HEAD_DIM - 1), half = t >> 7;
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
             out[h * HEAD_DIM + t] = __int_as_float(0x7fc00000);   // position outside the cache
         return;
     }
-    const int chunks = P / CHUNK + 1;
+    const int chunks = P / chunk_size + 1;
     float m = -INFINITY, l = 0.0f, acc = 0.0f;
     if (half < chunks)
         merge_combine_batch(b, half, chunks, m, l, acc);
@@ -496,10 +498,10 @@ __device__ __forceinline__ void rotate8(float* own, const float* partner, const 
     }
 }
 
-// One workgroup = one KV head x one chunk of 64 cache positions, the same
+// One workgroup = one KV head x one chunk of 128 cache positions, the same
 // function as attention_partial_kernel with every intermediate kept in
 // registers.  Thread (wave w, lane l) takes the 8-value slice dg = l % 16
-// of positions w * 16 + l / 16 + 4 j (j < 4) for both the scores and the
+// of positions 32 w + l / 16 + 4 j (j < 8) for both the scores and the
 // values, so its softmax weights never leave its registers: each wave keeps
 // its own running maximum and sum, sums across its four rows with lane
 // swaps, and the four waves merge (with rescaling) through LDS at one
@@ -512,13 +514,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
                                                                       const int32_t* __restrict__ position,
                                                                       __half* k_cache, __half* v_cache,
                                                                       float* __restrict__ workspace, int capacity,
-                                                                      int rotary)
+                                                                      int rotary, int max_chunks)
 {
+    // max_chunks: the workspace's partials per head (its 64-position layout);
+    // this grid has ceil(capacity / 128) chunks
     const int g = blockIdx.x;                 // KV head
-    const int kv_heads = gridDim.x, max_chunks = gridDim.y;
+    const int kv_heads = gridDim.x;
     const int heads = GROUP * kv_heads;
     const int chunk = blockIdx.y;
-    const int start = chunk * CHUNK;
+    const int start = chunk * FCHUNK;
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int dg = lane & 15, row = lane >> 4;
@@ -551,19 +555,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
     // only on the valid path) behind the position's round trip.
     const int P = *position;                  // index of the new token
     const bool valid = P >= 0 && P < capacity && start <= P;
-    const int count = min(CHUNK, P + 1 - start);
-    const int newp = valid ? P - start : CHUNK;   // the new token's slot in this chunk (< CHUNK when owned)
+    const int count = min(FCHUNK, P + 1 - start);
+    const int newp = valid ? P - start : FCHUNK;   // the new token's slot in this chunk (< FCHUNK when owned)
 
     // 2. K and V rows of this thread's positions (rows clamped into the
     //    cache; positions past the count are masked below)
     __half* kc = k_cache + static_cast<int64_t>(g) * capacity * HEAD_DIM;
     __half* vc = v_cache + static_cast<int64_t>(g) * capacity * HEAD_DIM;
     //    (an invalid chunk leaves them unloaded: its results are not stored)
-    uint4 kr[4], vr[4];
+    uint4 kr[FPPL], vr[FPPL];
     if (valid) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int64_t r = min(start + wave * 16 + row + 4 * j, capacity - 1);
+        for (int j = 0; j < FPPL; j++) {
+            const int64_t r = min(start + wave * (FCHUNK / 4) + row + 4 * j, capacity - 1);
             kr[j] = *reinterpret_cast<const uint4*>(kc + r * HEAD_DIM + 8 * dg);
             vr[j] = *reinterpret_cast<const uint4*>(vc + r * HEAD_DIM + 8 * dg);
         }
@@ -586,10 +590,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
     // exponentials with the hardware exp2 (__expf): both within a few ulp
     // of the exact forms, far inside the attention tolerance
     const float rscale = 1.0f / sqrtf(static_cast<float>(HEAD_DIM));
-    float sc[GROUP][4];
+    float sc[GROUP][FPPL];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int p = wave * 16 + row + 4 * j;
+    for (int j = 0; j < FPPL; j++) {
+        const int p = wave * (FCHUNK / 4) + row + 4 * j;
         float k8[8];
         if (p == newp) {
 #pragma unroll
@@ -613,12 +617,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
     float m[GROUP], l[GROUP], acc[GROUP][8];
 #pragma unroll
     for (int h = 0; h < GROUP; h++) {
-        float mh = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+        float mh = sc[h][0];
+#pragma unroll
+        for (int j = 1; j < FPPL; j++)
+            mh = fmaxf(mh, sc[h][j]);
         mh = rows_max(mh);
         m[h] = mh;
         float lh = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < FPPL; j++) {
             const float e = sc[h][j] == -INFINITY ? 0.0f : __expf(sc[h][j] - mh);
             sc[h][j] = e;
             lh += e;
@@ -629,8 +636,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
             acc[h][e] = 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int p = wave * 16 + row + 4 * j;
+    for (int j = 0; j < FPPL; j++) {
+        const int p = wave * (FCHUNK / 4) + row + 4 * j;
         float v8[8];
         if (p == newp) {
 #pragma unroll
@@ -647,8 +654,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
     }
 
     // the owner's 16 lanes append the new row (positions of a lane are
-    // wave * 16 + row + 4 j, so the new one is in row newp % 4 of wave newp / 16)
-    if (newp < CHUNK && (newp >> 4) == wave && (newp & 3) == row) {   // newp < CHUNK only when valid
+    // wave * 32 + row + 4 j, so the new one is in row newp % 4 of wave newp / 32)
+    if (newp < FCHUNK && newp / (FCHUNK / 4) == wave && (newp & 3) == row) {   // newp < FCHUNK only when valid
         __half kh[8], vh[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -869,12 +876,13 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
     const int group = a.heads / a.kv_heads;
     const dim3 grid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>(a.max_chunks));
     if (a.rotary_dim % 16 == 0) {
+        const dim3 fgrid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>((a.capacity + FCHUNK - 1) / FCHUNK));
         // slices of 8 values and their rotary partners are whole
         switch (group) {
 #define SI_CHUNK(G)                                                                                               \
     case G:                                                                                                       \
-        hipLaunchKernelGGL((attention_chunk_kernel<G>), grid, dim3(ATT_THREADS), 0, s, a.qkv, a.position,         \
-                           a.k_cache, a.v_cache, a.workspace, a.capacity, a.rotary_dim);                         \
+        hipLaunchKernelGGL((attention_chunk_kernel<G>), fgrid, dim3(ATT_THREADS), 0, s, a.qkv, a.position,        \
+                           a.k_cache, a.v_cache, a.workspace, a.capacity, a.rotary_dim, a.max_chunks);           \
         break;
         SI_CHUNK(1)
         SI_CHUNK(2)
@@ -887,7 +895,7 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
         if (e != hipSuccess)
             return e;
         hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a.workspace,
-                       a.position, a.out, a.capacity, a.max_chunks);
+                       a.position, a.out, a.capacity, a.max_chunks, FCHUNK);
         return hipGetLastError();
     }
     switch (group) {
@@ -901,7 +909,7 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
     if (e != hipSuccess)
         return e;
     hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a.workspace,
-                       a.position, a.out, a.capacity, a.max_chunks);
+                       a.position, a.out, a.capacity, a.max_chunks, CHUNK);
     return hipGetLastError();
 }
 
