@@ -318,6 +318,7 @@ def bench_read_ceiling(hip, shapes, copies, dev_w, host_w):
     """Plain-read ceiling: the same bytes, read once by a streaming kernel
     (si_hip_checksum), in the same plan structure (one launch per weight
     tensor, the step's four in order, rotating over the copies)."""
+    from sharpinference_amd import native
     acc = hip.alloc(4 * native.CHECKSUM_PARTS)
     read_plan = hip.record(lambda: [hip.checksum(dev_w[c][k].ptr, host_w[k].nbytes, acc.ptr)
                                     for c in range(copies) for k in range(len(shapes))])
@@ -482,15 +483,31 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
         # the same model as the reference's program form: 292 separate
         # dispatches through the C++ host executor
         from sharpinference_amd import host_program
-        prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True)
+        prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True, prompt_rows=context)
         for l in range(cfg.layers):
             prog.load_kv(l, *kv)
         prog.forward_token(1, context)
         op_us = sorted(prog.measure_us(8) for _ in range(5))[2]
+        # prefill_fused_16: one batch of 16 prompt rows; attention cost grows
+        # linearly with the batch's start, so the batch starting halfway
+        # through a `context`-token prompt prices the prompt's average batch
+        prog.upload("fused_embeddings", np.random.default_rng(9).standard_normal(
+            (context, cfg.hidden)).astype(np.float32) * 0.05)
+        prefill = {}
+        for start in (0, context // 2 - 8, context - 16):
+            prog.upload("control", np.array([start, 16], np.int32))
+            prefill[start] = sorted(prog.measure_us(4, "prefill_fused_16") for _ in range(3))[1]
+        mid = prefill[context // 2 - 8]
         op_program = {"us_per_token": r1(op_us), "tok_s": r1(1e6 / op_us), "dispatches": prog.dispatch_count(),
-                      "form": "transformer.* / quant.mat-vec instructions, one launch each (two for attention)"}
+                      "form": "transformer.* / quant.mat-vec instructions, one launch each (two for attention)",
+                      "prefill_fused_16": {
+                          "us_per_batch_by_start": {str(k): r1(v) for k, v in prefill.items()},
+                          "prompt_tok_s": r1(16e6 / mid), "dispatches": prog.dispatch_count("prefill_fused_16"),
+                          "workload": f"16 prompt rows per batch; rate at the middle batch of a {context}-token "
+                                      "prompt (the prompt average: attention is linear in the start)"}}
         prog.close()
-        log(f"decode op-by-op program: {op_us:.1f} us/token ({1e6 / op_us:.0f} tok/s)")
+        log(f"decode op-by-op program: {op_us:.1f} us/token ({1e6 / op_us:.0f} tok/s); prefill_fused_16 "
+            + ", ".join(f"start {k}: {v:.0f} us" for k, v in prefill.items()) + f" ({16e6 / mid:.0f} prompt tok/s)")
     out = {"workload": "Phi-4-mini decode step, 32 layers, Q4_K layers, Q8_0 embedding/head 200064x3072, "
                        f"fp16 KV cache with {context} tokens, batch 1",
            "us_per_token": r1(us), "tok_s": r1(1e6 / us),
