@@ -460,7 +460,10 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
         sess.load_kv(l, *kv)
     log(f"decode: model on device in {time.time() - t0:.1f} s")
     sess.set_control(1, context)
-    sess.plan.launch()
+    if eager:   # warm-up without a plan replay: kernel-trace profiles of this run contain no graph launch
+        hip.phi4_decode(sess.model)
+    else:
+        sess.plan.launch()
     hip.sync()
     us = sorted(sess.plan.measure_us(16) for _ in range(5))[2] if replay_timing else float("nan")
     step_bytes = cfg.weight_bytes_per_token() + cfg.kv_bytes(context + 1)
@@ -547,7 +550,10 @@ def bench_rwkv_decode(hip, tokens: int = 64, cpu: bool = True, replay_timing: bo
     sess = rwkv7.Rwkv7DecodeSession(hip, cfg, weights, state)
     log(f"rwkv7: model on device in {time.time() - t0:.1f} s")
     sess.control.upload(np.array([1], np.int32))
-    sess.plan.launch()
+    if eager:
+        hip.rwkv7_decode(sess.model)
+    else:
+        sess.plan.launch()
     hip.sync()
     us = sorted(sess.plan.measure_us(16) for _ in range(5))[2] if replay_timing else float("nan")
     step_bytes = cfg.weight_bytes_per_token()

@@ -16,11 +16,20 @@
 //     each W row exactly as the CPU decoder does (FP32, one rounding per
 //     operation), round them to bf16 and write a double-buffered LDS tile;
 //     the raw bytes are loaded a step ahead;
+//   * the workgroup's X tile of the step is loaded with coalesced 16-byte
+//     loads (8 lanes per 128-byte token row, a step ahead; X is small and
+//     stays in L2) into a swizzled LDS tile;
 //   * each wave multiplies its MW token rows by the tile with
 //     v_mfma_f32_32x32x16_bf16 (MW/32 x NT accumulator tiles of 32 x 32
-//     FP32), its X fragments loaded a step ahead straight from global memory
-//     (X is small and stays in L2 / the Infinity Cache);
+//     FP32), both fragments read from LDS;
 //   * the tile is the largest whose grid still covers the 256 CUs.
+//
+// Loading the fragments straight from global memory instead (each load
+// instruction then spans 32 token or W rows, 32 cache lines) measured about
+// half the speed of this form: the address / tag work of such loads, not
+// the matrix cores or the decode, bounds it.  In this form the LDS fragment
+// reads and the tile stores take most of the time; the matrix-core work is
+// hidden under them.
 //
 // MFMA fragment layout (32x32x16 bf16): lane l holds A[l % 32][8*(l/32)+e]
 // and B[8*(l/32)+e][l % 32] for e = 0..7; accumulator register r of lane l
