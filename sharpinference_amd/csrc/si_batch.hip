@@ -124,8 +124,13 @@ __global__ __launch_bounds__(THREADS) void batch_gather_rows_kernel(const float*
         out[e] = table[src * width + (e - static_cast<int64_t>(row) * width)];
 }
 
-// One workgroup per live row (the decode form's operation order).
-template <bool RESIDUAL>
+// One workgroup per live row (the decode form's operation order).  With
+// PER > 0 (width <= PER * NORM_THREADS) a thread requests its PER values,
+// their residuals and norm weights together and keeps them in registers
+// (one memory round trip before the reduction instead of one per value and
+// a re-read of the stored sum); PER = 0 is the loop form for wider rows.
+// Both forms do the same operations in the same order.
+template <bool RESIDUAL, int PER>
 __global__ __launch_bounds__(NORM_THREADS) void batch_rms_norm_kernel(const float* __restrict__ hidden,
                                                                       const float* __restrict__ residual,
                                                                       const float* __restrict__ weight,
@@ -139,6 +144,35 @@ __global__ __launch_bounds__(NORM_THREADS) void batch_rms_norm_kernel(const floa
         return;   // the whole workgroup, before any barrier
     const int64_t base = static_cast<int64_t>(row) * width;
     float ss = 0.0f;
+    if constexpr (PER > 0) {
+        float v[PER], wt[PER];
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int j = min(static_cast<int>(threadIdx.x) + k * NORM_THREADS, width - 1);   // clamped in the row
+            v[k] = hidden[base + j];
+            if (RESIDUAL)
+                v[k] = v[k] + residual[base + j];
+            wt[k] = weight[j];
+        }
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int j = static_cast<int>(threadIdx.x) + k * NORM_THREADS;
+            if (j < width) {
+                if (RESIDUAL)
+                    updated[base + j] = v[k];
+                ss = fmaf(v[k], v[k], ss);
+            }
+        }
+        const float total = block_sum<NORM_THREADS>(ss, red);
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(width) + eps);
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int j = static_cast<int>(threadIdx.x) + k * NORM_THREADS;
+            if (j < width)
+                out[base + j] = v[k] * scale * wt[k];
+        }
+        return;
+    }
     for (int j = threadIdx.x; j < width; j += NORM_THREADS) {
         float v = hidden[base + j];
         if (RESIDUAL) {
@@ -389,81 +423,105 @@ __global__ __launch_bounds__(THREADS) void batch_select_last_kernel(const float*
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+typedef uint32_t u32_a2 __attribute__((aligned(2)));   // 4 bytes at a 2-byte aligned address
+
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) { return *reinterpret_cast<const u32_a2*>(p); }
 
-// Elements 8g .. 8g + 7 of 32-column block `blk` of a row, dequantised as
-// the CpuVm decode does (one rounding per operation).
+// Raw words of elements 8g .. 8g + 7 of one 32-column block of a row (plain
+// word loads; every bit extraction happens in decode8, so a pass can issue
+// the loads of all its blocks before it decodes the first):
+//   F32: 8 floats; F16: 8 halves (4 words); Q8_0 {fp16 d; int8 q[32]}: d and
+//   q[8g..8g+7]; Q4_0 {fp16 d; u8 qs[16]}: d and qs[8 (g % 2) ..] (elements
+//   0..15 are the low nibbles, 16..31 the high ones); Q4_K: the super-block's
+//   16-byte header (d, dmin, 12 scale bytes) and the 8 quant bytes of the
+//   sub-block's chunk.
 template <int FMT>
-__device__ __forceinline__ void decode8(const uint8_t* row, int blk, int g, float* w);
+struct Raw8 {
+    uint32_t w[FMT == FMT_F32 ? 8 : FMT == FMT_Q4_K ? 6 : 4];
+};
 
-template <>
-__device__ __forceinline__ void decode8<FMT_F32>(const uint8_t* row, int blk, int g, float* w)
+template <int FMT>
+__device__ __forceinline__ Raw8<FMT> load_raw8(const uint8_t* row, int blk, int g)
 {
-    load8(reinterpret_cast<const float*>(row) + 32 * blk + 8 * g, w);
-}
-
-template <>
-__device__ __forceinline__ void decode8<FMT_F16>(const uint8_t* row, int blk, int g, float* w)
-{
-    load8(reinterpret_cast<const __half*>(row) + 32 * blk + 8 * g, w);
-}
-
-template <>
-__device__ __forceinline__ void decode8<FMT_Q8_0>(const uint8_t* row, int blk, int g, float* w)
-{
-    const uint8_t* b = row + 34 * static_cast<int64_t>(blk);
-    const float d = half_bits(ld_u16(b));
-    const uint8_t* q = b + 2 + 8 * g;   // 2-byte aligned
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t two = ld_u16(q + 2 * i);
-        w[2 * i] = d * static_cast<float>(static_cast<int8_t>(two & 0xffu));
-        w[2 * i + 1] = d * static_cast<float>(static_cast<int8_t>(two >> 8));
-    }
-}
-
-template <>
-__device__ __forceinline__ void decode8<FMT_Q4_0>(const uint8_t* row, int blk, int g, float* w)
-{
-    const uint8_t* b = row + 18 * static_cast<int64_t>(blk);
-    const float d = half_bits(ld_u16(b));
-    const uint8_t* q = b + 2 + 8 * (g & 1);   // elements 0..15: low nibbles, 16..31: high nibbles
-    const int sh = g < 2 ? 0 : 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t two = ld_u16(q + 2 * i);
-        w[2 * i] = d * static_cast<float>(static_cast<int>((two >> sh) & 15u) - 8);
-        w[2 * i + 1] = d * static_cast<float>(static_cast<int>((two >> (8 + sh)) & 15u) - 8);
-    }
-}
-
-template <>
-__device__ __forceinline__ void decode8<FMT_Q4_K>(const uint8_t* row, int blk, int g, float* w)
-{
-    const uint8_t* sb = row + 144 * static_cast<int64_t>(blk >> 3);
-    const int j = blk & 7;   // sub-block: chunk j / 2, low nibbles for even j
-    const uint4 h = *reinterpret_cast<const uint4*>(sb);
-    const uint32_t sw[3] = {h.y, h.z, h.w};
-    auto sbyte = [&](int i) { return static_cast<int>((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
-    int sc, m;
-    if (j < 4) {
-        sc = sbyte(j) & 63;
-        m = sbyte(j + 4) & 63;
+    Raw8<FMT> r;
+    if constexpr (FMT == FMT_F32) {
+        const uint4* p = reinterpret_cast<const uint4*>(row + 128 * static_cast<int64_t>(blk) + 32 * g);
+        const uint4 a = p[0], b = p[1];
+        r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+        r.w[4] = b.x; r.w[5] = b.y; r.w[6] = b.z; r.w[7] = b.w;
+    } else if constexpr (FMT == FMT_F16) {
+        const uint4 a = *reinterpret_cast<const uint4*>(row + 64 * static_cast<int64_t>(blk) + 16 * g);
+        r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+    } else if constexpr (FMT == FMT_Q8_0) {
+        const uint8_t* b = row + 34 * static_cast<int64_t>(blk);
+        r.w[0] = ld_u16(b);
+        r.w[1] = ld_u32_a2(b + 2 + 8 * g);
+        r.w[2] = ld_u32_a2(b + 6 + 8 * g);
+    } else if constexpr (FMT == FMT_Q4_0) {
+        const uint8_t* b = row + 18 * static_cast<int64_t>(blk);
+        r.w[0] = ld_u16(b);
+        r.w[1] = ld_u32_a2(b + 2 + 8 * (g & 1));
+        r.w[2] = ld_u32_a2(b + 6 + 8 * (g & 1));
     } else {
-        sc = (sbyte(j + 4) & 15) | ((sbyte(j - 4) >> 6) << 4);
-        m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+        const uint8_t* sb = row + 144 * static_cast<int64_t>(blk >> 3);
+        const uint4 h = *reinterpret_cast<const uint4*>(sb);
+        const uint2 q = *reinterpret_cast<const uint2*>(sb + 16 + 32 * ((blk & 7) >> 1) + 8 * g);
+        r.w[0] = h.x; r.w[1] = h.y; r.w[2] = h.z; r.w[3] = h.w;
+        r.w[4] = q.x; r.w[5] = q.y;
     }
-    const float d1 = __fmul_rn(half_bits(h.x), static_cast<float>(sc));
-    const float m1 = __fmul_rn(half_bits(h.x >> 16), static_cast<float>(m));
-    const uint2 q = *reinterpret_cast<const uint2*>(sb + 16 + 32 * (j >> 1) + 8 * g);
-    const int sh = (j & 1) * 4;
+    return r;
+}
+
+// The 8 values dequantised as the CpuVm decode does (one rounding per
+// operation).
+template <int FMT>
+__device__ __forceinline__ void decode8(const Raw8<FMT>& r, int blk, int g, float* w)
+{
+    if constexpr (FMT == FMT_F32) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const uint32_t word = i < 4 ? q.x : q.y;
-        const float n = static_cast<float>((word >> (8 * (i & 3) + sh)) & 15u);
-        w[i] = __fsub_rn(__fmul_rn(d1, n), m1);
+        for (int i = 0; i < 8; i++)
+            w[i] = __uint_as_float(r.w[i]);
+    } else if constexpr (FMT == FMT_F16) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            w[2 * k] = half_bits(r.w[k]);
+            w[2 * k + 1] = half_bits(r.w[k] >> 16);
+        }
+    } else if constexpr (FMT == FMT_Q8_0) {
+        const float d = half_bits(r.w[0]);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            w[i] = d * static_cast<float>(static_cast<int8_t>((r.w[1 + i / 4] >> (8 * (i & 3))) & 0xffu));
+    } else if constexpr (FMT == FMT_Q4_0) {
+        const float d = half_bits(r.w[0]);
+        const int sh = g < 2 ? 0 : 4;   // elements 0..15: low nibbles, 16..31: high nibbles
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            w[i] = d * static_cast<float>(static_cast<int>((r.w[1 + i / 4] >> (8 * (i & 3) + sh)) & 15u) - 8);
+    } else {
+        const int j = blk & 7;   // sub-block: chunk j / 2, low nibbles for even j
+        auto sbyte = [&](int i) { return static_cast<int>((r.w[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu); };
+        int sc, m;
+        if (j < 4) {
+            sc = sbyte(j) & 63;
+            m = sbyte(j + 4) & 63;
+        } else {
+            sc = (sbyte(j + 4) & 15) | ((sbyte(j - 4) >> 6) << 4);
+            m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+        }
+        const float d1 = __fmul_rn(half_bits(r.w[0]), static_cast<float>(sc));
+        const float m1 = __fmul_rn(half_bits(r.w[0] >> 16), static_cast<float>(m));
+        const int sh = (j & 1) * 4;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float n = static_cast<float>((r.w[4 + i / 4] >> (8 * (i & 3) + sh)) & 15u);
+            w[i] = __fsub_rn(__fmul_rn(d1, n), m1);
+        }
     }
 }
+
+constexpr int MV_PASS = 8;   // blocks per wave whose loads are issued together
 
 // One workgroup = 16 output rows x 16 batch rows, its four waves splitting
 // the 32-column blocks (wave w takes blocks w, w + 4, ...) and adding their
@@ -472,7 +530,12 @@ __device__ __forceinline__ void decode8<FMT_Q4_K>(const uint8_t* row, int blk, i
 // columns of batch row t0 + r; eight v_mfma_f32_16x16x4_f32 take k = 8g + s
 // (s < 8) from lane group g: the sum over k is the row's dot product in any
 // order.  D[i][j] of the tile (batch row t0 + i, output row o0 + j) is held
-// by lane j + 16 (i / 4), element i % 4.
+// by lane j + 16 (i / 4), element i % 4.  A wave works in passes of MV_PASS
+// blocks: the W words and X values of all of a pass's blocks are requested
+// before the first is decoded (block indexes past the row are clamped and
+// their products skipped), so a pass costs one memory round trip, not one
+// per block; a grid holds only one to four workgroups per CU, too few waves
+// to hide the round trips otherwise.
 template <int FMT>
 __global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __restrict__ W,
                                                                const float* __restrict__ X, float* __restrict__ Y,
@@ -491,13 +554,26 @@ __global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __
     const float* xrow = X + static_cast<int64_t>(t0 + (tok ? r : 0)) * cols + 8 * g;
     const int nb = cols / 32;
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int b = wave; b < nb; b += 4) {
-        float w[8], x[8];
-        decode8<FMT>(wrow, b, g, w);
-        load8(xrow + 32 * b, x);
+    for (int b0 = wave; b0 < nb; b0 += 4 * MV_PASS) {
+        Raw8<FMT> raw[MV_PASS];
+        float x[MV_PASS][8];
 #pragma unroll
-        for (int s = 0; s < 8; s++)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(tok ? x[s] : 0.0f, w[s], acc, 0, 0, 0);
+        for (int u = 0; u < MV_PASS; u++) {
+            const int b = min(b0 + 4 * u, nb - 1);
+            raw[u] = load_raw8<FMT>(wrow, b, g);
+            load8(xrow + 32 * b, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < MV_PASS; u++) {
+            const int b = b0 + 4 * u;
+            if (b < nb) {   // uniform across the wave
+                float w[8];
+                decode8<FMT>(raw[u], b, g, w);
+#pragma unroll
+                for (int s = 0; s < 8; s++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(tok ? x[u][s] : 0.0f, w[s], acc, 0, 0, 0);
+            }
+        }
     }
     red[wave][lane] = acc;
     __syncthreads();
@@ -532,12 +608,25 @@ hipError_t launch_batch_gather_rows(const float* table, int64_t table_rows, int 
 hipError_t launch_batch_rms_norm(const float* hidden, const float* residual, const float* weight, float* updated,
                                  float* out, int batch, int width, float eps, const int32_t* control, hipStream_t s)
 {
-    if (residual)
-        hipLaunchKernelGGL((batch_rms_norm_kernel<true>), dim3(static_cast<unsigned>(batch)), dim3(NORM_THREADS), 0, s,
-                           hidden, residual, weight, updated, out, width, eps, control);
+    auto go = [&](auto per) {
+        constexpr int PER = decltype(per)::value;
+        if (residual)
+            hipLaunchKernelGGL((batch_rms_norm_kernel<true, PER>), dim3(static_cast<unsigned>(batch)),
+                               dim3(NORM_THREADS), 0, s, hidden, residual, weight, updated, out, width, eps, control);
+        else
+            hipLaunchKernelGGL((batch_rms_norm_kernel<false, PER>), dim3(static_cast<unsigned>(batch)),
+                               dim3(NORM_THREADS), 0, s, hidden, nullptr, weight, nullptr, out, width, eps, control);
+    };
+    if (width <= NORM_THREADS)
+        go(std::integral_constant<int, 1>{});
+    else if (width <= 2 * NORM_THREADS)
+        go(std::integral_constant<int, 2>{});
+    else if (width <= 4 * NORM_THREADS)
+        go(std::integral_constant<int, 4>{});
+    else if (width <= 8 * NORM_THREADS)
+        go(std::integral_constant<int, 8>{});
     else
-        hipLaunchKernelGGL((batch_rms_norm_kernel<false>), dim3(static_cast<unsigned>(batch)), dim3(NORM_THREADS), 0,
-                           s, hidden, nullptr, weight, nullptr, out, width, eps, control);
+        go(std::integral_constant<int, 0>{});
     return hipGetLastError();
 }
 

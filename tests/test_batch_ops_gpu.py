@@ -40,6 +40,37 @@ def _filled(hip, shape):
     return hip.to_device(np.full(shape, SENTINEL, np.float32))
 
 
+def _check_norms(hip, ctl, live, B, H, rng):
+    x = rng.standard_normal((B, H)).astype(np.float32)
+    r = rng.standard_normal((B, H)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    dx, dr, dw = hip.to_device(x), hip.to_device(r), hip.to_device(w)
+    do, du = _filled(hip, (B, H)), _filled(hip, (B, H))
+    hip.batch_rms_norm(dx.ptr, dw.ptr, ctl.ptr, do.ptr, B, H, 1e-5)
+    got = do.readback(np.float32).reshape(B, H)
+    x64 = x.astype(np.float64)
+    for i in range(live):
+        _close(got[i], x64[i] / np.sqrt(np.mean(x64[i] ** 2) + 1e-5) * w, 1e-6, f"rms-norm width {H} row {i}")
+    assert np.all(got[live:] == SENTINEL)
+    hip.batch_residual_rms_norm(dx.ptr, dr.ptr, dw.ptr, ctl.ptr, du.ptr, do.ptr, B, H, 1e-5)
+    upd, got = du.readback(np.float32).reshape(B, H), do.readback(np.float32).reshape(B, H)
+    assert np.array_equal(upd[:live], (x + r)[:live]) and np.all(upd[live:] == SENTINEL)
+    u64 = (x + r).astype(np.float64)
+    for i in range(live):
+        _close(got[i], u64[i] / np.sqrt(np.mean(u64[i] ** 2) + 1e-5) * w, 1e-6, f"residual width {H} row {i}")
+    assert np.all(got[live:] == SENTINEL)
+
+
+@pytest.mark.parametrize("H", [1, 1024, 1500, 4097, 8192, 9000])
+def test_rms_norm_widths(hip, H):
+    """Every register form of the batched norms (1, 2, 4 and 8 values per
+    thread) and the loop form past 8192, at widths that leave a partial row
+    of threads."""
+    B = 5
+    rng = np.random.default_rng(H)
+    _check_norms(hip, _control(hip, 0, 4), 4, B, H, rng)
+
+
 @pytest.mark.parametrize("start,valid", [(0, 16), (5, 7), (3, 0)])
 def test_row_operators(hip, start, valid):
     B, H = 16, 3072
@@ -74,6 +105,8 @@ def test_row_operators(hip, start, valid):
     for i in range(live):
         _close(got[i], u64[i] / np.sqrt(np.mean(u64[i] ** 2) + 1e-5) * w, 1e-6, f"residual row {i}")
     assert np.all(got[live:] == SENTINEL)
+
+    _check_norms(hip, ctl, live, B, 700, rng)   # one value per thread, a partial row of threads
 
     # swiglu over [gate | up] rows
     F = 8192
