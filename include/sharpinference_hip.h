@@ -186,7 +186,7 @@ int si_hip_gemv_fused(si_hip_context* ctx, int format, const void* w, const floa
 
 /* One product of si_hip_gemv_batch: y = output(W . input_xform(x)). */
 typedef struct si_hip_gemv_op {
-    int32_t format;              /* SI_HIP_Q8_0 / Q4_0 / Q4_K                                  */
+    int32_t format;              /* SI_HIP_Q8_0 / Q4_0 / Q4_K / F16 / F32                      */
     int32_t input_xform;         /* si_hip_xform                                               */
     int32_t output;              /* si_hip_output                                              */
     int32_t reserved;            /* 0                                                          */
