@@ -280,10 +280,12 @@ def test_small_dense_phi4_decode_steps_match_oracle(hip, fmt):
 def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
     """The full decode workload: 32 layers, Phi-4-mini shapes, Q4_K layers, Q8_0
     embedding and head (200064 x 3072), fp16 KV cache with 2048 tokens of
-    N(0, 1) context, one new token."""
+    N(0, 1) context, then three consecutive tokens (positions 2048..2050,
+    each step attending to the rows the previous ones appended; the last
+    token near the end of the vocabulary)."""
     cfg = phi4.Phi4Config()
     weights = phi4.synth_weights(cfg, seed=31)
     kv = phi4.synth_kv(cfg, length=2048, seed=32)
-    results, _, _ = _run_steps(hip, cfg, weights, kv, [(4242, 2048)])
-    g, gl, o, ol = results[0]
-    _check_logits(g, gl, o, ol, "phi4-mini step")
+    results, _, _ = _run_steps(hip, cfg, weights, kv, [(4242, 2048), (17, 2049), (200000, 2050)])
+    for i, (g, gl, o, ol) in enumerate(results):
+        _check_logits(g, gl, o, ol, f"phi4-mini step {i}")

@@ -109,13 +109,14 @@ def test_phi4_mini_program_at_2048_tokens_matches_oracle(hip):
             prog.load_kv(l, k, v)
             ref.k[l][...] = k
             ref.v[l][...] = v
-        g = prog.forward_token(4242, 2048)
-        o, ol = ref.step(4242, 2048)
-        _gate(prog.read_logits(), ol, "phi4-mini program")
-        top2 = np.sort(ol)[-2:]
-        if top2[1] - top2[0] > 1e-3 * max(1.0, abs(top2[1])):
-            assert g == o
-        print(f"op-by-op program: {prog.measure_us(4):.1f} us per token (position 2049)")
+        for token, pos in ((4242, 2048), (17, 2049)):   # the second step attends to the row the first appended
+            g = prog.forward_token(token, pos)
+            o, ol = ref.step(token, pos)
+            _gate(prog.read_logits(), ol, f"phi4-mini program at position {pos}")
+            top2 = np.sort(ol)[-2:]
+            if top2[1] - top2[0] > 1e-3 * max(1.0, abs(top2[1])):
+                assert g == o
+        print(f"op-by-op program: {prog.measure_us(4):.1f} us per token (position 2050)")
     finally:
         prog.close()
 
