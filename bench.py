@@ -84,6 +84,10 @@ def main() -> int:
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before timing, copy this many MiB device-to-device once (a plain copy of "
                          "known size that scales the HBM byte counters of a profiler run)")
+    ap.add_argument("--prefill-vendor", action="store_true",
+                    help="only torch's dense bf16 linear (hipBLASLt) at the prefill shapes with bf16 W (no "
+                         "dequant): a library reference, not a product path; torch's own HIP runtime does "
+                         "not share a process with this library's, so the leg runs alone")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -94,6 +98,10 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
+
+    if args.prefill_vendor:   # before this library is loaded
+        print(json.dumps({"vendor_dense_bf16": bench_vendor_dense()}), flush=True)
+        return 0
 
     from sharpinference_amd import native
 
@@ -419,6 +427,45 @@ def bench_prefill(hip, rng, m: int = 512):
     tflops = total_flops / total_us / 1e6
     out.update({"us_total": round(total_us, 1), "TFLOPs": round(tflops, 1),
                 "mfma_bf16_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+    return out
+
+
+def bench_vendor_dense(m: int = 512):
+    """The vendor library's dense bf16 product at the prefill shapes:
+    torch.nn.functional.linear (hipBLASLt) of bf16 X [m, K] by bf16 W [N, K]
+    (four weight copies rotated), bf16 out, timed with events on torch's
+    stream (median of 5 samples of 20 launches).  W here is already dense
+    bf16 (3.6x the bytes of Q4_0 and no decode), so this is a reference
+    for what a plain GEMM reaches at these shapes, not a product path."""
+    import torch
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    out = {"library": "torch.nn.functional.linear (hipBLASLt), bf16 in / out", "tokens": m, "shapes": {}}
+    total_flops, total_us = 0.0, 0.0
+    for name, rows, cols in LAYER_Q4_0:
+        x = torch.randn(m, cols, device=dev, dtype=torch.bfloat16, generator=gen)
+        ws = [torch.randn(rows, cols, device=dev, dtype=torch.bfloat16, generator=gen) for _ in range(4)]
+        for i in range(8):
+            torch.nn.functional.linear(x, ws[i % 4])
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(20):
+                torch.nn.functional.linear(x, ws[i % 4])
+            b.record()
+            b.synchronize()
+            samples.append(a.elapsed_time(b) * 1e3 / 20)
+        us = sorted(samples)[2]
+        flops = 2.0 * m * rows * cols
+        total_flops += flops
+        total_us += us
+        out["shapes"][name] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1)}
+        log(f"  vendor dense bf16 {name:8s} m={m} {rows}x{cols}: {us:.1f} us, {flops / us / 1e6:.1f} TFLOP/s")
+        del x, ws
+    out.update({"us_total": round(total_us, 1), "TFLOPs": round(total_flops / total_us / 1e6, 1)})
+    log(f"vendor dense bf16 total: {total_us:.1f} us, {out['TFLOPs']} TFLOP/s")
     return out
 
 
