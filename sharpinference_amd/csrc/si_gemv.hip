@@ -1456,11 +1456,14 @@ hipError_t launch_fast_dense(const GemvOp* ops, int n, int64_t rows64, int64_t c
         switch (cols) {
         case 1024: return launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
         case 2048: return mid ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
-        // one unit per lane, the row's 48 units split over 3 waves; 12 or
-        // 16 rows per workgroup (the Phi-4 F16 shapes: qkv 8.68 -> 8.34, o
-        // 6.06 -> 5.58, gate/up with SwiGLU rows 20.1 -> 18.8, tied head
-        // 211 -> 197 us against 4 rows per workgroup or 3 units per lane)
-        case 3072: return mid ? launch_tiled<FMT, 16, 1, 1, 3, 12>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 3, 9>(ops, n, s);
+        // one unit per lane, the row's 48 units split over 3 waves; 12, 16
+        // or 20 rows per workgroup (one workgroup per CU at 3072 and 5120
+        // rows).  The Phi-4 F16 shapes against 4 rows per workgroup or 3
+        // units per lane: qkv 8.68 -> 7.86, o 6.06 -> 5.58, gate/up with
+        // SwiGLU rows 20.1 -> 18.8, tied head 211 -> 197 us
+        case 3072: return mid              ? launch_tiled<FMT, 16, 1, 1, 3, 12>(ops, n, s)
+                          : rows64 >= 5120 ? launch_tiled<FMT, 16, 1, 1, 3, 15>(ops, n, s)
+                                           : launch_tiled<FMT, 16, 1, 1, 3, 9>(ops, n, s);
         case 4096: return mid ? launch_tiled<FMT, 16, 2, 1, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
         case 6144: return mid ? launch_tiled<FMT, 16, 3, 1, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 6, 6>(ops, n, s);
         case 8192: return mid ? launch_tiled<FMT, 16, 2, 1, 4, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
