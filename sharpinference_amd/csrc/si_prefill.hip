@@ -716,7 +716,215 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
     }
 }
 
+// 16 x 16 x 32 block form (v_mfma_f32_16x16x32_bf16; lane l holds
+// A[l % 16][8 * (l / 16) + e], B[8 * (l / 16) + e][l % 16] and D rows
+// 4 * (l / 16) + r of column l % 16, as checked on the GPU).  A group of 4
+// waves in a 2 x 2 layout: wave (wn, wm) owns 16*WN W rows x 16*WM tokens of
+// the 32*WN x 32*WM tile, so tiles such as 96 rows x 64 tokens give 256
+// workgroups for a 3072 x 512 product (one per CU, where the 32 x 32 form
+// above leaves a quarter of the CUs idle).  A step covers BPS blocks; KS
+// groups of 4 waves split the steps (two waves per SIMD) and add through
+// LDS.  The W and X tiles are stored as 16-byte chunks, chunk c of row r at
+// c ^ (r & 15) (16 chunks a row) or c ^ ((r >> 1) & 7) (8 chunks), so the
+// fragment reads (16 rows, one chunk) are free of bank conflicts.  Same
+// exact decode, ring of D steps in flight and one barrier per step as the
+// kernels above.
+template <int BPS>
+__device__ __forceinline__ int m16_off(int r, int c)
+{
+    constexpr int CPR = 4 * BPS;
+    return r * CPR + (CPR == 8 ? (c ^ ((r >> 1) & 7)) : (c ^ (r & 15)));
+}
+
+template <int FMT, int WN, int WM, int BPS, int D, int KS>
+__global__ __launch_bounds__(PF_THREADS * KS) void prefill_m16_kernel(const uint8_t* __restrict__ W,
+                                                                       const __bf16* __restrict__ X,
+                                                                       float* __restrict__ Y, int M, int N, int K,
+                                                                       int64_t row_bytes)
+{
+    constexpr int NROWS = 32 * WN, TROWS = 32 * WM, CPR = 4 * BPS;
+    constexpr int WI = NROWS * BPS * 2 / PF_THREADS;      // 16-value W items per thread per step
+    constexpr int XL = TROWS * CPR / PF_THREADS;          // 16-byte X chunks per thread per step
+    static_assert(WI * PF_THREADS == NROWS * BPS * 2 && XL * PF_THREADS == TROWS * CPR, "whole items per thread");
+    static_assert(BPS == 2 || BPS == 4, "8 or 16 chunks a row");
+    static_assert(D % 2 == 0, "ring groups start on even steps, so a slot's LDS buffer is fixed");
+    constexpr int GROUP_CHUNKS = 2 * (NROWS + TROWS) * CPR;   // a step group's double-buffered W and X tiles
+    static_assert((KS - 1) * WM * WN * 4 * PF_THREADS * 4 <= KS * GROUP_CHUNKS * 16, "the partial sums fit");
+    __shared__ __attribute__((aligned(16))) u32x4 pool[KS * GROUP_CHUNKS];
+
+    const int t = threadIdx.x % PF_THREADS, kh = threadIdx.x / PF_THREADS;
+    const int lane = t & 63, wave = t >> 6;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int li = lane & 15, lg = lane >> 4;
+    const int n0 = blockIdx.x * NROWS, m0 = blockIdx.y * TROWS;
+    const int nsteps = K / (32 * BPS) / KS;              // the launcher makes 32 * BPS * KS divide K
+    const int step0 = kh * nsteps;
+    u32x4* const gbase = pool + kh * GROUP_CHUNKS;
+    auto wt = [&](int buf) { return gbase + buf * NROWS * CPR; };
+    auto xt = [&](int buf) { return gbase + 2 * NROWS * CPR + buf * TROWS * CPR; };
+
+    // X chunk e of this thread: token row item / CPR, chunk item % CPR
+    uint32_t xoff[XL];
+    int xdst[XL];
+    const int xc = t % CPR;
+#pragma unroll
+    for (int e = 0; e < XL; e++) {
+        const int r = (t + PF_THREADS * e) / CPR;
+        xoff[e] = static_cast<uint32_t>(min(m0 + r, M - 1)) * static_cast<uint32_t>(2 * K) + 16u * xc;
+        xdst[e] = m16_off<BPS>(r, xc);
+    }
+    const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(X);
+    // W item i: half t % 2 of block (t / 2) % BPS of tile row (t + 256 i) / (2 BPS)
+    uint32_t wrow[WI];
+    int wr[WI];
+#pragma unroll
+    for (int i = 0; i < WI; i++) {
+        wr[i] = (t + PF_THREADS * i) / (2 * BPS);
+        wrow[i] = static_cast<uint32_t>(min(n0 + wr[i], N - 1)) * static_cast<uint32_t>(row_bytes);
+    }
+    const int wh = t & 1, wbo = (t >> 1) % BPS;
+
+    f32x4 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++)
+            acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    RawW<FMT> raw[D][WI];
+    u32x4 xr[D][XL];
+    auto load_step = [&](int ls, RawW<FMT> (&wd)[WI], u32x4 (&xd)[XL]) {
+        const int step = step0 + ls;
+        const int blk = BPS * step + wbo;
+#pragma unroll
+        for (int i = 0; i < WI; i++)
+            wd[i] = load_raw<FMT>(W, wrow[i], blk, wh);
+        const uint32_t col_bytes = static_cast<uint32_t>(64 * BPS * step);
+#pragma unroll
+        for (int e = 0; e < XL; e++)
+            xd[e] = *reinterpret_cast<const u32x4*>(xbytes + (xoff[e] + col_bytes));
+    };
+    auto store_step = [&](int ls, const RawW<FMT> (&wsrc)[WI], const u32x4 (&xsrc)[XL], int buf) {
+        const int blk = BPS * (step0 + ls) + wbo;
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            bf16x8 v0, v1;
+            int c0, c1;
+            decode_raw<FMT>(wsrc[i], blk, wh, v0, v1, c0, c1);
+            *reinterpret_cast<bf16x8*>(wt(buf) + m16_off<BPS>(wr[i], 4 * wbo + (c0 >> 3))) = v0;
+            *reinterpret_cast<bf16x8*>(wt(buf) + m16_off<BPS>(wr[i], 4 * wbo + (c1 >> 3))) = v1;
+        }
+#pragma unroll
+        for (int e = 0; e < XL; e++)
+            xt(buf)[xdst[e]] = xsrc[e];
+    };
+    auto mfma_step = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < BPS; kk++) {
+            const int c = 4 * kk + lg;                     // the fragment's chunk of the step
+            bf16x8 a[WM], b[WN];
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+                a[i] = *reinterpret_cast<const bf16x8*>(xt(buf) + m16_off<BPS>(16 * (WM * wm + i) + li, c));
+#pragma unroll
+            for (int j = 0; j < WN; j++)
+                b[j] = *reinterpret_cast<const bf16x8*>(wt(buf) + m16_off<BPS>(16 * (WN * wn + j) + li, c));
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // prologue: local step 0 in LDS; steps 1..D in flight
+    {
+        RawW<FMT> w0[WI];
+        u32x4 x0[XL];
+        load_step(0, w0, x0);
+#pragma unroll
+        for (int u = 0; u < D; u++)
+            load_step(min(u + 1, nsteps - 1), raw[(u + 1) % D], xr[(u + 1) % D]);
+        store_step(0, w0, x0, 0);
+    }
+    __syncthreads();
+    int base = 0;
+    for (; base + D < nsteps; base += D) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            const int ls = base + u;
+            const int next = (u + 1) % D;
+            mfma_step(u & 1);
+            store_step(ls + 1, raw[next], xr[next], (u + 1) & 1);
+            load_step(min(ls + 1 + D, nsteps - 1), raw[next], xr[next]);
+            interleave_step<BPS * WM * WN>();
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+        const int ls = base + u;
+        if (ls < nsteps) {
+            mfma_step(u & 1);
+            if (ls + 1 < nsteps)
+                store_step(ls + 1, raw[(u + 1) % D], xr[(u + 1) % D], (u + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // the other step groups add their sums into group 0 through LDS (every
+    // tile read ended at the last barrier)
+    if constexpr (KS > 1) {
+        constexpr int PER = WM * WN * 4;
+        float* red = reinterpret_cast<float*>(pool);
+        if (kh > 0) {
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        red[((kh - 1) * PER + (i * WN + j) * 4 + r) * PF_THREADS + t] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kh > 0)
+            return;
+#pragma unroll
+        for (int o = 1; o < KS; o++)
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc[i][j][r] += red[((o - 1) * PER + (i * WN + j) * 4 + r) * PF_THREADS + t];
+    }
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            const int n = n0 + 16 * (WN * wn + j) + li;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * (WM * wm + i) + 4 * lg + r;
+                if (m < M && n < N)
+                    Y[static_cast<int64_t>(m) * N + n] = acc[i][j][r];
+            }
+        }
+}
+
 constexpr int NUM_CUS = 256;
+
+template <int FMT, int WN, int WM, int BPS, int KS, int D = PF_DEPTH>
+hipError_t launch_prefill_m16(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
+{
+    const int64_t rb = row_bytes(FMT, k);
+    const dim3 grid(static_cast<unsigned>((n + 32 * WN - 1) / (32 * WN)), static_cast<unsigned>((m + 32 * WM - 1) / (32 * WM)));
+    hipLaunchKernelGGL((prefill_m16_kernel<FMT, WN, WM, BPS, D, KS>), grid, dim3(PF_THREADS * KS), 0, s,
+                       static_cast<const uint8_t*>(w), static_cast<const __bf16*>(x), y, static_cast<int>(m),
+                       static_cast<int>(n), static_cast<int>(k), rb);
+    return hipGetLastError();
+}
 
 template <int FMT, int MW, int NT, int KS, bool COMPACT, int D = PF_DEPTH>
 hipError_t launch_prefill_shape(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
@@ -748,6 +956,10 @@ hipError_t launch_prefill_ws(const void* w, const void* x, float* y, int64_t m, 
 //     when that grid has at least 128 workgroups: up to one per
 //     CU two step groups of 4 waves with compact tiles (160 KiB, two waves
 //     per SIMD) when they divide the steps, else the padded tile (84 KiB);
+//   * otherwise, when K is a multiple of 256 and 96-row x 64-token tiles
+//     give 128..256 workgroups, the 16 x 16 block form with that tile, 128
+//     columns per step and the steps split between two groups of 4 waves
+//     (o_proj 28.4 -> 25.7 us, down 72.4 -> 61.0 us at 512 tokens);
 //   * otherwise 128 tokens x 64 rows with the steps split between two
 //     groups of 4 waves when they divide evenly (two waves per SIMD
 //     overlap their phases).
@@ -762,6 +974,9 @@ hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m,
     if (big >= NUM_CUS / 2)
         return steps % 2 == 0 ? launch_prefill_shape<FMT, 64, 2, 2, true>(w, x, y, m, n, k, s)
                               : launch_prefill_shape<FMT, 64, 2, 1, false>(w, x, y, m, n, k, s);
+    const int64_t m16 = wgs(64, 96);
+    if (k % 256 == 0 && m16 >= NUM_CUS / 2 && m16 <= NUM_CUS)
+        return launch_prefill_m16<FMT, 3, 2, 4, 2>(w, x, y, m, n, k, s);
     if (steps % 2 == 0)
         return launch_prefill_shape<FMT, 32, 2, 2, false>(w, x, y, m, n, k, s);
     return launch_prefill_shape<FMT, 32, 2, 1, false>(w, x, y, m, n, k, s);

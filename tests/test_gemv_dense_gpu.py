@@ -195,7 +195,7 @@ def bf16_round(a):
 
 
 PREFILL = [(f, m, n, k) for f in DENSE for (m, n, k) in [(7, 64, 256), (300, 100, 768), (513, 33, 1024),
-                                                         (512, 3072, 3072)]]
+                                                         (512, 3072, 3072), (256, 3000, 256)]]
 
 
 @pytest.mark.parametrize("fmt,m,rows,cols", PREFILL, ids=[f"{NAMES[f]}-m{m}-{n}x{k}" for f, m, n, k in PREFILL])

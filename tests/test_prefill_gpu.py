@@ -56,6 +56,12 @@ CASES = [(f, m, n, k) for f in FORMATS for (m, n, k) in SMALL]
 CASES += [(f, m, n, k) for f in (native.Q8_0, native.Q4_0)
           for (m, n, k) in [(5, 40, 160), (130, 64, 224), (512, 8192, 96), (512, 8192, 160), (600, 16384, 64),
                             (300, 32768, 96), (520, 16448, 544)]]
+# the 16 x 16 block form (96-row x 64-token tiles, 128..256 of them, K a
+# multiple of 256): every format with a row tail; one step per group; token
+# and row tails; three steps per group
+CASES += [(f, 256, 3000, 256) for f in FORMATS]
+CASES += [(f, m, n, k) for f in (native.Q8_0, native.Q4_0)
+          for (m, n, k) in [(512, 3072, 256), (500, 3000, 512), (200, 6000, 768)]]
 
 
 @pytest.mark.parametrize("fmt,m,rows,cols", CASES, ids=[f"{NAMES[f]}-m{m}-{n}x{k}" for f, m, n, k in CASES])
