@@ -9,7 +9,7 @@
 // core.mat-vec per token row, and the batched prefill matvec of the D3D12
 // transformer program (GpuBatchTransformerInstructions.cs:224-279), whose B=16
 // token batch re-reads W per token.  Here every W element is decoded once per
-// workgroup tile of 128 or 256 tokens:
+// workgroup tile of 64, 128 or 256 tokens:
 //
 //   * a workgroup (4 waves) owns 32*NT rows of W and 4*MW token rows of X;
 //   * per step of two 32-column blocks, the 256 threads decode the blocks of
@@ -22,7 +22,9 @@
 //   * each wave multiplies its MW token rows by the tile with
 //     v_mfma_f32_32x32x16_bf16 (MW/32 x NT accumulator tiles of 32 x 32
 //     FP32), both fragments read from LDS;
-//   * the tile is the largest whose grid still covers the 256 CUs.
+//   * the tile is the largest whose grid still covers the 256 CUs; grids
+//     of 3072 x 512 outputs use a 16 x 16 block form (prefill_m16_kernel
+//     below) whose 96-row x 64-token tiles give one workgroup per CU.
 //
 // Loading the fragments straight from global memory instead (each load
 // instruction then spans 32 token or W rows, 32 cache lines) measured about
