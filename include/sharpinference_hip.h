@@ -487,6 +487,19 @@ int si_hip_phi4_workspace_bytes(const si_hip_phi4_model* model, uint64_t* bytes)
  * 866-919) and Phi4TextSession.ForwardToken (Phi4TextModel.cs:329-344). */
 int si_hip_phi4_decode(si_hip_context* ctx, const si_hip_phi4_model* model);
 
+/* The same step for positions up to a bound: every layer's attention covers
+ * only the first position_bound / 128 + 1 chunks of 128 cache positions
+ * and requests their K / V rows together with the position (the full-cache
+ * step waits for the position first).  Serves every position below
+ * limit = min(capacity, 128 * (position_bound / 128 + 1)); replayed with
+ * control[1] >= limit, the step writes NaN attention outputs (so NaN
+ * logits) and appends nothing to the caches.  0 <= position_bound <
+ * capacity and rotary_dim a multiple of 16, else an error.  No counterpart
+ * in the reference (its program attends over the cache it is given each
+ * token): for callers that record one plan per range of positions, as the
+ * Phi-4 session here does (one per 128 positions, recorded on first use). */
+int si_hip_phi4_decode_bounded(si_hip_context* ctx, const si_hip_phi4_model* model, int position_bound);
+
 /* ---- RWKV-7 decode step ------------------------------------------------------------ */
 
 /* out[b][r] = sum_c matrix[b][r][c] * vector[b][c], FP32.  Replaces:

@@ -509,7 +509,11 @@ __device__ __forceinline__ void rotate8(float* own, const float* partner, const 
 // read straight from the step's qkv vector and rotated in registers; the
 // 16 lanes holding the new token's position round it to fp16 and append it.
 // The pointers a wave needs first arrive as preloaded scalar arguments.
-template <int GROUP>
+// BOUNDED: the grid holds only chunks that start at or below every position
+// the caller replays it with (a step recorded for a range of positions), so
+// every chunk's K / V rows are requested together with the position instead
+// of after it.
+template <int GROUP, bool BOUNDED>
 __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const float* __restrict__ qkv,
                                                                       const int32_t* __restrict__ position,
                                                                       __half* k_cache, __half* v_cache,
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
     __half* vc = v_cache + static_cast<int64_t>(g) * capacity * HEAD_DIM;
     //    (an invalid chunk leaves them unloaded: its results are not stored)
     uint4 kr[FPPL], vr[FPPL];
-    if (valid) {
+    if (BOUNDED || valid) {
 #pragma unroll
         for (int j = 0; j < FPPL; j++) {
             const int64_t r = min(start + wave * (FCHUNK / 4) + row + 4 * j, capacity - 1);
@@ -876,28 +880,40 @@ hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep)
     const int group = a.heads / a.kv_heads;
     const dim3 grid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>(a.max_chunks));
     if (a.rotary_dim % 16 == 0) {
-        const dim3 fgrid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>((a.capacity + FCHUNK - 1) / FCHUNK));
+        const int all = (a.capacity + FCHUNK - 1) / FCHUNK;
+        const bool bounded = a.chunk_bound > 0;
+        if (bounded && a.chunk_bound > all)
+            return hipErrorInvalidValue;
+        const dim3 fgrid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>(bounded ? a.chunk_bound : all));
         // slices of 8 values and their rotary partners are whole
-        switch (group) {
-#define SI_CHUNK(G)                                                                                               \
-    case G:                                                                                                       \
-        hipLaunchKernelGGL((attention_chunk_kernel<G>), fgrid, dim3(ATT_THREADS), 0, s, a.qkv, a.position,        \
+        switch (group * 2 + (bounded ? 1 : 0)) {
+#define SI_CHUNK(G, B)                                                                                            \
+    case G * 2 + B:                                                                                               \
+        hipLaunchKernelGGL((attention_chunk_kernel<G, B>), fgrid, dim3(ATT_THREADS), 0, s, a.qkv, a.position,     \
                            a.k_cache, a.v_cache, a.workspace, a.capacity, a.rotary_dim, a.max_chunks);           \
         break;
-        SI_CHUNK(1)
-        SI_CHUNK(2)
-        SI_CHUNK(3)
-        SI_CHUNK(4)
+        SI_CHUNK(1, 0)
+        SI_CHUNK(2, 0)
+        SI_CHUNK(3, 0)
+        SI_CHUNK(4, 0)
+        SI_CHUNK(1, 1)
+        SI_CHUNK(2, 1)
+        SI_CHUNK(3, 1)
+        SI_CHUNK(4, 1)
 #undef SI_CHUNK
         default: return hipErrorInvalidValue;
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess)
             return e;
+        // positions past the chunks of a bounded grid count as outside the cache
+        const int limit = bounded ? min(a.capacity, a.chunk_bound * FCHUNK) : a.capacity;
         hipLaunchKernelGGL(attention_combine_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, a.workspace,
-                       a.position, a.out, a.capacity, a.max_chunks, FCHUNK);
+                       a.position, a.out, limit, a.max_chunks, FCHUNK);
         return hipGetLastError();
     }
+    if (a.chunk_bound > 0)
+        return hipErrorNotSupported;   // the bounded grid is built for rotary widths that are multiples of 16
     switch (group) {
     case 1: hipLaunchKernelGGL((attention_partial_kernel<1>), grid, dim3(ATT_THREADS), 0, s, a); break;
     case 2: hipLaunchKernelGGL((attention_partial_kernel<2>), grid, dim3(ATT_THREADS), 0, s, a); break;

@@ -26,6 +26,11 @@ struct AttentionArgs {
     int max_chunks;        // ceil(capacity / 64)
     float rope_base;
     float rope_scale;
+    // > 0: the chunk grid covers only the first chunk_bound 128-position
+    // chunks, whose K / V rows are requested before the position returns;
+    // a position at or past chunk_bound * 128 yields NaN outputs and no
+    // cache append.  0: the grid covers the whole cache.
+    int chunk_bound = 0;
 };
 
 int64_t attention_workspace_floats(int heads, int capacity);

@@ -119,7 +119,9 @@ int phi4_check(si_hip_context* ctx, const si_hip_phi4_model* m)
 }
 
 // Launches one decode step on the context stream (recorded when capturing).
-hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
+// chunk_bound > 0: the attention grids cover the first chunk_bound
+// 128-position chunks only (a step recorded for a range of positions).
+hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m, int chunk_bound)
 {
     hipStream_t s = ctx->stream;
     const int H = m->hidden;
@@ -160,7 +162,9 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m)
         if (e != hipSuccess) break;
         a.k_cache = L.k_cache;
         a.v_cache = L.v_cache;
-        e = si::launch_attention(attention_args(&a), s, false);
+        si::AttentionArgs aa = attention_args(&a);
+        aa.chunk_bound = chunk_bound;
+        e = si::launch_attention(aa, s, false);
         if (e != hipSuccess) break;
         // hidden += W_o . attn
         e = si::launch_gemv(m->weight_format, L.o, m->attn, m->hidden_state, H, H, m->hidden_state, s, nullptr);
@@ -453,8 +457,28 @@ int si_hip_phi4_decode(si_hip_context* ctx, const si_hip_phi4_model* model)
         return hip_fail(ctx, g.err, "hipSetDevice");
     if (const int rc = phi4_check(ctx, model))
         return rc;
-    const hipError_t e = phi4_step(ctx, model);
+    const hipError_t e = phi4_step(ctx, model, 0);
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "phi4 decode step");
+}
+
+int si_hip_phi4_decode_bounded(si_hip_context* ctx, const si_hip_phi4_model* model, int position_bound)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "phi4_decode_bounded: null context");
+    Enter g(ctx);
+    if (g.err != hipSuccess)
+        return hip_fail(ctx, g.err, "hipSetDevice");
+    if (const int rc = phi4_check(ctx, model))
+        return rc;
+    if (position_bound < 0 || position_bound >= model->capacity)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "phi4_decode_bounded: position bound %d outside the cache (capacity %d)",
+                    position_bound, model->capacity);
+    if (model->rotary_dim % 16 != 0)
+        return fail(ctx, SI_HIP_ERR_UNSUPPORTED,
+                    "phi4_decode_bounded: rotary_dim %d (the bounded attention grid needs a multiple of 16)",
+                    model->rotary_dim);
+    const hipError_t e = phi4_step(ctx, model, position_bound / 128 + 1);
+    return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "phi4 decode step (bounded)");
 }
 
 }  // extern "C"

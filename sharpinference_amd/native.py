@@ -222,6 +222,7 @@ SIGNATURES.update({
     "si_hip_batch_select_last": ([_vp, _vp, _vp, _vp, _i32, _i64], _i32),
     "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
     "si_hip_phi4_decode": ([_vp, ctypes.POINTER(Phi4Model)], _i32),
+    "si_hip_phi4_decode_bounded": ([_vp, ctypes.POINTER(Phi4Model), _i32], _i32),
     "si_hip_batched_matvec": ([_vp, _vp, _vp, _vp, _i32, _i32, _i32], _i32),
     "si_hip_layernorm": ([_vp, _vp, _vp, _vp, _i32, ctypes.c_float, _vp], _i32),
     "si_hip_rwkv7_wkv": ([_vp, ctypes.POINTER(Rwkv7WkvArgs)], _i32),
@@ -486,6 +487,10 @@ class HipContext:
 
     def phi4_decode(self, model: Phi4Model) -> None:
         self._call(lib().si_hip_phi4_decode, ctypes.byref(model))
+
+    def phi4_decode_bounded(self, model: Phi4Model, position_bound: int) -> None:
+        """The step for positions below min(capacity, 128 * (position_bound // 128 + 1))."""
+        self._call(lib().si_hip_phi4_decode_bounded, ctypes.byref(model), int(position_bound))
 
     def batched_matvec(self, matrix: int, vector: int, out: int, batch: int, rows: int, cols: int) -> None:
         self._call(lib().si_hip_batched_matvec, ctypes.c_void_p(int(matrix)), ctypes.c_void_p(int(vector)),

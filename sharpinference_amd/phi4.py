@@ -3,9 +3,11 @@
 The host half of the reference's Phi4D3D12TextSession
 (SharpInference.Architectures.Phi4.D3D12/Phi4D3D12TextSession.cs): it owns
 the device tensors of one model (block-quantized weights kept in their GGUF
-bytes, FP32 norms, fp16 KV caches), records the whole decode step once as a
-plan through si_hip_phi4_decode, and runs ForwardToken (:212-226) as
-control upload -> one plan replay -> next-token readback.
+bytes, FP32 norms, fp16 KV caches), records the whole decode step as a plan
+per range of 128 positions (si_hip_phi4_decode_bounded, recorded on first
+use: its attention reads only the chunks those positions can reach, and
+requests them without waiting for the position), and runs ForwardToken
+(:212-226) as control upload -> one plan replay -> next-token readback.
 """
 from __future__ import annotations
 
@@ -117,7 +119,11 @@ class Phi4Weights:
 
 
 class Phi4DecodeSession:
-    """Device-resident model + one recorded decode plan."""
+    """Device-resident model + the decode step recorded as one plan per
+    range of 128 positions (one plan over the whole cache when the rotary
+    width is not a multiple of 16)."""
+
+    POSITION_RANGE = 128
 
     def __init__(self, hip: native.HipContext, cfg: Phi4Config, weights: Phi4Weights):
         self.hip = hip
@@ -160,7 +166,8 @@ class Phi4DecodeSession:
             self.logits.ptr, 0, self.next_token.ptr)
         self.workspace = self._alloc(native.phi4_workspace_bytes(self.model))
         self.model.workspace = self.workspace.ptr
-        self.plan = hip.record(lambda: hip.phi4_decode(self.model))
+        self._plans: Dict[int, native.Plan] = {}
+        self._control_position = 0
         self.position = 0
 
     # -- buffers -------------------------------------------------------------------
@@ -212,8 +219,31 @@ class Phi4DecodeSession:
         return L["k_cache"].readback(np.uint16).reshape(shape), L["v_cache"].readback(np.uint16).reshape(shape)
 
     # -- decoding -------------------------------------------------------------------
+    def plan_for(self, position: int) -> "native.Plan":
+        """The recorded step serving `position` (recorded on first use)."""
+        cfg = self.cfg
+        if cfg.rotary_dim % 16:
+            key, bound = -1, None
+        else:
+            key = max(0, position) // self.POSITION_RANGE
+            bound = min(cfg.capacity - 1, self.POSITION_RANGE * key + self.POSITION_RANGE - 1)
+        plan = self._plans.get(key)
+        if plan is None:
+            if bound is None:
+                plan = self.hip.record(lambda: self.hip.phi4_decode(self.model))
+            else:
+                plan = self.hip.record(lambda: self.hip.phi4_decode_bounded(self.model, bound))
+            self._plans[key] = plan
+        return plan
+
+    @property
+    def plan(self) -> "native.Plan":
+        """The step for the position of the last set_control."""
+        return self.plan_for(self._control_position)
+
     def set_control(self, token: int, position: int) -> None:
         self.control.upload(np.array([token, position], np.int32))
+        self._control_position = position
 
     def forward_token(self, token: int, position: Optional[int] = None) -> int:
         """One decode step; returns the argmax token (greedy next token)."""
@@ -222,7 +252,7 @@ class Phi4DecodeSession:
         if not 0 <= position < self.cfg.capacity:
             raise ValueError(f"position {position} outside the KV capacity {self.cfg.capacity}")
         self.set_control(token, position)
-        self.plan.launch()
+        self.plan_for(position).launch()
         nxt = int(self.next_token.readback(np.int32, 1)[0])
         self.position = position + 1
         return nxt
@@ -231,9 +261,9 @@ class Phi4DecodeSession:
         return self.logits.readback(np.float32, self.cfg.vocab)
 
     def close(self) -> None:
-        if self.plan is not None:
-            self.plan.destroy()
-            self.plan = None
+        for plan in self._plans.values():
+            plan.destroy()
+        self._plans = {}
         for b in self._bufs:
             b.free()
         self._bufs = []

@@ -277,6 +277,66 @@ def test_small_dense_phi4_decode_steps_match_oracle(hip, fmt):
         _check_logits(g, gl, o, ol, f"{native.FORMAT_NAMES[fmt]} step {i}")
 
 
+def test_position_range_plans_across_chunk_edges(hip):
+    """The session records one plan per 128 positions (attention grid of the
+    chunks those positions reach): steps on both sides of the chunk edges
+    127 | 128 and 255 | 256, the last position of the cache, and a return
+    to an earlier range, each against the oracle."""
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=3000, capacity=300,
+                          rope_scale=1.19)
+    weights = phi4.synth_weights(cfg, seed=25)
+    kv = phi4.synth_kv(cfg, length=126, seed=26)
+    steps = [(5, 126), (6, 127), (7, 128), (8, 129), (9, 255), (10, 256), (11, 299), (12, 130)]
+    results, kv_gpu, ref = _run_steps(hip, cfg, weights, kv, steps)
+    for i, (g, gl, o, ol) in enumerate(results):
+        _check_logits(g, gl, o, ol, f"step {i} at position {steps[i][1]}")
+    for l in range(cfg.layers):
+        for which in (0, 1):
+            a = kv_gpu[l][which].view(np.float16).astype(np.float32)
+            b = (ref.k if which == 0 else ref.v)[l].view(np.float16).astype(np.float32)
+            assert np.allclose(a, b, rtol=2e-3, atol=2e-3), (l, which)
+
+
+def test_bounded_step_rejects_positions_past_its_range(hip):
+    """A step recorded for positions 0..127 replayed at position 200: NaN
+    logits and no cache append at 200; the session's own plan for that
+    position then matches the oracle.  Bounds outside the cache and rotary
+    widths the bounded grid does not cover are refused."""
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=2000, capacity=256)
+    weights = phi4.synth_weights(cfg, seed=27)
+    kv = phi4.synth_kv(cfg, length=200, seed=28)
+    sess = phi4.Phi4DecodeSession(hip, cfg, weights)
+    ref = orc.Phi4Oracle(cfg, weights)
+    try:
+        for l, (k, v) in enumerate(kv):
+            sess.load_kv(l, k, v)
+            ref.k[l][...] = k
+            ref.v[l][...] = v
+        before = [sess.read_kv(l) for l in range(cfg.layers)]
+        low = hip.record(lambda: hip.phi4_decode_bounded(sess.model, 127))
+        sess.set_control(3, 200)
+        low.launch()
+        assert np.all(np.isnan(sess.read_logits()))
+        for l in range(cfg.layers):
+            k, v = sess.read_kv(l)
+            assert np.array_equal(k, before[l][0]) and np.array_equal(v, before[l][1]), l
+        low.destroy()
+        g = sess.forward_token(3, 200)
+        o, ol = ref.step(3, 200)
+        _check_logits(g, sess.read_logits(), o, ol, "position 200 through its own plan")
+        for bad in (-1, cfg.capacity):
+            with pytest.raises(native.HipError) as e:
+                hip.phi4_decode_bounded(sess.model, bad)
+            assert e.value.status == native.ERR_ARGUMENT
+        sess.model.rotary_dim = 88
+        with pytest.raises(native.HipError) as e:
+            hip.phi4_decode_bounded(sess.model, 100)
+        assert e.value.status == native.ERR_UNSUPPORTED
+        sess.model.rotary_dim = cfg.rotary_dim
+    finally:
+        sess.close()
+
+
 def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
     """The full decode workload: 32 layers, Phi-4-mini shapes, Q4_K layers, Q8_0
     embedding and head (200064 x 3072), fp16 KV cache with 2048 tokens of
