@@ -31,7 +31,9 @@ def dense(fmt, rows, cols, seed, sigma=0.02):
 # every entry of the dense shape table (small and >= 12288-row variants)
 SHAPES = {
     native.F16: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (2048, 2048), (12288, 2048), (1000, 1024),
-                 (12288, 4096), (300, 4096), (12289, 6144), (40, 6144), (13000, 8192), (1, 3072)],
+                 (12288, 4096), (300, 4096), (12289, 6144), (40, 6144), (13000, 8192), (1, 3072),
+                 # row tails of the 3072-column tiles (20, 12 and 16 rows per workgroup)
+                 (5121, 3072), (3001, 3072), (12290, 3072), (200, 3072)],
     native.F32: [(3072, 3072), (1024, 1024), (5000, 2048), (333, 8192), (13000, 4096), (100, 6144), (2, 3072)],
 }
 CASES = [(f, r, c) for f in DENSE for (r, c) in SHAPES[f]]
