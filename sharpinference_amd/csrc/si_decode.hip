@@ -15,6 +15,7 @@
 // rounded values back.
 #include "si_internal.hpp"
 #include "si_decode.hpp"
+#include "si_lanes.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -124,16 +125,6 @@ __device__ __forceinline__ void unpack8(const uint4& r, float* f)
     }
 }
 
-template <int N>
-__device__ __forceinline__ float row_sum(float v)
-{
-    // sum over aligned groups of N (<= 16) lanes with DPP
-    if constexpr (N >= 2) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-    if constexpr (N >= 4) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-    if constexpr (N >= 8) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
-    if constexpr (N >= 16) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
-    return v;
-}
 
 // Once per step: the rotary table of the new position (frequency
 // 1 / base^(2i / R), cos / sin scaled by rope_scale), shared by every layer
@@ -452,23 +443,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_partial_kernel(Attentio
     }
 }
 
-// Swaps between the halves (32 lanes) and the row pairs (16 lanes) of a
-// wave: after both steps every lane holds the combination of the four lanes
-// l, l ^ 16, l ^ 32, l ^ 48 (its column of the wave's four rows).
-__device__ __forceinline__ float rows_sum(float v)
-{
-    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-__device__ __forceinline__ float rows_max(float v)
-{
-    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
 
 __device__ __forceinline__ void load8(const float* p, float* f)
 {

@@ -17,6 +17,7 @@
 // launches are the op-by-op form a VM program dispatches.
 #include "si_internal.hpp"
 #include "si_transformer.hpp"
+#include "si_lanes.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -273,6 +274,214 @@ __global__ __launch_bounds__(HEAD) void gqa_merge_kernel(GqaArgs a)
     a.output[static_cast<int64_t>(head) * HEAD + d] = O / L;
 }
 
+// head_size 128, group G <= 4: one workgroup = one KV head x 128 cache rows
+// (the decode step's register-resident form, without its rotary and
+// append: rope-kv-write has already rotated the query and written the row).
+// Thread (wave w, lane l) takes the 8-value slice l % 16 of rows
+// 32 w + l / 16 + 4 j (j < 8) for both the scores and the values, so the
+// softmax weights stay in its registers: each wave keeps its maximum and
+// sum, sums across its four rows with lane swaps, and the four waves merge
+// (with rescaling) through LDS at one barrier.  Rows past the active range
+// count as absent.  Partials (m, l, o) of each query head and chunk go to
+// the workspace at the 64-row layout's index (chunk < its chunk count).
+constexpr int GQA_FCHUNK = 128;
+
+template <typename T>
+struct CacheSlice {   // 8 consecutive values of one cache row as loaded
+    uint4 w[sizeof(T) == 2 ? 1 : 2];
+};
+template <typename T>
+__device__ __forceinline__ CacheSlice<T> load_slice(const T* p)
+{
+    CacheSlice<T> r;
+#pragma unroll
+    for (int i = 0; i < (sizeof(T) == 2 ? 1 : 2); i++)
+        r.w[i] = reinterpret_cast<const uint4*>(p)[i];
+    return r;
+}
+__device__ __forceinline__ void unpack_slice(const CacheSlice<__half>& r, float* f)
+{
+    const uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        f[2 * k] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[k] & 0xffffu)));
+        f[2 * k + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[k] >> 16)));
+    }
+}
+__device__ __forceinline__ void unpack_slice(const CacheSlice<float>& r, float* f)
+{
+    f[0] = __uint_as_float(r.w[0].x); f[1] = __uint_as_float(r.w[0].y);
+    f[2] = __uint_as_float(r.w[0].z); f[3] = __uint_as_float(r.w[0].w);
+    f[4] = __uint_as_float(r.w[1].x); f[5] = __uint_as_float(r.w[1].y);
+    f[6] = __uint_as_float(r.w[1].z); f[7] = __uint_as_float(r.w[1].w);
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(GQA_THREADS) void gqa_chunk_kernel(GqaArgs a, const T* __restrict__ kc,
+                                                                const T* __restrict__ vc)
+{
+    constexpr int HEAD = 128, PPL = GQA_FCHUNK / 16;   // rows per lane
+    const int g = blockIdx.x, chunk = blockIdx.y;
+    const int start = chunk * GQA_FCHUNK;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int dg = lane & 15, row = lane >> 4;
+    float q[G][8];
+#pragma unroll
+    for (int h = 0; h < G; h++)
+        load8(a.query + static_cast<int64_t>(g * G + h) * HEAD + 8 * dg, q[h]);
+    const int active = min(max(*a.position, 0), a.context - 1);
+    const bool valid = start <= active;
+    const int count = min(GQA_FCHUNK, active + 1 - start);
+    const int64_t row_stride = static_cast<int64_t>(a.kv_heads) * HEAD;
+    const T* kb = kc + static_cast<int64_t>(g) * HEAD + 8 * dg;
+    const T* vb = vc + static_cast<int64_t>(g) * HEAD + 8 * dg;
+    CacheSlice<T> kr[PPL], vr[PPL];
+    if (valid) {   // a chunk past the active rows loads nothing and stores nothing
+#pragma unroll
+        for (int j = 0; j < PPL; j++) {
+            const int64_t r = min(start + wave * (GQA_FCHUNK / 4) + row + 4 * j, a.context - 1);
+            kr[j] = load_slice(kb + r * row_stride);
+            vr[j] = load_slice(vb + r * row_stride);
+        }
+    }
+    // scores q.k / sqrt(128) (a 16-lane row holds one cache row), masked
+    // past the count; exponentials with the hardware exp2 (__expf)
+    const float rscale = 1.0f / sqrtf(static_cast<float>(HEAD));
+    float sc[G][PPL];
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        const int p = wave * (GQA_FCHUNK / 4) + row + 4 * j;
+        float k8[8];
+        unpack_slice(kr[j], k8);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                d = fmaf(q[h][e], k8[e], d);
+            d = row_sum<16>(d);
+            sc[h][j] = p < count ? d * rscale : -INFINITY;
+        }
+    }
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float mh = sc[h][0];
+#pragma unroll
+        for (int j = 1; j < PPL; j++)
+            mh = fmaxf(mh, sc[h][j]);
+        mh = rows_max(mh);
+        m[h] = mh;
+        float lh = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PPL; j++) {
+            const float e = sc[h][j] == -INFINITY ? 0.0f : __expf(sc[h][j] - mh);
+            sc[h][j] = e;
+            lh += e;
+        }
+        l[h] = lh;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            acc[h][e] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        const int p = wave * (GQA_FCHUNK / 4) + row + 4 * j;
+        float v8[8];
+        unpack_slice(vr[j], v8);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            v8[e] = p < count ? v8[e] : 0.0f;   // rows past the count may hold anything
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                acc[h][e] = fmaf(sc[h][j], v8[e], acc[h][e]);
+    }
+    __shared__ float red[4][G][HEAD];
+    __shared__ float wm[4][G], wl[4][G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        l[h] = rows_sum(l[h]);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            acc[h][e] = rows_sum(acc[h][e]);
+    }
+    if (row == 0) {
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                red[wave][h][8 * dg + e] = acc[h][e];
+        if (dg == 0)
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                wm[wave][h] = m[h];
+                wl[wave][h] = l[h];
+            }
+    }
+    __syncthreads();
+    if (!valid)
+        return;
+    for (int i = t; i < G * HEAD; i += GQA_THREADS) {
+        const int h = i / HEAD, d = i % HEAD;
+        const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));   // finite: row start is active
+        float o = 0.0f, lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = wm[w][h] == -INFINITY ? 0.0f : __expf(wm[w][h] - M);   // a wave without active rows adds nothing
+            o = fmaf(red[w][h][d], f, o);
+            lsum = fmaf(wl[w][h], f, lsum);
+        }
+        float* dst = a.workspace + (static_cast<int64_t>(g * G + h) * a.chunks + chunk) * (HEAD + 2);
+        dst[2 + d] = o;
+        if (d == 0) {
+            dst[0] = M;
+            dst[1] = lsum;
+        }
+    }
+}
+
+// The merge of CHUNK-row partials: one workgroup per query head, batches of
+// 8 chunks requested together, merged online (m, l, o rescaled per batch).
+template <int HEAD, int CHUNK>
+__global__ __launch_bounds__(HEAD) void gqa_merge_chunks_kernel(GqaArgs a)
+{
+    const int head = blockIdx.x, d = threadIdx.x;
+    const int active = min(max(*a.position, 0), a.context - 1);
+    const int n = active / CHUNK + 1;
+    const float* src = a.workspace + static_cast<int64_t>(head) * a.chunks * (HEAD + 2);
+    float m = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += 8) {
+        float mc[8], lc[8], oc[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float* pc = src + static_cast<int64_t>(min(c0 + u, n - 1)) * (HEAD + 2);
+            mc[u] = pc[0];
+            lc[u] = pc[1];
+            oc[u] = pc[2 + d];
+        }
+        float bm = m;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u < n)
+                bm = fmaxf(bm, mc[u]);
+        const float r = __expf(m - bm);   // m = -inf before the first batch: r = 0
+        L *= r;
+        O *= r;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u < n) {
+                const float e = __expf(mc[u] - bm);
+                L = fmaf(lc[u], e, L);
+                O = fmaf(oc[u], e, O);
+            }
+        m = bm;
+    }
+    a.output[static_cast<int64_t>(head) * HEAD + d] = O / L;
+}
+
 }  // namespace
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, int n, float eps, hipStream_t s)
@@ -317,6 +526,33 @@ hipError_t launch_gqa(const GqaArgs& a, hipStream_t s)
 {
     const dim3 grid(static_cast<unsigned>(a.query_heads), static_cast<unsigned>(a.chunks));
     const dim3 heads(static_cast<unsigned>(a.query_heads));
+    const int group = a.kv_heads > 0 ? a.query_heads / a.kv_heads : 0;
+    if (a.head_size == 128 && group >= 1 && group <= 4 && group * a.kv_heads == a.query_heads) {
+        // the register-resident form over 128-row chunks
+        const dim3 fgrid(static_cast<unsigned>(a.kv_heads), static_cast<unsigned>((a.context + GQA_FCHUNK - 1) / GQA_FCHUNK));
+        switch (group * 2 + (a.cache_fp16 ? 1 : 0)) {
+#define SI_GQA_CHUNK(G, F, T)                                                                                     \
+    case G * 2 + F:                                                                                               \
+        hipLaunchKernelGGL((gqa_chunk_kernel<T, G>), fgrid, dim3(GQA_THREADS), 0, s, a,                          \
+                           static_cast<const T*>(a.key_cache), static_cast<const T*>(a.value_cache));            \
+        break;
+        SI_GQA_CHUNK(1, 0, float)
+        SI_GQA_CHUNK(2, 0, float)
+        SI_GQA_CHUNK(3, 0, float)
+        SI_GQA_CHUNK(4, 0, float)
+        SI_GQA_CHUNK(1, 1, __half)
+        SI_GQA_CHUNK(2, 1, __half)
+        SI_GQA_CHUNK(3, 1, __half)
+        SI_GQA_CHUNK(4, 1, __half)
+#undef SI_GQA_CHUNK
+        default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return e;
+        hipLaunchKernelGGL((gqa_merge_chunks_kernel<128, GQA_FCHUNK>), heads, dim3(128), 0, s, a);
+        return hipGetLastError();
+    }
 #define SI_GQA(T, H)                                                                                              \
     do {                                                                                                          \
         hipLaunchKernelGGL((gqa_partial_kernel<T, H>), grid, dim3(GQA_THREADS), 0, s, a,                         \

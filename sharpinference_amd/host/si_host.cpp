@@ -772,6 +772,178 @@ void HipVmExecutor::Launch(const InstructionRecording& r)
     }
 }
 
+namespace {
+
+bool IsGemv(const std::vector<HipVmDispatch>& ds, size_t k)
+{
+    return k < ds.size() && (ds[k].recording.operation == "si_hip_gemv" || ds[k].recording.operation == "si_hip_gemv.dense");
+}
+
+bool IsOp(const std::vector<HipVmDispatch>& ds, size_t k, const char* op)
+{
+    return k < ds.size() && ds[k].recording.operation == op;
+}
+
+// The same slot bytes (both tensor parameters).
+bool SameView(const InstructionParameter* a, const InstructionParameter* b)
+{
+    return a && b && a->source == b->source && a->byte_offset == b->byte_offset &&
+           a->tensor.ByteLength() == b->tensor.ByteLength();
+}
+
+// No dispatch after index i reads `slot` before one overwrites it whole:
+// its contents after dispatch i are never observed inside the entry and are
+// replaced before the entry ends.
+bool DeadAfter(const std::vector<HipVmDispatch>& ds, size_t i, const std::string& slot, uint64_t slot_bytes)
+{
+    for (size_t j = i + 1; j < ds.size(); j++) {
+        bool reads = false, overwrites = false;
+        for (const auto& p : ds[j].recording.parameters) {
+            if (p.kind != InstructionParameter::Kind::Tensor || p.source != slot)
+                continue;
+            if (p.access != GraphResourceAccess::Write)
+                reads = true;
+            else if (p.byte_offset == 0 && p.tensor.ByteLength() >= slot_bytes)
+                overwrites = true;
+        }
+        if (reads)
+            return false;
+        if (overwrites)
+            return true;
+    }
+    return false;
+}
+
+// Column count of a mat-vec recording, and whether the fused transforms
+// cover it (the tiled kernel's column set, dword-aligned operands).
+int64_t GemvColumns(const InstructionRecording& g)
+{
+    if (g.operation == "si_hip_gemv")
+        return std::stoll(Find(g.parameters, "columns")->value);
+    const auto* w = Find(g.parameters, "weight");
+    if (!w)
+        w = Find(g.parameters, "matrix");
+    return static_cast<int64_t>(w->tensor.dimensions[1]);
+}
+
+bool FusableColumns(const InstructionRecording& g)
+{
+    const int64_t c = GemvColumns(g);
+    return c == 1024 || c == 2048 || c == 3072 || c == 4096 || c == 6144 || c == 8192;
+}
+
+bool Aligned16(const InstructionParameter* p) { return p && p->byte_offset % 16 == 0; }
+
+}  // namespace
+
+void HipVmExecutor::LaunchGemvFused(const InstructionRecording& g, const void* x, void* y, const void* residual,
+                                    int xform, const void* norm_weight, float eps)
+{
+    const auto* w = Find(g.parameters, "weight");
+    if (!w)
+        w = Find(g.parameters, "matrix");
+    const int fmt = g.operation == "si_hip_gemv" ? FormatId(Find(g.parameters, "format")->value)
+                    : w->tensor.element_type == GraphElementType::Float16 ? SI_HIP_F16
+                                                                          : SI_HIP_F32;
+    Check(si_hip_gemv_fused(context_, fmt, Address(*w), static_cast<const float*>(x), static_cast<float*>(y),
+                            static_cast<int64_t>(w->tensor.dimensions[0]), GemvColumns(g),
+                            static_cast<const float*>(residual), xform, static_cast<const float*>(norm_weight), eps,
+                            nullptr),
+          context_);
+}
+
+size_t HipVmExecutor::FuseAt(const std::vector<HipVmDispatch>& ds, size_t i, bool launch, int* launches)
+{
+    const auto slot_bytes = [&](const InstructionParameter* p) {
+        return program_.Slots()[program_.SlotIndex(p->source)].tensor.ByteLength();
+    };
+    const auto param = [&](size_t k, const char* n) { return Find(ds[k].recording.parameters, n); };
+    *launches = 0;
+    // rms-norm -> mat-vec
+    if (IsOp(ds, i, "si_hip_rms_norm") && IsGemv(ds, i + 1)) {
+        const auto* out = param(i, "output");
+        if (SameView(out, param(i + 1, "input")) && DeadAfter(ds, i + 1, out->source, slot_bytes(out)) &&
+            FusableColumns(ds[i + 1].recording) && Aligned16(param(i, "input")) && Aligned16(param(i, "weight"))) {
+            if (launch)
+                LaunchGemvFused(ds[i + 1].recording, Address(*param(i, "input")), Address(*param(i + 1, "output")),
+                                nullptr, SI_HIP_X_RMSNORM, Address(*param(i, "weight")),
+                                std::stof(param(i, "epsilon")->value));
+            *launches = 1;
+            return 2;
+        }
+    }
+    // [swiglu ->] mat-vec [-> residual-rms-norm -> mat-vec]
+    size_t j = i;
+    const InstructionParameter* swiglu_in = nullptr;
+    if (IsOp(ds, i, "si_hip_swiglu") && IsGemv(ds, i + 1)) {
+        const auto* out = param(i, "output");
+        const auto* in = param(i, "gate_up");
+        if (SameView(out, param(i + 1, "input")) && DeadAfter(ds, i + 1, out->source, slot_bytes(out)) &&
+            FusableColumns(ds[i + 1].recording) && Aligned16(in) &&
+            in->tensor.ElementCount() == 2 * static_cast<uint64_t>(GemvColumns(ds[i + 1].recording))) {
+            swiglu_in = in;
+            j = i + 1;
+        }
+    }
+    if (!IsGemv(ds, j))
+        return 0;
+    const InstructionParameter* x1 = swiglu_in ? swiglu_in : param(j, "input");
+    const int xf1 = swiglu_in ? SI_HIP_X_SWIGLU : SI_HIP_X_PLAIN;
+    if (IsOp(ds, j + 1, "si_hip_residual_rms_norm") && IsGemv(ds, j + 2)) {
+        const auto* product = param(j, "output");
+        const auto* normed = param(j + 1, "output");
+        if (SameView(product, param(j + 1, "residual")) && SameView(normed, param(j + 2, "input")) &&
+            DeadAfter(ds, j + 1, product->source, slot_bytes(product)) &&
+            DeadAfter(ds, j + 2, normed->source, slot_bytes(normed)) && FusableColumns(ds[j + 2].recording) &&
+            Aligned16(param(j + 1, "updated")) && Aligned16(param(j + 1, "weight"))) {
+            if (launch) {
+                // updated = hidden + W1 . x1 (the residual add of the norm, in the product's output)
+                LaunchGemvFused(ds[j].recording, Address(*x1), Address(*param(j + 1, "updated")),
+                                Address(*param(j + 1, "hidden")), xf1, nullptr, 0.0f);
+                LaunchGemvFused(ds[j + 2].recording, Address(*param(j + 1, "updated")),
+                                Address(*param(j + 2, "output")), nullptr, SI_HIP_X_RMSNORM,
+                                Address(*param(j + 1, "weight")), std::stof(param(j + 1, "epsilon")->value));
+            }
+            *launches = 2;
+            return j + 3 - i;
+        }
+    }
+    if (swiglu_in) {
+        if (launch)
+            LaunchGemvFused(ds[j].recording, Address(*x1), Address(*param(j, "output")), nullptr, SI_HIP_X_SWIGLU,
+                            nullptr, 0.0f);
+        *launches = 1;
+        return j + 1 - i;
+    }
+    return 0;
+}
+
+void HipVmExecutor::SetDispatchFusion(bool on)
+{
+    if (on == fuse_)
+        return;
+    for (auto& kv : plans_)
+        si_hip_plan_destroy(kv.second);
+    plans_.clear();
+    fuse_ = on;
+}
+
+int HipVmExecutor::LaunchCount(const std::string& entry)
+{
+    const auto it = program_.Entries().find(entry);
+    if (it == program_.Entries().end())
+        throw ArgumentException("Unknown entry '" + entry + "'.");
+    const auto& ds = it->second;
+    int count = 0;
+    for (size_t i = 0; i < ds.size();) {
+        int n = 0;
+        const size_t used = fuse_ ? FuseAt(ds, i, false, &n) : 0;
+        count += used ? n : 1;
+        i += used ? used : 1;
+    }
+    return count;
+}
+
 si_hip_plan* HipVmExecutor::PrepareEntry(const std::string& entry)
 {
     const auto it = program_.Entries().find(entry);
@@ -782,8 +954,14 @@ si_hip_plan* HipVmExecutor::PrepareEntry(const std::string& entry)
         return cached->second;
     Check(si_hip_plan_begin(context_), context_);
     try {
-        for (const auto& d : it->second)
-            Launch(d.recording);
+        const auto& ds = it->second;
+        for (size_t i = 0; i < ds.size();) {
+            int n = 0;
+            const size_t used = fuse_ ? FuseAt(ds, i, true, &n) : 0;
+            if (used == 0)
+                Launch(ds[i].recording);
+            i += used ? used : 1;
+        }
     } catch (...) {
         si_hip_plan* broken = nullptr;
         if (si_hip_plan_end(context_, &broken) == SI_HIP_OK)

@@ -466,6 +466,21 @@ std::string Sha256Hex(const void* data, size_t length);
 // The executor of a HipVmProgram on one device (D3D12VmExecutor.cs): one
 // persistent device buffer per slot, exact-size uploads, entries recorded
 // once into plans and replayed with one submission.
+//
+// Dispatch fusion (on unless switched off): when an entry is recorded, a
+// mat-vec whose input comes from the dispatch just before it takes that
+// dispatch's work into its own launch, as the reference's graph optimizer
+// elides a cast its consumer can absorb (VmGraphOptimizer.cs:198-299):
+//   rms-norm -> mat-vec            : one mat-vec with the RMSNorm fused in;
+//   swiglu -> mat-vec              : one mat-vec with SwiGLU fused in;
+//   mat-vec -> residual-rms-norm -> mat-vec : the first mat-vec adds the
+//                                    residual into the updated hidden state,
+//                                    the second fuses the RMSNorm.
+// Only when every intermediate the fused launches no longer write (the
+// normalised vector, the SwiGLU output, the first product) is overwritten
+// later in the entry before anything reads it, so no dispatch of the entry
+// and no read-back after it observes a difference beyond FP32 rounding (the
+// fused RMSNorm scales each row's sum instead of each input).
 class HipVmExecutor {
 public:
     explicit HipVmExecutor(HipVmProgram program, int device = 0);
@@ -486,11 +501,22 @@ public:
     // GPU microseconds per replay over `repetitions` (1..1024) back-to-back
     // replays (D3D12VmExecutor.cs:452-478).
     double MeasureGpuMicroseconds(const std::string& entry, int repetitions = 8);
+    // Switches dispatch fusion (recorded plans are dropped and re-recorded).
+    void SetDispatchFusion(bool on);
+    bool DispatchFusion() const { return fuse_; }
+    // Launches one recording of `entry` makes with the current fusion setting.
+    int LaunchCount(const std::string& entry);
 
 private:
     si_hip_plan* PrepareEntry(const std::string& entry);
     void Launch(const InstructionRecording& recording);
     void* Address(const InstructionParameter& parameter) const;
+    // The fused group starting at dispatch i: its dispatch count (0: none),
+    // and, when `launch`, the launches it makes (their count in *launches).
+    size_t FuseAt(const std::vector<HipVmDispatch>& ds, size_t i, bool launch, int* launches);
+    void LaunchGemvFused(const InstructionRecording& gemv, const void* x, void* y, const void* residual, int xform,
+                         const void* norm_weight, float eps);
+    bool fuse_ = true;
 
     HipVmProgram program_;
     si_hip_context* context_ = nullptr;

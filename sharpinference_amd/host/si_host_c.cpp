@@ -146,6 +146,24 @@ int sih_program_measure_us(sih_program* program, const char* entry, int repetiti
     });
 }
 
+int sih_program_set_fusion(sih_program* program, int on)
+{
+    return Guard([&] {
+        if (!program)
+            throw ArgumentException("sih_program_set_fusion: null argument");
+        program->executor->SetDispatchFusion(on != 0);
+    });
+}
+
+int sih_program_launch_count(sih_program* program, const char* entry, int* count)
+{
+    return Guard([&] {
+        if (!program || !entry || !count)
+            throw ArgumentException("sih_program_launch_count: null argument");
+        *count = program->executor->LaunchCount(entry);
+    });
+}
+
 int sih_program_dispatch_count(const sih_program* program, const char* entry, int* count)
 {
     return Guard([&] {

@@ -37,6 +37,11 @@ int sih_program_readback(sih_program* program, const char* slot, void* bytes, ui
 int sih_program_execute(sih_program* program, const char* entry);
 int sih_program_measure_us(sih_program* program, const char* entry, int repetitions, double* microseconds);
 int sih_program_dispatch_count(const sih_program* program, const char* entry, int* count);
+/* Dispatch fusion of the executor (on by default; HipVmExecutor's comment
+ * lists the fused pairs): on = 0 switches it off (plans are re-recorded). */
+int sih_program_set_fusion(sih_program* program, int on);
+/* Launches one execution of `entry` makes with the current fusion setting. */
+int sih_program_launch_count(sih_program* program, const char* entry, int* count);
 /* VmProgram XML of the program (the reference's schema, target "Hip"):
  * with buffer NULL only *length (bytes, without a terminator) is set. */
 int sih_program_serialize(const sih_program* program, char* buffer, uint64_t capacity, uint64_t* length);

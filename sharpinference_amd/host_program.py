@@ -54,6 +54,8 @@ def host_lib() -> ctypes.CDLL:
             "sih_program_execute": [vp, cp],
             "sih_program_measure_us": [vp, cp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)],
             "sih_program_dispatch_count": [vp, cp, ctypes.POINTER(ctypes.c_int)],
+            "sih_program_set_fusion": [vp, ctypes.c_int],
+            "sih_program_launch_count": [vp, cp, ctypes.POINTER(ctypes.c_int)],
             "sih_program_serialize": [vp, vp, u64, ctypes.POINTER(u64)],
             "sih_program_create_from_xml": [cp, ctypes.c_int, ctypes.POINTER(vp)],
             "sih_program_export_artifact": [vp, vp, u64, ctypes.POINTER(u64)],
@@ -137,6 +139,18 @@ class Phi4OpProgram:
     def dispatch_count(self, entry: str = "decode") -> int:
         n = ctypes.c_int(0)
         _check(host_lib().sih_program_dispatch_count(self._h, entry.encode(), ctypes.byref(n)))
+        return n.value
+
+    def set_fusion(self, on: bool) -> None:
+        """Dispatch fusion of the executor (on by default): a mat-vec takes in
+        the rms-norm / swiglu / residual-rms-norm before it when the skipped
+        intermediates are overwritten before anything reads them."""
+        _check(host_lib().sih_program_set_fusion(self._h, int(bool(on))))
+
+    def launch_count(self, entry: str = "decode") -> int:
+        """Launches one execution of `entry` makes with the current fusion setting."""
+        n = ctypes.c_int(0)
+        _check(host_lib().sih_program_launch_count(self._h, entry.encode(), ctypes.byref(n)))
         return n.value
 
     def load_kv(self, layer: int, k_fp16: np.ndarray, v_fp16: np.ndarray) -> None:

@@ -28,11 +28,24 @@ def _gate(gl, ol, what):
     assert np.all(d <= bound), f"{what}: worst {np.max(d / bound):.2f} of the gate"
 
 
-def _steps_vs_oracle(cfg, weights, kv, steps):
+def fused_launches(layers):
+    """Launches of the decode entry with dispatch fusion: gather, the first
+    rms-norm in the qkv mat-vec, six per layer (rope-kv-write, attention, the
+    output mat-vec adding the residual, the up mat-vec with the norm, the
+    down mat-vec with SwiGLU and the residual, the next qkv mat-vec with the
+    norm); the last layer keeps the intermediates the entry leaves behind
+    (eight dispatches), then the head and argmax."""
+    return 2 + 6 * (layers - 1) + 8 + 2
+
+
+def _steps_vs_oracle(cfg, weights, kv, steps, fuse=True):
     prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True)
     ref = orc.Phi4Oracle(cfg, weights)
     try:
         assert prog.dispatch_count() == 2 + 9 * cfg.layers + 2
+        if not fuse:
+            prog.set_fusion(False)
+        assert prog.launch_count() == (fused_launches(cfg.layers) if fuse else prog.dispatch_count())
         for l, (k, v) in enumerate(kv):
             prog.load_kv(l, k, v)
             ref.k[l][...] = k
@@ -53,12 +66,38 @@ def _steps_vs_oracle(cfg, weights, kv, steps):
         prog.close()
 
 
-def test_small_quantized_program_matches_oracle(hip):
+@pytest.mark.parametrize("fuse", [True, False], ids=["fused", "dispatch-by-dispatch"])
+def test_small_quantized_program_matches_oracle(hip, fuse):
     cfg = phi4.Phi4Config(layers=3, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=5000, capacity=256,
                           rope_scale=1.19)
     weights = phi4.synth_weights(cfg, seed=41)
     kv = phi4.synth_kv(cfg, length=70, seed=42)
-    _steps_vs_oracle(cfg, weights, kv, [(11, 70), (4999, 71), (0, 72), (123, 0)])
+    _steps_vs_oracle(cfg, weights, kv, [(11, 70), (4999, 71), (0, 72), (123, 0)], fuse)
+
+
+def test_fusion_keeps_the_intermediates_an_entry_leaves(hip):
+    """What the entry leaves in its intermediate slots is unchanged by the
+    fusion (the last layer's normalised vector, SwiGLU output and products
+    are written as the dispatches write them), and the logits agree to FP32
+    rounding."""
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=3000, capacity=128)
+    weights = phi4.synth_weights(cfg, seed=49)
+    kv = phi4.synth_kv(cfg, length=40, seed=50)
+    out = {}
+    for fuse in (True, False):
+        prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True)
+        try:
+            prog.set_fusion(fuse)
+            for l, (k, v) in enumerate(kv):
+                prog.load_kv(l, k, v)
+            prog.forward_token(9, 40)
+            out[fuse] = {s: prog.readback(s, np.float32).copy()
+                         for s in ("normalized", "activated", "projected", "down", "hidden", "logits")}
+        finally:
+            prog.close()
+    for s, a in out[True].items():
+        b = out[False][s]
+        assert np.allclose(a, b, rtol=1e-4, atol=1e-4 * max(1.0, float(np.max(np.abs(b))))), s
 
 
 @pytest.mark.parametrize("fmt", [native.F16, native.F32], ids=["f16", "f32"])

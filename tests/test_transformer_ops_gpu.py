@@ -150,7 +150,9 @@ def _gqa(hip, fmt, heads, kv_heads, head, context, position, seed):
 @pytest.mark.parametrize("fmt", [native.F32, native.F16], ids=["f32", "f16"])
 @pytest.mark.parametrize("heads,kv_heads,head,context,position",
                          [(24, 8, 128, 4096, 2048), (24, 8, 128, 64, 0), (8, 8, 64, 300, 299), (4, 2, 256, 128, 77),
-                          (6, 2, 128, 100, 500), (6, 2, 128, 100, -3)])
+                          (6, 2, 128, 100, 500), (6, 2, 128, 100, -3),
+                          # head 128 (128-row chunks): groups 1, 2 and 4, chunk edges and a partial last chunk
+                          (8, 8, 128, 300, 299), (16, 4, 128, 1000, 129), (4, 2, 128, 257, 256), (16, 4, 128, 4096, 4095)])
 def test_grouped_query_attention(hip, fmt, heads, kv_heads, head, context, position):
     q, kc, vc, out, t64, active = _gqa(hip, fmt, heads, kv_heads, head, context, position, heads + head + position)
     assert np.linalg.norm(out - t64) / np.linalg.norm(t64) <= 1e-5
