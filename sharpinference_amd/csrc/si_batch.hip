@@ -249,7 +249,7 @@ __global__ __launch_bounds__(THREADS) void batch_rope_kv_write_kernel(BatchRopeA
 // group's queries of every live row are staged in LDS, and each query's four
 // dot products are summed across the 16 lanes with DPP.  Positions past a
 // row's own position get -FLT_MAX; a chunk wholly past the batch's last
-// position writes only those.
+// position writes only those, with coalesced stores and no products.
 template <typename T>
 __global__ __launch_bounds__(THREADS) void batch_gqa_scores_kernel(BatchAttentionArgs a, const T* __restrict__ kc)
 {
@@ -261,21 +261,30 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_scores_kernel(BatchAttentio
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int dg = lane & 15, row = lane >> 4;
     const int j0 = chunk * BATCH_CHUNK;
+    const int64_t last = static_cast<int64_t>(start) + valid - 1;   // the batch's last position
+    const bool any = nq > 0 && last >= 0 && j0 <= last;
+    if (!any) {
+        // every score of the chunk is masked: coalesced -FLT_MAX stores, no products
+        const int jn = min(BATCH_CHUNK, a.context - j0);
+        for (int i = t; i < nq * BATCH_CHUNK; i += THREADS) {
+            const int qi = i / BATCH_CHUNK, jj = i % BATCH_CHUNK;
+            const int r = qi / group, h = g * group + qi % group;
+            if (jj < jn)
+                a.out[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j0 + jj] = -FLT_MAX;
+        }
+        return;   // the whole workgroup (no barrier is reached)
+    }
+    float k[4][8];   // requested before the queries are staged
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int j = min(j0 + wave * 16 + row + 4 * i, a.context - 1);
+        load8(kc + (static_cast<int64_t>(j) * a.kv_heads + g) * BATCH_HEAD + 8 * dg, k[i]);
+    }
     for (int i = t; i < nq * (BATCH_HEAD / 4); i += THREADS) {
         const int qi = i / (BATCH_HEAD / 4), c4 = i % (BATCH_HEAD / 4);
         const int r = qi / group, h = g * group + qi % group;
         qs[i] = reinterpret_cast<const float4*>(a.query +
                                                 (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD)[c4];
-    }
-    const int64_t last = static_cast<int64_t>(start) + valid - 1;   // the batch's last position
-    const bool any = nq > 0 && last >= 0 && j0 <= last;
-    float k[4][8];
-    if (any) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int j = min(j0 + wave * 16 + row + 4 * i, a.context - 1);
-            load8(kc + (static_cast<int64_t>(j) * a.kv_heads + g) * BATCH_HEAD + 8 * dg, k[i]);
-        }
     }
     __syncthreads();
     const float scale = 1.0f / sqrtf(static_cast<float>(BATCH_HEAD));
@@ -283,8 +292,8 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_scores_kernel(BatchAttentio
     for (int qi = 0; qi < nq; qi++) {
         const int r = qi / group, h = g * group + qi % group;
         const int64_t active = static_cast<int64_t>(start) + r;
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (any) {
+        float s[4];
+        {
             const float4 q0 = qs[qi * (BATCH_HEAD / 4) + 2 * dg], q1 = qs[qi * (BATCH_HEAD / 4) + 2 * dg + 1];
             const float q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
@@ -330,12 +339,14 @@ __global__ __launch_bounds__(THREADS) void batch_causal_softmax_kernel(const flo
 }
 
 // Values, first pass: one workgroup per (KV head, 64 cache positions); lane
-// l holds channels 2l, 2l + 1 and wave w the queries w, w + 4, ... (eight at
-// a time); the chunk's probabilities of every live query are staged in LDS.
+// l holds channels 2l, 2l + 1 and wave w the queries w, w + 4, ...; the
+// chunk's probabilities of every live query are staged in LDS.
 // Partial sums over the chunk's positions up to the batch's last position
 // go to the workspace [chunk][row][head][128]; the second pass adds the
 // chunks up to each row's own position in order.
 constexpr int VQ = 8;   // queries per wave per pass
+constexpr int VPASSES = (BATCH_MAX * BATCH_GROUP_MAX + 4 * VQ - 1) / (4 * VQ);   // passes covering every query
+constexpr int VB = 16;  // value rows requested together
 
 template <typename T>
 __global__ __launch_bounds__(THREADS) void batch_gqa_values_partial_kernel(BatchAttentionArgs a,
@@ -361,34 +372,50 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_values_partial_kernel(Batch
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const T* vbase = vc + static_cast<int64_t>(g) * BATCH_HEAD + 2 * lane;
     const int64_t vstride = static_cast<int64_t>(a.kv_heads) * BATCH_HEAD;
-    for (int q0 = wave; q0 < nq; q0 += 4 * VQ) {
-        float2 acc[VQ];
+    // every query pass of the wave (queries wave + 32 p + 4 m) accumulates
+    // while the chunk's V rows stream through in batches of VB, requested
+    // together: one memory round trip per batch instead of one per row
+    float2 acc[VPASSES][VQ];
+#pragma unroll
+    for (int p = 0; p < VPASSES; p++)
 #pragma unroll
         for (int m = 0; m < VQ; m++)
-            acc[m] = make_float2(0.0f, 0.0f);
-        for (int jj = 0; jj < jn; jj++) {
-            const float2 v = load2(vbase + static_cast<int64_t>(j0 + jj) * vstride);
+            acc[p][m] = make_float2(0.0f, 0.0f);
+    for (int jb = 0; jb < jn; jb += VB) {
+        float2 v[VB];
 #pragma unroll
-            for (int m = 0; m < VQ; m++) {
-                const int qi = q0 + 4 * m;
-                if (qi < nq) {
-                    const float p = ps[qi][jj];
-                    acc[m].x = fmaf(p, v.x, acc[m].x);
-                    acc[m].y = fmaf(p, v.y, acc[m].y);
-                }
+        for (int u = 0; u < VB; u++)
+            v[u] = load2(vbase + static_cast<int64_t>(j0 + min(jb + u, jn - 1)) * vstride);
+#pragma unroll
+        for (int u = 0; u < VB; u++) {
+            const int jj = jb + u;
+            if (jj < jn) {   // uniform across the workgroup
+#pragma unroll
+                for (int p = 0; p < VPASSES; p++)
+#pragma unroll
+                    for (int m = 0; m < VQ; m++) {
+                        const int qi = wave + 4 * VQ * p + 4 * m;
+                        if (qi < nq) {
+                            const float w = ps[qi][jj];
+                            acc[p][m].x = fmaf(w, v[u].x, acc[p][m].x);
+                            acc[p][m].y = fmaf(w, v[u].y, acc[p][m].y);
+                        }
+                    }
             }
         }
+    }
+#pragma unroll
+    for (int p = 0; p < VPASSES; p++)
 #pragma unroll
         for (int m = 0; m < VQ; m++) {
-            const int qi = q0 + 4 * m;
+            const int qi = wave + 4 * VQ * p + 4 * m;
             if (qi < nq) {
                 const int r = qi / group, h = g * group + qi % group;
                 float* dst = a.workspace +
                              ((static_cast<int64_t>(chunk) * a.batch + r) * a.query_heads + h) * BATCH_HEAD + 2 * lane;
-                *reinterpret_cast<float2*>(dst) = acc[m];
+                *reinterpret_cast<float2*>(dst) = acc[p][m];
             }
         }
-    }
 }
 
 // Values, second pass: one workgroup per (live row, query head).
