@@ -32,6 +32,8 @@ namespace {
 constexpr int NORM_THREADS = 1024;
 constexpr int THREADS = 256;
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float half_bits(uint32_t h)
 {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xffffu)));
@@ -244,26 +246,29 @@ __global__ __launch_bounds__(THREADS) void batch_rope_kv_write_kernel(BatchRopeA
 
 // ---- attention ---------------------------------------------------------------------------
 
-// One workgroup per (KV head, 64 cache positions): each lane holds an
-// 8-value slice of four positions' keys (16 lanes per position), the
-// group's queries of every live row are staged in LDS, and each query's four
-// dot products are summed across the 16 lanes with DPP.  Positions past a
-// row's own position get -FLT_MAX; a chunk wholly past the batch's last
-// position writes only those, with coalesced stores and no products.
+// Scores: one workgroup per (KV head, 64 cache positions).  Wave w takes
+// positions j0 + 16 w + n (n < 16) as the 16 columns of its
+// v_mfma_f32_16x16x4_f32 products and the live queries (query qi = row *
+// group + head in group) 16 a pass as the rows.  Lane (n, c) = (l % 16,
+// l / 16) holds dims 32 c .. 32 c + 31 of position n's key and of the
+// pass's query n; instruction s (s < 32) takes dim 32 c + s from lane group
+// c, so the 32 products add up all 128 dims of each query-key dot product
+// (in another order).  D[i][n] (query 16 p + i, position n) is element i % 4
+// of lane n + 16 (i / 4).  The next pass's queries are requested before the
+// current pass's products.  Positions past a row's own position get
+// -FLT_MAX; a chunk wholly past the batch's last position writes only those,
+// with coalesced stores and no products.
 template <typename T>
 __global__ __launch_bounds__(THREADS) void batch_gqa_scores_kernel(BatchAttentionArgs a, const T* __restrict__ kc)
 {
-    __shared__ float4 qs[BATCH_MAX * BATCH_GROUP_MAX * (BATCH_HEAD / 4)];
     const int g = blockIdx.x, chunk = blockIdx.y;
     const int group = a.query_heads / a.kv_heads;
     const int start = a.control[0], valid = min(a.control[1], a.batch);
-    const int nq = max(valid, 0) * group;   // query qi = row * group + head-in-group
+    const int nq = max(valid, 0) * group;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int dg = lane & 15, row = lane >> 4;
     const int j0 = chunk * BATCH_CHUNK;
     const int64_t last = static_cast<int64_t>(start) + valid - 1;   // the batch's last position
-    const bool any = nq > 0 && last >= 0 && j0 <= last;
-    if (!any) {
+    if (nq == 0 || last < 0 || j0 > last) {
         // every score of the chunk is masked: coalesced -FLT_MAX stores, no products
         const int jn = min(BATCH_CHUNK, a.context - j0);
         for (int i = t; i < nq * BATCH_CHUNK; i += THREADS) {
@@ -272,48 +277,70 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_scores_kernel(BatchAttentio
             if (jj < jn)
                 a.out[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j0 + jj] = -FLT_MAX;
         }
-        return;   // the whole workgroup (no barrier is reached)
+        return;
     }
-    float k[4][8];   // requested before the queries are staged
+    const int n = lane & 15, c = lane >> 4;
+    const int j = j0 + 16 * wave + n;   // this lane's key position
+    float k[32];
+    {
+        const T* src = kc + (static_cast<int64_t>(min(j, a.context - 1)) * a.kv_heads + g) * BATCH_HEAD + 32 * c;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int j = min(j0 + wave * 16 + row + 4 * i, a.context - 1);
-        load8(kc + (static_cast<int64_t>(j) * a.kv_heads + g) * BATCH_HEAD + 8 * dg, k[i]);
+        for (int i = 0; i < 4; i++)
+            load8(src + 8 * i, k + 8 * i);
     }
-    for (int i = t; i < nq * (BATCH_HEAD / 4); i += THREADS) {
-        const int qi = i / (BATCH_HEAD / 4), c4 = i % (BATCH_HEAD / 4);
-        const int r = qi / group, h = g * group + qi % group;
-        qs[i] = reinterpret_cast<const float4*>(a.query +
-                                                (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD)[c4];
-    }
-    __syncthreads();
+    auto load_q = [&](int p, float* q) {
+        const int qi = 16 * p + n;
+        if (qi < nq) {
+            const int r = qi / group, h = g * group + qi % group;
+            const float* src = a.query + (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + 32 * c;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                load8(src + 8 * i, q + 8 * i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++)
+                q[i] = 0.0f;
+        }
+    };
     const float scale = 1.0f / sqrtf(static_cast<float>(BATCH_HEAD));
-    const int j = j0 + wave * 16 + row + 4 * dg;   // the position lane dg < 4 of this row stores
-    for (int qi = 0; qi < nq; qi++) {
-        const int r = qi / group, h = g * group + qi % group;
-        const int64_t active = static_cast<int64_t>(start) + r;
-        float s[4];
-        {
-            const float4 q0 = qs[qi * (BATCH_HEAD / 4) + 2 * dg], q1 = qs[qi * (BATCH_HEAD / 4) + 2 * dg + 1];
-            const float q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    auto run = [&](int p, const float* q) {
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float d = 0.0f;
+        for (int s = 0; s < 32; s++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(q[s], k[s], acc, 0, 0, 0);
+        if (j >= a.context)
+            return;
 #pragma unroll
-                for (int c = 0; c < 8; c++)
-                    d = fmaf(q[c], k[i][c], d);
-                s[i] = row_sum16(d);
+        for (int e = 0; e < 4; e++) {
+            const int qi = 16 * p + 4 * c + e;
+            if (qi < nq) {
+                const int r = qi / group, h = g * group + qi % group;
+                const int64_t active = static_cast<int64_t>(start) + r;
+                a.out[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j] =
+                    active >= 0 && j <= active ? acc[e] * scale : -FLT_MAX;
             }
         }
-        if (dg < 4 && j < a.context) {
-            const float sv = dg == 0 ? s[0] : dg == 1 ? s[1] : dg == 2 ? s[2] : s[3];
-            const float v = active >= 0 && j <= active ? sv * scale : -FLT_MAX;
-            a.out[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j] = v;
-        }
+    };
+    const int passes = (nq + 15) / 16;
+    float q0[32], q1[32];
+    load_q(0, q0);
+    for (int p = 0; p < passes; p += 2) {
+        if (p + 1 < passes)
+            load_q(p + 1, q1);
+        run(p, q0);
+        if (p + 2 < passes)
+            load_q(p + 2, q0);
+        if (p + 1 < passes)
+            run(p + 1, q1);
     }
 }
 
-// One workgroup per (live row, query head).
+// One workgroup per (live row, query head).  Up to SOFTMAX_HELD positions a
+// thread (context up to THREADS * SOFTMAX_HELD) the scores are read once and
+// held in registers for the max, the sum and the write; longer rows read
+// them three times.
+constexpr int SOFTMAX_HELD = 16;
+
 __global__ __launch_bounds__(THREADS) void batch_causal_softmax_kernel(const float* __restrict__ scores,
                                                                        float* __restrict__ probs, int heads,
                                                                        int context,
@@ -326,33 +353,61 @@ __global__ __launch_bounds__(THREADS) void batch_causal_softmax_kernel(const flo
     const int64_t active = static_cast<int64_t>(control[0]) + r;
     const int last = active < 0 ? -1 : static_cast<int>(min(active, static_cast<int64_t>(context) - 1));
     const int64_t base = (static_cast<int64_t>(r) * heads + h) * context;
+    const int t = threadIdx.x;
+    if (last < THREADS * SOFTMAX_HELD) {
+        float v[SOFTMAX_HELD];
+        float m = -FLT_MAX;
+#pragma unroll
+        for (int i = 0; i < SOFTMAX_HELD; i++) {
+            const int j = t + THREADS * i;
+            v[i] = j <= last ? scores[base + j] : -FLT_MAX;
+            m = fmaxf(m, v[i]);
+        }
+        m = block_max<THREADS>(m, red);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SOFTMAX_HELD; i++) {
+            const int j = t + THREADS * i;
+            v[i] = j <= last ? expf(v[i] - m) : 0.0f;
+            sum += v[i];
+        }
+        sum = block_sum<THREADS>(sum, red);
+#pragma unroll
+        for (int i = 0; i < SOFTMAX_HELD; i++) {
+            const int j = t + THREADS * i;
+            if (j < context)
+                probs[base + j] = j <= last ? v[i] / sum : 0.0f;
+        }
+        for (int j = t + THREADS * SOFTMAX_HELD; j < context; j += THREADS)
+            probs[base + j] = 0.0f;
+        return;
+    }
     float m = -FLT_MAX;
-    for (int j = threadIdx.x; j <= last; j += THREADS)
+    for (int j = t; j <= last; j += THREADS)
         m = fmaxf(m, scores[base + j]);
     m = block_max<THREADS>(m, red);
     float sum = 0.0f;
-    for (int j = threadIdx.x; j <= last; j += THREADS)
+    for (int j = t; j <= last; j += THREADS)
         sum += expf(scores[base + j] - m);
     sum = block_sum<THREADS>(sum, red);
-    for (int j = threadIdx.x; j < context; j += THREADS)
+    for (int j = t; j < context; j += THREADS)
         probs[base + j] = j <= last ? expf(scores[base + j] - m) / sum : 0.0f;
 }
 
-// Values, first pass: one workgroup per (KV head, 64 cache positions); lane
-// l holds channels 2l, 2l + 1 and wave w the queries w, w + 4, ...; the
-// chunk's probabilities of every live query are staged in LDS.
-// Partial sums over the chunk's positions up to the batch's last position
-// go to the workspace [chunk][row][head][128]; the second pass adds the
-// chunks up to each row's own position in order.
-constexpr int VQ = 8;   // queries per wave per pass
-constexpr int VPASSES = (BATCH_MAX * BATCH_GROUP_MAX + 4 * VQ - 1) / (4 * VQ);   // passes covering every query
-constexpr int VB = 16;  // value rows requested together
-
+// Values, first pass: one workgroup per (KV head, 64 cache positions).  Wave
+// w takes channels 32 w .. 32 w + 31 as two 16-column tiles of its
+// v_mfma_f32_16x16x4_f32 products, column n of tile u being channel 32 w +
+// 2 n + u (one channel pair per lane and position), and the live queries 16
+// a pass as the rows.  Instruction s (s < 16) takes position j0 + 16 c + s
+// from lane group c = l / 16, so a lane's probabilities are 16 consecutive
+// floats of its query's row.  Positions past the batch's last position (or
+// the context) take probability 0 and value 0, whatever the cache holds
+// there.  Partial sums go to the workspace [chunk][row][head][128]; the
+// second pass adds the chunks up to each row's own position in order.
 template <typename T>
 __global__ __launch_bounds__(THREADS) void batch_gqa_values_partial_kernel(BatchAttentionArgs a,
                                                                            const T* __restrict__ vc)
 {
-    __shared__ float ps[BATCH_MAX * BATCH_GROUP_MAX][BATCH_CHUNK];
     const int g = blockIdx.x, chunk = blockIdx.y;
     const int group = a.query_heads / a.kv_heads;
     const int start = a.control[0], valid = min(a.control[1], a.batch);
@@ -361,64 +416,82 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_values_partial_kernel(Batch
     const int j0 = chunk * BATCH_CHUNK;
     if (nq == 0 || last < 0 || j0 > last)
         return;   // the whole workgroup: no live position in this chunk
-    const int jn = static_cast<int>(min(static_cast<int64_t>(BATCH_CHUNK), min(last, static_cast<int64_t>(a.context) - 1) - j0 + 1));
-    for (int i = threadIdx.x; i < nq * BATCH_CHUNK; i += THREADS) {
-        const int qi = i / BATCH_CHUNK, jj = i % BATCH_CHUNK;
-        const int r = qi / group, h = g * group + qi % group;
-        ps[qi][jj] = jj < jn ? a.probabilities[(static_cast<int64_t>(r) * a.query_heads + h) * a.context + j0 + jj]
-                             : 0.0f;
-    }
-    __syncthreads();
+    const int jl = static_cast<int>(min(last, static_cast<int64_t>(a.context) - 1));   // last position read
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const T* vbase = vc + static_cast<int64_t>(g) * BATCH_HEAD + 2 * lane;
-    const int64_t vstride = static_cast<int64_t>(a.kv_heads) * BATCH_HEAD;
-    // every query pass of the wave (queries wave + 32 p + 4 m) accumulates
-    // while the chunk's V rows stream through in batches of VB, requested
-    // together: one memory round trip per batch instead of one per row
-    float2 acc[VPASSES][VQ];
+    const int n = lane & 15, c = lane >> 4;
+    const int jc = j0 + 16 * c;   // the lane group's first position
+    float2 v[16];
+    {
+        const T* src = vc + static_cast<int64_t>(g) * BATCH_HEAD + 32 * wave + 2 * n;
+        const int64_t stride = static_cast<int64_t>(a.kv_heads) * BATCH_HEAD;
 #pragma unroll
-    for (int p = 0; p < VPASSES; p++)
-#pragma unroll
-        for (int m = 0; m < VQ; m++)
-            acc[p][m] = make_float2(0.0f, 0.0f);
-    for (int jb = 0; jb < jn; jb += VB) {
-        float2 v[VB];
-#pragma unroll
-        for (int u = 0; u < VB; u++)
-            v[u] = load2(vbase + static_cast<int64_t>(j0 + min(jb + u, jn - 1)) * vstride);
-#pragma unroll
-        for (int u = 0; u < VB; u++) {
-            const int jj = jb + u;
-            if (jj < jn) {   // uniform across the workgroup
-#pragma unroll
-                for (int p = 0; p < VPASSES; p++)
-#pragma unroll
-                    for (int m = 0; m < VQ; m++) {
-                        const int qi = wave + 4 * VQ * p + 4 * m;
-                        if (qi < nq) {
-                            const float w = ps[qi][jj];
-                            acc[p][m].x = fmaf(w, v[u].x, acc[p][m].x);
-                            acc[p][m].y = fmaf(w, v[u].y, acc[p][m].y);
-                        }
-                    }
-            }
+        for (int s = 0; s < 16; s++) {
+            const float2 f = load2(src + min(jc + s, jl) * stride);   // rows past jl: read jl's, use 0
+            v[s] = jc + s <= jl ? f : make_float2(0.0f, 0.0f);
         }
     }
+    const bool whole = jc + 15 <= jl && (a.context & 3) == 0 &&
+                       (reinterpret_cast<uintptr_t>(a.probabilities) & 15) == 0;
+    auto load_p = [&](int p, float* pr) {
+        const int qi = 16 * p + n;
+        if (qi < nq) {
+            const int r = qi / group, h = g * group + qi % group;
+            const float* src = a.probabilities + (static_cast<int64_t>(r) * a.query_heads + h) * a.context + jc;
+            if (whole) {
 #pragma unroll
-    for (int p = 0; p < VPASSES; p++)
+                for (int i = 0; i < 4; i++) {
+                    const float4 f = reinterpret_cast<const float4*>(src)[i];
+                    pr[4 * i] = f.x; pr[4 * i + 1] = f.y; pr[4 * i + 2] = f.z; pr[4 * i + 3] = f.w;
+                }
+            } else {
 #pragma unroll
-        for (int m = 0; m < VQ; m++) {
-            const int qi = wave + 4 * VQ * p + 4 * m;
+                for (int s = 0; s < 16; s++) {
+                    const float f = src[max(min(s, jl - jc), j0 - jc)];   // inside the row
+                    pr[s] = jc + s <= jl ? f : 0.0f;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+                pr[s] = 0.0f;
+        }
+    };
+    auto run = [&](int p, const float* pr) {
+        floatx4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            lo = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[s], v[s].x, lo, 0, 0, 0);
+            hi = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[s], v[s].y, hi, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int qi = 16 * p + 4 * c + e;
             if (qi < nq) {
                 const int r = qi / group, h = g * group + qi % group;
-                float* dst = a.workspace +
-                             ((static_cast<int64_t>(chunk) * a.batch + r) * a.query_heads + h) * BATCH_HEAD + 2 * lane;
-                *reinterpret_cast<float2*>(dst) = acc[p][m];
+                float* dst = a.workspace + ((static_cast<int64_t>(chunk) * a.batch + r) * a.query_heads + h) *
+                                               BATCH_HEAD + 32 * wave + 2 * n;
+                *reinterpret_cast<float2*>(dst) = make_float2(lo[e], hi[e]);
             }
         }
+    };
+    const int passes = (nq + 15) / 16;
+    float p0[16], p1[16];
+    load_p(0, p0);
+    for (int p = 0; p < passes; p += 2) {
+        if (p + 1 < passes)
+            load_p(p + 1, p1);
+        run(p, p0);
+        if (p + 2 < passes)
+            load_p(p + 2, p0);
+        if (p + 1 < passes)
+            run(p + 1, p1);
+    }
 }
 
-// Values, second pass: one workgroup per (live row, query head).
+// Values, second pass: one workgroup per (live row, query head); the chunk
+// partials are requested VALUES_BATCH at a time and added in chunk order.
+constexpr int VALUES_BATCH = 8;
+
 __global__ __launch_bounds__(BATCH_HEAD) void batch_gqa_values_reduce_kernel(BatchAttentionArgs a)
 {
     const int r = blockIdx.x / a.query_heads, h = blockIdx.x % a.query_heads;
@@ -430,8 +503,15 @@ __global__ __launch_bounds__(BATCH_HEAD) void batch_gqa_values_reduce_kernel(Bat
         const int n = static_cast<int>(min(active, static_cast<int64_t>(a.context) - 1) / BATCH_CHUNK) + 1;
         const float* src = a.workspace + (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + threadIdx.x;
         const int64_t cstride = static_cast<int64_t>(a.batch) * a.query_heads * BATCH_HEAD;
-        for (int c = 0; c < n; c++)
-            sum += src[c * cstride];
+        for (int c0 = 0; c0 < n; c0 += VALUES_BATCH) {
+            float part[VALUES_BATCH];
+#pragma unroll
+            for (int i = 0; i < VALUES_BATCH; i++)
+                part[i] = c0 + i < n ? src[(c0 + i) * cstride] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < VALUES_BATCH; i++)
+                sum += part[i];
+        }
     }
     a.out[(static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + threadIdx.x] = sum;
 }
@@ -448,7 +528,6 @@ __global__ __launch_bounds__(THREADS) void batch_select_last_kernel(const float*
 
 // ---- batched matrix-vector product on the FP32 matrix cores ------------------------------
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 typedef uint32_t u32_a2 __attribute__((aligned(2)));   // 4 bytes at a 2-byte aligned address
 
