@@ -71,15 +71,6 @@ __device__ __forceinline__ float block_max(float v, float* red)
     return t;
 }
 
-// Sum over the 16 lanes of a DPP row (every lane of the row gets it).
-__device__ __forceinline__ float row_sum16(float v)
-{
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
-    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
-}
-
 __device__ __forceinline__ void load8(const float* p, float* f)
 {
     const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
@@ -711,6 +702,192 @@ __global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __
     }
 }
 
+
+// ---- the same product over an LDS ring filled by asynchronous loads -----------------------
+//
+// For Q4_0, Q8_0 and Q4_K with columns % 256 == 0.  A workgroup of RING_WAVES
+// waves owns 16 output rows x 16 batch rows and walks the columns in chunks of
+// 256.  Each chunk's X tile (16 rows x 256 values, rows 1040 bytes apart) and
+// W tile (the 16 rows' 256-column slices, contiguous in memory) are copied
+// into one stage of an LDS ring by global_load_lds_dwordx4: each lane's 16
+// bytes land at the instruction's LDS base + 16 x lane, with no VGPR held
+// while the copy is in flight, so RING - 1 chunks are requested ahead of the
+// one being multiplied (a register double buffer holds one: 97.8 -> 83 us
+// for the Phi-4 layer's four Q4_K products at 16 rows, 116 -> 71 us in Q4_0).
+// Every load is 16 bytes of a contiguous run (the W rows are whole 144- or
+// 272-byte slices, the X rows whole 1 KB), so the vector cache sees a fraction
+// of the accesses of per-row fragment loads.
+//
+// Wave w multiplies block w of the chunk (32 columns): lane (r, g) = (l % 16,
+// l / 16) reads the X values of batch row r at columns 4g..4g+3 and
+// 16+4g..16+4g+3 of the block (two 16-byte LDS reads; the 1040-byte row pitch
+// puts the 16 rows of one read on distinct banks) and decodes the same 8
+// weights of output row r, then eight v_mfma_f32_16x16x4_f32 add them up as in
+// batch_matvec_kernel.  Per chunk a wave waits for its own copies of that
+// chunk (s_waitcnt vmcnt counts the copies still allowed in flight) and then
+// meets the other waves at a barrier, after which every copy of the chunk is
+// visible and every wave is done with the stage the next request reuses.
+constexpr int RING_WAVES = 8;
+constexpr int RING_CHUNK = 256;                 // columns per stage
+constexpr int RING_XPITCH = RING_CHUNK + 4;     // floats per staged X row
+
+template <int FMT>
+constexpr int ring_row_bytes()   // bytes of one W row per 256 columns
+{
+    return FMT == FMT_Q8_0 ? 272 : 144;
+}
+
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// One asynchronous 16-byte copy per lane from global memory into LDS at
+// lds_base + 16 x lane.  The wave-uniform LDS base goes in M0 (the compiler
+// writes it there as the operand's register); the s_nop is the wait state an
+// LDS-bound load needs after an M0 write.
+__device__ __forceinline__ void copy16_to_lds(const void* src, uint32_t lds_base)
+{
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+
+// Waits until at most N of this wave's copies are in flight, then meets the
+// workgroup's other waves.
+template <int N>
+__device__ __forceinline__ void ring_wait_barrier()
+{
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// The 8 weights of block b of a staged W row slice at columns 4g..4g+3 and
+// 16+4g..16+4g+3 of the block, dequantised as decode8 does.
+template <int FMT>
+__device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, float* w)
+{
+    if constexpr (FMT == FMT_Q8_0) {
+        const uint8_t* blk = row + 34 * b;
+        const float d = half_bits(lds_u16(blk));
+        const uint32_t lo = lds_u16(blk + 2 + 4 * g) | (lds_u16(blk + 4 + 4 * g) << 16);
+        const uint32_t hi = lds_u16(blk + 18 + 4 * g) | (lds_u16(blk + 20 + 4 * g) << 16);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            w[e] = d * static_cast<float>(static_cast<int8_t>((lo >> (8 * e)) & 0xffu));
+            w[4 + e] = d * static_cast<float>(static_cast<int8_t>((hi >> (8 * e)) & 0xffu));
+        }
+    } else if constexpr (FMT == FMT_Q4_0) {
+        const uint8_t* blk = row + 18 * b;
+        const float d = half_bits(lds_u16(blk));
+        const uint32_t q = lds_u16(blk + 2 + 4 * g) | (lds_u16(blk + 4 + 4 * g) << 16);   // qs[4g..4g+3]
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            w[e] = d * static_cast<float>(static_cast<int>((q >> (8 * e)) & 15u) - 8);            // element 4g+e
+            w[4 + e] = d * static_cast<float>(static_cast<int>((q >> (8 * e + 4)) & 15u) - 8);    // element 16+4g+e
+        }
+    } else {   // Q4_K: the slice is one super-block, b its sub-block
+        const uint4 h = *reinterpret_cast<const uint4*>(row);
+        const uint32_t sw[3] = {h.y, h.z, h.w};
+        auto sbyte = [&](int i) { return static_cast<int>((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+        int sc, m;
+        if (b < 4) {
+            sc = sbyte(b) & 63;
+            m = sbyte(b + 4) & 63;
+        } else {
+            sc = (sbyte(b + 4) & 15) | ((sbyte(b - 4) >> 6) << 4);
+            m = (sbyte(b + 4) >> 4) | ((sbyte(b) >> 6) << 4);
+        }
+        const float d1 = __fmul_rn(half_bits(h.x), static_cast<float>(sc));
+        const float m1 = __fmul_rn(half_bits(h.x >> 16), static_cast<float>(m));
+        const int sh = (b & 1) * 4;   // low nibbles for even sub-blocks
+        const uint8_t* qs = row + 16 + 32 * (b >> 1);
+        const uint32_t lo = lds_u32(qs + 4 * g), hi = lds_u32(qs + 16 + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            w[e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((lo >> (8 * e + sh)) & 15u)), m1);
+            w[4 + e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((hi >> (8 * e + sh)) & 15u)), m1);
+        }
+    }
+}
+
+template <int FMT, int RING>
+__global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
+    const uint8_t* __restrict__ W, const float* __restrict__ X, float* __restrict__ Y, int batch, int rows, int cols,
+    int64_t row_bytes, const int32_t* __restrict__ control)
+{
+    constexpr int WROW = ring_row_bytes<FMT>();
+    constexpr int XBYTES = 16 * RING_XPITCH * 4, STAGE = XBYTES + 16 * WROW;
+    constexpr int XROWS = 16 / RING_WAVES;                     // X rows each wave copies
+    constexpr int PIECES = WROW / 16;                          // 16-byte pieces per W row slice
+    constexpr int WPIECES = 16 * PIECES / RING_WAVES;          // W pieces each wave copies
+    constexpr int WCOPIES = (WPIECES + 63) / 64;
+    constexpr int COPIES = XROWS + WCOPIES;                    // copy instructions per wave and chunk
+    static_assert(RING_CHUNK / 32 == RING_WAVES, "one block per wave and chunk");
+    static_assert(WPIECES > 64 * (WCOPIES - 1), "every copy instruction has a live lane");
+    static_assert((RING - 2) * COPIES < 64, "vmcnt range");
+    __shared__ __align__(16) uint8_t ring[RING * STAGE];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = lane & 15, g = lane >> 4;
+    const int o0 = static_cast<int>(blockIdx.x) * 16, t0 = static_cast<int>(blockIdx.y) * 16;
+    const int live = min(control[1], batch) - t0;   // live batch rows of this tile
+    if (live <= 0)
+        return;   // the whole workgroup, before any copy or barrier
+    const int nc = cols / RING_CHUNK;
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+    auto request = [&](int c) {   // chunk c into stage c % RING
+        const uint32_t st = base + static_cast<uint32_t>((c % RING) * STAGE);
+#pragma unroll
+        for (int k = 0; k < XROWS; k++) {
+            const int row = XROWS * wave + k;   // rows past the live ones repeat the last live row
+            copy16_to_lds(X + static_cast<int64_t>(t0 + min(row, live - 1)) * cols + RING_CHUNK * c + 4 * lane,
+                          __builtin_amdgcn_readfirstlane(st + row * RING_XPITCH * 4));
+        }
+#pragma unroll
+        for (int j = 0; j < WCOPIES; j++) {
+            const int q = 64 * j + lane;
+            if (q < WPIECES) {
+                const int p = wave * WPIECES + q, row = p / PIECES, piece = p % PIECES;
+                copy16_to_lds(W + static_cast<int64_t>(min(o0 + row, rows - 1)) * row_bytes +
+                                  static_cast<int64_t>(WROW) * c + 16 * piece,
+                              __builtin_amdgcn_readfirstlane(st + XBYTES + 16 * (wave * WPIECES + 64 * j)));
+            }
+        }
+    };
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < RING - 1 && c < nc; c++)
+        request(c);
+    for (int c = 0; c < nc; c++) {
+        if (c + RING - 2 < nc)
+            ring_wait_barrier<(RING - 2) * COPIES>();   // chunks c + 1 .. c + RING - 2 may stay in flight
+        else
+            ring_wait_barrier<0>();
+        if (c + RING - 1 < nc)
+            request(c + RING - 1);   // into the stage of chunk c - 1, which every wave is done with
+        const uint8_t* st = ring + (c % RING) * STAGE;
+        const float* xrow = reinterpret_cast<const float*>(st) + r * RING_XPITCH + 32 * wave;
+        const float4 x0 = *reinterpret_cast<const float4*>(xrow + 4 * g);
+        const float4 x1 = *reinterpret_cast<const float4*>(xrow + 16 + 4 * g);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float w[8];
+        decode_staged<FMT>(st + XBYTES + r * WROW, wave, g, w);
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s], w[s], acc, 0, 0, 0);
+    }
+    __syncthreads();   // every wave is done with the ring
+    floatx4* red = reinterpret_cast<floatx4*>(ring);
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        floatx4 v = red[lane];
+#pragma unroll
+        for (int k = 1; k < RING_WAVES; k++)
+            v += red[k * 64 + lane];
+        const int o = o0 + r;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int i = 4 * g + m;
+            if (i < live && o < rows)
+                Y[static_cast<int64_t>(t0 + i) * rows + o] = v[m];
+        }
+    }
+}
+
 }  // namespace
 
 int64_t batch_values_workspace_floats(int batch, int query_heads, int context)
@@ -828,6 +1005,15 @@ hipError_t launch_batch_matvec(int fmt, const void* w, const float* x, float* y,
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int64_t rb = row_bytes(fmt, cols);
     const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    if (cols % RING_CHUNK == 0) {   // weight and input are 16-byte aligned (checked by the ABI)
+        const dim3 block(64 * RING_WAVES);
+        switch (fmt) {
+        case FMT_Q8_0: hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q8_0, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control); return hipGetLastError();
+        case FMT_Q4_0: hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_0, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control); return hipGetLastError();
+        case FMT_Q4_K: hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_K, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control); return hipGetLastError();
+        default: break;
+        }
+    }
     switch (fmt) {
     case FMT_Q8_0: hipLaunchKernelGGL((batch_matvec_kernel<FMT_Q8_0>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
     case FMT_Q4_0: hipLaunchKernelGGL((batch_matvec_kernel<FMT_Q4_0>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;

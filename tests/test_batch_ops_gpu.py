@@ -132,7 +132,10 @@ def test_row_operators(hip, start, valid):
 
 MATVEC_CASES = [(native.Q4_0, 5120, 3072, 16, 16), (native.Q4_0, 3072, 8192, 16, 11), (native.Q8_0, 3072, 3072, 16, 3),
                 (native.Q4_K, 3072, 3072, 16, 16), (native.Q4_K, 100, 512, 5, 5), (native.F16, 3072, 3072, 16, 9),
-                (native.F32, 77, 1024, 16, 16), (native.Q8_0, 17, 96, 1, 1)]
+                (native.F32, 77, 1024, 16, 16), (native.Q8_0, 17, 96, 1, 1),
+                # the LDS-ring form (columns % 256 == 0): one chunk, odd chunk counts, ragged rows and batches
+                (native.Q4_K, 40, 256, 3, 2), (native.Q8_0, 50, 768, 16, 16), (native.Q4_0, 16, 1280, 7, 7),
+                (native.Q4_0, 33, 256, 16, 16), (native.Q8_0, 5, 512, 2, 1)]
 
 
 @pytest.mark.parametrize("fmt,rows,cols,batch,valid", MATVEC_CASES,
