@@ -703,39 +703,36 @@ __global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __
 }
 
 
-// ---- the same product over an LDS ring filled by asynchronous loads -----------------------
+// ---- the same product over per-wave LDS rings filled by asynchronous loads ----------------
 //
 // For Q4_0, Q8_0 and Q4_K with columns % 256 == 0.  A workgroup of RING_WAVES
-// waves owns 16 output rows x 16 batch rows and walks the columns in chunks of
-// 256.  Each chunk's X tile (16 rows x 256 values, rows 1040 bytes apart) and
-// W tile (the 16 rows' 256-column slices, contiguous in memory) are copied
-// into one stage of an LDS ring by global_load_lds_dwordx4: each lane's 16
-// bytes land at the instruction's LDS base + 16 x lane, with no VGPR held
-// while the copy is in flight, so RING - 1 chunks are requested ahead of the
-// one being multiplied (a register double buffer holds one: 97.8 -> 83 us
-// for the Phi-4 layer's four Q4_K products at 16 rows, 116 -> 71 us in Q4_0).
-// Every load is 16 bytes of a contiguous run (the W rows are whole 144- or
-// 272-byte slices, the X rows whole 1 KB), so the vector cache sees a fraction
-// of the accesses of per-row fragment loads.
+// = 8 waves owns 16 output rows x 16 batch rows; wave w multiplies the
+// 32-column blocks w, w + 8, w + 16, ... and copies exactly the bytes it
+// multiplies into a ring of its own in LDS with global_load_lds_dwordx4: each
+// lane's 16 bytes land at the instruction's LDS base + 16 x lane, no VGPR is
+// held while a copy is in flight, and RING - 1 blocks are requested ahead of
+// the one being multiplied.  A wave waits only for its own copies (s_waitcnt
+// vmcnt), so the loop has no barrier and the waves of a CU drift freely,
+// overlapping one's decode with another's matrix products.  Against X and W
+// fragments loaded into registers one pass ahead, the Phi-4 layer's four
+// Q4_K products at 16 rows take 74 instead of 102 us (Q4_0: 68 against 116);
+// a ring shared by the workgroup, with a barrier per 256 columns, took 84.
 //
-// Wave w multiplies block w of the chunk (32 columns): lane (r, g) = (l % 16,
-// l / 16) reads the X values of batch row r at columns 4g..4g+3 and
-// 16+4g..16+4g+3 of the block (two 16-byte LDS reads; the 1040-byte row pitch
-// puts the 16 rows of one read on distinct banks) and decodes the same 8
-// weights of output row r, then eight v_mfma_f32_16x16x4_f32 add them up as in
-// batch_matvec_kernel.  Per chunk a wave waits for its own copies of that
-// chunk (s_waitcnt vmcnt counts the copies still allowed in flight) and then
-// meets the other waves at a barrier, after which every copy of the chunk is
-// visible and every wave is done with the stage the next request reuses.
+// One stage per block: X of the 16 batch rows (2 copies of 1 KB; copy h,
+// lane i holds row 8h + i/8, 16-byte piece (i % 8) ^ ((row >> 1) & 7) of the
+// block, so a read of piece p by the 16 rows hits 16 distinct 4-bank groups)
+// and the 16 weight rows' bytes of the block (one copy, three 16-byte pieces
+// a row, 48 bytes apart: Q4_K the super-block header and the 32 quant bytes
+// of the sub-block pair; Q4_0 / Q8_0 the aligned 32 / 48 bytes around the
+// 18- / 34-byte block, which never pass the end of its 8-block group, a
+// multiple of 16 bytes).  Lane (r, g) = (l % 16, l / 16) multiplies columns
+// 4g..4g+3 and 16+4g..16+4g+3 of the block: eight v_mfma_f32_16x16x4_f32 on
+// two accumulators (even and odd instructions), added at the end.
 constexpr int RING_WAVES = 8;
-constexpr int RING_CHUNK = 256;                 // columns per stage
-constexpr int RING_XPITCH = RING_CHUNK + 4;     // floats per staged X row
-
-template <int FMT>
-constexpr int ring_row_bytes()   // bytes of one W row per 256 columns
-{
-    return FMT == FMT_Q8_0 ? 272 : 144;
-}
+constexpr int RING_XBYTES = 16 * 32 * 4;        // X bytes of a stage
+constexpr int RING_WPITCH = 48;                 // bytes per weight row of a stage
+constexpr int RING_STAGE = RING_XBYTES + 16 * RING_WPITCH;
+constexpr int RING_COPIES = 3;                  // copy instructions per stage
 
 __device__ __forceinline__ uint32_t lds_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
@@ -749,21 +746,35 @@ __device__ __forceinline__ void copy16_to_lds(const void* src, uint32_t lds_base
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
 }
 
-// Waits until at most N of this wave's copies are in flight, then meets the
-// workgroup's other waves.
+// Waits until at most N of this wave's memory loads (copies included) are in
+// flight.
 template <int N>
-__device__ __forceinline__ void ring_wait_barrier()
+__device__ __forceinline__ void wait_copies()
 {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// The 8 weights of block b of a staged W row slice at columns 4g..4g+3 and
-// 16+4g..16+4g+3 of the block, dequantised as decode8 does.
+// Source of weight piece j (0..2) of block b in a row: Q4_K the header (j =
+// 0) and the quant bytes of the sub-block pair; Q4_0 the 16-byte aligned 32
+// bytes holding the block (piece 2 repeats piece 1); Q8_0 the aligned 48.
+template <int FMT>
+__device__ __forceinline__ int64_t ring_piece(int b, int j)
+{
+    if constexpr (FMT == FMT_Q4_K)
+        return 144 * static_cast<int64_t>(b >> 3) + (j == 0 ? 0 : 16 + 32 * ((b & 7) >> 1) + 16 * (j - 1));
+    else if constexpr (FMT == FMT_Q4_0)
+        return ((18 * static_cast<int64_t>(b)) & ~int64_t{15}) + 16 * min(j, 1);
+    else
+        return ((34 * static_cast<int64_t>(b)) & ~int64_t{15}) + 16 * j;
+}
+
+// The 8 weights of block b at columns 4g..4g+3 and 16+4g..16+4g+3 from its
+// staged row pieces, dequantised as decode8 does.
 template <int FMT>
 __device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, float* w)
 {
     if constexpr (FMT == FMT_Q8_0) {
-        const uint8_t* blk = row + 34 * b;
+        const uint8_t* blk = row + ((34 * b) & 15);
         const float d = half_bits(lds_u16(blk));
         const uint32_t lo = lds_u16(blk + 2 + 4 * g) | (lds_u16(blk + 4 + 4 * g) << 16);
         const uint32_t hi = lds_u16(blk + 18 + 4 * g) | (lds_u16(blk + 20 + 4 * g) << 16);
@@ -773,7 +784,7 @@ __device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, 
             w[4 + e] = d * static_cast<float>(static_cast<int8_t>((hi >> (8 * e)) & 0xffu));
         }
     } else if constexpr (FMT == FMT_Q4_0) {
-        const uint8_t* blk = row + 18 * b;
+        const uint8_t* blk = row + ((18 * b) & 15);
         const float d = half_bits(lds_u16(blk));
         const uint32_t q = lds_u16(blk + 2 + 4 * g) | (lds_u16(blk + 4 + 4 * g) << 16);   // qs[4g..4g+3]
 #pragma unroll
@@ -781,23 +792,23 @@ __device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, 
             w[e] = d * static_cast<float>(static_cast<int>((q >> (8 * e)) & 15u) - 8);            // element 4g+e
             w[4 + e] = d * static_cast<float>(static_cast<int>((q >> (8 * e + 4)) & 15u) - 8);    // element 16+4g+e
         }
-    } else {   // Q4_K: the slice is one super-block, b its sub-block
+    } else {   // Q4_K sub-block j of the super-block
+        const int j = b & 7;
         const uint4 h = *reinterpret_cast<const uint4*>(row);
         const uint32_t sw[3] = {h.y, h.z, h.w};
         auto sbyte = [&](int i) { return static_cast<int>((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
         int sc, m;
-        if (b < 4) {
-            sc = sbyte(b) & 63;
-            m = sbyte(b + 4) & 63;
+        if (j < 4) {
+            sc = sbyte(j) & 63;
+            m = sbyte(j + 4) & 63;
         } else {
-            sc = (sbyte(b + 4) & 15) | ((sbyte(b - 4) >> 6) << 4);
-            m = (sbyte(b + 4) >> 4) | ((sbyte(b) >> 6) << 4);
+            sc = (sbyte(j + 4) & 15) | ((sbyte(j - 4) >> 6) << 4);
+            m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
         }
         const float d1 = __fmul_rn(half_bits(h.x), static_cast<float>(sc));
         const float m1 = __fmul_rn(half_bits(h.x >> 16), static_cast<float>(m));
-        const int sh = (b & 1) * 4;   // low nibbles for even sub-blocks
-        const uint8_t* qs = row + 16 + 32 * (b >> 1);
-        const uint32_t lo = lds_u32(qs + 4 * g), hi = lds_u32(qs + 16 + 4 * g);
+        const int sh = (j & 1) * 4;   // low nibbles for even sub-blocks
+        const uint32_t lo = lds_u32(row + 16 + 4 * g), hi = lds_u32(row + 32 + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             w[e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((lo >> (8 * e + sh)) & 15u)), m1);
@@ -811,67 +822,58 @@ __global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ X, float* __restrict__ Y, int batch, int rows, int cols,
     int64_t row_bytes, const int32_t* __restrict__ control)
 {
-    constexpr int WROW = ring_row_bytes<FMT>();
-    constexpr int XBYTES = 16 * RING_XPITCH * 4, STAGE = XBYTES + 16 * WROW;
-    constexpr int XROWS = 16 / RING_WAVES;                     // X rows each wave copies
-    constexpr int PIECES = WROW / 16;                          // 16-byte pieces per W row slice
-    constexpr int WPIECES = 16 * PIECES / RING_WAVES;          // W pieces each wave copies
-    constexpr int WCOPIES = (WPIECES + 63) / 64;
-    constexpr int COPIES = XROWS + WCOPIES;                    // copy instructions per wave and chunk
-    static_assert(RING_CHUNK / 32 == RING_WAVES, "one block per wave and chunk");
-    static_assert(WPIECES > 64 * (WCOPIES - 1), "every copy instruction has a live lane");
-    static_assert((RING - 2) * COPIES < 64, "vmcnt range");
-    __shared__ __align__(16) uint8_t ring[RING * STAGE];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = lane & 15, g = lane >> 4;
+    constexpr int WAVE_RING = RING * RING_STAGE;
+    static_assert(RING >= 2 && (RING - 2) * RING_COPIES < 64, "vmcnt range");
+    __shared__ __align__(16) uint8_t ring[RING_WAVES * WAVE_RING];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
     const int o0 = static_cast<int>(blockIdx.x) * 16, t0 = static_cast<int>(blockIdx.y) * 16;
     const int live = min(control[1], batch) - t0;   // live batch rows of this tile
     if (live <= 0)
         return;   // the whole workgroup, before any copy or barrier
-    const int nc = cols / RING_CHUNK;
-    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
-    auto request = [&](int c) {   // chunk c into stage c % RING
-        const uint32_t st = base + static_cast<uint32_t>((c % RING) * STAGE);
+    const int nk = cols / (32 * RING_WAVES);        // blocks of each wave: b = wave + 8 k
+    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) + wave * WAVE_RING;
+    const int xrow = lane >> 3, xslot = lane & 7;   // X copy lane: row 8h + xrow, slot xslot
+    const int wrow = lane / 3, wpiece = lane % 3;   // weight copy lane (lanes < 48)
+    const uint8_t* wsrc = W + static_cast<int64_t>(min(o0 + wrow, rows - 1)) * row_bytes;
+    auto request = [&](int k) {   // block wave + 8k into stage k % RING
+        const int b = wave + RING_WAVES * k;
+        const uint32_t st = base + static_cast<uint32_t>((k % RING) * RING_STAGE);
 #pragma unroll
-        for (int k = 0; k < XROWS; k++) {
-            const int row = XROWS * wave + k;   // rows past the live ones repeat the last live row
-            copy16_to_lds(X + static_cast<int64_t>(t0 + min(row, live - 1)) * cols + RING_CHUNK * c + 4 * lane,
-                          __builtin_amdgcn_readfirstlane(st + row * RING_XPITCH * 4));
+        for (int h = 0; h < 2; h++) {
+            const int row = 8 * h + xrow, piece = xslot ^ ((row >> 1) & 7);   // rows past the live ones repeat the last
+            copy16_to_lds(X + static_cast<int64_t>(t0 + min(row, live - 1)) * cols + 32 * b + 4 * piece,
+                          __builtin_amdgcn_readfirstlane(st + 1024 * h));
         }
-#pragma unroll
-        for (int j = 0; j < WCOPIES; j++) {
-            const int q = 64 * j + lane;
-            if (q < WPIECES) {
-                const int p = wave * WPIECES + q, row = p / PIECES, piece = p % PIECES;
-                copy16_to_lds(W + static_cast<int64_t>(min(o0 + row, rows - 1)) * row_bytes +
-                                  static_cast<int64_t>(WROW) * c + 16 * piece,
-                              __builtin_amdgcn_readfirstlane(st + XBYTES + 16 * (wave * WPIECES + 64 * j)));
-            }
-        }
+        if (lane < 48)
+            copy16_to_lds(wsrc + ring_piece<FMT>(b, wpiece), __builtin_amdgcn_readfirstlane(st + RING_XBYTES));
     };
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < RING - 1 && c < nc; c++)
-        request(c);
-    for (int c = 0; c < nc; c++) {
-        if (c + RING - 2 < nc)
-            ring_wait_barrier<(RING - 2) * COPIES>();   // chunks c + 1 .. c + RING - 2 may stay in flight
+    floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < RING - 1 && k < nk; k++)
+        request(k);
+    const int sw = (r >> 1) & 7;
+    for (int k = 0; k < nk; k++) {
+        if (k + RING - 2 < nk)
+            wait_copies<(RING - 2) * RING_COPIES>();   // blocks k + 1 .. k + RING - 2 may stay in flight
         else
-            ring_wait_barrier<0>();
-        if (c + RING - 1 < nc)
-            request(c + RING - 1);   // into the stage of chunk c - 1, which every wave is done with
-        const uint8_t* st = ring + (c % RING) * STAGE;
-        const float* xrow = reinterpret_cast<const float*>(st) + r * RING_XPITCH + 32 * wave;
-        const float4 x0 = *reinterpret_cast<const float4*>(xrow + 4 * g);
-        const float4 x1 = *reinterpret_cast<const float4*>(xrow + 16 + 4 * g);
+            wait_copies<0>();
+        if (k + RING - 1 < nk)
+            request(k + RING - 1);   // into the stage of block k - 1, whose reads have returned
+        const uint8_t* st = ring + wave * WAVE_RING + (k % RING) * RING_STAGE;
+        const float* xr = reinterpret_cast<const float*>(st + 128 * r);
+        const float4 x0 = *reinterpret_cast<const float4*>(xr + 4 * (g ^ sw));
+        const float4 x1 = *reinterpret_cast<const float4*>(xr + 4 * ((4 + g) ^ sw));
         const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float w[8];
-        decode_staged<FMT>(st + XBYTES + r * WROW, wave, g, w);
+        decode_staged<FMT>(st + RING_XBYTES + RING_WPITCH * r, wave + RING_WAVES * k, g, w);
 #pragma unroll
-        for (int s = 0; s < 8; s++)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s], w[s], acc, 0, 0, 0);
+        for (int s = 0; s < 8; s += 2) {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s], w[s], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s + 1], w[s + 1], acc1, 0, 0, 0);
+        }
     }
-    __syncthreads();   // every wave is done with the ring
+    __syncthreads();   // every wave is done with its ring
     floatx4* red = reinterpret_cast<floatx4*>(ring);
-    red[wave * 64 + lane] = acc;
+    red[wave * 64 + lane] = acc0 + acc1;
     __syncthreads();
     if (wave == 0) {
         floatx4 v = red[lane];
@@ -1005,12 +1007,24 @@ hipError_t launch_batch_matvec(int fmt, const void* w, const float* x, float* y,
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int64_t rb = row_bytes(fmt, cols);
     const int r = static_cast<int>(rows), c = static_cast<int>(cols);
-    if (cols % RING_CHUNK == 0) {   // weight and input are 16-byte aligned (checked by the ABI)
+    if (cols % (32 * RING_WAVES) == 0) {   // weight and input are 16-byte aligned (checked by the ABI)
+        // three stages a wave keep two workgroups on a CU (67.6 KB of LDS
+        // each); grids of at most one workgroup per CU take four
+        const bool deep = (rows + 15) / 16 <= 256;
         const dim3 block(64 * RING_WAVES);
         switch (fmt) {
-        case FMT_Q8_0: hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q8_0, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control); return hipGetLastError();
-        case FMT_Q4_0: hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_0, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control); return hipGetLastError();
-        case FMT_Q4_K: hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_K, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control); return hipGetLastError();
+        case FMT_Q8_0:
+            if (deep) hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q8_0, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
+            else hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q8_0, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
+            return hipGetLastError();
+        case FMT_Q4_0:
+            if (deep) hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_0, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
+            else hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_0, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
+            return hipGetLastError();
+        case FMT_Q4_K:
+            if (deep) hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_K, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
+            else hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_K, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
+            return hipGetLastError();
         default: break;
         }
     }
