@@ -84,6 +84,10 @@ def main() -> int:
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before timing, copy this many MiB device-to-device once (a plain copy of "
                          "known size that scales the HBM byte counters of a profiler run)")
+    ap.add_argument("--batch-ops", action="store_true",
+                    help="only the batched prefill operators at 16 rows (the Phi-4 Q4_K layer mat-vecs and the "
+                         "attention chain), launched eagerly and event-timed: a kernel trace of this run sees "
+                         "every launch")
     ap.add_argument("--prefill-vendor", action="store_true",
                     help="only torch's dense bf16 linear (hipBLASLt) at the prefill shapes with bf16 W (no "
                          "dequant): a library reference, not a product path; torch's own HIP runtime does "
@@ -104,6 +108,13 @@ def main() -> int:
         return 0
 
     from sharpinference_amd import native
+
+    if args.batch_ops:
+        hip = native.HipContext(0)
+        res = bench_batch_ops(hip)
+        hip.close()
+        print(json.dumps({"batch_ops": res}), flush=True)
+        return 0
 
     if args.decode_only:
         hip = native.HipContext(0)
@@ -427,6 +438,68 @@ def bench_prefill(hip, rng, m: int = 512):
     tflops = total_flops / total_us / 1e6
     out.update({"us_total": round(total_us, 1), "TFLOPs": round(tflops, 1),
                 "mfma_bf16_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+    return out
+
+
+def bench_batch_ops(hip, rows: int = 16, context: int = 4096):
+    """The batched prefill operators of the op-by-op program at 16 rows,
+    launched eagerly (no plan): the four Phi-4-mini Q4_K layer mat-vecs
+    (batch_matvec) and the attention chain (scores, causal softmax, values)
+    over an fp16 cache of `context` positions, 24 query and 8 KV heads, for
+    batches starting at 0 and at context / 2 - 16.  Each op event-timed,
+    median of 5 samples of 20 back-to-back launches."""
+    from sharpinference_amd import native, phi4
+    cfg = phi4.Phi4Config()
+    rng = np.random.default_rng(11)
+
+    def timed(fn):
+        fn()
+        samples = []
+        for _ in range(5):
+            hip.timer_begin()
+            for _ in range(20):
+                fn()
+            samples.append(hip.timer_end() * 1e3 / 20)
+        return sorted(samples)[2]
+
+    ctl = hip.to_device(np.array([0, rows], np.int32))
+    out = {"rows": rows, "matvec_us": {}, "attention_us": {}}
+    flops, total = 0.0, 0.0
+    for name, (r, c) in cfg.layer_shapes().items():
+        w = hip.to_device(phi4.synth_blocks(cfg.weight_format, r, c, rng))
+        x = hip.to_device(rng.standard_normal((rows, c)).astype(np.float32))
+        y = hip.alloc(rows * r * 4)
+        us = timed(lambda: hip.batch_matvec(cfg.weight_format, w.ptr, x.ptr, ctl.ptr, y.ptr, rows, r, c))
+        out["matvec_us"][name] = r1(us)
+        flops += 2.0 * rows * r * c
+        total += us
+        for b in (w, x, y):
+            b.free()
+    out["matvec_layer_us"] = r1(total)
+    out["matvec_tflops"] = r1(flops / total / 1e6)
+    heads, kv, head = cfg.heads, cfg.kv_heads, cfg.head_dim
+    q = hip.to_device(rng.standard_normal((rows, heads * head)).astype(np.float32))
+    kc = hip.to_device(rng.standard_normal((context, kv, head)).astype(np.float16))
+    vc = hip.to_device(rng.standard_normal((context, kv, head)).astype(np.float16))
+    sc, pr = hip.alloc(4 * rows * heads * context), hip.alloc(4 * rows * heads * context)
+    att = hip.alloc(4 * rows * heads * head)
+    ws = hip.alloc(native.batch_values_workspace_bytes(rows, heads, context))
+    for start in (0, context // 2 - 16):
+        ctl.upload(np.array([start, rows], np.int32))
+        a_s = native.BatchAttentionArgs(q.ptr, pr.ptr, kc.ptr, ctl.ptr, sc.ptr, ws.ptr, native.F16, rows, heads, kv,
+                                        head, context)
+        a_v = native.BatchAttentionArgs(q.ptr, pr.ptr, vc.ptr, ctl.ptr, att.ptr, ws.ptr, native.F16, rows, heads, kv,
+                                        head, context)
+        out["attention_us"][str(start)] = {
+            "scores": r1(timed(lambda: hip.batch_gqa_scores(a_s))),
+            "softmax": r1(timed(lambda: hip.batch_causal_softmax(sc.ptr, ctl.ptr, pr.ptr, rows, heads, context))),
+            "values": r1(timed(lambda: hip.batch_gqa_values(a_v)))}
+    for b in (ctl, q, kc, vc, sc, pr, att, ws):
+        b.free()
+    log("batch ops: mat-vec " + ", ".join(f"{k} {v} us" for k, v in out["matvec_us"].items())
+        + f" ({out['matvec_layer_us']} us, {out['matvec_tflops']} TFLOP/s); attention "
+        + "; ".join(f"start {k}: " + ", ".join(f"{n} {v} us" for n, v in d.items())
+                    for k, d in out["attention_us"].items()))
     return out
 
 
