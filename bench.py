@@ -444,8 +444,9 @@ def bench_prefill(hip, rng, m: int = 512):
 def bench_batch_ops(hip, rows: int = 16, context: int = 4096):
     """The batched prefill operators of the op-by-op program at 16 rows,
     launched eagerly (no plan): the four Phi-4-mini Q4_K layer mat-vecs
-    (batch_matvec) and the attention chain (scores, causal softmax, values)
-    over an fp16 cache of `context` positions, 24 query and 8 KV heads, for
+    (batch_matvec) and the attention chain (scores, causal softmax, values,
+    and the three fused into two launches) over an fp16 cache of `context`
+    positions, 24 query and 8 KV heads, for
     batches starting at 0 and at context / 2 - 16.  Each op event-timed,
     median of 5 samples of 20 back-to-back launches."""
     from sharpinference_amd import native, phi4
@@ -490,10 +491,13 @@ def bench_batch_ops(hip, rows: int = 16, context: int = 4096):
                                         head, context)
         a_v = native.BatchAttentionArgs(q.ptr, pr.ptr, vc.ptr, ctl.ptr, att.ptr, ws.ptr, native.F16, rows, heads, kv,
                                         head, context)
+        a_f = native.BatchAttentionArgs(q.ptr, 0, kc.ptr, ctl.ptr, att.ptr, ws.ptr, native.F16, rows, heads, kv,
+                                        head, context)
         out["attention_us"][str(start)] = {
             "scores": r1(timed(lambda: hip.batch_gqa_scores(a_s))),
             "softmax": r1(timed(lambda: hip.batch_causal_softmax(sc.ptr, ctl.ptr, pr.ptr, rows, heads, context))),
-            "values": r1(timed(lambda: hip.batch_gqa_values(a_v)))}
+            "values": r1(timed(lambda: hip.batch_gqa_values(a_v))),
+            "fused": r1(timed(lambda: hip.batch_gqa_attention(a_f, vc.ptr)))}
     for b in (ctl, q, kc, vc, sc, pr, att, ws):
         b.free()
     log("batch ops: mat-vec " + ", ".join(f"{k} {v} us" for k, v in out["matvec_us"].items())
@@ -651,6 +655,21 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
                       "kind": "port", "sample": "1 warm-up + 3 oracle decode steps (median) at position "
                                                 f"{context}, same weights and cache"}
         log(f"decode cpu: {sec * 1e3:.1f} ms/token on {threads} threads")
+        if op_program is not None:
+            # the prompt batch's 16 rows as 16 oracle token steps at the
+            # middle batch's positions (each step also computes the vocabulary
+            # head, which the batched program computes once per batch)
+            mid = context // 2 - 8
+            t0 = time.perf_counter()
+            for r in range(16):
+                model.step(1, mid + r, threads)
+            batch_s = time.perf_counter() - t0
+            op_program["prefill_fused_16"]["cpu"] = {
+                "prompt_tok_s": round(16.0 / batch_s, 2), "ms_per_batch": round(batch_s * 1e3, 1), "cores": threads,
+                "kind": "port", "sample": f"16 oracle token steps at positions {mid}..{mid + 15} (one batch), each "
+                                          "with the vocabulary head"}
+            log(f"prefill_fused_16 cpu: {batch_s * 1e3:.0f} ms per 16-row batch on {threads} threads "
+                f"({16.0 / batch_s:.1f} prompt tok/s)")
         del model
     del weights
     return out

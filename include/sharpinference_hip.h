@@ -437,6 +437,19 @@ int si_hip_batch_causal_softmax(si_hip_context* ctx, const float* scores, const 
  * transformer.batch-gqa-values (GpuBatchTransformerInstructions.cs:544-598). */
 int si_hip_batch_gqa_values(si_hip_context* ctx, const si_hip_batch_attention_args* args);
 
+/* si_hip_batch_gqa_scores, si_hip_batch_causal_softmax and
+ * si_hip_batch_gqa_values in two launches, for callers that never read the
+ * scores or probabilities: args->query, args->cache (the key cache),
+ * args->output (the values' output) and args->workspace (at least
+ * si_hip_batch_values_workspace_bytes) as for those calls,
+ * args->probabilities unused, and the value cache.  The output equals the
+ * three calls' up to FP32 rounding (each 64-position chunk's exponentials
+ * are taken against the chunk's own largest score and the chunks rescaled
+ * when they are added).  No counterpart in the reference: the C++ host's
+ * executor uses it when it fuses those three dispatches of a program. */
+int si_hip_batch_gqa_attention(si_hip_context* ctx, const si_hip_batch_attention_args* args,
+                               const void* value_cache);
+
 int si_hip_batch_values_workspace_bytes(int batch, int query_heads, int context, uint64_t* bytes);
 
 /* output = input[valid - 1] when 0 < valid <= batch.  Replaces:

@@ -16,6 +16,8 @@
 //   batch-causal-softmax     :472-542  softmax over columns <= start + r, 0 elsewhere
 //   batch-gqa-values         :544-598  sum over columns <= start + r of p * v
 //   batch-select-last        :600-625  out = in[valid - 1]
+//   (scores, softmax and values fused into two launches for programs whose
+//   scores and probabilities are not read afterwards: no reference operator)
 //
 // Caches are [context][kv_heads][head] (FP32 as in the reference, or fp16).
 // The attention launches are built for 128-value heads.
@@ -507,6 +509,243 @@ __global__ __launch_bounds__(BATCH_HEAD) void batch_gqa_values_reduce_kernel(Bat
     a.out[(static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + threadIdx.x] = sum;
 }
 
+// ---- scores, causal softmax and values in two launches ------------------------------------
+//
+// First pass: one workgroup per (KV head, 64 positions) holding a live
+// position.  The group's scores of the chunk come from the matrix cores as
+// in batch_gqa_scores_kernel (positions past a row's own position, or past
+// the batch's last one, -inf) into an LDS tile; one wave per query turns its
+// row of the tile into exp(s - m), m the row's largest score in the chunk, and
+// l, their sum; the tile times the chunk's V rows (requested before the
+// scores) as in batch_gqa_values_partial_kernel goes to the workspace with
+// (m, l).  Second pass: per (row, head), the chunks up to the row's own
+// position merge as sum_c exp(m_c - M) acc_c / sum_c exp(m_c - M) l_c, M the
+// largest m_c: the causal softmax's weighted sum, rounded in another order.
+// A row with no position of the chunk at or before its own gets m = -inf,
+// l = 0, and a zero row of P; the merge never reads such a chunk for it.
+constexpr int FLASH_PITCH = BATCH_CHUNK + 4;   // floats per query row of the tile (rows 4 banks apart)
+
+template <typename T>
+__global__ __launch_bounds__(THREADS) void batch_gqa_flash_partial_kernel(BatchAttentionArgs a,
+                                                                          const T* __restrict__ kc,
+                                                                          const T* __restrict__ vc)
+{
+    __shared__ __align__(16) float tile[BATCH_MAX * BATCH_GROUP_MAX * FLASH_PITCH];
+    const int g = blockIdx.x, chunk = blockIdx.y;
+    const int group = a.query_heads / a.kv_heads;
+    const int start = a.control[0], valid = min(a.control[1], a.batch);
+    const int nq = max(valid, 0) * group;
+    const int64_t last = static_cast<int64_t>(start) + valid - 1;
+    const int j0 = chunk * BATCH_CHUNK;
+    if (nq == 0 || last < 0 || j0 > last)
+        return;   // the whole workgroup: no live position in this chunk
+    const int jl = static_cast<int>(min(last, static_cast<int64_t>(a.context) - 1));   // last position read
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, c = lane >> 4;
+    const int64_t entries = static_cast<int64_t>(a.batch) * a.query_heads;
+    const int64_t chunks = (a.context + BATCH_CHUNK - 1) / BATCH_CHUNK;
+    // V rows: positions jc + s (s < 16) of lane group c, channels 32 wave + 2n and + 1
+    const int jc = j0 + 16 * c;
+    float2 v[16];
+    {
+        const T* src = vc + static_cast<int64_t>(g) * BATCH_HEAD + 32 * wave + 2 * n;
+        const int64_t stride = static_cast<int64_t>(a.kv_heads) * BATCH_HEAD;
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const float2 f = load2(src + min(jc + s, jl) * stride);   // rows past jl: read jl's, use 0
+            v[s] = jc + s <= jl ? f : make_float2(0.0f, 0.0f);
+        }
+    }
+    // keys: position j of this lane, dims 32c .. 32c + 31
+    const int j = j0 + 16 * wave + n;
+    float k[32];
+    {
+        const T* src = kc + (static_cast<int64_t>(min(j, jl)) * a.kv_heads + g) * BATCH_HEAD + 32 * c;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            load8(src + 8 * i, k + 8 * i);
+    }
+    auto load_q = [&](int p, float* q) {
+        const int qi = 16 * p + n;
+        if (qi < nq) {
+            const int r = qi / group, h = g * group + qi % group;
+            const float* src = a.query + (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + 32 * c;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                load8(src + 8 * i, q + 8 * i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++)
+                q[i] = 0.0f;
+        }
+    };
+    const float scale = 1.0f / sqrtf(static_cast<float>(BATCH_HEAD));
+    auto score_pass = [&](int p, const float* q) {
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 32; s++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(q[s], k[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int qi = 16 * p + 4 * c + e;
+            if (qi < nq) {
+                const int64_t active = static_cast<int64_t>(start) + qi / group;
+                tile[qi * FLASH_PITCH + 16 * wave + n] = j <= jl && j <= active ? acc[e] * scale : -INFINITY;
+            }
+        }
+    };
+    const int passes = (nq + 15) / 16;
+    {
+        float q0[32], q1[32];
+        load_q(0, q0);
+        for (int p = 0; p < passes; p += 2) {
+            if (p + 1 < passes)
+                load_q(p + 1, q1);
+            score_pass(p, q0);
+            if (p + 2 < passes)
+                load_q(p + 2, q0);
+            if (p + 1 < passes)
+                score_pass(p + 1, q1);
+        }
+    }
+    __syncthreads();
+    float* ml = a.workspace + chunks * entries * BATCH_HEAD;   // (m, l) per [chunk][row][head]
+    // four queries a wave at a time (queries wave, wave + 4, ... ), their
+    // reductions interleaved
+    constexpr int SQ = 4;
+    for (int q0 = wave; q0 < nq; q0 += SQ * (THREADS / 64)) {
+        float sc[SQ], m[SQ], e[SQ], l[SQ];
+#pragma unroll
+        for (int u = 0; u < SQ; u++) {
+            const int qi = q0 + u * (THREADS / 64);
+            sc[u] = qi < nq ? tile[qi * FLASH_PITCH + lane] : -INFINITY;
+            m[u] = sc[u];
+        }
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int u = 0; u < SQ; u++)
+                m[u] = fmaxf(m[u], __shfl_xor(m[u], off));
+#pragma unroll
+        for (int u = 0; u < SQ; u++) {
+            e[u] = m[u] == -INFINITY ? 0.0f : expf(sc[u] - m[u]);
+            l[u] = e[u];
+        }
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int u = 0; u < SQ; u++)
+                l[u] += __shfl_xor(l[u], off);
+#pragma unroll
+        for (int u = 0; u < SQ; u++) {
+            const int qi = q0 + u * (THREADS / 64);
+            if (qi < nq) {
+                tile[qi * FLASH_PITCH + lane] = e[u];
+                if (lane == 0) {
+                    const int r = qi / group, h = g * group + qi % group;
+                    float* dst = ml + ((static_cast<int64_t>(chunk) * a.batch + r) * a.query_heads + h) * 2;
+                    dst[0] = m[u];
+                    dst[1] = l[u];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    auto load_p = [&](int p, float* pr) {
+        const int qi = 16 * p + n;
+        if (qi < nq) {
+            const float4* src = reinterpret_cast<const float4*>(tile + qi * FLASH_PITCH + 16 * c);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 f = src[i];
+                pr[4 * i] = f.x; pr[4 * i + 1] = f.y; pr[4 * i + 2] = f.z; pr[4 * i + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+                pr[s] = 0.0f;
+        }
+    };
+    for (int p = 0; p < passes; p++) {
+        float pr[16];
+        load_p(p, pr);
+        floatx4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            lo = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[s], v[s].x, lo, 0, 0, 0);
+            hi = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[s], v[s].y, hi, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int qi = 16 * p + 4 * c + e;
+            if (qi < nq) {
+                const int r = qi / group, h = g * group + qi % group;
+                float* dst = a.workspace + ((static_cast<int64_t>(chunk) * a.batch + r) * a.query_heads + h) *
+                                               BATCH_HEAD + 32 * wave + 2 * n;
+                *reinterpret_cast<float2*>(dst) = make_float2(lo[e], hi[e]);
+            }
+        }
+    }
+}
+
+// Second pass: one workgroup per (live row, query head), a thread per
+// channel.  The chunks' (m, l) are read at once (thread t takes chunks t and
+// t + 128: a context of at most 16384 positions has 256 chunks), the weights
+// exp(m_c - M) go through LDS, and the partial sums are requested
+// VALUES_BATCH chunks at a time.
+constexpr int FLASH_MAX_CHUNKS = 2 * BATCH_HEAD;
+
+__global__ __launch_bounds__(BATCH_HEAD) void batch_gqa_flash_merge_kernel(BatchAttentionArgs a)
+{
+    __shared__ float weight[FLASH_MAX_CHUNKS];
+    __shared__ float red[BATCH_HEAD / 64];
+    const int r = blockIdx.x / a.query_heads, h = blockIdx.x % a.query_heads;
+    if (r >= min(a.control[1], a.batch))
+        return;
+    const int64_t active = static_cast<int64_t>(a.control[0]) + r;
+    const int64_t o = (static_cast<int64_t>(r) * a.query_heads + h) * BATCH_HEAD + threadIdx.x;
+    if (active < 0) {   // the whole workgroup
+        a.out[o] = 0.0f;
+        return;
+    }
+    const int t = threadIdx.x;
+    const int nch = static_cast<int>(min(active, static_cast<int64_t>(a.context) - 1) / BATCH_CHUNK) + 1;
+    const int64_t entries = static_cast<int64_t>(a.batch) * a.query_heads;
+    const int64_t chunks = (a.context + BATCH_CHUNK - 1) / BATCH_CHUNK;
+    const int64_t e0 = static_cast<int64_t>(r) * a.query_heads + h;
+    const float* ml = a.workspace + chunks * entries * BATCH_HEAD + 2 * e0;
+    float m[2], l[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int c = t + BATCH_HEAD * i;
+        const float2 f = c < nch ? *reinterpret_cast<const float2*>(ml + c * 2 * entries) : make_float2(-INFINITY, 0.0f);
+        m[i] = f.x;
+        l[i] = f.y;
+    }
+    const float M = block_max<BATCH_HEAD>(fmaxf(m[0], m[1]), red);   // finite: chunk 0 holds position 0
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int c = t + BATCH_HEAD * i;
+        if (c < nch) {
+            const float w = m[i] == -INFINITY ? 0.0f : expf(m[i] - M);
+            weight[c] = w;
+            lsum += w * l[i];
+        }
+    }
+    const float L = block_sum<BATCH_HEAD>(lsum, red);   // its barriers publish the weights
+    const float* part = a.workspace + e0 * BATCH_HEAD + t;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += VALUES_BATCH) {
+        float pv[VALUES_BATCH];
+#pragma unroll
+        for (int i = 0; i < VALUES_BATCH; i++)
+            pv[i] = part[static_cast<int64_t>(min(c0 + i, nch - 1)) * entries * BATCH_HEAD];
+#pragma unroll
+        for (int i = 0; i < VALUES_BATCH; i++)
+            if (c0 + i < nch)
+                acc += weight[c0 + i] * pv[i];
+    }
+    a.out[o] = acc / L;
+}
+
 __global__ __launch_bounds__(THREADS) void batch_select_last_kernel(const float* __restrict__ input,
                                                                     float* __restrict__ out, int batch, int width,
                                                                     const int32_t* __restrict__ control)
@@ -894,7 +1133,8 @@ __global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
 
 int64_t batch_values_workspace_floats(int batch, int query_heads, int context)
 {
-    return static_cast<int64_t>((context + BATCH_CHUNK - 1) / BATCH_CHUNK) * batch * query_heads * BATCH_HEAD;
+    // chunk partials [chunk][row][head][128], then the fused form's (m, l) per [chunk][row][head]
+    return static_cast<int64_t>((context + BATCH_CHUNK - 1) / BATCH_CHUNK) * batch * query_heads * (BATCH_HEAD + 2);
 }
 
 hipError_t launch_batch_gather_rows(const float* table, int64_t table_rows, int width, const int32_t* control,
@@ -988,6 +1228,24 @@ hipError_t launch_batch_gqa_values(const BatchAttentionArgs& a, hipStream_t s)
     if (e != hipSuccess)
         return e;
     hipLaunchKernelGGL(batch_gqa_values_reduce_kernel, dim3(static_cast<unsigned>(a.batch * a.query_heads)),
+                       dim3(BATCH_HEAD), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_gqa_attention(const BatchAttentionArgs& a, const void* value_cache, hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>(a.kv_heads),
+                    static_cast<unsigned>((a.context + BATCH_CHUNK - 1) / BATCH_CHUNK));
+    if (a.cache_fp16)
+        hipLaunchKernelGGL((batch_gqa_flash_partial_kernel<__half>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<const __half*>(a.cache), static_cast<const __half*>(value_cache));
+    else
+        hipLaunchKernelGGL((batch_gqa_flash_partial_kernel<float>), grid, dim3(THREADS), 0, s, a,
+                           static_cast<const float*>(a.cache), static_cast<const float*>(value_cache));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(batch_gqa_flash_merge_kernel, dim3(static_cast<unsigned>(a.batch * a.query_heads)),
                        dim3(BATCH_HEAD), 0, s, a);
     return hipGetLastError();
 }

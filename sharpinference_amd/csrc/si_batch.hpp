@@ -58,6 +58,10 @@ hipError_t launch_batch_gqa_scores(const BatchAttentionArgs& a, hipStream_t s);
 hipError_t launch_batch_causal_softmax(const float* scores, float* probabilities, int batch, int heads, int context,
                                        const int32_t* control, hipStream_t s);
 hipError_t launch_batch_gqa_values(const BatchAttentionArgs& a, hipStream_t s);
+// scores, causal softmax and values in two launches: a.cache is the key cache,
+// a.query the queries, a.out the values' output, a.workspace the values'
+// workspace; a.probabilities is not used.
+hipError_t launch_batch_gqa_attention(const BatchAttentionArgs& a, const void* value_cache, hipStream_t s);
 hipError_t launch_batch_select_last(const float* input, float* out, int batch, int width, const int32_t* control,
                                     hipStream_t s);
 // y[t][o] = sum_k x[t][k] W[o][k] for t < min(batch, valid), FP32 products

@@ -60,8 +60,8 @@ int launched(si_hip_context* ctx, hipError_t e, const char* op)
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, op);
 }
 
-// The attention launches' shared checks; `values` selects the values form.
-int check_attention(si_hip_context* ctx, const char* op, const si_hip_batch_attention_args* a, bool values)
+// The attention launches' shape checks.
+int check_attention_shape(si_hip_context* ctx, const char* op, const si_hip_batch_attention_args* a)
 {
     if (!a)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: null arguments", op);
@@ -78,6 +78,15 @@ int check_attention(si_hip_context* ctx, const char* op, const si_hip_batch_atte
                     a->query_heads, si::BATCH_GROUP_MAX, a->kv_heads);
     if (a->context < 1 || a->context > 16384)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: context %d outside 1..16384", op, a->context);
+    return SI_HIP_OK;
+}
+
+// The attention launches' shared checks; `values` selects the values form.
+int check_attention(si_hip_context* ctx, const char* op, const si_hip_batch_attention_args* a, bool values)
+{
+    if (const int rc = check_attention_shape(ctx, op, a))
+        return rc;
+    const int cb = cache_bytes(a->cache_format);
     const uint64_t q_b = static_cast<uint64_t>(a->batch) * a->query_heads * si::BATCH_HEAD * 4;
     const uint64_t s_b = static_cast<uint64_t>(a->batch) * a->query_heads * a->context * 4;
     const uint64_t c_b = static_cast<uint64_t>(a->context) * a->kv_heads * si::BATCH_HEAD * cb;
@@ -322,6 +331,27 @@ int si_hip_batch_gqa_values(si_hip_context* ctx, const si_hip_batch_attention_ar
     if (const int rc = check_attention(ctx, "batch_gqa_values", a, true))
         return rc;
     return launched(ctx, si::launch_batch_gqa_values(attention(a), ctx->stream), "batch_gqa_values");
+}
+
+int si_hip_batch_gqa_attention(si_hip_context* ctx, const si_hip_batch_attention_args* a, const void* value_cache)
+{
+    if (!ctx)
+        return fail(nullptr, SI_HIP_ERR_ARGUMENT, "batch_gqa_attention: null context");
+    Enter g(ctx);
+    const char* op = "batch_gqa_attention";
+    if (const int rc = check_attention_shape(ctx, op, a))
+        return rc;
+    const uint64_t q_b = static_cast<uint64_t>(a->batch) * a->query_heads * si::BATCH_HEAD * 4;
+    const uint64_t c_b = static_cast<uint64_t>(a->context) * a->kv_heads * si::BATCH_HEAD * cache_bytes(a->cache_format);
+    const uint64_t ws_b = static_cast<uint64_t>(si::batch_values_workspace_floats(a->batch, a->query_heads, a->context)) * 4;
+    if (check_ptr(ctx, op, a->query, "query", 16) || check_ptr(ctx, op, a->cache, "cache", 16) ||
+        check_ptr(ctx, op, value_cache, "value_cache", 16) || check_ptr(ctx, op, a->control, "control") ||
+        check_ptr(ctx, op, a->output, "output", 8) || check_ptr(ctx, op, a->workspace, "workspace", 8))
+        return SI_HIP_ERR_ARGUMENT;
+    if (check_disjoint(ctx, op, {{a->output, q_b}, {a->workspace, ws_b}},
+                       {{a->query, q_b}, {a->cache, c_b}, {value_cache, c_b}, {a->control, 8}}))
+        return SI_HIP_ERR_ARGUMENT;
+    return launched(ctx, si::launch_batch_gqa_attention(attention(a), value_cache, ctx->stream), op);
 }
 
 int si_hip_batch_values_workspace_bytes(int batch, int query_heads, int context, uint64_t* bytes)

@@ -852,6 +852,25 @@ void HipVmExecutor::LaunchGemvFused(const InstructionRecording& g, const void* x
           context_);
 }
 
+void HipVmExecutor::LaunchBatchAttentionFused(const InstructionRecording& sr, const InstructionRecording& vr)
+{
+    const auto& k = Find(sr.parameters, "key_cache")->tensor;
+    const auto& sd = Find(sr.parameters, "scores")->tensor.dimensions;
+    si_hip_batch_attention_args a{};
+    a.query = static_cast<const float*>(Address(*Find(sr.parameters, "query")));
+    a.cache = Address(*Find(sr.parameters, "key_cache"));
+    a.control = static_cast<const int32_t*>(Address(*Find(sr.parameters, "control")));
+    a.output = static_cast<float*>(Address(*Find(vr.parameters, "output")));
+    a.workspace = static_cast<float*>(scratch_);
+    a.cache_format = k.element_type == GraphElementType::Float16 ? SI_HIP_F16 : SI_HIP_F32;
+    a.batch = static_cast<int32_t>(sd[0]);
+    a.query_heads = static_cast<int32_t>(sd[1]);
+    a.kv_heads = static_cast<int32_t>(k.dimensions[1]);
+    a.head_size = static_cast<int32_t>(k.dimensions[2]);
+    a.context = static_cast<int32_t>(k.dimensions[0]);
+    Check(si_hip_batch_gqa_attention(context_, &a, Address(*Find(vr.parameters, "value_cache"))), context_);
+}
+
 size_t HipVmExecutor::FuseAt(const std::vector<HipVmDispatch>& ds, size_t i, bool launch, int* launches)
 {
     const auto slot_bytes = [&](const InstructionParameter* p) {
@@ -859,6 +878,26 @@ size_t HipVmExecutor::FuseAt(const std::vector<HipVmDispatch>& ds, size_t i, boo
     };
     const auto param = [&](size_t k, const char* n) { return Find(ds[k].recording.parameters, n); };
     *launches = 0;
+    // batch gqa-scores -> causal-softmax -> gqa-values, when nothing reads the
+    // scores or probabilities afterwards: si_hip_batch_gqa_attention
+    if (IsOp(ds, i, "si_hip_batch_gqa_scores") && IsOp(ds, i + 1, "si_hip_batch_causal_softmax") &&
+        IsOp(ds, i + 2, "si_hip_batch_gqa_values")) {
+        const auto* sc = param(i, "scores");
+        const auto* pr = param(i + 1, "probabilities");
+        const auto* kc = param(i, "key_cache");
+        const auto* vc = param(i + 2, "value_cache");
+        if (SameView(sc, param(i + 1, "scores")) && SameView(pr, param(i + 2, "probabilities")) &&
+            SameView(param(i, "control"), param(i + 1, "control")) &&
+            SameView(param(i, "control"), param(i + 2, "control")) &&
+            kc->tensor.element_type == vc->tensor.element_type && kc->tensor.dimensions == vc->tensor.dimensions &&
+            sc->tensor.dimensions == pr->tensor.dimensions && DeadAfter(ds, i + 2, sc->source, slot_bytes(sc)) &&
+            DeadAfter(ds, i + 2, pr->source, slot_bytes(pr))) {
+            if (launch)
+                LaunchBatchAttentionFused(ds[i].recording, ds[i + 2].recording);
+            *launches = 1;
+            return 3;
+        }
+    }
     // rms-norm -> mat-vec
     if (IsOp(ds, i, "si_hip_rms_norm") && IsGemv(ds, i + 1)) {
         const auto* out = param(i, "output");

@@ -516,6 +516,7 @@ private:
     size_t FuseAt(const std::vector<HipVmDispatch>& ds, size_t i, bool launch, int* launches);
     void LaunchGemvFused(const InstructionRecording& gemv, const void* x, void* y, const void* residual, int xform,
                          const void* norm_weight, float eps);
+    void LaunchBatchAttentionFused(const InstructionRecording& scores, const InstructionRecording& values);
     bool fuse_ = true;
 
     HipVmProgram program_;

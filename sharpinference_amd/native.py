@@ -218,6 +218,7 @@ SIGNATURES.update({
     "si_hip_batch_gqa_scores": ([_vp, ctypes.POINTER(BatchAttentionArgs)], _i32),
     "si_hip_batch_causal_softmax": ([_vp, _vp, _vp, _vp, _i32, _i32, _i64], _i32),
     "si_hip_batch_gqa_values": ([_vp, ctypes.POINTER(BatchAttentionArgs)], _i32),
+    "si_hip_batch_gqa_attention": ([_vp, ctypes.POINTER(BatchAttentionArgs), _vp], _i32),
     "si_hip_batch_values_workspace_bytes": ([_i32, _i32, _i32, ctypes.POINTER(_u64)], _i32),
     "si_hip_batch_select_last": ([_vp, _vp, _vp, _vp, _i32, _i64], _i32),
     "si_hip_phi4_workspace_bytes": ([ctypes.POINTER(Phi4Model), ctypes.POINTER(_u64)], _i32),
@@ -481,6 +482,10 @@ class HipContext:
 
     def batch_gqa_values(self, args: "BatchAttentionArgs") -> None:
         self._call(lib().si_hip_batch_gqa_values, ctypes.byref(args))
+
+    def batch_gqa_attention(self, args: "BatchAttentionArgs", value_cache: int) -> None:
+        """Scores, causal softmax and values in two launches (args.cache the key cache)."""
+        self._call(lib().si_hip_batch_gqa_attention, ctypes.byref(args), _p(value_cache))
 
     def batch_select_last(self, x: int, control: int, out: int, batch: int, width: int) -> None:
         self._call(lib().si_hip_batch_select_last, _p(x), _p(control), _p(out), batch, width)

@@ -254,6 +254,46 @@ def test_batch_attention_chain(hip, fmt, heads, kv_heads, context, start, valid)
         b.free()
 
 
+@pytest.mark.parametrize("fmt", [native.F32, native.F16], ids=["f32", "f16"])
+@pytest.mark.parametrize("heads,kv_heads,context,start,valid",
+                         [(24, 8, 4096, 2040, 16), (6, 2, 300, 0, 16), (8, 8, 64, 50, 5), (32, 4, 1024, 1016, 9),
+                          (24, 8, 4096, 0, 16), (16, 2, 200, 130, 16), (8, 4, 100, 95, 3)])
+def test_batch_attention_fused(hip, fmt, heads, kv_heads, context, start, valid):
+    """si_hip_batch_gqa_attention: the scores / softmax / values chain in two
+    launches, against the float64 softmax-weighted sum over positions <= the
+    row's own (chunks rescaled by their own maxima: FP32 rounding only)."""
+    B, head = 16, 128
+    group = heads // kv_heads
+    rng = np.random.default_rng(3 * heads + context + start)
+    dt = np.float32 if fmt == native.F32 else np.float16
+    q = rng.standard_normal((B, heads * head)).astype(np.float32)
+    kc = rng.standard_normal((context, kv_heads, head)).astype(dt)
+    vc = rng.standard_normal((context, kv_heads, head)).astype(dt)
+    dq, dk, dv, ctl = hip.to_device(q), hip.to_device(kc), hip.to_device(vc), _control(hip, start, valid)
+    dout = _filled(hip, (B, heads * head))
+    ws = hip.alloc(native.batch_values_workspace_bytes(B, heads, context))
+    args = native.BatchAttentionArgs(dq.ptr, 0, dk.ptr, ctl.ptr, dout.ptr, ws.ptr, fmt, B, heads, kv_heads, head,
+                                     context)
+    hip.batch_gqa_attention(args, dv.ptr)
+    out = dout.readback(np.float32).reshape(B, heads * head)
+    for r in range(B):
+        if r >= valid:
+            assert np.all(out[r] == SENTINEL), f"row {r} written"
+            continue
+        act = min(start + r, context - 1)
+        truth = np.empty(heads * head)
+        for h in range(heads):
+            K = kc[:act + 1, h // group].astype(np.float64)
+            V = vc[:act + 1, h // group].astype(np.float64)
+            s64 = K @ q[r, h * head:(h + 1) * head].astype(np.float64) / np.sqrt(head)
+            p = np.exp(s64 - s64.max())
+            truth[h * head:(h + 1) * head] = (p / p.sum()) @ V
+        assert np.linalg.norm(out[r] - truth) / np.linalg.norm(truth) <= 1e-5, f"row {r}"
+        _close(out[r], truth, 1e-3, f"row {r}")
+    for b in (dq, dk, dv, ctl, dout, ws):
+        b.free()
+
+
 def test_batch_rejections(hip):
     buf = hip.alloc(1 << 22)
     p = buf.ptr
@@ -278,4 +318,9 @@ def test_batch_rejections(hip):
     assert status(lambda: hip.batch_gqa_scores(a)) == native.ERR_ARGUMENT                          # 9 heads per KV head
     a = native.BatchAttentionArgs(p, p, p + 65536, ctl, p + 131072, p + 131072, native.F32, 4, 4, 2, 128, 16)
     assert status(lambda: hip.batch_gqa_values(a)) == native.ERR_ARGUMENT                          # workspace = output
+    a = native.BatchAttentionArgs(p, 0, p + 65536, ctl, p + 131072, p + 262144, native.F32, 4, 4, 2, 128, 16)
+    assert status(lambda: hip.batch_gqa_attention(a, p + 65536 + 8)) == native.ERR_ARGUMENT        # misaligned V
+    assert status(lambda: hip.batch_gqa_attention(a, p + 131072)) == native.ERR_ARGUMENT           # V = output
+    a = native.BatchAttentionArgs(p, 0, p + 65536, ctl, p + 131072, p + 262144, native.F32, 4, 18, 2, 128, 16)
+    assert status(lambda: hip.batch_gqa_attention(a, p + 98304)) == native.ERR_ARGUMENT            # 9 heads per KV
     buf.free()

@@ -54,6 +54,9 @@ def test_prefill_then_decode_matches_float64_model(hip, prompt):
     ref = Float64Phi4(SimpleNamespace(**cfg.__dict__), weights, zeros, zeros, cache_dtype=np.float64)
     try:
         assert prog.dispatch_count("prefill_fused_16") == 2 + 11 * cfg.layers + 3
+        # scores -> softmax -> values run as one fused call in every layer but
+        # the last, whose scores and probabilities the entry leaves behind
+        assert prog.launch_count("prefill_fused_16") == 2 + 11 * cfg.layers + 3 - 2 * (cfg.layers - 1)
         g = prog.prefill_embeddings(_embeddings(cfg, weights, tokens))
         for pos, t in enumerate(tokens):
             truth = ref.step(int(t), pos)
