@@ -23,6 +23,7 @@
 // The attention launches are built for 128-value heads.
 #include "si_batch.hpp"
 #include "si_internal.hpp"
+#include "si_lanes.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -580,10 +581,13 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_flash_partial_kernel(BatchA
     };
     const float scale = 1.0f / sqrtf(static_cast<float>(BATCH_HEAD));
     auto score_pass = [&](int p, const float* q) {
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};   // two product chains
 #pragma unroll
-        for (int s = 0; s < 32; s++)
+        for (int s = 0; s < 32; s += 2) {
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(q[s], k[s], acc, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(q[s + 1], k[s + 1], acc1, 0, 0, 0);
+        }
+        acc += acc1;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int qi = 16 * p + 4 * c + e;
@@ -620,19 +624,17 @@ __global__ __launch_bounds__(THREADS) void batch_gqa_flash_partial_kernel(BatchA
             sc[u] = qi < nq ? tile[qi * FLASH_PITCH + lane] : -INFINITY;
             m[u] = sc[u];
         }
-        for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-            for (int u = 0; u < SQ; u++)
-                m[u] = fmaxf(m[u], __shfl_xor(m[u], off));
+        for (int u = 0; u < SQ; u++)
+            m[u] = rows_max(row_max<16>(m[u]));   // DPP within rows of 16, then across the 4 rows
 #pragma unroll
         for (int u = 0; u < SQ; u++) {
             e[u] = m[u] == -INFINITY ? 0.0f : expf(sc[u] - m[u]);
             l[u] = e[u];
         }
-        for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-            for (int u = 0; u < SQ; u++)
-                l[u] += __shfl_xor(l[u], off);
+        for (int u = 0; u < SQ; u++)
+            l[u] = rows_sum(row_sum<16>(l[u]));
 #pragma unroll
         for (int u = 0; u < SQ; u++) {
             const int qi = q0 + u * (THREADS / 64);

@@ -16,6 +16,17 @@ __device__ __forceinline__ float row_sum(float v)
     return v;
 }
 
+// Maximum over aligned groups of N (<= 16) lanes with DPP.
+template <int N>
+__device__ __forceinline__ float row_max(float v)
+{
+    if constexpr (N >= 2) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    if constexpr (N >= 4) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    if constexpr (N >= 8) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
+    if constexpr (N >= 16) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
+    return v;
+}
+
 // Swaps between the halves (32 lanes) and the row pairs (16 lanes) of a
 // wave: after both steps every lane holds the combination of the four lanes
 // l, l ^ 16, l ^ 32, l ^ 48 (its column of the wave's four rows).
