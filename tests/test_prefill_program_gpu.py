@@ -165,3 +165,39 @@ def test_program_loaded_from_xml_and_artifact_runs_identically(hip):
     finally:
         for p in programs:
             p.close()
+
+
+def test_prefill_fusion_keeps_what_the_entry_leaves(hip):
+    """The fused attention (scores -> softmax -> values as one call in every
+    layer but the last) leaves the same last-layer scores and probabilities
+    behind, and the prompt's hidden state, caches and logits agree with the
+    dispatch-by-dispatch entry to FP32 rounding."""
+    cfg = phi4.Phi4Config(layers=3, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=3000, capacity=96,
+                          rope_scale=1.19)
+    weights = phi4.synth_weights(cfg, seed=71)
+    tokens = np.random.default_rng(72).integers(0, cfg.vocab, 40)
+    out = {}
+    for fuse in (True, False):
+        prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True, prompt_rows=40)
+        try:
+            prog.set_fusion(fuse)
+            expected = 2 + 11 * cfg.layers + 3 - (2 * (cfg.layers - 1) if fuse else 0)
+            assert prog.launch_count("prefill_fused_16") == expected
+            prog.prefill_embeddings(_embeddings(cfg, weights, tokens))
+            out[fuse] = {s: prog.readback(s, np.float32).copy()
+                         for s in ("batch_scores", "batch_probabilities", "batch_hidden", "logits")}
+            out[fuse]["k"], out[fuse]["v"] = (a.copy() for a in prog.read_kv(cfg.layers - 1))
+        finally:
+            prog.close()
+    for s in ("batch_scores", "batch_probabilities"):
+        # written by the last layer's own dispatches in both forms, from inputs that differ by the
+        # earlier layers' rounding (carried through the fp16 caches): the same masked entries, the
+        # rest close
+        a, b = np.asarray(out[True][s], np.float64), np.asarray(out[False][s], np.float64)
+        live = b > -1e30
+        assert np.array_equal(a > -1e30, live), s
+        assert np.allclose(a[live], b[live], rtol=1e-3, atol=1e-3 * float(np.max(np.abs(b[live])))), s
+    for s in ("batch_hidden", "logits", "k", "v"):
+        a, b = np.asarray(out[True][s], np.float64), np.asarray(out[False][s], np.float64)
+        assert np.allclose(a, b, rtol=1e-3, atol=1e-3 * max(1.0, float(np.max(np.abs(b))))), s
+
