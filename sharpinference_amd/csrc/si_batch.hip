@@ -1028,32 +1028,34 @@ __device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, 
         const uint8_t* blk = row + ((18 * b) & 15);
         const float d = half_bits(lds_u16(blk));
         const uint32_t q = lds_u16(blk + 2 + 4 * g) | (lds_u16(blk + 4 + 4 * g) << 16);   // qs[4g..4g+3]
+        const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;                   // one nibble per byte
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            w[e] = d * static_cast<float>(static_cast<int>((q >> (8 * e)) & 15u) - 8);            // element 4g+e
-            w[4 + e] = d * static_cast<float>(static_cast<int>((q >> (8 * e + 4)) & 15u) - 8);    // element 16+4g+e
+        for (int e = 0; e < 4; e++) {   // n - 8 and d (n - 8) are exact in FP32
+            w[e] = d * (static_cast<float>((lo >> (8 * e)) & 0xffu) - 8.0f);       // element 4g+e
+            w[4 + e] = d * (static_cast<float>((hi >> (8 * e)) & 0xffu) - 8.0f);   // element 16+4g+e
         }
-    } else {   // Q4_K sub-block j of the super-block
+    } else {   // Q4_K sub-block j of the super-block (j is the same for the whole wave)
         const int j = b & 7;
-        const uint4 h = *reinterpret_cast<const uint4*>(row);
-        const uint32_t sw[3] = {h.y, h.z, h.w};
-        auto sbyte = [&](int i) { return static_cast<int>((sw[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+        const uint32_t dd = lds_u32(row);   // d, dmin
+        const uint8_t* sb = row + 4;        // the 12 scale bytes
         int sc, m;
         if (j < 4) {
-            sc = sbyte(j) & 63;
-            m = sbyte(j + 4) & 63;
+            sc = sb[j] & 63;
+            m = sb[j + 4] & 63;
         } else {
-            sc = (sbyte(j + 4) & 15) | ((sbyte(j - 4) >> 6) << 4);
-            m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+            const int both = sb[j + 4];
+            sc = (both & 15) | ((sb[j - 4] >> 6) << 4);
+            m = (both >> 4) | ((sb[j] >> 6) << 4);
         }
-        const float d1 = __fmul_rn(half_bits(h.x), static_cast<float>(sc));
-        const float m1 = __fmul_rn(half_bits(h.x >> 16), static_cast<float>(m));
+        const float d1 = __fmul_rn(half_bits(dd), static_cast<float>(sc));
+        const float m1 = __fmul_rn(half_bits(dd >> 16), static_cast<float>(m));
         const int sh = (j & 1) * 4;   // low nibbles for even sub-blocks
-        const uint32_t lo = lds_u32(row + 16 + 4 * g), hi = lds_u32(row + 32 + 4 * g);
+        const uint32_t lo = (lds_u32(row + 16 + 4 * g) >> sh) & 0x0F0F0F0Fu;   // one nibble per byte
+        const uint32_t hi = (lds_u32(row + 32 + 4 * g) >> sh) & 0x0F0F0F0Fu;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            w[e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((lo >> (8 * e + sh)) & 15u)), m1);
-            w[4 + e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((hi >> (8 * e + sh)) & 15u)), m1);
+            w[e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((lo >> (8 * e)) & 0xffu)), m1);
+            w[4 + e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((hi >> (8 * e)) & 0xffu)), m1);
         }
     }
 }
@@ -1092,6 +1094,7 @@ __global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
     for (int k = 0; k < RING - 1 && k < nk; k++)
         request(k);
     const int sw = (r >> 1) & 7;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);   // the wave index as a scalar: block indexes are wave-uniform
     for (int k = 0; k < nk; k++) {
         if (k + RING - 2 < nk)
             wait_copies<(RING - 2) * RING_COPIES>();   // blocks k + 1 .. k + RING - 2 may stay in flight
@@ -1105,7 +1108,7 @@ __global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
         const float4 x1 = *reinterpret_cast<const float4*>(xr + 4 * ((4 + g) ^ sw));
         const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float w[8];
-        decode_staged<FMT>(st + RING_XBYTES + RING_WPITCH * r, wave + RING_WAVES * k, g, w);
+        decode_staged<FMT>(st + RING_XBYTES + RING_WPITCH * r, wv + RING_WAVES * k, g, w);
 #pragma unroll
         for (int s = 0; s < 8; s += 2) {
             acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s], w[s], acc0, 0, 0, 0);
