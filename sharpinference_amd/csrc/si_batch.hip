@@ -1060,26 +1060,26 @@ __device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, 
     }
 }
 
-template <int FMT, int RING>
-__global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
+template <int FMT, int RING, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void batch_matvec_ring_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ X, float* __restrict__ Y, int batch, int rows, int cols,
     int64_t row_bytes, const int32_t* __restrict__ control)
 {
     constexpr int WAVE_RING = RING * RING_STAGE;
     static_assert(RING >= 2 && (RING - 2) * RING_COPIES < 64, "vmcnt range");
-    __shared__ __align__(16) uint8_t ring[RING_WAVES * WAVE_RING];
+    __shared__ __align__(16) uint8_t ring[WAVES * WAVE_RING];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
     const int o0 = static_cast<int>(blockIdx.x) * 16, t0 = static_cast<int>(blockIdx.y) * 16;
     const int live = min(control[1], batch) - t0;   // live batch rows of this tile
     if (live <= 0)
         return;   // the whole workgroup, before any copy or barrier
-    const int nk = cols / (32 * RING_WAVES);        // blocks of each wave: b = wave + 8 k
+    const int nk = cols / (32 * WAVES);        // blocks of each wave: b = wave + WAVES k
     const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) + wave * WAVE_RING;
     const int xrow = lane >> 3, xslot = lane & 7;   // X copy lane: row 8h + xrow, slot xslot
     const int wrow = lane / 3, wpiece = lane % 3;   // weight copy lane (lanes < 48)
     const uint8_t* wsrc = W + static_cast<int64_t>(min(o0 + wrow, rows - 1)) * row_bytes;
     auto request = [&](int k) {   // block wave + 8k into stage k % RING
-        const int b = wave + RING_WAVES * k;
+        const int b = wave + WAVES * k;
         const uint32_t st = base + static_cast<uint32_t>((k % RING) * RING_STAGE);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -1108,7 +1108,7 @@ __global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
         const float4 x1 = *reinterpret_cast<const float4*>(xr + 4 * ((4 + g) ^ sw));
         const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float w[8];
-        decode_staged<FMT>(st + RING_XBYTES + RING_WPITCH * r, wv + RING_WAVES * k, g, w);
+        decode_staged<FMT>(st + RING_XBYTES + RING_WPITCH * r, wv + WAVES * k, g, w);
 #pragma unroll
         for (int s = 0; s < 8; s += 2) {
             acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s], w[s], acc0, 0, 0, 0);
@@ -1122,7 +1122,7 @@ __global__ __launch_bounds__(64 * RING_WAVES) void batch_matvec_ring_kernel(
     if (wave == 0) {
         floatx4 v = red[lane];
 #pragma unroll
-        for (int k = 1; k < RING_WAVES; k++)
+        for (int k = 1; k < WAVES; k++)
             v += red[k * 64 + lane];
         const int o = o0 + r;
 #pragma unroll
@@ -1271,25 +1271,32 @@ hipError_t launch_batch_matvec(int fmt, const void* w, const float* x, float* y,
     const int64_t rb = row_bytes(fmt, cols);
     const int r = static_cast<int>(rows), c = static_cast<int>(cols);
     if (cols % (32 * RING_WAVES) == 0) {   // weight and input are 16-byte aligned (checked by the ABI)
-        // three stages a wave keep two workgroups on a CU (67.6 KB of LDS
-        // each); grids of at most one workgroup per CU take four
-        const bool deep = (rows + 15) / 16 <= 256;
-        const dim3 block(64 * RING_WAVES);
+        // grids of more than one workgroup per CU: 8 waves with three stages
+        // each (67.6 KB of LDS, two workgroups a CU); smaller grids: 16 waves
+        // (four a SIMD on the CUs they occupy) when the blocks divide, else 8
+        // waves with four stages
+        const bool small = (rows + 15) / 16 <= 256;
+        const bool wide = small && cols % (32 * 2 * RING_WAVES) == 0;
+#define SI_RING_LAUNCH(F)                                                                                              \
+    do {                                                                                                              \
+        if (wide)                                                                                                     \
+            hipLaunchKernelGGL((batch_matvec_ring_kernel<F, 3, 2 * RING_WAVES>), grid, dim3(128 * RING_WAVES), 0, s,  \
+                               wb, x, y, batch, r, c, rb, control);                                                   \
+        else if (small)                                                                                               \
+            hipLaunchKernelGGL((batch_matvec_ring_kernel<F, 4, RING_WAVES>), grid, dim3(64 * RING_WAVES), 0, s, wb,   \
+                               x, y, batch, r, c, rb, control);                                                       \
+        else                                                                                                          \
+            hipLaunchKernelGGL((batch_matvec_ring_kernel<F, 3, RING_WAVES>), grid, dim3(64 * RING_WAVES), 0, s, wb,   \
+                               x, y, batch, r, c, rb, control);                                                       \
+        return hipGetLastError();                                                                                     \
+    } while (0)
         switch (fmt) {
-        case FMT_Q8_0:
-            if (deep) hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q8_0, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
-            else hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q8_0, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
-            return hipGetLastError();
-        case FMT_Q4_0:
-            if (deep) hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_0, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
-            else hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_0, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
-            return hipGetLastError();
-        case FMT_Q4_K:
-            if (deep) hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_K, 4>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
-            else hipLaunchKernelGGL((batch_matvec_ring_kernel<FMT_Q4_K, 3>), grid, block, 0, s, wb, x, y, batch, r, c, rb, control);
-            return hipGetLastError();
+        case FMT_Q8_0: SI_RING_LAUNCH(FMT_Q8_0);
+        case FMT_Q4_0: SI_RING_LAUNCH(FMT_Q4_0);
+        case FMT_Q4_K: SI_RING_LAUNCH(FMT_Q4_K);
         default: break;
         }
+#undef SI_RING_LAUNCH
     }
     switch (fmt) {
     case FMT_Q8_0: hipLaunchKernelGGL((batch_matvec_kernel<FMT_Q8_0>), grid, dim3(THREADS), 0, s, wb, x, y, batch, r, c, rb, control); break;
