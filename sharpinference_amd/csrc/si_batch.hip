@@ -946,9 +946,11 @@ __global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __
 
 // ---- the same product over per-wave LDS rings filled by asynchronous loads ----------------
 //
-// For Q4_0, Q8_0 and Q4_K with columns % 256 == 0.  A workgroup of RING_WAVES
-// = 8 waves owns 16 output rows x 16 batch rows; wave w multiplies the
-// 32-column blocks w, w + 8, w + 16, ... and copies exactly the bytes it
+// For Q4_0, Q8_0 and Q4_K with columns % 256 == 0.  A workgroup of WAVES
+// (8, or 16 for grids that leave CUs without a second workgroup) owns 16
+// output rows x 16 batch rows; wave w multiplies the 32-column blocks w,
+// w + WAVES, w + 2 WAVES, ... (for Q4_K always sub-block w % 8 of a
+// super-block) and copies exactly the bytes it
 // multiplies into a ring of its own in LDS with global_load_lds_dwordx4: each
 // lane's 16 bytes land at the instruction's LDS base + 16 x lane, no VGPR is
 // held while a copy is in flight, and RING - 1 blocks are requested ahead of
@@ -969,7 +971,7 @@ __global__ __launch_bounds__(THREADS) void batch_matvec_kernel(const uint8_t* __
 // multiple of 16 bytes).  Lane (r, g) = (l % 16, l / 16) multiplies columns
 // 4g..4g+3 and 16+4g..16+4g+3 of the block: eight v_mfma_f32_16x16x4_f32 on
 // two accumulators (even and odd instructions), added at the end.
-constexpr int RING_WAVES = 8;
+constexpr int RING_WAVES = 8;                  // waves of the default workgroup
 constexpr int RING_XBYTES = 16 * 32 * 4;        // X bytes of a stage
 constexpr int RING_WPITCH = 48;                 // bytes per weight row of a stage
 constexpr int RING_STAGE = RING_XBYTES + 16 * RING_WPITCH;
