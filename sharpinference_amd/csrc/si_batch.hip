@@ -1076,27 +1076,37 @@ __global__ __launch_bounds__(64 * WAVES) void batch_matvec_ring_kernel(
     if (live <= 0)
         return;   // the whole workgroup, before any copy or barrier
     const int nk = cols / (32 * WAVES);        // blocks of each wave: b = wave + WAVES k
-    const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) + wave * WAVE_RING;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);   // the wave index as a scalar: block indexes are wave-uniform
+    const uint32_t base = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) + wv * WAVE_RING);
+    // per-lane sources of block wv (k = 0); block wv + WAVES k is WAVES
+    // blocks further along the same rows (for the weights a fixed byte step:
+    // WAVES blocks of 8-block groups, each group a multiple of 16 bytes)
     const int xrow = lane >> 3, xslot = lane & 7;   // X copy lane: row 8h + xrow, slot xslot
+    const float* xsrc[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int row = 8 * h + xrow, piece = xslot ^ ((row >> 1) & 7);   // rows past the live ones repeat the last
+        xsrc[h] = X + static_cast<int64_t>(t0 + min(row, live - 1)) * cols + 32 * wv + 4 * piece;
+    }
     const int wrow = lane / 3, wpiece = lane % 3;   // weight copy lane (lanes < 48)
-    const uint8_t* wsrc = W + static_cast<int64_t>(min(o0 + wrow, rows - 1)) * row_bytes;
-    auto request = [&](int k) {   // block wave + 8k into stage k % RING
-        const int b = wave + WAVES * k;
+    const uint8_t* wsrc = W + static_cast<int64_t>(min(o0 + wrow, rows - 1)) * row_bytes + ring_piece<FMT>(wv, wpiece);
+    constexpr int64_t WSTEP = FMT == FMT_Q4_K ? 144 * WAVES / 8 : (FMT == FMT_Q4_0 ? 18 : 34) * WAVES;
+    auto request = [&](int k) {   // block wv + WAVES k into stage k % RING
         const uint32_t st = base + static_cast<uint32_t>((k % RING) * RING_STAGE);
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int row = 8 * h + xrow, piece = xslot ^ ((row >> 1) & 7);   // rows past the live ones repeat the last
-            copy16_to_lds(X + static_cast<int64_t>(t0 + min(row, live - 1)) * cols + 32 * b + 4 * piece,
-                          __builtin_amdgcn_readfirstlane(st + 1024 * h));
-        }
+        for (int h = 0; h < 2; h++)
+            copy16_to_lds(xsrc[h] + static_cast<int64_t>(32 * WAVES) * k, st + 1024 * h);
         if (lane < 48)
-            copy16_to_lds(wsrc + ring_piece<FMT>(b, wpiece), __builtin_amdgcn_readfirstlane(st + RING_XBYTES));
+            copy16_to_lds(wsrc + WSTEP * k, st + RING_XBYTES);
     };
     floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k = 0; k < RING - 1 && k < nk; k++)
         request(k);
     const int sw = (r >> 1) & 7;
-    const int wv = __builtin_amdgcn_readfirstlane(wave);   // the wave index as a scalar: block indexes are wave-uniform
+    // this lane's read offsets inside a stage
+    const int xo0 = 128 * r + 16 * (g ^ sw), xo1 = 128 * r + 16 * ((4 + g) ^ sw), wo = RING_XBYTES + RING_WPITCH * r;
+    const uint8_t* ring_w = ring + wv * WAVE_RING;
     for (int k = 0; k < nk; k++) {
         if (k + RING - 2 < nk)
             wait_copies<(RING - 2) * RING_COPIES>();   // blocks k + 1 .. k + RING - 2 may stay in flight
@@ -1104,13 +1114,12 @@ __global__ __launch_bounds__(64 * WAVES) void batch_matvec_ring_kernel(
             wait_copies<0>();
         if (k + RING - 1 < nk)
             request(k + RING - 1);   // into the stage of block k - 1, whose reads have returned
-        const uint8_t* st = ring + wave * WAVE_RING + (k % RING) * RING_STAGE;
-        const float* xr = reinterpret_cast<const float*>(st + 128 * r);
-        const float4 x0 = *reinterpret_cast<const float4*>(xr + 4 * (g ^ sw));
-        const float4 x1 = *reinterpret_cast<const float4*>(xr + 4 * ((4 + g) ^ sw));
+        const uint8_t* st = ring_w + (k % RING) * RING_STAGE;
+        const float4 x0 = *reinterpret_cast<const float4*>(st + xo0);
+        const float4 x1 = *reinterpret_cast<const float4*>(st + xo1);
         const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float w[8];
-        decode_staged<FMT>(st + RING_XBYTES + RING_WPITCH * r, wv + WAVES * k, g, w);
+        decode_staged<FMT>(st + wo, wv + WAVES * k, g, w);
 #pragma unroll
         for (int s = 0; s < 8; s += 2) {
             acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[s], w[s], acc0, 0, 0, 0);
