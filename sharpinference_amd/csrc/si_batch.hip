@@ -1011,6 +1011,17 @@ __device__ __forceinline__ int64_t ring_piece(int b, int j)
         return ((34 * static_cast<int64_t>(b)) & ~int64_t{15}) + 16 * j;
 }
 
+// The four bytes of a word as floats, one v_cvt_f32_ubyteN each (written
+// out: the compiler folds a preceding nibble mask into per-byte bit-field
+// extracts otherwise).
+__device__ __forceinline__ void bytes_to_float(uint32_t v, float* f)
+{
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f[0]) : "v"(v));
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f[1]) : "v"(v));
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f[2]) : "v"(v));
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f[3]) : "v"(v));
+}
+
 // The 8 weights of block b at columns 4g..4g+3 and 16+4g..16+4g+3 from its
 // staged row pieces, dequantised as decode8 does.
 template <int FMT>
@@ -1030,34 +1041,39 @@ __device__ __forceinline__ void decode_staged(const uint8_t* row, int b, int g, 
         const uint8_t* blk = row + ((18 * b) & 15);
         const float d = half_bits(lds_u16(blk));
         const uint32_t q = lds_u16(blk + 2 + 4 * g) | (lds_u16(blk + 4 + 4 * g) << 16);   // qs[4g..4g+3]
-        const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;                   // one nibble per byte
+        float nl[4], nh[4];
+        bytes_to_float(q & 0x0F0F0F0Fu, nl);          // one nibble per byte
+        bytes_to_float((q >> 4) & 0x0F0F0F0Fu, nh);
 #pragma unroll
         for (int e = 0; e < 4; e++) {   // n - 8 and d (n - 8) are exact in FP32
-            w[e] = d * (static_cast<float>((lo >> (8 * e)) & 0xffu) - 8.0f);       // element 4g+e
-            w[4 + e] = d * (static_cast<float>((hi >> (8 * e)) & 0xffu) - 8.0f);   // element 16+4g+e
+            w[e] = d * (nl[e] - 8.0f);       // element 4g+e
+            w[4 + e] = d * (nh[e] - 8.0f);   // element 16+4g+e
         }
     } else {   // Q4_K sub-block j of the super-block (j is the same for the whole wave)
         const int j = b & 7;
-        const uint32_t dd = lds_u32(row);   // d, dmin
-        const uint8_t* sb = row + 4;        // the 12 scale bytes
+        const uint4 h = *reinterpret_cast<const uint4*>(row);   // d, dmin; 12 scale bytes
+        const int sh8 = 8 * (j & 3);                              // byte j % 4 of a scale word
         int sc, m;
         if (j < 4) {
-            sc = sb[j] & 63;
-            m = sb[j + 4] & 63;
+            sc = static_cast<int>(__builtin_amdgcn_ubfe(h.y, sh8, 6));
+            m = static_cast<int>(__builtin_amdgcn_ubfe(h.z, sh8, 6));
         } else {
-            const int both = sb[j + 4];
-            sc = (both & 15) | ((sb[j - 4] >> 6) << 4);
-            m = (both >> 4) | ((sb[j] >> 6) << 4);
+            const int both = static_cast<int>(__builtin_amdgcn_ubfe(h.w, sh8, 8));
+            sc = (both & 15) | (static_cast<int>(__builtin_amdgcn_ubfe(h.y, sh8 + 6, 2)) << 4);
+            m = (both >> 4) | (static_cast<int>(__builtin_amdgcn_ubfe(h.z, sh8 + 6, 2)) << 4);
         }
-        const float d1 = __fmul_rn(half_bits(dd), static_cast<float>(sc));
-        const float m1 = __fmul_rn(half_bits(dd >> 16), static_cast<float>(m));
+        const float d1 = __fmul_rn(half_bits(h.x), static_cast<float>(sc));
+        const float m1 = __fmul_rn(half_bits(h.x >> 16), static_cast<float>(m));
         const int sh = (j & 1) * 4;   // low nibbles for even sub-blocks
         const uint32_t lo = (lds_u32(row + 16 + 4 * g) >> sh) & 0x0F0F0F0Fu;   // one nibble per byte
         const uint32_t hi = (lds_u32(row + 32 + 4 * g) >> sh) & 0x0F0F0F0Fu;
+        float nl[4], nh[4];
+        bytes_to_float(lo, nl);
+        bytes_to_float(hi, nh);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            w[e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((lo >> (8 * e)) & 0xffu)), m1);
-            w[4 + e] = __fsub_rn(__fmul_rn(d1, static_cast<float>((hi >> (8 * e)) & 0xffu)), m1);
+            w[e] = __fsub_rn(__fmul_rn(d1, nl[e]), m1);
+            w[4 + e] = __fsub_rn(__fmul_rn(d1, nh[e]), m1);
         }
     }
 }
