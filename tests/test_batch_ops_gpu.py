@@ -207,7 +207,8 @@ def test_batch_rope_kv_write(hip, fmt, start, valid, context):
 
 @pytest.mark.parametrize("fmt", [native.F32, native.F16], ids=["f32", "f16"])
 @pytest.mark.parametrize("heads,kv_heads,context,start,valid",
-                         [(24, 8, 4096, 2040, 16), (6, 2, 300, 0, 16), (8, 8, 64, 50, 5), (32, 4, 1024, 1016, 9)])
+                         [(24, 8, 4096, 2040, 16), (6, 2, 300, 0, 16), (8, 8, 64, 50, 5), (32, 4, 1024, 1016, 9),
+                          (8, 2, 100, 90, 16)])
 def test_batch_attention_chain(hip, fmt, heads, kv_heads, context, start, valid):
     B, head = 16, 128
     group = heads // kv_heads
@@ -257,7 +258,8 @@ def test_batch_attention_chain(hip, fmt, heads, kv_heads, context, start, valid)
 @pytest.mark.parametrize("fmt", [native.F32, native.F16], ids=["f32", "f16"])
 @pytest.mark.parametrize("heads,kv_heads,context,start,valid",
                          [(24, 8, 4096, 2040, 16), (6, 2, 300, 0, 16), (8, 8, 64, 50, 5), (32, 4, 1024, 1016, 9),
-                          (24, 8, 4096, 0, 16), (16, 2, 200, 130, 16), (8, 4, 100, 95, 3)])
+                          (24, 8, 4096, 0, 16), (16, 2, 200, 130, 16), (8, 4, 100, 95, 3),
+                          (8, 2, 100, 90, 16)])   # rows past the context attend to all of it
 def test_batch_attention_fused(hip, fmt, heads, kv_heads, context, start, valid):
     """si_hip_batch_gqa_attention: the scores / softmax / values chain in two
     launches, against the float64 softmax-weighted sum over positions <= the
