@@ -61,6 +61,31 @@ def synth_weights(fmt: int, rows: int, cols: int, rng: np.random.Generator) -> n
     raise ValueError(fmt)
 
 
+def plan_schedule(n: int, copies: int) -> list:
+    """Plan launches of n layer-set steps: ("round",) for each whole round of
+    `copies` steps (one plan holding the round), then ("rest", r) for the r
+    remaining steps (one plan holding them)."""
+    full, rest = divmod(n, copies)
+    return [("round",)] * full + ([("rest", rest)] if rest else [])
+
+
+def one_plan_schedule(n: int, copies: int) -> list:
+    """Plan launches of n steps with one plan per step: ("one", c) for the
+    step over weight copy c."""
+    return [("one", i % copies) for i in range(n)]
+
+
+def warmup_schedule(steps: int, warmup: int, copies: int) -> list:
+    """Untimed launches before timing: the warm-up steps themselves, every
+    plan the timed region launches that they did not, then every one-step
+    plan once, so that no plan is launched for the first time while timed."""
+    keys = plan_schedule(max(warmup, 1), copies)
+    for key in plan_schedule(steps, copies) + one_plan_schedule(min(steps, copies), copies):
+        if key not in keys:
+            keys.append(key)
+    return keys
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,24 +190,24 @@ def main() -> int:
     # Submission: one recorded plan holds a round of `copies` steps (each step
     # = the layer's GEMVs, in order on the stream, over one weight copy), as
     # a model's layers share one submission; a remainder of steps uses
-    # one-step plans.  Launching one small plan per step instead adds a
-    # plan-launch gap to every step, reported as `one_plan_per_step`.
+    # one plan holding those steps.  Launching one small plan per step instead
+    # adds a plan-launch gap to every step, reported as `one_plan_per_step`.
     round_plan = record_steps(0, copies)
     plans = [record_steps(c, 1) for c in range(copies)]
     rest_plans = {}
+    for key in warmup_schedule(args.steps, args.warmup, copies):
+        if key[0] == "rest" and key[1] not in rest_plans:
+            rest_plans[key[1]] = record_steps(0, key[1])
 
-    def run_steps(n: int) -> None:
-        """n steps = whole rounds of `copies` steps plus one plan holding the
-        remaining steps (recorded once per remainder, before any timing)."""
-        full, rest = divmod(n, copies)
-        if full:
-            hip.launch_sequence([round_plan], full)
-        if rest:
-            hip.launch_sequence([rest_plans[rest]], 1)
+    def plan_of(key):
+        if key[0] == "round":
+            return round_plan
+        return rest_plans[key[1]] if key[0] == "rest" else plans[key[1]]
 
-    for n in (max(args.warmup, 1), args.steps):
-        if n % copies and n % copies not in rest_plans:
-            rest_plans[n % copies] = record_steps(0, n % copies)
+    def launch(keys) -> None:
+        """Launches the plans named by `keys`, in order, on the library's stream."""
+        if keys:
+            hip.launch_sequence([plan_of(k) for k in keys], len(keys))
 
     # per-shape plans (rotation over copies) for the per-kernel breakdown
     shape_plans = {}
@@ -202,22 +227,24 @@ def main() -> int:
         dst.free()
         log(f"calibration copy of {args.copy_calibration_mib} MiB done")
 
-    log(f"warmup {args.warmup} steps")
-    run_steps(max(args.warmup, 1))
-    hip.launch_sequence(plans, max(args.warmup, 1))
+    # warm-up: the W steps, then every plan the timed region launches that
+    # those steps did not (a graph's first launch pays its upload and the
+    # first touch of its kernels), then every one-step plan
+    log(f"warmup {args.warmup} steps + every plan the timed region launches")
+    launch(warmup_schedule(args.steps, args.warmup, copies))
     hip.sync()
 
     log(f"timing {args.steps} steps")
     hip.sync()
     hip.timer_begin()
-    run_steps(args.steps)
+    launch(plan_schedule(args.steps, copies))
     ms = hip.timer_end()
     hip.sync()
     s_per_step = ms / 1e3 / args.steps
     gbs = bytes_per_step / s_per_step / 1e9
     log(f"{ms:.3f} ms for {args.steps} steps -> {s_per_step * 1e6:.2f} us/step, {gbs:.1f} GB/s")
     hip.timer_begin()
-    hip.launch_sequence(plans, args.steps)
+    launch(one_plan_schedule(args.steps, copies))
     ms1 = hip.timer_end()
     one_plan = {"us_per_step": round(ms1 * 1e3 / args.steps, 3),
                 "GBs": round(bytes_per_step / (ms1 / 1e3 / args.steps) / 1e9, 1)}

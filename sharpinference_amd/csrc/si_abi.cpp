@@ -401,6 +401,15 @@ int si_hip_plan_end(si_hip_context* ctx, si_hip_plan** out)
         (void)hipGraphDestroy(graph);
         return hip_fail(ctx, e, "hipGraphInstantiate");
     }
+    // Upload the executable graph now, on the plan's stream, so that its first
+    // launch (a session's first token, a bench's first timed step) does not
+    // pay for it.
+    e = hipGraphUpload(exec, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        return hip_fail(ctx, e, "hipGraphUpload");
+    }
     auto* plan = new si_hip_plan();
     plan->ctx = ctx;
     plan->graph = graph;

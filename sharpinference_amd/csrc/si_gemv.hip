@@ -107,9 +107,12 @@ __device__ __forceinline__ int group8_sum_i32(int v)
 
 // ---- x as integer digit planes ----------------------------------------------
 // Each 32-column block of the staged x is scaled by a power of two 2^s
-// chosen from the block's largest magnitude M (M * 2^s < 2^21) and rounded
-// to integers X (|X| <= 2^21; the rounding is below 2^-22 M per value,
-// finer than the FP32 rounding of a sum that holds M).  X + 0x808080 has
+// chosen from the block's largest magnitude M (2^20 <= M * 2^s < 2^21) and
+// rounded to integers X (|X| <= 2^21; the rounding is at most half a unit,
+// 2^-s / 2 <= 2^-21 M per value).  So x is rounded per 32-column block to a
+// 21-bit grid, where the FP32 reference multiplies the FP32 x itself
+// (CpuHalfMatrixOperators.cs:29-41); the products' error stays within the
+// mat-vec tolerance but is not the reference's FP32 rounding.  X + 0x808080 has
 // bytes b0, b1, b2 in [0, 255]; the signed bytes d_p = b_p - 128 are its
 // balanced base-256 digits, X = d0 + 256 d1 + 65536 d2 (|d2| <= 32).  Plane p
 // packs d_p of 4 consecutive values into one word, so a 4-bit weight word

@@ -23,9 +23,10 @@ from .synth import synth_blocks  # noqa: F401  (re-exported for callers of this 
 
 # Phi4TextModel.cs:18 (RotarySize): the rotary width when a file does not name one.
 REFERENCE_ROTARY_SIZE = 96
-# Norm weights the reference's RmsNorm reads (Float32 or Float16,
-# Phi4TextModel.cs:116-127); BF16 is widened the same way.
-NORM_TYPES = (native.F32, native.F16, native.BF16)
+# Norm weights the reference's RmsNorm reads: Float32 or Float16
+# (Phi4TextModel.cs:116-127; HalfValues throws for any other type,
+# GgufModelFile.cs:374-377), so a BF16 norm is rejected as it is there.
+NORM_TYPES = (native.F32, native.F16)
 
 
 @dataclass
@@ -191,7 +192,7 @@ class Phi4DecodeSession:
         67-99).  Every tensor's type and dimensions are checked against the
         configuration first (check_gguf_tensors), then the projections and
         the embedding are uploaded once, unchanged, from the mapping; norm
-        weights stored as Float16 / BF16 are widened to FP32 on the host
+        weights stored as Float16 are widened to FP32 on the host
         (they are a few KB) so the kernels read FP32 norms."""
         cfg = Phi4Config.from_gguf(g, capacity)
         norms = check_gguf_tensors(g, cfg)
@@ -304,8 +305,6 @@ def check_gguf_tensors(g, cfg: Phi4Config) -> Dict[str, np.ndarray]:
         t = want(name, (H,), NORM_TYPES)
         if t.type == native.F16:
             widened[name] = g.host_bytes(name).view(np.float16).astype(np.float32)
-        elif t.type == native.BF16:
-            widened[name] = (g.host_bytes(name).view(np.uint16).astype(np.uint32) << 16).view(np.float32)
     return widened
 
 

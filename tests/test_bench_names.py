@@ -38,3 +38,31 @@ def test_the_check_finds_a_missing_import(tmp_path):
     p.write_text("import os\n\ndef f():\n    return os.sep + native.X\n\ndef g():\n    from x import native\n"
                  "    return native\n")
     assert _unbound_globals(p) == ["f: native"]
+
+
+def _bench_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_under_test", ROOT / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.mark.parametrize("copies", [1, 2, 5, 12, 13])
+@pytest.mark.parametrize("warmup", [0, 1, 5, 12, 40])
+@pytest.mark.parametrize("steps", [1, 5, 11, 12, 20, 25, 400])
+def test_every_timed_plan_is_warmed(steps, warmup, copies):
+    """No plan is launched for the first time inside a timed region: the
+    layer-set steps and the one-plan-per-step loop both launch only plans
+    that the warm-up launched."""
+    b = _bench_module()
+    warmed = set(b.warmup_schedule(steps, warmup, copies))
+    timed = b.plan_schedule(steps, copies) + b.one_plan_schedule(steps, copies)
+    assert set(timed) <= warmed
+    # the timed schedules run exactly `steps` steps over the rotation
+    n = sum(copies if k == ("round",) else k[1] for k in b.plan_schedule(steps, copies))
+    assert n == steps
+    assert len(b.one_plan_schedule(steps, copies)) == steps
+    # the warm-up holds at least the requested warm-up steps
+    w = sum(copies if k == ("round",) else k[1] for k in b.plan_schedule(max(warmup, 1), copies))
+    assert w == max(warmup, 1)

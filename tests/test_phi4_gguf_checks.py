@@ -40,19 +40,25 @@ def test_config_follows_the_reference(tmp_path):
                 phi4.Phi4Config.from_gguf(g)
 
 
-@pytest.mark.parametrize("norm_type", [native.F16, native.BF16], ids=["f16", "bf16"])
-def test_half_norms_are_widened_to_fp32(tmp_path, norm_type):
-    with gguf.GgufFile(_write(tmp_path, norm_type=norm_type)) as g:
+def test_half_norms_are_widened_to_fp32(tmp_path):
+    with gguf.GgufFile(_write(tmp_path, norm_type=native.F16)) as g:
         cfg = phi4.Phi4Config.from_gguf(g)
         widened = phi4.check_gguf_tensors(g, cfg)
         names = {"output_norm.weight"} | {f"blk.{l}.{n}.weight" for l in range(2) for n in ("attn_norm", "ffn_norm")}
         assert set(widened) == names
         for n in names:
-            raw = g.host_bytes(n)
-            exact = raw.view(np.float16).astype(np.float64) if norm_type == native.F16 else \
-                (raw.view(np.uint16).astype(np.uint64) << 16).astype(np.uint32).view(np.float32).astype(np.float64)
+            exact = g.host_bytes(n).view(np.float16).astype(np.float64)
             assert widened[n].dtype == np.float32 and widened[n].shape == (cfg.hidden,)
             assert np.array_equal(widened[n].astype(np.float64), exact)
+
+
+def test_bf16_norms_are_rejected_as_the_reference_does(tmp_path):
+    """RmsNorm reads FloatValues or HalfValues (Phi4TextModel.cs:116-127),
+    and HalfValues throws for a tensor that is not Float16
+    (GgufModelFile.cs:374-377): a BF16 norm does not load there."""
+    with gguf.GgufFile(_write(tmp_path, norm_type=native.BF16)) as g:
+        with pytest.raises(ValueError, match=r"output_norm\.weight: tensor type bf16"):
+            phi4.check_gguf_tensors(g, phi4.Phi4Config.from_gguf(g))
 
 
 def test_mis_shaped_and_mis_typed_tensors_are_rejected_before_upload(tmp_path):
