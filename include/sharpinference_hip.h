@@ -599,6 +599,65 @@ int si_hip_rwkv7_workspace_bytes(const si_hip_rwkv7_model* model, uint64_t* byte
  * 190-292) run by a VM executor. */
 int si_hip_rwkv7_decode(si_hip_context* ctx, const si_hip_rwkv7_model* model);
 
+/* ---- T0 primitive and portable tensor operators ---------------------------------- */
+
+/* The operators an unfused logical graph dispatches between its mat-vecs
+ * (the portable RWKV-7 forward-token graph, PortableRwkv7GraphProvider.cs:
+ * 13-295), one launch each, on dense FP32 tensors.  An output that overlaps
+ * an input is rejected (ARGUMENT), as the reference rejects in-place
+ * operator writes (GpuTierZeroInstruction.cs:461-463). */
+typedef enum si_hip_t0_op {
+    SI_HIP_T0_COPY = 0,        /* core.copy          input                                       */
+    SI_HIP_T0_ADD = 1,         /* core.add           left + right                                */
+    SI_HIP_T0_SUBTRACT = 2,    /* core.subtract      left - right                                */
+    SI_HIP_T0_MULTIPLY = 3,    /* core.multiply      left * right                                */
+    SI_HIP_T0_DIVIDE = 4,      /* core.divide        left / right                                */
+    SI_HIP_T0_MAXIMUM = 5,     /* core.maximum       NaN if either is NaN; +0 above -0            */
+    SI_HIP_T0_EXP = 6,         /* core.exp                                                       */
+    SI_HIP_T0_TANH = 7,        /* core.tanh          tanh(0) = 0 exactly                         */
+    SI_HIP_T0_SIGMOID = 8,     /* core.sigmoid       1 / (1 + exp(-x))                           */
+    SI_HIP_T0_RSQRT = 9,       /* core.rsqrt         1 / sqrt(x)                                 */
+    SI_HIP_T0_SQUARE = 10,     /* core.square        x * x                                       */
+    SI_HIP_T0_RELU = 11,       /* core.relu          maximum(x, 0)                               */
+} si_hip_t0_op;
+
+/* output[i] = op(left[i]) or op(left[i], right[i]) for i < count (right is
+ * ignored by the unary operators).  Replaces: the elementwise T0 operators
+ * (GpuTierZeroInstruction.cs:376-386, CpuPrimitiveOperatorBackend.cs:25-90). */
+int si_hip_t0_elementwise(si_hip_context* ctx, int op, const float* left, const float* right, float* output,
+                          int64_t count);
+/* output[i] = FP32 value of the fp16 input[i].  Replaces: core.tensor.cast-f16-f32
+ * (PortableTensorOperationContracts.cs:54, GpuTierZeroInstruction.cs:425-428). */
+int si_hip_t0_cast_f16_f32(si_hip_context* ctx, const void* input, float* output, int64_t count);
+/* output[i] = value (finite).  Replaces: core.tensor.fill (PortableTensorOperationContracts.cs:12-20,53). */
+int si_hip_t0_fill(si_hip_context* ctx, float value, float* output, int64_t count);
+/* output[r] = sum over c of input[r][c], divided by cols when mean != 0.
+ * Replaces: core.tensor.reduce-last-sum / -mean (rows = the leading
+ * dimensions' product) and core.reduce-sum / -mean (rows = 1)
+ * (PortableTensorOperationContracts.cs:59-60,166-172; GpuTierZeroInstruction.cs:387-393,446-451). */
+int si_hip_t0_reduce_last(si_hip_context* ctx, int mean, const float* input, float* output, int64_t rows,
+                          int64_t cols);
+/* Broadcast of a rank 1..4 tensor to a rank 1..4 shape: trailing
+ * dimensions aligned, each input axis 1 (repeated) or equal to the
+ * output's.  Replaces: core.tensor.broadcast (PortableTensorOperationContracts.cs:58,158-164). */
+int si_hip_t0_broadcast(si_hip_context* ctx, const float* input, int input_rank, const int64_t* input_dims,
+                        float* output, int output_rank, const int64_t* output_dims);
+/* output = input[..., start:start+length, ...] along `axis` (rank kept,
+ * row-major).  Replaces: core.tensor.slice (PortableTensorOperationContracts.cs:
+ * 24-40,56,138-149). */
+int si_hip_t0_slice(si_hip_context* ctx, const float* input, int rank, const int64_t* input_dims, int axis,
+                    int64_t start, int64_t length, float* output);
+/* output[h][i][j] = left[h][i] * right[h][j].  Replaces: core.tensor.head-outer
+ * (PortableTensorOperationContracts.cs:61,174-182). */
+int si_hip_t0_head_outer(si_hip_context* ctx, const float* left, const float* right, float* output, int64_t heads,
+                         int64_t rows, int64_t cols);
+/* si_hip_gemv pinned to the any-shape kernel (one wave per output row,
+ * path 2) whatever the shape: the mat-vec a program selects as serial.
+ * Replaces: the serial core.mat-vec form (GpuTierZeroInstruction.cs:386-396),
+ * chosen by GpuMatVecMode.Serial (GpuMatVecOptimization.cs:36-37). */
+int si_hip_gemv_any_shape(si_hip_context* ctx, int format, const void* w, const float* x, float* y, int64_t rows,
+                          int64_t cols);
+
 /* ---- GGUF model files ------------------------------------------------------------ */
 
 /* A GGUF v3 file mapped read-only: metadata, tensor directory and the

@@ -39,6 +39,8 @@ SOURCES = [
     "si_ops.cpp",
     "si_batch.hip",
     "si_batch_abi.cpp",
+    "si_t0.hip",
+    "si_t0_abi.cpp",
 ]
 
 

@@ -1520,6 +1520,8 @@ bool tiled_ok(const GemvOp& op)
 
 int kind_of(const GemvOp& op)
 {
+    if (op.any_shape)
+        return PATH_GENERIC;
     if (tiled_ok(op))
         return PATH_FAST;
     const int64_t nb = op.cols / block_elems(op.fmt);

@@ -81,6 +81,8 @@ struct GemvOp {
     const float* copy_src = nullptr;     // side job of the op's first workgroup:
     float* copy_dst = nullptr;           //   copy_dst[0..copy_n) = copy_src[0..copy_n)
     int64_t copy_n = 0;
+    bool any_shape = false;              // plain products only: run the any-shape kernel (one wave per
+                                         // row) whatever the shape, as a serial mat-vec is pinned
 };
 
 // Which kernel a launch used; reported to the caller for tests and profiles.

@@ -503,7 +503,29 @@ void HipVmProgram::AddDispatch(const std::string& entry, std::shared_ptr<const I
     instruction->Invoke(recorder, parameters, precision);
     const KernelPrecisionProfile resolved = instruction->Adapt(parameters, precision).precision;
     for (auto& r : recorder.recordings)
-        entries_[entry].push_back({instruction, std::move(r), precision, resolved});
+        entries_[entry].push_back({instruction, std::move(r), precision, resolved, {}});
+}
+
+void HipVmProgram::AddKernelDispatch(const std::string& entry, std::shared_ptr<const Instruction> instruction,
+                                     const std::vector<InstructionParameter>& parameters,
+                                     const PrecisionRequirement& precision, const HipVmKernelLaunch& launch)
+{
+    auto& ds = entries_[entry];
+    const size_t before = ds.size();
+    AddDispatch(entry, std::move(instruction), parameters, precision);
+    for (size_t i = before; i < ds.size(); i++) {
+        HipVmDispatch& d = ds[i];
+        if (!launch.implementation_variant.empty()) {
+            if (launch.implementation_variant != "any_shape" ||
+                (d.recording.operation != "si_hip_gemv" && d.recording.operation != "si_hip_gemv.dense")) {
+                ds.resize(before);
+                throw NotSupportedException("Instruction '" + d.instruction->Name() + "' has no '" +
+                                            launch.implementation_variant + "' implementation.");
+            }
+            d.recording.operation += ".any_shape";
+        }
+        d.launch = launch;
+    }
 }
 
 // ---- HipVmExecutor -------------------------------------------------------------------------
@@ -601,7 +623,20 @@ void HipVmExecutor::Launch(const InstructionRecording& r)
     const auto I = [&](const InstructionRecording& rec, const char* n) {
         return static_cast<const int32_t*>(Address(*Find(rec.parameters, n)));
     };
-    if (r.operation == "si_hip_gemv") {
+    if (LaunchTierZeroOp(context_, r, [&](const InstructionParameter& p) { return Address(p); }))
+        return;
+    if (r.operation == "si_hip_gemv.any_shape" || r.operation == "si_hip_gemv.dense.any_shape") {
+        const auto* w = Find(r.parameters, "weight");
+        if (!w)
+            w = Find(r.parameters, "matrix");
+        const bool quant = r.operation == "si_hip_gemv.any_shape";
+        const int fmt = quant ? FormatId(attr("format"))
+                        : w->tensor.element_type == GraphElementType::Float16 ? SI_HIP_F16
+                                                                              : SI_HIP_F32;
+        Check(si_hip_gemv_any_shape(context_, fmt, Address(*w), F(r, "input"), Fw(r, "output"), w->tensor.dimensions[0],
+                                    quant ? std::stoll(attr("columns")) : w->tensor.dimensions[1]),
+              context_);
+    } else if (r.operation == "si_hip_gemv") {
         const auto* w = Find(r.parameters, "weight");
         if (!w)
             w = Find(r.parameters, "matrix");

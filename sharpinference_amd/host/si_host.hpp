@@ -28,6 +28,7 @@
 #include "sharpinference_hip.h"
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <stdexcept>
@@ -370,6 +371,18 @@ public:
 // Every HIP collection of this library behind one registry.
 std::shared_ptr<const InstructionRegistry> DefaultHipRegistry();
 
+// The other T0 operators of the TierZeroFloat32 collection on HIP (copy,
+// add, subtract, multiply, divide, maximum, exp, tanh, sigmoid, rsqrt,
+// square, relu, reduce-sum, reduce-mean and the core.tensor fill,
+// cast-f16-f32, reshape, slice, broadcast, reduce-last-sum / -mean,
+// head-outer; TierZeroOperationContracts.cs, PortableTensorOperationContracts.cs),
+// or null for another name.
+std::shared_ptr<const Instruction> MakeTierZeroOpInstruction(const std::string& name);
+// Launches a recording of one of those operators (si_hip_t0_*) with the
+// parameters' device addresses; false when the recording is not one.
+bool LaunchTierZeroOp(si_hip_context* ctx, const InstructionRecording& recording,
+                      const std::function<void*(const InstructionParameter&)>& address);
+
 // ---- program and executor (VmProgram, D3D12VmExecutor) ------------------------------------
 
 // VmSlotScope (VmProgram.cs:9): model-lifetime, session-lifetime (KV
@@ -384,11 +397,27 @@ struct HipVmSlot {
     std::string binding_key;   // empty: none
 };
 
+// A lowered program's dispatch (VmDispatch, VmProgram.cs): the kernel
+// definition it instantiates (one per distinct operator), its thread group
+// and grid, and an implementation variant of the instruction
+// ("any_shape": a mat-vec pinned to the serial any-shape kernel).  A
+// program built dispatch by dispatch leaves `definition` empty and its
+// operators are written inline.  The grid is the program's record of the
+// dispatch (the reference's formula); the HIP library sizes each launch
+// itself from the operands.
+struct HipVmKernelLaunch {
+    std::string definition;
+    uint32_t threads = 0;
+    uint32_t groups[3] = {1, 1, 1};
+    std::string implementation_variant;
+};
+
 struct HipVmDispatch {
     std::shared_ptr<const Instruction> instruction;
     InstructionRecording recording;
     PrecisionRequirement precision{GraphElementType::Float32, GraphElementType::Float32};
     KernelPrecisionProfile resolved{GraphElementType::Float32, GraphElementType::Float32};   // the adapted signature's
+    HipVmKernelLaunch launch;
 };
 
 // VmStateEntry (VmProgram.cs:46): a named piece of session state and its slot.
@@ -410,6 +439,13 @@ public:
     // may not overlap others (NotSupportedException).
     void AddDispatch(const std::string& entry, std::shared_ptr<const Instruction> instruction,
                      const std::vector<InstructionParameter>& parameters, const PrecisionRequirement& precision);
+    // AddDispatch for a lowered program: the dispatch also records its
+    // kernel definition and grid, and an implementation variant replaces the
+    // recording's C ABI operation ("any_shape" on a mat-vec: the serial
+    // any-shape kernel); another variant raises NotSupportedException.
+    void AddKernelDispatch(const std::string& entry, std::shared_ptr<const Instruction> instruction,
+                           const std::vector<InstructionParameter>& parameters, const PrecisionRequirement& precision,
+                           const HipVmKernelLaunch& launch);
 
     const std::vector<HipVmSlot>& Slots() const { return slots_; }
     const std::map<std::string, std::vector<HipVmDispatch>>& Entries() const { return entries_; }

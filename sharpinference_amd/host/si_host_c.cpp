@@ -2,6 +2,7 @@
 // HipVmExecutor and BuildPhi4DecodeProgram.
 #include "si_host_c.h"
 
+#include "si_graph.hpp"
 #include "si_host.hpp"
 
 #include <algorithm>
@@ -14,6 +15,7 @@ using namespace sharpinference;
 struct sih_program {
     HipVmProgram program;
     std::unique_ptr<HipVmExecutor> executor;
+    std::string report;   // graph programs: the lowering report (JSON)
 };
 
 namespace {
@@ -49,6 +51,96 @@ int Guard(Fn&& f)
         g_error = e.what();
         return SI_HIP_ERR_DEVICE;
     }
+}
+
+ModelTensorCatalog Catalog(const sih_model_tensor* tensors, int count, int64_t vocabulary, int64_t embedding,
+                           int64_t layers)
+{
+    if (!tensors || count < 1)
+        throw ArgumentException("a catalog needs at least one tensor");
+    ModelTensorCatalog c;
+    c.vocabulary = vocabulary;
+    c.embedding = embedding;
+    c.layers = layers;
+    for (int i = 0; i < count; i++) {
+        const sih_model_tensor& t = tensors[i];
+        if (!t.name || t.rank < 1 || t.rank > 4)
+            throw ArgumentException("catalog tensor " + std::to_string(i) + ": null name or rank outside 1..4");
+        if (!c.tensors.emplace(t.name, ModelTensor{t.type, std::vector<int64_t>(t.dims, t.dims + t.rank)}).second)
+            throw ArgumentException(std::string("duplicate catalog tensor '") + t.name + "'");
+    }
+    return c;
+}
+
+HipVmOptimizationOptions Options(const sih_graph_options* o)
+{
+    HipVmOptimizationOptions opt;
+    if (!o)
+        return opt;
+    opt.reuse_local_storage = o->reuse_local_storage != 0;
+    opt.weight_views = o->weight_views != 0;
+    opt.native_half_weights = o->native_half_weights != 0;
+    opt.threads_per_group = o->threads_per_group;
+    if (o->matvec_mode >= 0) {
+        if (o->matvec_mode > 3 || o->matvec_mode == static_cast<int>(GpuMatVecMode::Profile))
+            throw ArgumentOutOfRangeException("matvec_mode");
+        opt.gpu_matvec.emplace(static_cast<GpuMatVecMode>(o->matvec_mode));
+    }
+    return opt;
+}
+
+void CopyOut(const std::string& text, char* buffer, uint64_t capacity, uint64_t* length)
+{
+    if (length)
+        *length = text.size();
+    if (buffer) {
+        if (capacity < text.size())
+            throw ArgumentException("buffer too small");
+        std::copy(text.begin(), text.end(), buffer);
+    }
+}
+
+std::string GraphJson(const LogicalGraph& g)
+{
+    const auto str = [](const std::string& s) { return "\"" + s + "\""; };
+    const auto list = [&](const std::vector<std::string>& v) {
+        std::string o = "[";
+        for (size_t i = 0; i < v.size(); i++)
+            o += (i ? "," : "") + str(v[i]);
+        return o + "]";
+    };
+    std::vector<std::string> state;
+    for (const auto& e : g.state)
+        state.push_back(e.name);
+    std::string j = "{\"name\":" + str(g.name) + ",\"architecture\":" + str(g.architecture) +
+                    ",\"stateSchema\":" + str(g.state_schema) + ",\"stateAbi\":" + str(g.state_abi) +
+                    ",\"inputs\":" + list(g.inputs) + ",\"outputs\":" + list(g.outputs) + ",\"state\":" +
+                    list(state) + ",\"resources\":[";
+    for (size_t i = 0; i < g.resources.size(); i++) {
+        const auto& r = g.resources[i];
+        j += (i ? "," : "") + std::string("{\"id\":") + str(r.id) + ",\"key\":" + str(r.binding_key) + ",\"kind\":" +
+             std::to_string(static_cast<int>(r.kind)) + ",\"type\":" +
+             std::to_string(static_cast<int>(r.tensor.element_type)) + ",\"dims\":[";
+        for (size_t k = 0; k < r.tensor.dimensions.size(); k++)
+            j += (k ? "," : "") + std::to_string(r.tensor.dimensions[k]);
+        j += "]}";
+    }
+    j += "],\"nodes\":[";
+    for (size_t i = 0; i < g.nodes.size(); i++) {
+        const auto& n = g.nodes[i];
+        j += (i ? "," : "") + std::string("{\"id\":") + str(n.id) + ",\"operation\":" + str(n.operation) +
+             ",\"dependencies\":" + list(n.dependencies) + ",\"bindings\":[";
+        for (size_t k = 0; k < n.resources.size(); k++)
+            j += (k ? "," : "") + std::string("[") + str(n.resources[k].port) + "," + str(n.resources[k].resource) +
+                 "," + std::to_string(static_cast<int>(n.resources[k].access)) + "]";
+        j += "],\"attributes\":{";
+        size_t k = 0;
+        for (const auto& [a, v] : n.attributes)
+            j += (k++ ? "," : "") + str(a) + ":" + str(v);
+        j += "}}";
+    }
+    j += "]}";
+    return j;
 }
 
 }  // namespace
@@ -234,5 +326,55 @@ int sih_program_import_artifact(const void* bytes, uint64_t length, int device, 
 }
 
 const char* sih_last_error(void) { return g_error.c_str(); }
+
+
+int sih_rwkv7_graph_program_create(const sih_model_tensor* tensors, int count, int64_t vocabulary, int64_t embedding,
+                                   int64_t layers, const sih_graph_options* options, int device, sih_program** out)
+{
+    return Guard([&] {
+        if (!out)
+            throw ArgumentException("sih_rwkv7_graph_program_create: null argument");
+        *out = nullptr;
+        HipVmOptimizationResult r =
+            OptimizeWithReport(BuildRwkv7Graph(Catalog(tensors, count, vocabulary, embedding, layers)), Options(options));
+        auto p = std::make_unique<sih_program>();
+        p->report = OptimizationReportJson(r);
+        p->program = r.program;
+        p->executor = std::make_unique<HipVmExecutor>(std::move(r.program), device);
+        *out = p.release();
+    });
+}
+
+int sih_program_report(const sih_program* program, char* buffer, uint64_t capacity, uint64_t* length)
+{
+    return Guard([&] {
+        if (!program || !length)
+            throw ArgumentException("sih_program_report: null argument");
+        CopyOut(program->report, buffer, capacity, length);
+    });
+}
+
+int sih_rwkv7_graph_describe(const sih_model_tensor* tensors, int count, int64_t vocabulary, int64_t embedding,
+                             int64_t layers, const sih_graph_options* options, char* graph_json, uint64_t graph_capacity,
+                             uint64_t* graph_length, char* report_json, uint64_t report_capacity,
+                             uint64_t* report_length, char* xml, uint64_t xml_capacity, uint64_t* xml_length)
+{
+    return Guard([&] {
+        const LogicalGraph g = BuildRwkv7Graph(Catalog(tensors, count, vocabulary, embedding, layers));
+        const HipVmOptimizationResult r = OptimizeWithReport(g, Options(options));
+        CopyOut(GraphJson(g), graph_json, graph_capacity, graph_length);
+        CopyOut(OptimizationReportJson(r), report_json, report_capacity, report_length);
+        CopyOut(SerializeVmProgram(r.program), xml, xml_capacity, xml_length);
+    });
+}
+
+int sih_program_xml_roundtrip(const char* xml, char* buffer, uint64_t capacity, uint64_t* length)
+{
+    return Guard([&] {
+        if (!xml || !length)
+            throw ArgumentException("sih_program_xml_roundtrip: null argument");
+        CopyOut(SerializeVmProgram(DeserializeVmProgram(xml)), buffer, capacity, length);
+    });
+}
 
 }  // extern "C"

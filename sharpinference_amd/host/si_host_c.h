@@ -53,6 +53,47 @@ int sih_program_export_artifact(const sih_program* program, void* buffer, uint64
 int sih_program_import_artifact(const void* bytes, uint64_t length, int device, sih_program** out);
 const char* sih_last_error(void);
 
+/* VmProgram XML read (every operator re-adapted on the HIP target, no
+ * device) and written again. */
+int sih_program_xml_roundtrip(const char* xml, char* buffer, uint64_t capacity, uint64_t* length);
+
+/* ---- logical graphs (si_graph.hpp) ------------------------------------------------- */
+
+/* One tensor of a model catalog. */
+typedef struct sih_model_tensor {
+    const char* name;
+    int32_t type;        /* GGUF type id: F32, F16, Q8_0, Q4_0, Q4_K */
+    int32_t rank;        /* 1..4 */
+    int64_t dims[4];     /* the catalog's dimensions (GGML order: a matrix is [input, output]) */
+} sih_model_tensor;
+
+/* VmOptimizationOptions of the lowering. */
+typedef struct sih_graph_options {
+    int32_t reuse_local_storage;   /* 1: local intermediates share slots (GraphResourceAllocator.PlanLocal) */
+    int32_t weight_views;          /* 1: reshapes / casts of weights become views */
+    int32_t native_half_weights;   /* 1: FP16 weights feed the matrix operators directly */
+    int32_t matvec_mode;           /* -1: no settings (cooperative by default); 0 Serial, 1 Cooperative,
+                                      3 Default (GpuMatVecMode; Profile needs the C++ interface) */
+    uint32_t threads_per_group;    /* 1..1024 */
+} sih_graph_options;
+
+/* The portable RWKV-7 forward-token graph of a catalog
+ * (PortableRwkv7GraphProvider.Build), lowered to a HIP VM program
+ * (VmGraphOptimizer.OptimizeWithReport) with its executor on `device`; the
+ * program's slots are "weight.<name>", "state.<layer>.<suffix>", "token",
+ * "logits" and "local.<n>", its entry "forward". */
+int sih_rwkv7_graph_program_create(const sih_model_tensor* tensors, int count, int64_t vocabulary, int64_t embedding,
+                                   int64_t layers, const sih_graph_options* options, int device, sih_program** out);
+/* The lowering's report (OptimizationReportJson) of a graph program. */
+int sih_program_report(const sih_program* program, char* buffer, uint64_t capacity, uint64_t* length);
+/* Without a device: the logical graph as JSON (resources, nodes with
+ * operation, bindings and attributes), the lowering report and the lowered
+ * program's XML.  Each buffer may be NULL (only its length is set). */
+int sih_rwkv7_graph_describe(const sih_model_tensor* tensors, int count, int64_t vocabulary, int64_t embedding,
+                             int64_t layers, const sih_graph_options* options, char* graph_json, uint64_t graph_capacity,
+                             uint64_t* graph_length, char* report_json, uint64_t report_capacity,
+                             uint64_t* report_length, char* xml, uint64_t xml_capacity, uint64_t* xml_length);
+
 #ifdef __cplusplus
 }
 #endif

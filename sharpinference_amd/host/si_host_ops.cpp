@@ -177,6 +177,8 @@ std::vector<std::shared_ptr<const Instruction>> HipTierZeroInstructions::QueryIn
         return {std::make_shared<TierZeroGatherRowInstruction>()};
     if (name == "core.tensor.batched-mat-vec")
         return {std::make_shared<TierZeroBatchedMatVecInstruction>()};
+    if (auto op = MakeTierZeroOpInstruction(name))
+        return {op};
     return {};
 }
 

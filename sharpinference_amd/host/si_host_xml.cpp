@@ -9,6 +9,7 @@
 #include <cstring>
 #include <tuple>
 #include <map>
+#include <functional>
 #include <set>
 #include <sstream>
 
@@ -370,6 +371,7 @@ const std::array<const char*, 3> kScopes{"Global", "Session", "Local"};
 const std::array<const char*, 2> kVmAccess{"ReadOnly", "ReadWrite"};
 const std::array<const char*, 3> kResourceAccess{"Read", "Write", "ReadWrite"};
 const std::array<const char*, 3> kDefinitionKinds{"Function", "Kernel", "Orchestration"};
+constexpr int kKernel = 1;
 constexpr int kOrchestration = 2;
 const char* kTarget = "Hip";
 const char* kExecutionTarget = "hip.gfx950";
@@ -451,6 +453,7 @@ std::string SerializeVmProgram(const HipVmProgram& program)
     for (const auto& s : program.state)
         state.Add(El("Entry")).Attr("name", s.name).Attr("slot", s.slot);
     XElement& definitions = root.Add(El("Definitions"));
+    std::set<std::string> kernels;   // kernel definitions written so far
     XElement entries = El("Entries");
     for (const auto& [entry, dispatches] : program.Entries()) {
         // the entry's distinct slot views become definition parameters
@@ -507,7 +510,25 @@ std::string SerializeVmProgram(const HipVmProgram& program)
             XElement& node = nodes.Add(El("Node"));
             node.Attr("id", id);
             node.Add(El("Dependencies"));
-            XElement& op = node.Add(El("Operator"));
+            // a lowered dispatch: the operator lives in its kernel definition
+            // (one per distinct operator), bound to the definition's parameters,
+            // and the orchestration dispatches it with its grid
+            XElement kernel_body = El("Operator");
+            const bool lowered = !d.launch.definition.empty();
+            XElement& op = lowered ? kernel_body : node.Add(El("Operator"));
+            if (lowered) {
+                std::vector<std::tuple<std::string, std::string, uint64_t>> ports;
+                for (const auto& [port, view, offset] : args)
+                    ports.emplace_back(port, port, offset);
+                XElement& dispatch = node.Add(El("Dispatch"));
+                dispatch.Attr("definition", d.launch.definition);
+                dispatch.Add(Arguments(args));
+                dispatch.Add(El("Groups"))
+                    .Attr("x", std::to_string(d.launch.groups[0]))
+                    .Attr("y", std::to_string(d.launch.groups[1]))
+                    .Attr("z", std::to_string(d.launch.groups[2]));
+                args = ports;
+            }
             op.Attr("name", ins.Name()).Attr("collection", ins.CollectionId());
             op.Add(Arguments(args));
             op.Add(El("Precision"))
@@ -525,6 +546,23 @@ std::string SerializeVmProgram(const HipVmProgram& program)
             XElement& ports = op.Add(El("ParameterAccesses"));
             for (const auto& [n, a] : accesses)
                 ports.Add(El("Port")).Attr("name", n).Attr("access", a);
+            if (lowered && kernels.insert(d.launch.definition).second) {
+                XElement& kd = definitions.Add(El("Definition"));
+                kd.Attr("id", d.launch.definition).Attr("kind", kDefinitionKinds[kKernel]);
+                kd.Add(El("Threads")).Attr("x", std::to_string(d.launch.threads)).Attr("y", "1").Attr("z", "1");
+                XElement& kp = kd.Add(El("Parameters"));
+                for (const auto& prm : d.recording.parameters)
+                    if (prm.kind == InstructionParameter::Kind::Tensor) {
+                        XElement& pe = kp.Add(El("Parameter"));
+                        pe.Attr("name", prm.name)
+                            .Attr("access", prm.access != GraphResourceAccess::Read ? "ReadWrite" : "ReadOnly");
+                        pe.Add(Tensor(prm.tensor));
+                    }
+                XElement& body = kd.Add(El("Nodes")).Add(El("Node"));
+                body.Attr("id", "body");
+                body.Add(El("Dependencies"));
+                body.Add(std::move(kernel_body));
+            }
             XElement& barrier = nodes.Add(El("Node"));
             barrier.Attr("id", "barrier_" + std::to_string(index));
             barrier.Add(El("Dependencies")).Add(El("NodeRef")).Attr("id", id);
@@ -595,11 +633,18 @@ HipVmProgram DeserializeVmProgram(const std::string& xml, const std::shared_ptr<
         int kind;
         std::map<std::string, Parameter> parameters;
         const XElement* nodes;
+        uint32_t threads = 0;
     };
     std::map<std::string, Definition> definitions;
     for (const auto& d : Container(root, "Definitions", "Definition")) {
         Check(d, "Definition", {"id", "kind"}, {"Threads", "Parameters", "Nodes"});
-        Definition def{static_cast<int>(EnumValue<int>(d, "kind", kDefinitionKinds)), {}, &One(d, "Nodes")};
+        Definition def{static_cast<int>(EnumValue<int>(d, "kind", kDefinitionKinds)), {}, &One(d, "Nodes"), 0};
+        if (const XElement* threads = OptionalOne(d, "Threads")) {
+            Check(*threads, "Threads", {"x", "y", "z"}, {});
+            def.threads = static_cast<uint32_t>(Integer(*threads, "x", true));
+            Integer(*threads, "y", true);
+            Integer(*threads, "z", true);
+        }
         for (const auto& pe : Container(d, "Parameters", "Parameter")) {
             Check(pe, "Parameter", {"name", "access"}, {"Tensor"});
             if (!def.parameters
@@ -652,31 +697,93 @@ HipVmProgram DeserializeVmProgram(const std::string& xml, const std::shared_ptr<
                 }
                 continue;   // every dispatch of a HIP plan is ordered after the previous one
             }
-            if (ins->name != "Operator")
+            // where a name bound by the operator's arguments lives: (tensor, access, slot, byte offset)
+            struct Bound {
+                TensorDescriptor tensor;
+                VmAccess access;
+                std::string slot;
+                uint64_t offset;
+            };
+            const auto orchestration_argument = [&](const std::string& name) -> Bound {
+                const auto pit = def.parameters.find(name);
+                const auto bit = bound.find(name);
+                if (pit == def.parameters.end() || bit == bound.end())
+                    Bad("Argument names an unbound parameter '" + name + "'.");
+                return {pit->second.tensor, pit->second.access, bit->second.first, bit->second.second};
+            };
+            HipVmKernelLaunch launch;
+            const XElement* op = ins;
+            std::function<Bound(const std::string&)> resolve = orchestration_argument;
+            std::map<std::string, Bound> kernel_bound;
+            if (ins->name == "Dispatch") {
+                Check(*ins, "Dispatch", {"definition"}, {"Arguments", "Groups"});
+                launch.definition = Required(*ins, "definition");
+                const auto kit = definitions.find(launch.definition);
+                if (kit == definitions.end() || kit->second.kind != kKernel)
+                    Bad("Dispatch names an unknown kernel definition '" + launch.definition + "'.");
+                const Definition& kernel = kit->second;
+                const XElement& groups = One(*ins, "Groups");
+                Check(groups, "Groups", {"x", "y", "z"}, {});
+                launch.groups[0] = static_cast<uint32_t>(Integer(groups, "x", true));
+                launch.groups[1] = static_cast<uint32_t>(Integer(groups, "y", true));
+                launch.groups[2] = static_cast<uint32_t>(Integer(groups, "z", true));
+                launch.threads = kernel.threads;
+                for (const auto& a : ReadArguments(*ins)) {
+                    const auto kp = kernel.parameters.find(a.parameter);
+                    if (kp == kernel.parameters.end())
+                        Bad("Dispatch binds an unknown kernel parameter '" + a.parameter + "'.");
+                    Bound b = orchestration_argument(a.source);
+                    if (kp->second.access == VmAccess::ReadWrite && b.access != VmAccess::ReadWrite)
+                        Bad("Dispatch binds writable kernel parameter '" + a.parameter + "' to a read-only one.");
+                    b.tensor = kp->second.tensor;
+                    b.access = kp->second.access;
+                    b.offset += a.offset;
+                    if (!kernel_bound.emplace(a.parameter, b).second)
+                        Bad("Dispatch binds '" + a.parameter + "' twice.");
+                }
+                if (kernel_bound.size() != kernel.parameters.size())
+                    Bad("Dispatch of '" + launch.definition + "' leaves kernel parameters unbound.");
+                const auto& knodes = kernel.nodes->children;
+                if (knodes.size() != 1)
+                    throw NotSupportedException("Kernel definition '" + launch.definition +
+                                                "': the HIP executor runs kernels of one operator.");
+                Check(knodes[0], "Node", {"id"}, {"Dependencies", "Operator"});
+                op = &One(knodes[0], "Operator");
+                resolve = [&](const std::string& name) -> Bound {
+                    const auto it = kernel_bound.find(name);
+                    if (it == kernel_bound.end())
+                        Bad("Operator argument names an unbound kernel parameter '" + name + "'.");
+                    return it->second;
+                };
+            } else if (ins->name != "Operator") {
                 throw NotSupportedException("Entry '" + entry + "': " + ins->name +
-                                            " nodes have no HIP execution (operators only).");
-            Check(*ins, "Operator", {"name", "collection"},
+                                            " nodes have no HIP execution (operators and dispatches only).");
+            }
+            Check(*op, "Operator", {"name", "collection"},
                   {"Arguments", "Precision", "ResolvedPrecision", "ExecutionConfiguration", "Attributes", "IndexBounds",
                    "ParameterAccesses"});
-            const XElement& prec = One(*ins, "Precision");
+            const XElement& prec = One(*op, "Precision");
             Check(prec, "Precision", {"minimumArithmeticType", "minimumAccumulatorType"}, {});
             const PrecisionRequirement requirement{
                 EnumValue<GraphElementType>(prec, "minimumArithmeticType", kElementTypes),
                 EnumValue<GraphElementType>(prec, "minimumAccumulatorType", kElementTypes)};
-            if (const XElement* rp = OptionalOne(*ins, "ResolvedPrecision")) {
+            if (const XElement* rp = OptionalOne(*op, "ResolvedPrecision")) {
                 Check(*rp, "ResolvedPrecision", {"arithmeticType", "accumulatorType"}, {});
                 EnumValue<GraphElementType>(*rp, "arithmeticType", kElementTypes);
                 EnumValue<GraphElementType>(*rp, "accumulatorType", kElementTypes);
             }
-            if (const XElement* ec = OptionalOne(*ins, "ExecutionConfiguration")) {
+            if (const XElement* ec = OptionalOne(*op, "ExecutionConfiguration")) {
                 Check(*ec, "ExecutionConfiguration", {"target", "implementation"}, {});
                 if (Required(*ec, "target") != kExecutionTarget)
                     Bad("Unknown execution configuration target.");
-                Required(*ec, "implementation");
+                const std::string& impl = Required(*ec, "implementation");
+                const std::string variant = ".any_shape";
+                if (impl.size() > variant.size() && impl.compare(impl.size() - variant.size(), variant.size(), variant) == 0)
+                    launch.implementation_variant = "any_shape";
             }
             std::vector<InstructionParameter> params;
             std::set<std::string> names;
-            if (const XElement* attrs = OptionalOne(*ins, "Attributes")) {
+            if (const XElement* attrs = OptionalOne(*op, "Attributes")) {
                 Check(*attrs, "Attributes", {}, {"Attribute"});
                 for (const auto& a : attrs->children) {
                     Check(a, "Attribute", {"name", "value"}, {});
@@ -685,13 +792,13 @@ HipVmProgram DeserializeVmProgram(const std::string& xml, const std::shared_ptr<
                     params.push_back(InstructionParameter::Attribute(Required(a, "name"), Required(a, "value")));
                 }
             }
-            if (const XElement* bounds = OptionalOne(*ins, "IndexBounds")) {
+            if (const XElement* bounds = OptionalOne(*op, "IndexBounds")) {
                 Check(*bounds, "IndexBounds", {}, {"Bound"});
                 if (!bounds->children.empty())
                     throw NotSupportedException("Index bounds have no HIP execution.");
             }
             std::map<std::string, GraphResourceAccess> accesses;
-            if (const XElement* ports = OptionalOne(*ins, "ParameterAccesses")) {
+            if (const XElement* ports = OptionalOne(*op, "ParameterAccesses")) {
                 Check(*ports, "ParameterAccesses", {}, {"Port"});
                 for (const auto& port : ports->children) {
                     Check(port, "Port", {"name", "access"}, {});
@@ -701,26 +808,24 @@ HipVmProgram DeserializeVmProgram(const std::string& xml, const std::shared_ptr<
                         Bad("Duplicate port access.");
                 }
             }
-            const auto instruction = registry->Resolve(Required(*ins, "collection"), Required(*ins, "name"),
+            const auto instruction = registry->Resolve(Required(*op, "collection"), Required(*op, "name"),
                                                        InstructionTarget::Hip());
-            for (const auto& a : ReadArguments(*ins)) {
-                const auto pit = def.parameters.find(a.source);
-                const auto bit = bound.find(a.source);
-                if (pit == def.parameters.end() || bit == bound.end())
-                    Bad("Operator argument '" + a.parameter + "' names an unbound parameter '" + a.source + "'.");
+            for (const auto& a : ReadArguments(*op)) {
+                const Bound b = resolve(a.source);
                 if (!names.insert(a.parameter).second)
                     Bad("Duplicate operator argument '" + a.parameter + "'.");
                 const auto acc = accesses.find(a.parameter);
-                const GraphResourceAccess access = acc != accesses.end() ? acc->second
-                                                   : pit->second.access == VmAccess::ReadWrite
-                                                       ? GraphResourceAccess::ReadWrite
-                                                       : GraphResourceAccess::Read;
-                if (access != GraphResourceAccess::Read && pit->second.access != VmAccess::ReadWrite)
+                const GraphResourceAccess access = acc != accesses.end()              ? acc->second
+                                                   : b.access == VmAccess::ReadWrite ? GraphResourceAccess::ReadWrite
+                                                                                     : GraphResourceAccess::Read;
+                if (access != GraphResourceAccess::Read && b.access != VmAccess::ReadWrite)
                     Bad("Operator argument '" + a.parameter + "' writes read-only parameter '" + a.source + "'.");
-                params.push_back(InstructionParameter::Tensor(a.parameter, pit->second.tensor, access, bit->second.first,
-                                                              bit->second.second + a.offset));
+                params.push_back(InstructionParameter::Tensor(a.parameter, b.tensor, access, b.slot, b.offset + a.offset));
             }
-            p.AddDispatch(entry, instruction, params, requirement);
+            if (launch.definition.empty() && launch.implementation_variant.empty())
+                p.AddDispatch(entry, instruction, params, requirement);
+            else
+                p.AddKernelDispatch(entry, instruction, params, requirement, launch);
         }
     }
     return p;

@@ -36,6 +36,23 @@ class Phi4Shape(ctypes.Structure):
          ("prompt_rows", ctypes.c_int32)]
 
 
+class ModelTensor(ctypes.Structure):
+    """sih_model_tensor (host/si_host_c.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("rank", ctypes.c_int32),
+                ("dims", ctypes.c_int64 * 4)]
+
+
+class GraphOptions(ctypes.Structure):
+    """sih_graph_options (host/si_host_c.h): VmOptimizationOptions of the lowering."""
+    _fields_ = [("reuse_local_storage", ctypes.c_int32), ("weight_views", ctypes.c_int32),
+                ("native_half_weights", ctypes.c_int32), ("matvec_mode", ctypes.c_int32),
+                ("threads_per_group", ctypes.c_uint32)]
+
+
+# GpuMatVecMode (GpuMatVecOptimization.cs:6); None: no settings (cooperative by default)
+MATVEC_MODES = {None: -1, "serial": 0, "cooperative": 1, "default": 3}
+
+
 def host_lib() -> ctypes.CDLL:
     """The host library (loads the HIP library it links against)."""
     global _host
@@ -60,6 +77,15 @@ def host_lib() -> ctypes.CDLL:
             "sih_program_create_from_xml": [cp, ctypes.c_int, ctypes.POINTER(vp)],
             "sih_program_export_artifact": [vp, vp, u64, ctypes.POINTER(u64)],
             "sih_program_import_artifact": [vp, u64, ctypes.c_int, ctypes.POINTER(vp)],
+            "sih_rwkv7_graph_program_create": [ctypes.POINTER(ModelTensor), ctypes.c_int, ctypes.c_int64,
+                                               ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(GraphOptions),
+                                               ctypes.c_int, ctypes.POINTER(vp)],
+            "sih_program_report": [vp, vp, u64, ctypes.POINTER(u64)],
+            "sih_program_xml_roundtrip": [cp, vp, u64, ctypes.POINTER(u64)],
+            "sih_rwkv7_graph_describe": [ctypes.POINTER(ModelTensor), ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_int64, ctypes.POINTER(GraphOptions), vp, u64,
+                                         ctypes.POINTER(u64), vp, u64, ctypes.POINTER(u64), vp, u64,
+                                         ctypes.POINTER(u64)],
         }
         for name, args in sigs.items():
             fn = getattr(l, name)
@@ -224,6 +250,189 @@ class Phi4OpProgram:
         us = ctypes.c_double(0.0)
         _check(host_lib().sih_program_measure_us(self._h, entry.encode(), repetitions, ctypes.byref(us)))
         return us.value
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            host_lib().sih_program_destroy(self._h)
+            self._h = None
+
+
+# ---- the RWKV-7 forward-token graph, lowered operator by operator ---------------------------------
+
+def rwkv7_catalog(cfg, weights):
+    """The model tensor catalog of an RWKV-7 model as the graph provider reads
+    it (PortableRwkv7GraphProvider.cs:13-64): name -> (GGUF type, catalog
+    dims, host array).  Matrices are GGML [input, output] (read as row-major
+    [output, input], :151-152); x_rwkvag is [6, width] (the r, w, k, v, a, g
+    mix rows); r_k is [head, heads] (the graph takes the head shape from it,
+    :17-27); layer 0 has no value LoRA (:235-242)."""
+    D, N = cfg.hidden, cfg.head_size
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    cat = {"emb.weight": (cfg.embed_format, [D, cfg.vocab], weights.embed),
+           "blocks.0.ln0.weight": (native.F32, [D], f32(weights.ln0_weight)),
+           "blocks.0.ln0.bias": (native.F32, [D], f32(weights.ln0_bias)),
+           "ln_out.weight": (native.F32, [D], f32(weights.ln_out_weight)),
+           "ln_out.bias": (native.F32, [D], f32(weights.ln_out_bias)),
+           "head.weight": (cfg.head_format, [D, cfg.vocab], weights.head)}
+    names = {"receptance": "att.receptance.weight", "key": "att.key.weight", "value": "att.value.weight",
+             "output": "att.output.weight", "w1": "att.w1", "w2": "att.w2", "a1": "att.a1", "a2": "att.a2",
+             "g1": "att.g1", "g2": "att.g2", "v1": "att.v1", "v2": "att.v2", "ffn_key": "ffn.key.weight",
+             "ffn_value": "ffn.value.weight"}
+    vectors = {"ln1_weight": "ln1.weight", "ln1_bias": "ln1.bias", "ln2_weight": "ln2.weight", "ln2_bias": "ln2.bias",
+               "w0": "att.w0", "a0": "att.a0", "v0": "att.v0", "k_k": "att.k_k", "k_a": "att.k_a",
+               "lnx_weight": "att.ln_x.weight", "lnx_bias": "att.ln_x.bias", "ffn_mix": "ffn.x_k"}
+    for l in range(cfg.layers):
+        W = weights.layers[l]
+        pre = f"blocks.{l}."
+        for key, (rows, cols) in cfg.matrix_shapes(l).items():
+            cat[pre + names[key]] = (cfg.weight_format, [cols, rows], W[key])
+        for key, name in vectors.items():
+            if key == "v0" and l == 0:
+                continue
+            cat[pre + name] = (native.F32, [D], f32(W[key]))
+        cat[pre + "att.r_k"] = (native.F32, [N, cfg.heads], f32(W["r_k"]))
+        cat[pre + "att.x_rwkvag"] = (native.F32, [6, D], f32(W["mix"]))
+    return cat
+
+
+def _catalog_array(catalog):
+    arr = (ModelTensor * len(catalog))()
+    keep = []
+    for i, (name, (fmt, dims, _)) in enumerate(sorted(catalog.items())):
+        b = name.encode()
+        keep.append(b)
+        d = (ctypes.c_int64 * 4)(*(list(dims) + [1] * (4 - len(dims))))
+        arr[i] = ModelTensor(b, fmt, len(dims), d)
+    return arr, keep
+
+
+def _options(matvec_mode=None, reuse_local_storage=True, weight_views=True, native_half_weights=True,
+             threads_per_group=64):
+    return GraphOptions(int(reuse_local_storage), int(weight_views), int(native_half_weights),
+                        MATVEC_MODES[matvec_mode], threads_per_group)
+
+
+def rwkv7_graph_describe(cfg, catalog, **options):
+    """Without a device: (graph, report, xml) for a catalog — the logical
+    graph and the lowering report as dicts, the lowered program's VmProgram
+    XML as text."""
+    import json
+    arr, keep = _catalog_array(catalog)
+    opt = _options(**options)
+    lens = [ctypes.c_uint64(0) for _ in range(3)]
+    lib = host_lib()
+    _check(lib.sih_rwkv7_graph_describe(arr, len(catalog), cfg.vocab, cfg.hidden, cfg.layers, ctypes.byref(opt),
+                                        None, 0, ctypes.byref(lens[0]), None, 0, ctypes.byref(lens[1]), None, 0,
+                                        ctypes.byref(lens[2])))
+    bufs = [ctypes.create_string_buffer(max(1, n.value)) for n in lens]
+    _check(lib.sih_rwkv7_graph_describe(arr, len(catalog), cfg.vocab, cfg.hidden, cfg.layers, ctypes.byref(opt),
+                                        bufs[0], lens[0].value, ctypes.byref(lens[0]), bufs[1], lens[1].value,
+                                        ctypes.byref(lens[1]), bufs[2], lens[2].value, ctypes.byref(lens[2])))
+    del keep
+    text = [b.raw[:n.value].decode() for b, n in zip(bufs, lens)]
+    return json.loads(text[0]), json.loads(text[1]), text[2]
+
+
+def xml_roundtrip(xml: str) -> str:
+    """VmProgram XML read (operators re-adapted on the HIP target, no device)
+    and written again."""
+    n = ctypes.c_uint64(0)
+    _check(host_lib().sih_program_xml_roundtrip(xml.encode(), None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(max(1, n.value))
+    _check(host_lib().sih_program_xml_roundtrip(xml.encode(), buf, n.value, ctypes.byref(n)))
+    return buf.raw[:n.value].decode()
+
+
+class Rwkv7GraphProgram:
+    """The portable RWKV-7 forward-token graph of one model, built from its
+    tensor catalog, lowered to a HIP VM program and run operator by operator
+    through the C++ executor (one launch per lowered node)."""
+
+    def __init__(self, cfg, weights, state=None, device: int = 0, xml: Optional[str] = None, **options):
+        """Builds the graph from the model's catalog and lowers it with
+        `options` (matvec_mode, reuse_local_storage, weight_views,
+        native_half_weights, threads_per_group), or loads a lowered program
+        from its VmProgram XML."""
+        self.cfg = cfg
+        catalog = rwkv7_catalog(cfg, weights)
+        h = ctypes.c_void_p()
+        if xml is not None:
+            _check(host_lib().sih_program_create_from_xml(xml.encode(), device, ctypes.byref(h)))
+        else:
+            arr, keep = _catalog_array(catalog)
+            opt = _options(**options)
+            _check(host_lib().sih_rwkv7_graph_program_create(arr, len(catalog), cfg.vocab, cfg.hidden, cfg.layers,
+                                                             ctypes.byref(opt), device, ctypes.byref(h)))
+        self._h = h
+        try:
+            for name, (_, _, data) in catalog.items():
+                self.upload("weight." + name, np.ascontiguousarray(data))
+            if state is not None:
+                self.load_state(state)
+        except Exception:
+            self.close()
+            raise
+
+    def upload(self, slot: str, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        _check(host_lib().sih_program_upload(self._h, slot.encode(), a.ctypes.data, a.nbytes))
+
+    def readback(self, slot: str, dtype) -> np.ndarray:
+        n = ctypes.c_uint64(0)
+        _check(host_lib().sih_program_slot_bytes(self._h, slot.encode(), ctypes.byref(n)))
+        out = np.empty(n.value, np.uint8)
+        _check(host_lib().sih_program_readback(self._h, slot.encode(), out.ctypes.data, out.nbytes))
+        return out.view(dtype)
+
+    def load_state(self, state) -> None:
+        for l, (att, ffn, wkv) in enumerate(state):
+            self.upload(f"state.{l}.att-previous", np.asarray(att, np.float32))
+            self.upload(f"state.{l}.ffn-previous", np.asarray(ffn, np.float32))
+            self.upload(f"state.{l}.wkv", np.asarray(wkv, np.float32))
+
+    def read_state(self, layer: int):
+        cfg = self.cfg
+        return (self.readback(f"state.{layer}.att-previous", np.float32),
+                self.readback(f"state.{layer}.ffn-previous", np.float32),
+                self.readback(f"state.{layer}.wkv", np.float32).reshape(cfg.heads, cfg.head_size, cfg.head_size))
+
+    def forward_token(self, token: int) -> np.ndarray:
+        """One token through the "forward" entry; returns the logits."""
+        self.upload("token", np.array([token], np.int32))
+        _check(host_lib().sih_program_execute(self._h, b"forward"))
+        return self.readback("logits", np.float32)
+
+    def report(self) -> dict:
+        """The lowering report: mat-vec calls and diagnostics, definitions,
+        local slots, per node its definition, implementation and grid."""
+        import json
+        n = ctypes.c_uint64(0)
+        _check(host_lib().sih_program_report(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(1, n.value))
+        _check(host_lib().sih_program_report(self._h, buf, n.value, ctypes.byref(n)))
+        return json.loads(buf.raw[:n.value].decode())
+
+    def dispatch_count(self) -> int:
+        n = ctypes.c_int(0)
+        _check(host_lib().sih_program_dispatch_count(self._h, b"forward", ctypes.byref(n)))
+        return n.value
+
+    def launch_count(self) -> int:
+        n = ctypes.c_int(0)
+        _check(host_lib().sih_program_launch_count(self._h, b"forward", ctypes.byref(n)))
+        return n.value
+
+    def measure_us(self, repetitions: int = 4) -> float:
+        us = ctypes.c_double(0.0)
+        _check(host_lib().sih_program_measure_us(self._h, b"forward", repetitions, ctypes.byref(us)))
+        return us.value
+
+    def to_xml(self) -> str:
+        n = ctypes.c_uint64(0)
+        _check(host_lib().sih_program_serialize(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value)
+        _check(host_lib().sih_program_serialize(self._h, buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value].decode()
 
     def close(self) -> None:
         if getattr(self, "_h", None):

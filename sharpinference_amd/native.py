@@ -229,7 +229,19 @@ SIGNATURES.update({
     "si_hip_rwkv7_wkv": ([_vp, ctypes.POINTER(Rwkv7WkvArgs)], _i32),
     "si_hip_rwkv7_workspace_bytes": ([ctypes.POINTER(Rwkv7Model), ctypes.POINTER(_u64)], _i32),
     "si_hip_rwkv7_decode": ([_vp, ctypes.POINTER(Rwkv7Model)], _i32),
+    "si_hip_t0_elementwise": ([_vp, _i32, _vp, _vp, _vp, _i64], _i32),
+    "si_hip_t0_cast_f16_f32": ([_vp, _vp, _vp, _i64], _i32),
+    "si_hip_t0_fill": ([_vp, ctypes.c_float, _vp, _i64], _i32),
+    "si_hip_t0_reduce_last": ([_vp, _i32, _vp, _vp, _i64, _i64], _i32),
+    "si_hip_t0_broadcast": ([_vp, _vp, _i32, ctypes.POINTER(_i64), _vp, _i32, ctypes.POINTER(_i64)], _i32),
+    "si_hip_t0_slice": ([_vp, _vp, _i32, ctypes.POINTER(_i64), _i32, _i64, _i64, _vp], _i32),
+    "si_hip_t0_head_outer": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64], _i32),
+    "si_hip_gemv_any_shape": ([_vp, _i32, _vp, _vp, _vp, _i64, _i64], _i32),
 })
+
+# si_hip_t0_op: the elementwise T0 operators
+T0_OPS = {"copy": 0, "add": 1, "subtract": 2, "multiply": 3, "divide": 4, "maximum": 5, "exp": 6, "tanh": 7,
+          "sigmoid": 8, "rsqrt": 9, "square": 10, "relu": 11}
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -500,6 +512,33 @@ class HipContext:
     def batched_matvec(self, matrix: int, vector: int, out: int, batch: int, rows: int, cols: int) -> None:
         self._call(lib().si_hip_batched_matvec, ctypes.c_void_p(int(matrix)), ctypes.c_void_p(int(vector)),
                    ctypes.c_void_p(int(out)), batch, rows, cols)
+
+    # -- T0 primitive and portable tensor operators --
+    def t0_elementwise(self, op: str, left: int, right: int, out: int, count: int) -> None:
+        self._call(lib().si_hip_t0_elementwise, T0_OPS[op], _p(left), _p(right), _p(out), int(count))
+
+    def t0_cast_f16_f32(self, x: int, out: int, count: int) -> None:
+        self._call(lib().si_hip_t0_cast_f16_f32, _p(x), _p(out), int(count))
+
+    def t0_fill(self, value: float, out: int, count: int) -> None:
+        self._call(lib().si_hip_t0_fill, ctypes.c_float(value), _p(out), int(count))
+
+    def t0_reduce_last(self, mean: bool, x: int, out: int, rows: int, cols: int) -> None:
+        self._call(lib().si_hip_t0_reduce_last, int(bool(mean)), _p(x), _p(out), int(rows), int(cols))
+
+    def t0_broadcast(self, x: int, in_dims, out: int, out_dims) -> None:
+        a, b = (_i64 * len(in_dims))(*in_dims), (_i64 * len(out_dims))(*out_dims)
+        self._call(lib().si_hip_t0_broadcast, _p(x), len(in_dims), a, _p(out), len(out_dims), b)
+
+    def t0_slice(self, x: int, in_dims, axis: int, start: int, length: int, out: int) -> None:
+        a = (_i64 * len(in_dims))(*in_dims)
+        self._call(lib().si_hip_t0_slice, _p(x), len(in_dims), a, int(axis), int(start), int(length), _p(out))
+
+    def t0_head_outer(self, left: int, right: int, out: int, heads: int, rows: int, cols: int) -> None:
+        self._call(lib().si_hip_t0_head_outer, _p(left), _p(right), _p(out), int(heads), int(rows), int(cols))
+
+    def gemv_any_shape(self, fmt: int, w: int, x: int, y: int, rows: int, cols: int) -> None:
+        self._call(lib().si_hip_gemv_any_shape, fmt, _p(w), _p(x), _p(y), int(rows), int(cols))
 
     def layernorm(self, x: int, weight: int, bias: int, n: int, eps: float, out: int) -> None:
         self._call(lib().si_hip_layernorm, ctypes.c_void_p(int(x)), ctypes.c_void_p(int(weight)),

@@ -135,7 +135,13 @@ MATVEC_CASES = [(native.Q4_0, 5120, 3072, 16, 16), (native.Q4_0, 3072, 8192, 16,
                 (native.F32, 77, 1024, 16, 16), (native.Q8_0, 17, 96, 1, 1),
                 # the LDS-ring form (columns % 256 == 0): one chunk, odd chunk counts, ragged rows and batches
                 (native.Q4_K, 40, 256, 3, 2), (native.Q8_0, 50, 768, 16, 16), (native.Q4_0, 16, 1280, 7, 7),
-                (native.Q4_0, 33, 256, 16, 16), (native.Q8_0, 5, 512, 2, 1)]
+                (native.Q4_0, 33, 256, 16, 16), (native.Q8_0, 5, 512, 2, 1),
+                # the Phi-4-mini Q4_K layer products of the prefill program at full size: qkv and gate_up run
+                # the 8-wave ring form of grids above 256 workgroups, down the 16-wave form; Q8_0 past 4096 rows
+                # (the 8-wave form), with ragged rows and a ragged batch
+                (native.Q4_K, 5120, 3072, 16, 16), (native.Q4_K, 16384, 3072, 16, 13),
+                (native.Q4_K, 3072, 8192, 16, 5), (native.Q4_K, 3072, 3072, 16, 11),
+                (native.Q8_0, 5120, 2048, 16, 16), (native.Q8_0, 4100, 768, 16, 9)]
 
 
 @pytest.mark.parametrize("fmt,rows,cols,batch,valid", MATVEC_CASES,

@@ -349,3 +349,16 @@ def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
     results, _, _ = _run_steps(hip, cfg, weights, kv, [(4242, 2048), (17, 2049), (200000, 2050)])
     for i, (g, gl, o, ol) in enumerate(results):
         _check_logits(g, gl, o, ol, f"phi4-mini step {i}")
+
+
+def test_phi4_mini_f16_decode_step_matches_oracle(hip):
+    """The benched F16 decode step at full size: Phi-4-mini shapes, 32 F16
+    layers (4 distinct weight sets, each layer its own device copy), the
+    tied F16 embedding / vocabulary head 200064 x 3072 (Phi4TextModel.cs:
+    53,95-105), fp16 cache with 2048 tokens, two consecutive steps."""
+    cfg = phi4.Phi4Config(weight_format=native.F16, embed_format=native.F16, head_format=native.F16)
+    weights = phi4.synth_weights(cfg, seed=33, distinct_layers=4, tied=True)
+    kv = phi4.synth_kv(cfg, length=2048, seed=34)
+    results, _, _ = _run_steps(hip, cfg, weights, kv, [(321, 2048), (199999, 2049)])
+    for i, (g, gl, o, ol) in enumerate(results):
+        _check_logits(g, gl, o, ol, f"phi4-mini f16 step {i}")

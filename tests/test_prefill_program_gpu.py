@@ -201,3 +201,46 @@ def test_prefill_fusion_keeps_what_the_entry_leaves(hip):
         a, b = np.asarray(out[True][s], np.float64), np.asarray(out[False][s], np.float64)
         assert np.allclose(a, b, rtol=1e-3, atol=1e-3 * max(1.0, float(np.max(np.abs(b))))), s
 
+
+
+def test_phi4_mini_prefill_batch_at_1016_matches_oracle(hip):
+    """The benched prefill entry at its full size: Phi-4-mini shapes, 32
+    layers, Q4_K layer products (the ring mat-vec forms of the large grids),
+    Q8_0 embedding and head (200064 x 3072), fp16 caches holding 1016 rows of
+    N(0, 1) context, one 16-row batch at control = [1016, 16]; against 16
+    oracle token steps at positions 1016..1031 on the same weights and
+    caches: the logits after the last row at the model gate, the greedy
+    token, and the 16 cache rows each layer appended."""
+    cfg = phi4.Phi4Config()
+    start, rows = 1016, 16
+    weights = phi4.synth_weights(cfg, seed=91, distinct_layers=4)
+    kv = phi4.synth_kv(cfg, length=start, seed=92)
+    tokens = np.random.default_rng(93).integers(0, cfg.vocab, rows)
+    emb = np.zeros((start + rows, cfg.hidden), np.float32)
+    rb = phi4.native.tensor_bytes(cfg.embed_format, 1, cfg.hidden)
+    for r, t in enumerate(tokens):   # the embedding rows of the batch's tokens, dequantised
+        emb[start + r] = orc.dequant(cfg.embed_format, weights.embed[int(t) * rb:(int(t) + 1) * rb], 1, cfg.hidden)
+    prog = host_program.Phi4OpProgram(cfg, weights, cache_fp16=True, prompt_rows=start + rows)
+    ref = orc.Phi4Oracle(cfg, weights)
+    try:
+        for l, (k, v) in enumerate(kv):
+            prog.load_kv(l, k, v)
+            ref.k[l][...] = k
+            ref.v[l][...] = v
+        prog.position = start
+        g = prog.prefill_embeddings(emb)
+        for r, t in enumerate(tokens):
+            o, ol = ref.step(int(t), start + r)
+        _gate(prog.read_logits(), ol, "phi4-mini prefill batch at 1016")
+        _greedy(g, ol, "phi4-mini prefill token")
+        assert prog.position == start + rows
+        for l in (0, 13, cfg.layers - 1):
+            k, v = prog.read_kv(l)
+            for got, want in ((k, ref.k[l]), (v, ref.v[l])):
+                w = want.view(np.float16).astype(np.float32)
+                assert np.array_equal(got[:, :start], w[:, :start]), f"layer {l}: context rows changed"
+                assert np.allclose(got[:, start:start + rows], w[:, start:start + rows], rtol=2e-3, atol=2e-3), \
+                    f"layer {l}: appended rows"
+                assert np.all(got[:, start + rows:] == 0), f"layer {l}: rows past the batch written"
+    finally:
+        prog.close()
