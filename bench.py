@@ -737,13 +737,31 @@ def bench_rwkv_decode(hip, tokens: int = 64, cpu: bool = True, replay_timing: bo
     sess.close()
     log(f"rwkv7: {us:.1f} us/token on device ({1e6 / us:.0f} tok/s, {gbs:.0f} GB/s), "
         f"{loop_s * 1e6:.1f} us/token with host round trips")
+    graph = None
+    if replay_timing:
+        # the same model as the reference's portable graph: built from the tensor catalog, lowered
+        # to a HIP VM program and run operator by operator through the C++ executor
+        from sharpinference_amd import host_program
+        prog = host_program.Rwkv7GraphProgram(cfg, weights, state)
+        prog.forward_token(1)
+        g_us = sorted(prog.measure_us(4) for _ in range(3))[1]
+        rep = prog.report()
+        graph = {"us_per_token": r1(g_us), "tok_s": r1(1e6 / g_us), "dispatches": prog.dispatch_count(),
+                 "definitions": rep["definitions"], "local_slots": rep["localSlots"],
+                 "matvec_calls": rep["matvec"]["calls"], "nodes_lowered_to_views": rep["removedNodes"],
+                 "form": "PortableRwkv7GraphProvider graph, one launch per lowered node (T0 / portable tensor "
+                         "operators and quant.mat-vec)"}
+        prog.close()
+        log(f"rwkv7 portable graph: {g_us:.1f} us/token ({1e6 / g_us:.0f} tok/s), {graph['dispatches']} dispatches, "
+            f"{graph['definitions']} definitions, {graph['local_slots']} local slots")
     out = {"workload": "RWKV-7 token step, 24 layers, width 2048 (32 heads x 64), FFN 8192, Q8_0 projections "
                        "and LoRA (ranks 96/96/64/256), Q8_0 embedding/head 65536x2048, batch 1",
            "us_per_token": r1(us), "tok_s": r1(1e6 / us), "bytes_per_token": step_bytes,
            "GBs": r1(gbs), "hbm_frac": None if gbs != gbs else round(gbs / HBM_PEAK_GBS, 4),
            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
            "loop_us_per_token": round(loop_s * 1e6, 1), "loop_tok_s": round(1.0 / loop_s, 1),
-           "layer_weights": "4 distinct layers uploaded as 24 separate device copies"}
+           "layer_weights": "4 distinct layers uploaded as 24 separate device copies",
+           "graph_program": graph}
     if cpu:
         import oracle as orc
         from types import SimpleNamespace

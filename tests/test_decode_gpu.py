@@ -351,14 +351,35 @@ def test_phi4_mini_decode_step_at_2048_tokens_matches_oracle(hip):
         _check_logits(g, gl, o, ol, f"phi4-mini step {i}")
 
 
-def test_phi4_mini_f16_decode_step_matches_oracle(hip):
+def test_phi4_mini_f16_decode_step_matches_float64_model(hip):
     """The benched F16 decode step at full size: Phi-4-mini shapes, 32 F16
     layers (4 distinct weight sets, each layer its own device copy), the
     tied F16 embedding / vocabulary head 200064 x 3072 (Phi4TextModel.cs:
-    53,95-105), fp16 cache with 2048 tokens, two consecutive steps."""
+    53,95-105), fp16 cache with 2048 tokens, two consecutive steps.
+
+    Truth: the float64 restatement of the model (Float64Phi4, exact F16
+    weights).  At this size FP32 rounding itself reaches the model gate: the
+    oracle (the CpuVm restatement in FP32) measures 1.05 and 1.11 of
+    3e-4 + 3e-4 |t| against float64 at these two steps, so two FP32
+    evaluations need not meet that gate against each other.  Gate: the GPU
+    and the oracle each within twice the model gate of float64, the GPU's
+    logits within 1e-4 L2-relative of float64, and the greedy token of
+    float64 when its top-2 margin exceeds 1e-3."""
+    from types import SimpleNamespace
+    from tests.test_oracle_phi4_step import Float64Phi4
     cfg = phi4.Phi4Config(weight_format=native.F16, embed_format=native.F16, head_format=native.F16)
     weights = phi4.synth_weights(cfg, seed=33, distinct_layers=4, tied=True)
     kv = phi4.synth_kv(cfg, length=2048, seed=34)
-    results, _, _ = _run_steps(hip, cfg, weights, kv, [(321, 2048), (199999, 2049)])
-    for i, (g, gl, o, ol) in enumerate(results):
-        _check_logits(g, gl, o, ol, f"phi4-mini f16 step {i}")
+    steps = [(321, 2048), (199999, 2049)]
+    results, _, _ = _run_steps(hip, cfg, weights, kv, steps)
+    truth = Float64Phi4(SimpleNamespace(**cfg.__dict__), weights, [k for k, _ in kv], [v for _, v in kv])
+    for i, ((tok, pos), (g, gl, o, ol)) in enumerate(zip(steps, results)):
+        t = truth.step(tok, pos)
+        gate = 2 * (3e-4 + 3e-4 * np.abs(t))
+        for name, y in (("gpu", gl), ("oracle", ol)):
+            d = np.abs(np.asarray(y, np.float64) - t)
+            assert np.all(d <= gate), f"{name} step {i}: worst {np.max(d / gate):.2f} of twice the gate"
+        assert np.linalg.norm(gl.astype(np.float64) - t) <= 1e-4 * np.linalg.norm(t), f"step {i} L2"
+        top2 = np.sort(t)[-2:]
+        if top2[1] - top2[0] > 1e-3 * max(1.0, abs(top2[1])):
+            assert g == int(np.argmax(t)), f"step {i} greedy token"

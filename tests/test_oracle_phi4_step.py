@@ -41,8 +41,20 @@ def _weights(cfg):
         down=[q(40 + l, H, F, 0.03) for l in range(L)])
 
 
-def _dq(w, rows, cols, fmt=orc.Q8_0):
-    return orc.dequant(fmt, w, rows, cols).astype(np.float64)
+def _dq(w, rows, cols, fmt=orc.Q8_0, memo=None):
+    """float64 values of a weight tensor; F16 / F32 bytes are converted by
+    numpy (exact), block formats by the pinned orc.dequant.  `memo` shares
+    one conversion between layers that reuse one host array."""
+    key = (id(w), rows, cols, fmt)
+    if memo is not None and key in memo:
+        return memo[key]
+    if fmt in (orc.F16, orc.F32):
+        out = np.frombuffer(w, np.float16 if fmt == orc.F16 else np.float32).reshape(rows, cols).astype(np.float64)
+    else:
+        out = orc.dequant(fmt, w, rows, cols).astype(np.float64)
+    if memo is not None:
+        memo[key] = out
+    return out
 
 
 class Float64Phi4:
@@ -54,17 +66,19 @@ class Float64Phi4:
         self.cfg, self.mut = cfg, mutation
         H, F, D, KVH = cfg.hidden, cfg.ffn, cfg.head_dim, cfg.kv_heads
         wf = getattr(cfg, "weight_format", orc.Q8_0)
-        self.embed = _dq(w.embed, cfg.vocab, H, cfg.embed_format)
-        self.head = _dq(w.lm_head, cfg.vocab, H, cfg.head_format)
+        memo = {}
+        _dq_ = lambda a, r, c, f: _dq(a, r, c, f, memo)
+        self.embed = _dq_(w.embed, cfg.vocab, H, cfg.embed_format)
+        self.head = _dq_(w.lm_head, cfg.vocab, H, cfg.head_format)
         self.onorm = w.output_norm.astype(np.float64)
         self.an = [a.astype(np.float64) for a in w.attn_norm]
         self.fn = [a.astype(np.float64) for a in w.ffn_norm]
         if mutation == "norms_swapped":
             self.an, self.fn = self.fn, self.an
-        self.qkv = [_dq(a, H + 2 * KVH * D, H, wf) for a in w.qkv]
-        self.o = [_dq(a, H, H, wf) for a in w.o]
-        self.up = [_dq(a, 2 * F, H, wf) for a in w.up]
-        self.down = [_dq(a, H, F, wf) for a in w.down]
+        self.qkv = [_dq_(a, H + 2 * KVH * D, H, wf) for a in w.qkv]
+        self.o = [_dq_(a, H, H, wf) for a in w.o]
+        self.up = [_dq_(a, 2 * F, H, wf) for a in w.up]
+        self.down = [_dq_(a, H, F, wf) for a in w.down]
         self.cache_dtype = cache_dtype
         self.k = [a.view(np.float16).astype(cache_dtype) for a in k_init]
         self.v = [a.view(np.float16).astype(cache_dtype) for a in v_init]
