@@ -21,6 +21,7 @@
 // from LDS once and reused for RL rows.  All weight loads of a lane are
 // issued before x is staged into LDS, so HBM latency overlaps the staging.
 #include "si_internal.hpp"
+#include "si_planes.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -90,52 +91,23 @@ __device__ __forceinline__ float group_sum(float v)
     return v;
 }
 
-// Maximum and sum of unsigned / signed integers over aligned groups of 8
-// lanes (same DPP lane moves as group_sum).
-__device__ __forceinline__ uint32_t group8_max_u32(uint32_t v)
-{
-    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
-    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
-    return max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x141, 0xF, 0xF, false)));
-}
-__device__ __forceinline__ int group8_sum_i32(int v)
-{
-    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
-    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
-    return v + __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
-}
-
 // ---- x as integer digit planes ----------------------------------------------
-// Each 32-column block of the staged x is scaled by a power of two 2^s
-// chosen from the block's largest magnitude M (2^20 <= M * 2^s < 2^21) and
-// rounded to integers X (|X| <= 2^21; the rounding is at most half a unit,
-// 2^-s / 2 <= 2^-21 M per value).  So x is rounded per 32-column block to a
-// 21-bit grid, where the FP32 reference multiplies the FP32 x itself
+// The staged x of the 4-bit formats (and of Q8_0 at some shapes) is held as
+// int8 digit planes (encode_planes: a power-of-two scale per 32-column
+// block, x rounded to a 21-bit grid, at most 2^-21 M per value for a block
+// of largest magnitude M).  The FP32 reference multiplies the FP32 x itself
 // (CpuHalfMatrixOperators.cs:29-41); the products' error stays within the
-// mat-vec tolerance but is not the reference's FP32 rounding.  X + 0x808080 has
-// bytes b0, b1, b2 in [0, 255]; the signed bytes d_p = b_p - 128 are its
-// balanced base-256 digits, X = d0 + 256 d1 + 65536 d2 (|d2| <= 32).  Plane p
-// packs d_p of 4 consecutive values into one word, so a 4-bit weight word
-// (nibbles masked into bytes 0..15) is multiplied with 4 values in one
-// v_dot4_i32_i8, exactly.  Per block and row, the three planes combine in
-// INT32 (Horner in 256: |sum q X| <= 32 * 15 * 2^21 < 2^31) and the block
-// enters the FP32 row sum once: d * 2^-s * sum((q - offset) * X).
+// mat-vec tolerance but is not the reference's FP32 rounding.  Per block
+// and row the planes' products combine in INT32 and the block enters the
+// FP32 row sum once: d * 2^-s * sum((q - offset) * X).
 //
 // LDS per 64-column unit (PLANE_UNIT words): block h's planes at 24h +
 // 8p + w (word w = values 4w..4w+3 of the block), then inv_0, inv_1
-// (2^-s, or NaN when the block holds a non-finite value or a magnitude
-// outside [2^-100, 2^100], whose products then take the per-weight FP32
-// form with x read from global memory), then aux_0, aux_1 (Q4_0: 8 sum(X)
-// as INT32; Q4_K: sum(X) 2^-s as FP32).  52 words: 16 lanes reading
+// (2^-s, or NaN when the block takes the per-weight FP32 form with x read
+// from global memory), then aux_0, aux_1 (Q4_0: 8 sum(X) as INT32; Q4_K:
+// sum(X) 2^-s as FP32; unused by Q8_0).  52 words: 16 lanes reading
 // consecutive units with 16-byte reads touch distinct banks.
 constexpr int PLANE_UNIT = 52;
-constexpr uint32_t BIG_BITS = 0x71800000u;    // 2^100
-constexpr uint32_t TINY_BITS = 0x0D800000u;   // 2^-100
-
-__device__ __forceinline__ int dot4_planes(uint32_t q, uint32_t p, int a)
-{
-    return __builtin_amdgcn_sdot4(static_cast<int>(q), static_cast<int>(p), a, false);
-}
 
 __device__ __forceinline__ float wave_sum(float v)
 {
@@ -191,6 +163,22 @@ struct QUnit<FMT_Q8_0> {
         const float d = h == 0 ? half_lo(v[0]) : half_hi(v[8]);
         return d * (a0 + a1);
     }
+
+    // Block h against x's digit planes P; inv = 2^-s.  sum(q X) scaled by
+    // 2^-s (exact) and by the block scale, as the per-weight form
+    // d * sum(q x) does.
+    __device__ __forceinline__ float planes(int h, const uint32_t* P, float inv, float /*aux*/, float acc) const
+    {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            q[k] = h == 0 ? __builtin_amdgcn_alignbit(v[k + 1], v[k], 16) : v[9 + k];
+        const float d = h == 0 ? half_lo(v[0]) : half_hi(v[8]);
+        return fmaf(d, q8_planes_sum(q, P) * inv, acc);
+    }
+
+    // Non-finite or huge x: the per-weight FP32 form above.
+    __device__ float half_exact(int h, const float4* x) const { return half(h, x, 0.0f); }
 };
 
 // Two Q4_0 blocks {fp16 d; u8 q[16]}: element j < 16 is the low nibble of
@@ -249,18 +237,7 @@ struct QUnit<FMT_Q4_0> {
                 hi[k] = (v[5 + k] >> 4) & M;
             }
         }
-        int s = 0;
-#pragma unroll
-        for (int p = 2; p >= 0; p--) {
-            if (p < 2)
-                s <<= 8;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                s = dot4_planes(lo[k], P[8 * p + k], s);
-                s = dot4_planes(hi[k], P[8 * p + 4 + k], s);
-            }
-        }
-        return fmaf(scale(h) * inv, static_cast<float>(s - sum8), acc);
+        return fmaf(scale(h) * inv, static_cast<float>(q4_planes_sum(lo, hi, P) - sum8), acc);
     }
 
     // Classification-exact form for non-finite or huge x: (nibble ^ 8) is
@@ -562,7 +539,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     static_assert(K % 32 == 0 && THREADS % 8 == 0, "x staging keeps 8-thread groups whole");
 
     constexpr bool PLANES = XM == 1;
-    static_assert(!PLANES || FMT == FMT_Q4_0 || FMT == FMT_Q4_K, "digit planes serve the 4-bit formats");
+    static_assert(!PLANES || FMT == FMT_Q4_0 || FMT == FMT_Q4_K || FMT == FMT_Q8_0, "digit planes serve the block formats");
     __shared__ float4 xs4[PLANES ? 1 : UPR * XS_UNIT / 4];
     __shared__ float bs[PLANES ? 1 : UPR * 2];
     __shared__ uint4 xp4[PLANES ? UPR * PLANE_UNIT / 4 : 1];
@@ -802,43 +779,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
 #pragma unroll
         for (int j = 0; j < XPT; j++) {
             const int i = threadIdx.x + j * THREADS;
-            const float4 v = xr[j];
-            // largest magnitude as bits (integer order = magnitude order;
-            // NaN sorts above inf), over the block's 8 threads
-            uint32_t mb = max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
-                              max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu));
-            mb = group8_max_u32(mb);
-            const bool exact = mb > BIG_BITS || (mb != 0u && mb < TINY_BITS);
-            const uint32_t e = max(mb >> 23, 27u);                  // biased exponent of M (zero blocks: 27)
-            // M < 2^(e - 126), so s = 147 - e gives M 2^s < 2^21
-            const float scale = __uint_as_float((274u - e) << 23);  // 2^s
-            const float inv = __uint_as_float((e - 20u) << 23);     // 2^-s
-            // X + 0x808080 from the FP32 bits of X + 1.5 * 2^23 (round to nearest even)
-            const uint32_t y0 = __float_as_uint(fmaf(v.x, scale, 0x1.8p23f)) - 0x4ABF7F80u;
-            const uint32_t y1 = __float_as_uint(fmaf(v.y, scale, 0x1.8p23f)) - 0x4ABF7F80u;
-            const uint32_t y2 = __float_as_uint(fmaf(v.z, scale, 0x1.8p23f)) - 0x4ABF7F80u;
-            const uint32_t y3 = __float_as_uint(fmaf(v.w, scale, 0x1.8p23f)) - 0x4ABF7F80u;
-            // byte transpose: plane p = byte p of y0..y3, then b - 128 as a signed byte
-            const uint32_t t01 = __builtin_amdgcn_perm(y1, y0, 0x06020400u);   // y0.b0 y1.b0 y0.b2 y1.b2
-            const uint32_t t23 = __builtin_amdgcn_perm(y3, y2, 0x06020400u);
-            const uint32_t u01 = __builtin_amdgcn_perm(y1, y0, 0x0c0c0501u);   // y0.b1 y1.b1
-            const uint32_t u23 = __builtin_amdgcn_perm(y3, y2, 0x0c0c0501u);
-            const uint32_t p0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
-            const uint32_t p1 = __builtin_amdgcn_perm(u23, u01, 0x05040100u) ^ 0x80808080u;
-            const uint32_t p2 = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
-            const int sx = group8_sum_i32(static_cast<int>((y0 + y1) + (y2 + y3)) - 4 * 0x808080);
+            const PlaneWords pl = encode_planes(xr[j]);   // the block's 8 threads together
             if (xin(j)) {
                 const int col = 4 * i;
                 const int h = (col >> 5) & 1;
                 uint32_t* ub = xp + (col >> 6) * PLANE_UNIT;
                 uint32_t* pw = ub + 24 * h + ((col >> 2) & 7);
-                pw[0] = p0;
-                pw[8] = p1;
-                pw[16] = p2;
+                pw[0] = pl.p[0];
+                pw[8] = pl.p[1];
+                pw[16] = pl.p[2];
                 if ((i & 7) == 0) {
-                    ub[48 + h] = exact ? 0x7fc00000u : __float_as_uint(inv);
-                    ub[50 + h] = FMT == FMT_Q4_0 ? static_cast<uint32_t>(8 * sx)
-                                                 : __float_as_uint(static_cast<float>(sx) * inv);
+                    ub[48 + h] = pl.exact ? 0x7fc00000u : __float_as_uint(pl.inv);
+                    ub[50 + h] = FMT == FMT_Q4_0 ? static_cast<uint32_t>(8 * pl.sum)
+                                                 : __float_as_uint(static_cast<float>(pl.sum) * pl.inv);
                 }
             }
         }
@@ -1408,11 +1361,26 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     const bool mid = rows64 >= 12288, tall = rows64 >= 49152;
     switch (cols) {
     case 1024: return mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
-    case 2048: return mid    ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s)
-                    : rows64 >= 8192 ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s)
-                    : rows64 >= 4096 ? launch_tiled<FMT, 16, 1, 1, 2, 8>(ops, n, s)   // the RWKV-7 time-mix table
-                                     : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
+    case 2048:
+        if constexpr (FMT == FMT_Q8_0) {
+            // x as digit planes (v_dot4_i32_i8 on the signed weight bytes):
+            // the RWKV-7 shapes, against FP32 staging with the tiles of the
+            // other formats: 65536-row head 27.2 -> 26.3 us (32 rows per
+            // workgroup), time-mix batch of 6656 rows 6.48 -> 5.72, FFN key
+            // 8192 rows 5.60 -> 5.48, output 2048 rows 2.65 -> 2.62
+            if (mid)
+                return launch_tiled<FMT, 16, 1, 2, 2, 8, 1>(ops, n, s);
+            return rows64 >= 4096 ? launch_tiled<FMT, 16, 1, 1, 2, 8, 1>(ops, n, s)
+                                  : launch_tiled<FMT, 16, 1, 1, 2, 4, 1>(ops, n, s);
+        }
+        return mid              ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s)
+               : rows64 >= 8192 ? launch_tiled<FMT, 16, 2, 1, 1, 4>(ops, n, s)
+               : rows64 >= 4096 ? launch_tiled<FMT, 16, 1, 1, 2, 8>(ops, n, s)
+                                : launch_tiled<FMT, 16, 1, 1, 2, 4>(ops, n, s);
     case 3072:
+        if constexpr (FMT == FMT_Q8_0)   // the 200064-row head: 104.0 -> 101.5 us with planes, 4 rows per lane group
+            if (tall)
+                return launch_tiled<FMT, 16, 3, 1, 1, 4, 1>(ops, n, s);
         if (tall)
             return launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s);
         if constexpr (FMT == FMT_Q8_0)

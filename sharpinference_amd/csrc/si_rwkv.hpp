@@ -34,7 +34,29 @@ struct WkvArgs {
     float* out;
     const float* copy_src;      // optional: copy_dst = copy_src ([heads * 64]), a state store
     float* copy_dst;
+    // In-kernel LoRA outputs.  lora_fmt 0: w_lora, a_lora, gate and v_lora
+    // are read as given.  lora_fmt Q8_0 / Q4_0: they are not read; each
+    // head's workgroup forms its 64 elements of up[m] . hid[m] itself, for
+    // the up matrices m = w2, a2, g2, v2 ([heads * 64, rank[m]] in that
+    // format, 16-byte aligned) and their FP32 hidden vectors hid[m] (the
+    // outputs of w1 with tanh, a1, g1 with sigmoid, v1; 16-byte aligned);
+    // rank[3] = 0 on the first layer.  Each element is its row's block
+    // products (the hidden vectors as digit planes, as the matrix-vector
+    // kernels stage x) summed in order.
+    int lora_fmt = 0;
+    const void* up[4] = {};
+    const float* hid[4] = {};
+    int rank[4] = {};
 };
+
+// Limits of the in-kernel LoRA outputs: the head's rows of the four up
+// matrices are staged in LDS, and a head forms at most 1536 block products
+// (the sum of the ranks at most 24 blocks of 32).
+constexpr int WKV_LORA_LDS_BYTES = 48 * 1024;
+constexpr int WKV_LORA_MAX_ITEMS = 1536;
+// Whether the in-kernel LoRA outputs take these arguments (format, ranks,
+// 16-byte aligned up matrices and hidden vectors, the limits above).
+bool wkv_lora_supported(const WkvArgs& a);
 
 hipError_t launch_rwkv_wkv(const WkvArgs& a, hipStream_t s);
 // out = ((x - mean) * (1 / sqrt(var + eps))) * w + b over n <= 8192 values,

@@ -160,17 +160,35 @@ hipError_t rwkv7_step(si_hip_context* ctx, const si_hip_rwkv7_model* m)
             tm(L.v1, 3, ws + o.hv, m->rank_v, si::OUT_PLAIN);
         e = si::launch_gemv_ops(a, na, s, nullptr);
         if (e != hipSuccess) break;
-        // 2. LoRA outputs
-        si::GemvOp b[4] = {mat(fmt, L.w2, ws + o.hw, ws + o.wl, D, m->rank_w),
-                           mat(fmt, L.a2, ws + o.ha, ws + o.al, D, m->rank_a),
-                           mat(fmt, L.g2, ws + o.hg, ws + o.g, D, m->rank_g),
-                           mat(fmt, L.v2, ws + o.hv, ws + o.vl, D, m->rank_v)};
-        e = si::launch_gemv_ops(b, l > 0 ? 4 : 3, s, nullptr);
-        if (e != hipSuccess) break;
-        // 3. time-mix core; att_prev = LayerNorm(x) now that its readers ran
+        // 2. LoRA outputs: formed inside the time-mix core's kernel where it
+        //    takes them (Q8_0 / Q4_0 up matrices within its LDS staging),
+        //    else one launch of the four short-row products
         si::WkvArgs w{};
         w.heads = m->heads;
         w.first_layer = l == 0;
+        w.lora_fmt = fmt;
+        w.up[0] = L.w2;
+        w.up[1] = L.a2;
+        w.up[2] = L.g2;
+        w.up[3] = l > 0 ? L.v2 : nullptr;
+        w.hid[0] = ws + o.hw;
+        w.hid[1] = ws + o.ha;
+        w.hid[2] = ws + o.hg;
+        w.hid[3] = l > 0 ? ws + o.hv : nullptr;
+        w.rank[0] = m->rank_w;
+        w.rank[1] = m->rank_a;
+        w.rank[2] = m->rank_g;
+        w.rank[3] = l > 0 ? m->rank_v : 0;
+        if (!si::wkv_lora_supported(w)) {
+            w.lora_fmt = 0;
+            si::GemvOp b[4] = {mat(fmt, L.w2, ws + o.hw, ws + o.wl, D, m->rank_w),
+                               mat(fmt, L.a2, ws + o.ha, ws + o.al, D, m->rank_a),
+                               mat(fmt, L.g2, ws + o.hg, ws + o.g, D, m->rank_g),
+                               mat(fmt, L.v2, ws + o.hv, ws + o.vl, D, m->rank_v)};
+            e = si::launch_gemv_ops(b, l > 0 ? 4 : 3, s, nullptr);
+            if (e != hipSuccess) break;
+        }
+        // 3. time-mix core; att_prev = LayerNorm(x) now that its readers ran
         w.r = ws + o.r;
         w.k = ws + o.k;
         w.v = ws + o.v;

@@ -53,7 +53,7 @@ def run_gemv(hip, fmt, w_host, x_host, rows, cols, residual=None, w_offset=0):
 # (>= 12288 rows) and tall (>= 49152 rows) variants for each column count.
 SHAPES = {
     native.Q8_0: [(3072, 3072), (2048, 2048), (8192, 2048), (2048, 8192), (4099, 3072), (1, 3072), (7, 8192),
-                  (65536, 2048), (12288, 4096), (50000, 3072)],
+                  (65536, 2048), (12288, 4096), (50000, 3072), (4100, 2048), (12289, 2048)],
     native.Q4_0: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (4099, 3072), (1, 4096), (33, 6144),
                   (16384, 8192), (12289, 6144), (49153, 3072)],
     native.Q4_K: [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (4099, 1024), (1, 2048), (33, 6144),
@@ -230,19 +230,21 @@ def test_nonfinite_sums_retain_classification(hip, fmt, cols):
             assert np.all(y == exp), (a, b, y)
 
 
-@pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("rows", [5120, 3072])
-def test_wide_and_finite_blocks_mix_in_one_row(hip, fmt, rows):
+WIDE_CASES = [(f, r, 3072) for f in FORMATS for r in (5120, 3072)] + [(native.Q8_0, 8192, 2048),
+                                                                       (native.Q8_0, 2048, 2048)]
+
+
+@pytest.mark.parametrize("fmt,rows,cols", WIDE_CASES, ids=[f"{NAMES[f]}-{r}x{c}" for f, r, c in WIDE_CASES])
+def test_wide_and_finite_blocks_mix_in_one_row(hip, fmt, rows, cols):
     """Blocks holding huge values (|x| > 2^100) take the per-weight form and
     the others the factored one, inside one row and one workgroup (the
-    one-workgroup-per-CU tiles at 3072 / 5120 rows): the sum stays within the
-    GEMV gate of the fp64 product.  A single +inf or NaN gives each row the
-    IEEE class of the dequantise-then-dot sum (0 * inf = NaN where the weight
-    is zero)."""
-    cols = 3072
+    one-workgroup-per-CU tiles at 3072 / 5120 rows, the Q8_0 digit-plane
+    tiles at 2048 columns): the sum stays within the GEMV gate of the fp64
+    product.  A single +inf or NaN gives each row the IEEE class of the
+    dequantise-then-dot sum (0 * inf = NaN where the weight is zero)."""
     w = orc.gen_quant(fmt, 77 + rows, rows, cols)
     x = orc.gen_normal_f32(78 + rows, cols, 0.0, 1.0)
-    x[[5, 700, 701, 2050]] = np.float32([3e33, -2e31, 5e30, -7e32])
+    x[[5, 700, 701, 2050 if cols > 2050 else 1050]] = np.float32([3e33, -2e31, 5e30, -7e32])
     y, _ = run_gemv(hip, fmt, w, x, rows, cols)
     assert_gemv_close(y, orc.gemv_f64(fmt, w, x, rows, cols), f"{NAMES[fmt]} huge blocks")
     wd = orc.dequant(fmt, w, rows, cols).reshape(rows, cols).astype(np.float64)
@@ -257,18 +259,28 @@ def test_wide_and_finite_blocks_mix_in_one_row(hip, fmt, rows):
         assert np.array_equal(y[fin], truth[fin].astype(np.float32)), f"{NAMES[fmt]} {bad}: inf rows differ"
 
 
-@pytest.mark.parametrize("fmt", [native.Q4_0, native.Q4_K])
-@pytest.mark.parametrize("rows", [16384, 5120, 3072])
-def test_digit_plane_block_scales(hip, fmt, rows):
-    """The 4-bit tiles at 3072 columns stage x as integer digit planes under
-    a power-of-two scale per 32 columns (the block's largest magnitude M
-    maps below 2^21).  Edge blocks: M exactly 2^100 (planes) and one ulp
-    above (per-weight form), M exactly 2^-100 (planes) and below it
-    (per-weight form, subnormals included), an all-zero block, and one
-    large value next to 31 small ones; every row within the GEMV gate of
-    the fp64 product."""
-    cols = 3072
+PLANE_TILES = [(native.Q4_0, 16384, 3072), (native.Q4_0, 5120, 3072), (native.Q4_0, 3072, 3072),
+               (native.Q4_K, 16384, 3072), (native.Q4_K, 5120, 3072), (native.Q4_K, 3072, 3072),
+               (native.Q8_0, 2048, 2048), (native.Q8_0, 6656, 2048), (native.Q8_0, 65536, 2048),
+               (native.Q8_0, 49160, 3072)]
+
+
+@pytest.mark.parametrize("fmt,rows,cols", PLANE_TILES, ids=[f"{NAMES[f]}-{r}x{c}" for f, r, c in PLANE_TILES])
+def test_digit_plane_block_scales(hip, fmt, rows, cols):
+    """The 4-bit tiles at 3072 columns and the Q8_0 tiles at 2048 columns
+    and at 3072 columns for tall matrices stage x as integer digit planes
+    under a power-of-two scale per 32 columns (the block's largest
+    magnitude M maps below 2^21).  Edge blocks: M exactly 2^100 (planes)
+    and one ulp above (per-weight form), M exactly 2^-100 (planes) and
+    below it (per-weight form, subnormals included), an all-zero block, and
+    one large value next to 31 small ones; every row within the GEMV gate
+    of the fp64 product.  Q8_0 weights get blocks of -128 and of 127 bytes
+    planted (the extremes of its plane sums)."""
     w = orc.gen_quant(fmt, 91 + rows, rows, cols)
+    if fmt == native.Q8_0:
+        wb = w.reshape(-1, 34)
+        wb[::7, 2:34] = 0x80
+        wb[3::11, 2:34] = 0x7F
     rng = np.random.default_rng(rows)
     big = orc.gen_normal_f32(92 + rows, cols, 0.0, 1.0)
     big[96] = np.float32(2.0 ** 100)

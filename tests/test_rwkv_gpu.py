@@ -10,6 +10,7 @@ the reference's model gate |d| <= 3e-4 + 3e-4 * |t|
 1e-4 * (1 + |t|), and the same greedy token when the oracle's top-2 margin
 exceeds the gate.
 """
+import dataclasses
 from types import SimpleNamespace
 
 import numpy as np
@@ -193,6 +194,29 @@ def test_small_step_sequence_matches_oracle(hip, ranks):
         token = 17
         for step in range(4):
             token = compare_step(sess, model, token, f"step {step}")
+    finally:
+        sess.close()
+
+
+@pytest.mark.parametrize("fmt,ranks", [(native.Q4_0, (32, 32, 32, 64)), (native.Q4_0, (256, 256, 256, 256)),
+                                       (native.Q8_0, (96, 96, 64, 256))],
+                         ids=["q4_0-ranks-32-64", "q4_0-ranks-256", "q8_0-ranks-96-256"])
+def test_lora_formats_step_sequence_matches_oracle(hip, fmt, ranks):
+    """The LoRA outputs are formed inside the time-mix core's kernel for
+    Q8_0 and Q4_0 weights whose up rows fit its LDS staging (Q8_0 at the
+    1.5B ranks 96 / 96 / 64 / 256, Q4_0 at small ranks) and by the separate
+    short-row products otherwise (Q4_0 at rank 256 for all four): three
+    layers, four greedy steps, logits and every layer's state against the
+    oracle."""
+    cfg = dataclasses.replace(small_cfg(layers=3, ranks=ranks), weight_format=fmt)
+    weights = rwkv7.synth_weights(cfg, seed=15)
+    st = rwkv7.synth_state(cfg, seed=16)
+    sess = rwkv7.Rwkv7DecodeSession(hip, cfg, weights, st)
+    model = orc.Rwkv7Oracle(oracle_cfg(cfg), weights, st)
+    try:
+        token = 29
+        for step in range(4):
+            token = compare_step(sess, model, token, f"{native.FORMAT_NAMES.get(fmt, fmt)} step {step}")
     finally:
         sess.close()
 
