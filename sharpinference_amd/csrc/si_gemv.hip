@@ -431,10 +431,11 @@ struct QUnit<FMT_F32> {
 // ---- launch descriptors -----------------------------------------------------
 
 // Device copy of one GemvOp.  A launch carries up to MAX_SEGS of them by
-// value and runs a 2D grid: grid row i is op i (as wide as the largest op
-// needs), so a workgroup reads its descriptor directly (one
-// kernel-argument round trip, no search over the table); workgroups past
-// their op's rows leave before any load or barrier.
+// value.  The tiled kernel runs a 1D grid of exactly the ops' workgroups
+// (op i from workgroup first[i]; a workgroup finds its op with a uniform
+// scan of the kernel arguments); the short-row and any-shape kernels run a
+// 2D grid, grid row i being op i (as wide as the largest op needs), whose
+// workgroups past their op's rows leave before any load or barrier.
 struct Seg {
     const uint8_t* w;
     const float* x;
@@ -461,6 +462,10 @@ template <int NS>
 struct Segs {
     Seg s[NS];
     int count;
+    // tiled kernel, NS > 1: a 1D grid, op i owning workgroups first[i] ..
+    // first[i + 1] - 1 (the short-row and any-shape kernels run one grid
+    // row per op instead)
+    int first[NS];
 };
 
 // Output function of one row (OUT_SWIGLU_ROWS is handled by the callers,
@@ -546,15 +551,21 @@ __global__ __launch_bounds__(64 * NW) void gemv_fast_kernel(const uint8_t* __res
     __shared__ float part[ROWS_PER_WG * KS];
     __shared__ float red[NW], red2[NW];
 
-    const Seg& sg = segs.s[NS == 1 ? 0 : blockIdx.y];   // the op of this grid row
-    const int b = static_cast<int>(blockIdx.x);
+    // the op of this workgroup (a uniform scan of the table's first
+    // workgroups) and the workgroup's index within it
+    int op = 0;
+    if constexpr (NS > 1) {
+#pragma unroll
+        for (int k = 1; k < NS; k++)
+            op = k < segs.count && static_cast<int>(blockIdx.x) >= segs.first[k] ? k : op;
+    }
+    const Seg& sg = segs.s[op];
+    const int b = static_cast<int>(blockIdx.x) - (NS == 1 ? 0 : segs.first[op]);
     const int rows = NS == 1 ? rows0 : sg.rows;
     const uint8_t* wbase = NS == 1 ? w0 : sg.w;
     const bool swiglu = FULL && (NS == 1 ? out0 : sg.out) == OUT_SWIGLU_ROWS;
     const int in_kind = FULL ? (NS == 1 ? in0 : sg.in) : static_cast<int>(XF_PLAIN);
     const int rb = b * (swiglu ? HALF : ROWS_PER_WG);   // first output row of this workgroup
-    if (NS > 1 && rb >= rows)
-        return;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: index math stays scalar
@@ -1291,9 +1302,9 @@ bool is_plain(const GemvOp& op)
     return op.in == XF_PLAIN && op.out == OUT_PLAIN && op.copy_n == 0;
 }
 
-// Builds the descriptor table of n ops and returns the launch grid: op i
-// takes ceil(rows / per_wg(op)) workgroups; a table of several ops runs one
-// grid row per op, as wide as the largest op needs.
+// Builds the descriptor table of n ops and returns the 2D launch grid: op
+// i takes ceil(rows / per_wg(op)) workgroups; a table of several ops runs
+// one grid row per op, as wide as the largest op needs.
 template <int NS, typename PerWg>
 dim3 fill_segs(Segs<NS>& t, const GemvOp* ops, int n, PerWg per_wg)
 {
@@ -1336,7 +1347,13 @@ hipError_t launch_tiled(const GemvOp* ops, int n, hipStream_t s)
                                s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
     } else {
         Segs<MAX_SEGS> t;
-        const dim3 grid = fill_segs(t, ops, n, per);
+        fill_segs(t, ops, n, per);
+        unsigned total = 0;   // 1D grid: op i's workgroups follow op i - 1's
+        for (int i = 0; i < n; i++) {
+            t.first[i] = static_cast<int>(total);
+            total += static_cast<unsigned>((ops[i].rows + per(ops[i]) - 1) / per(ops[i]));
+        }
+        const dim3 grid(total);
         if (ln)
             hipLaunchKernelGGL((gemv_fast_kernel<FMT, LK, UPL, RL, KS, NW, MAX_SEGS, true, 4, XM>), grid, dim3(64 * NW),
                                0, s, w0, o.x, o.residual, o.norm_weight, rows0, o.out, o.in, static_cast<int>(o.copy_n), t);
@@ -1363,14 +1380,13 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     case 1024: return mid ? launch_tiled<FMT, 16, 1, 2, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 1, 4>(ops, n, s);
     case 2048:
         if constexpr (FMT == FMT_Q8_0) {
-            // x as digit planes (v_dot4_i32_i8 on the signed weight bytes):
-            // the RWKV-7 shapes, against FP32 staging with the tiles of the
-            // other formats: 65536-row head 27.2 -> 26.3 us (32 rows per
-            // workgroup), time-mix batch of 6656 rows 6.48 -> 5.72, FFN key
-            // 8192 rows 5.60 -> 5.48, output 2048 rows 2.65 -> 2.62
-            if (mid)
-                return launch_tiled<FMT, 16, 1, 2, 2, 8, 1>(ops, n, s);
-            return rows64 >= 4096 ? launch_tiled<FMT, 16, 1, 1, 2, 8, 1>(ops, n, s)
+            // x as digit planes (v_dot4_i32_i8 on the signed weight bytes),
+            // 32 rows per workgroup from 4096 rows: the RWKV-7 shapes with
+            // weights streamed from HBM, against FP32 staging with the tiles
+            // of the other formats: time-mix batch of 6656 rows 7.42 -> 6.07
+            // us, FFN key 8192 rows 6.32 -> 5.90, 65536-row head 27.2 ->
+            // 26.3, output 2048 rows 2.66 -> 2.62
+            return rows64 >= 4096 ? launch_tiled<FMT, 16, 1, 2, 2, 8, 1>(ops, n, s)
                                   : launch_tiled<FMT, 16, 1, 1, 2, 4, 1>(ops, n, s);
         }
         return mid              ? launch_tiled<FMT, 16, 2, 2, 1, 4>(ops, n, s)

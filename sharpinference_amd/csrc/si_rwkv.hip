@@ -196,10 +196,10 @@ __global__ __launch_bounds__(LF ? LORA_THREADS : WKV_THREADS) void rwkv_wkv_kern
 
     // Every global load is issued here, before any result is waited for:
     // the state tile, then (wave 0, one element per lane) the head vectors,
-    // the GroupNorm affine and gate, and the side copy's value.  Loads are
+    // the GroupNorm affine and gate, and the side copies' values.  Loads are
     // unconditional (the first layer's value inputs read v instead of the
     // v_lora / v0 / v_first it does not use), so no branch holds them back
-    // behind an earlier round trip; the side copy is stored at the end.
+    // behind an earlier round trip; the side copies are stored at the end.
     float4 sv[4];
     if (state_thread) {
 #pragma unroll
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(LF ? LORA_THREADS : WKV_THREADS) void rwkv_wkv_kern
     const int e = o + (t & (N - 1));
     const bool first = a.first_layer != 0;
     float kk = 0.0f, wl = 0.0f, w0 = 0.0f, al = 0.0f, a0 = 0.0f, kkk = 0.0f, kka = 0.0f, vv = 0.0f, vf = 0.0f,
-          vl = 0.0f, v0 = 0.0f, rr = 0.0f, rk = 0.0f, lw = 0.0f, lb = 0.0f, gt = 0.0f, cp = 0.0f;
+          vl = 0.0f, v0 = 0.0f, rr = 0.0f, rk = 0.0f, lw = 0.0f, lb = 0.0f, gt = 0.0f, cp = 0.0f, cp2 = 0.0f;
     if (t < N) {
         kk = a.k[e];
         w0 = a.w0[e];
@@ -224,6 +224,7 @@ __global__ __launch_bounds__(LF ? LORA_THREADS : WKV_THREADS) void rwkv_wkv_kern
         lw = a.lnx_weight[e];
         lb = a.lnx_bias[e];
         cp = (a.copy_src ? a.copy_src : a.v)[e];
+        cp2 = (a.copy2_src ? a.copy2_src : a.v)[e];
         if constexpr (LF == 0) {
             wl = a.w_lora[e];
             al = a.a_lora[e];
@@ -365,6 +366,8 @@ __global__ __launch_bounds__(LF ? LORA_THREADS : WKV_THREADS) void rwkv_wkv_kern
         a.out[o + t] = (ln + s_value[t] * s_bonus) * gt;
         if (a.copy_src)
             a.copy_dst[o + t] = cp;
+        if (a.copy2_src)
+            a.copy2_dst[o + t] = cp2;
     }
 }
 

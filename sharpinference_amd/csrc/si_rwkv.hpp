@@ -34,6 +34,8 @@ struct WkvArgs {
     float* out;
     const float* copy_src;      // optional: copy_dst = copy_src ([heads * 64]), a state store
     float* copy_dst;
+    const float* copy2_src = nullptr;   // optional: a second such store
+    float* copy2_dst = nullptr;
     // In-kernel LoRA outputs.  lora_fmt 0: w_lora, a_lora, gate and v_lora
     // are read as given.  lora_fmt Q8_0 / Q4_0: they are not read; each
     // head's workgroup forms its 64 elements of up[m] . hid[m] itself, for

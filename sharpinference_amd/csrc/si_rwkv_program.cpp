@@ -209,6 +209,13 @@ hipError_t rwkv7_step(si_hip_context* ctx, const si_hip_rwkv7_model* m)
         w.out = ws + o.att;
         w.copy_src = ws + o.ln1;
         w.copy_dst = L.att_prev;
+        // the previous layer's ffn_prev = its LayerNorm(x) of step 5, now
+        // that its FFN key product (the reader) has run; the value product
+        // then carries no side copy (the last layer's store rides on the head)
+        if (l > 0) {
+            w.copy2_src = ws + o.ln2;
+            w.copy2_dst = m->layer[l - 1].ffn_prev;
+        }
         e = si::launch_rwkv_wkv(w, s);
         if (e != hipSuccess) break;
         // 4. x += output . att
@@ -226,12 +233,10 @@ hipError_t rwkv7_step(si_hip_context* ctx, const si_hip_rwkv7_model* m)
         key.norm_out = ws + o.ln2;
         e = si::launch_gemv_ops(&key, 1, s, nullptr);
         if (e != hipSuccess) break;
-        // 6. x += ffn_value . hidden; ffn_prev = LayerNorm(x) of step 5
+        // 6. x += ffn_value . hidden (ffn_prev = LayerNorm(x) of step 5 is
+        //    stored by the next layer's time-mix core or by the head)
         si::GemvOp val = mat(fmt, L.ffn_value, ws + o.hid, x, D, F);
         val.residual = x;
-        val.copy_src = ws + o.ln2;
-        val.copy_dst = L.ffn_prev;
-        val.copy_n = D;
         e = si::launch_gemv_ops(&val, 1, s, nullptr);
     }
     if (e == hipSuccess) {   // logits = head . ln_out(x) (:290-291)
@@ -240,6 +245,9 @@ hipError_t rwkv7_step(si_hip_context* ctx, const si_hip_rwkv7_model* m)
         head.norm_weight = m->ln_out_weight;
         head.norm_bias = m->ln_out_bias;
         head.eps = LN_EPS;
+        head.copy_src = ws + o.ln2;   // the last layer's ffn_prev
+        head.copy_dst = m->layer[m->layers - 1].ffn_prev;
+        head.copy_n = D;
         e = si::launch_gemv_ops(&head, 1, s, nullptr);
     }
     if (e == hipSuccess)
