@@ -1401,11 +1401,14 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
             return launch_tiled<FMT, 16, 3, 2, 1, 4>(ops, n, s);
         if constexpr (FMT == FMT_Q8_0)
             return mid ? launch_tiled<FMT, 16, 3, 1, 1, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
+        else if (mid)   // Q4_K: the Phi-4-mini gate / up rows (RMSNorm and SwiGLU fused), weights from HBM:
+                        // 8 waves 8.26 -> 7.85 us (Q4_0 plain: 4 waves 6.95, 8 waves 7.03)
+            return FMT == FMT_Q4_K ? launch_tiled<FMT, 16, 3, 1, 1, 8, 1>(ops, n, s)
+                                   : launch_tiled<FMT, 16, 3, 1, 1, 4, 1>(ops, n, s);
         else   // Q4 formats: wide workgroups (one per CU at 3072 and 5120 rows)
             // stage x once per CU instead of once per 4 rows, as digit planes
             // for the integer dot products
-            return mid              ? launch_tiled<FMT, 16, 3, 1, 1, 4, 1>(ops, n, s)
-                   : rows64 >= 5120 ? launch_tiled<FMT, 16, 1, 1, 3, 15, 1>(ops, n, s)
+            return rows64 >= 5120   ? launch_tiled<FMT, 16, 1, 1, 3, 15, 1>(ops, n, s)
                    : rows64 >= 3072 ? launch_tiled<FMT, 16, 1, 1, 3, 12, 1>(ops, n, s)
                                     : launch_tiled<FMT, 16, 1, 1, 3, 3>(ops, n, s);
     case 4096: return mid ? launch_tiled<FMT, 16, 2, 2, 2, 4>(ops, n, s) : launch_tiled<FMT, 16, 1, 1, 4, 4>(ops, n, s);
@@ -1413,10 +1416,11 @@ hipError_t launch_fast(const GemvOp* ops, int n, int64_t rows64, int64_t cols, h
     case 8192:
         if (mid)
             return launch_tiled<FMT, 16, 4, 2, 2, 4>(ops, n, s);
-        if constexpr (FMT == FMT_Q4_K)   // 12 rows per workgroup, 256 workgroups at 3072 rows
-            return launch_tiled<FMT, 16, 2, 1, 4, 12, 1>(ops, n, s);
         // 4 rows per workgroup: deriving digit planes of 8192 values would
-        // cost more than the integer products save
+        // cost more than the integer products save (weights from HBM, 3072
+        // rows: Q4_K 5.53 us against 5.64 with planes and 12 rows per
+        // workgroup; Q4_0 5.52 against 5.61; RWKV-7's Q8_0 2048 rows 5.46
+        // against 5.50)
         return launch_tiled<FMT, 16, 1, 1, 8, 8>(ops, n, s);
     default: return hipErrorNotSupported;
     }
