@@ -113,11 +113,17 @@ int si_hip_init(int device, si_hip_context** out)
         delete ctx;
         return hip_fail(nullptr, e, "hipGetSymbolAddress (attention scratch)");
     }
+    // the prefill's split-K partial sums (its small grids run unsplit without it)
+    if (hipMalloc(&ctx->prefill_split, si::PREFILL_SPLIT_BYTES) != hipSuccess) {
+        (void)hipGetLastError();
+        ctx->prefill_split = nullptr;
+    }
     if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&ctx->t0)) != hipSuccess || (e = hipEventCreate(&ctx->t1)) != hipSuccess) {
         hip_fail(nullptr, e, "init");
         if (ctx->t0) (void)hipEventDestroy(ctx->t0);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+        if (ctx->prefill_split) (void)hipFree(ctx->prefill_split);
         delete ctx;
         return SI_HIP_ERR_DEVICE;
     }
@@ -140,6 +146,8 @@ int si_hip_destroy(si_hip_context* ctx)
         (void)hipEventDestroy(ctx->t0);
         (void)hipEventDestroy(ctx->t1);
         (void)hipStreamDestroy(ctx->stream);
+        if (ctx->prefill_split)
+            (void)hipFree(ctx->prefill_split);
     }
     delete ctx;
     return SI_HIP_OK;
@@ -342,7 +350,7 @@ int si_hip_gemm_prefill(si_hip_context* ctx, int format, const void* w, const vo
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "gemm_prefill: output overlaps an input");
     if (wbytes > UINT32_MAX || xbytes > UINT32_MAX)
         return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "gemm_prefill: W and X must each be smaller than 4 GiB");
-    const hipError_t e = si::launch_prefill(format, w, x_bf16, y, m, rows, cols, ctx->stream);
+    const hipError_t e = si::launch_prefill(format, w, x_bf16, y, m, rows, cols, ctx->stream, ctx->prefill_split);
     return e == hipSuccess ? SI_HIP_OK : hip_fail(ctx, e, "gemm_prefill launch");
 }
 

@@ -18,6 +18,7 @@ struct si_hip_context {
     bool timer_open = false;
     bool recording = false;
     float* attention_scratch = nullptr;   // device address of the library's attention scratch on `device`
+    void* prefill_split = nullptr;        // si::PREFILL_SPLIT_BYTES for the prefill's split-K partial sums (or null)
     std::string error;
     std::recursive_mutex gate;
 };

@@ -98,8 +98,12 @@ hipError_t launch_gemv_ops(const GemvOp* ops, int count, hipStream_t stream, int
 hipError_t launch_gemv(int fmt, const void* w, const float* x, float* y, int64_t rows, int64_t cols,
                        const float* residual, hipStream_t stream, int* path);
 bool gemv_tiled_cols(int64_t cols);
+// `split` (optional, PREFILL_SPLIT_BYTES, 16-byte aligned) holds the split-K
+// partial sums of the grids that use it; without it those grids take the
+// unsplit kernels.  Launches sharing one split buffer must be ordered.
+constexpr int64_t PREFILL_SPLIT_BYTES = 32ll << 20;
 hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, int64_t m, int64_t rows,
-                          int64_t cols, hipStream_t stream);
+                          int64_t cols, hipStream_t stream, void* split = nullptr);
 hipError_t launch_dequant(int fmt, const void* w, float* out, int64_t rows, int64_t cols,
                           hipStream_t stream);
 hipError_t launch_fill_u32(void* dst, uint32_t value, uint64_t count, hipStream_t stream);

@@ -38,6 +38,8 @@
 // is C[8*(r/4) + 4*(l/32) + r%4][l % 32].
 #include "si_internal.hpp"
 
+#include <algorithm>
+
 #include <hip/hip_fp16.h>
 
 namespace si {
@@ -547,11 +549,18 @@ __global__ __launch_bounds__(PF_THREADS * KS) void prefill_mfma_kernel(const uin
 // wave's matrix-core work and another wave's decode at the same time.  One
 // barrier per step; the same exact W decode and swizzled layouts as the
 // kernel above.
+//
+// Split K (splits > 1, for grids with fewer tiles than CUs): workgroup z
+// takes a contiguous range of the steps and stores its FP32 tile to `part`
+// (the tile's slot of split z); prefill_reduce_kernel then adds each
+// output's partial sums in split order 0, 1, ... (a fixed order, so results
+// are reproducible run to run) and writes Y.
 template <int FMT, int MW, int NT, int D>
 __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_t* __restrict__ W,
                                                                     const __bf16* __restrict__ X,
                                                                     float* __restrict__ Y, int M, int N, int K,
-                                                                    int64_t row_bytes)
+                                                                    int64_t row_bytes, int splits,
+                                                                    float4* __restrict__ part)
 {
     constexpr int MT = MW / 32;
     constexpr int NROWS = 32 * NT;
@@ -575,7 +584,14 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
     const int mw0 = blockIdx.y * TROWS;
     const int g = lane >> 5, li = lane & 31;
     const int nblk = K / 32;
-    const int nsteps = (nblk + BPS - 1) / BPS;
+    // this workgroup's steps: [s0, s0 + nsteps) of the K range (the
+    // launcher keeps every split non-empty)
+    const int steps_all = (nblk + BPS - 1) / BPS;
+    const int per = (steps_all + splits - 1) / splits;
+    const int s0 = static_cast<int>(blockIdx.z) * per;
+    const int nsteps = min(per, steps_all - s0);
+    constexpr int TILE4 = PF_THREADS * MT * NT * 4;       // float4 values of a tile's FP32 sums
+    const int tile = blockIdx.x + gridDim.x * blockIdx.y;
 
     if (consumer) {
         f32x16 acc[MT][NT];
@@ -587,7 +603,7 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
         auto mfma_step = [&](int step, int buf, bool guarded) {
 #pragma unroll
             for (int bo = 0; bo < BPS; bo++) {
-                if (!guarded || BPS * step + bo < nblk) {
+                if (!guarded || BPS * (s0 + step) + bo < nblk) {
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
                         const int c = 4 * bo + 2 * h + g;
@@ -627,17 +643,33 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
                 __syncthreads();
             }
         }
-        const int m0 = mw0 + wave * MW;
+        if (splits > 1) {
+            // this split's sums: float4 j * 256 + t holds registers 4 (j % 4) ..
+            // of accumulator tile j / 4 = mt * NT + nt of thread t
+            float4* dst = part + (static_cast<int64_t>(tile) * splits + blockIdx.z) * TILE4;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
+            for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const int n = n0 + 32 * nt + li;
+                for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int m = m0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (m < M && n < N)
-                        Y[static_cast<int64_t>(m) * N + n] = acc[mt][nt][r];
+                    for (int r4 = 0; r4 < 4; r4++) {
+                        const f32x16& a = acc[mt][nt];
+                        dst[((mt * NT + nt) * 4 + r4) * PF_THREADS + t] =
+                            make_float4(a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]);
+                    }
+        } else {
+            const int m0 = mw0 + wave * MW;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const int n = n0 + 32 * nt + li;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = m0 + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3);
+                        if (m < M && n < N)
+                            Y[static_cast<int64_t>(m) * N + n] = acc[mt][nt][r];
+                    }
                 }
             }
         }
@@ -663,17 +695,17 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
         RawW<FMT> raw[D][WI];
         u32x4 xr[D][XL];
         auto load_step = [&](int step, RawW<FMT> (&wdst)[WI], u32x4 (&xdst_regs)[XL]) {
-            const int blk = min(BPS * step + wbo, nblk - 1);
+            const int blk = min(BPS * (s0 + step) + wbo, nblk - 1);
 #pragma unroll
             for (int i = 0; i < WI; i++)
                 wdst[i] = load_raw<FMT>(W, wrow[i], blk, wh);
-            const int col = min(BPS * 32 * step + xcol, K - 8);
+            const int col = min(BPS * 32 * (s0 + step) + xcol, K - 8);
 #pragma unroll
             for (int e = 0; e < XL; e++)
                 xdst_regs[e] = *reinterpret_cast<const u32x4*>(xbytes + (xoff[e] + static_cast<uint32_t>(2 * col)));
         };
         auto store_step = [&](int step, const RawW<FMT> (&wsrc)[WI], const u32x4 (&xsrc_regs)[XL], int buf) {
-            const int blk = min(BPS * step + wbo, nblk - 1);
+            const int blk = min(BPS * (s0 + step) + wbo, nblk - 1);
 #pragma unroll
             for (int i = 0; i < WI; i++) {
                 bf16x8 v0, v1;
@@ -715,6 +747,41 @@ __global__ __launch_bounds__(2 * PF_THREADS) void prefill_ws_kernel(const uint8_
                 __syncthreads();
             }
         }
+    }
+}
+
+// Sums the split-K partials of prefill_ws_kernel in split order and writes
+// Y: thread i of the grid takes float4 i % TILE4 of tile i / TILE4 (the
+// layout the kernel's consumer threads store).
+template <int MW, int NT>
+__global__ __launch_bounds__(PF_THREADS) void prefill_reduce_kernel(const float4* __restrict__ part,
+                                                                    float* __restrict__ Y, int M, int N, int splits,
+                                                                    int tiles_n)
+{
+    constexpr int MT = MW / 32;
+    constexpr int TILE4 = PF_THREADS * MT * NT * 4;
+    const int64_t gi = static_cast<int64_t>(blockIdx.x) * PF_THREADS + threadIdx.x;
+    const int tile = static_cast<int>(gi / TILE4), i = static_cast<int>(gi % TILE4);
+    const float4* src = part + static_cast<int64_t>(tile) * splits * TILE4 + i;
+    float4 v = src[0];
+    for (int q = 1; q < splits; q++) {
+        const float4 w = src[static_cast<int64_t>(q) * TILE4];
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+    }
+    // float4 i = registers 4 r4 .. of accumulator tile (mt, nt) of consumer thread ct
+    const int ct = i % PF_THREADS, j = i / PF_THREADS;
+    const int r4 = j & 3, tnt = (j >> 2) % NT, tmt = (j >> 2) / NT;
+    const int cw = ct >> 6, cl = ct & 63;
+    const int n = (tile % tiles_n) * 32 * NT + 32 * tnt + (cl & 31);
+    const int m = (tile / tiles_n) * 4 * MW + cw * MW + 32 * tmt + 8 * r4 + 4 * (cl >> 5);
+    if (n < N) {
+        if (m < M) Y[static_cast<int64_t>(m) * N + n] = v.x;
+        if (m + 1 < M) Y[static_cast<int64_t>(m + 1) * N + n] = v.y;
+        if (m + 2 < M) Y[static_cast<int64_t>(m + 2) * N + n] = v.z;
+        if (m + 3 < M) Y[static_cast<int64_t>(m + 3) * N + n] = v.w;
     }
 }
 
@@ -939,21 +1006,51 @@ hipError_t launch_prefill_shape(const void* w, const void* x, float* y, int64_t 
     return hipGetLastError();
 }
 
+// splits > 1 needs `part` for tiles x splits x the tile's FP32 sums
+// (prefill_part_bytes) and runs the reduction as a second launch.
+template <int MW, int NT>
+constexpr int64_t prefill_tile_bytes() { return static_cast<int64_t>(PF_THREADS) * (MW / 32) * NT * 4 * 16; }
+
 template <int FMT, int MW, int NT, int D = PF_DEPTH>
-hipError_t launch_prefill_ws(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
+hipError_t launch_prefill_ws(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s,
+                             int splits = 1, float4* part = nullptr)
 {
     const int64_t rb = row_bytes(FMT, k);
-    const dim3 grid(static_cast<unsigned>((n + 32 * NT - 1) / (32 * NT)), static_cast<unsigned>((m + 4 * MW - 1) / (4 * MW)));
-    hipLaunchKernelGGL((prefill_ws_kernel<FMT, MW, NT, D>), grid, dim3(2 * PF_THREADS), 0, s,
-                       static_cast<const uint8_t*>(w), static_cast<const __bf16*>(x), y, static_cast<int>(m),
-                       static_cast<int>(n), static_cast<int>(k), rb);
+    const unsigned tn = static_cast<unsigned>((n + 32 * NT - 1) / (32 * NT)), tm = static_cast<unsigned>((m + 4 * MW - 1) / (4 * MW));
+    hipLaunchKernelGGL((prefill_ws_kernel<FMT, MW, NT, D>), dim3(tn, tm, static_cast<unsigned>(splits)),
+                       dim3(2 * PF_THREADS), 0, s, static_cast<const uint8_t*>(w), static_cast<const __bf16*>(x), y,
+                       static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), rb, splits, part);
+    if (splits > 1) {
+        constexpr int64_t TILE4 = prefill_tile_bytes<MW, NT>() / 16;
+        const int64_t threads = static_cast<int64_t>(tn) * tm * TILE4;
+        hipLaunchKernelGGL((prefill_reduce_kernel<MW, NT>), dim3(static_cast<unsigned>(threads / PF_THREADS)),
+                           dim3(PF_THREADS), 0, s, part, y, static_cast<int>(m), static_cast<int>(n), splits,
+                           static_cast<int>(tn));
+    }
     return hipGetLastError();
+}
+
+// Split count for the warp-specialised kernel on a grid of `tiles` tiles
+// and `steps` 64-column steps: about one workgroup per CU, at least
+// `min_steps` steps a split, every split non-empty.
+inline int prefill_splits(int64_t tiles, int64_t steps, int cus, int min_steps)
+{
+    int64_t want = std::min<int64_t>(cus / std::max<int64_t>(tiles, 1), steps / min_steps);
+    if (want < 2)
+        return 1;
+    const int64_t per = (steps + want - 1) / want;
+    return static_cast<int>((steps + per - 1) / per);
 }
 
 // Tile choice (measured on the Phi-4-mini projections at 512 tokens):
 //   * grids of more than 256 workgroups of 256 tokens x 64 rows: the
 //     warp-specialised kernel with 256 x 128 tiles (64 x 128 consumer wave
 //     tiles; gate_up 76 -> 67 us);
+//   * with a split buffer, K split over about one workgroup per CU of the
+//     same 256 x 128 tiles (at least 16 steps a split) when the 256 x 64
+//     grid has 128..256 workgroups or K >= 4096: qkv 42.0 -> 37.2 us (3
+//     splits), down 65.5 -> 50.0 us (5 splits); o_proj (3072 columns, 96
+//     workgroups of 256 x 64) stays on the 16 x 16 form (26.4 against 28.2);
 //   * 256 tokens x 64 rows (64 x 64 wave tiles, each fragment used twice)
 //     when that grid has at least 128 workgroups: up to one per
 //     CU two step groups of 4 waves with compact tiles (160 KiB, two waves
@@ -966,13 +1063,23 @@ hipError_t launch_prefill_ws(const void* w, const void* x, float* y, int64_t m, 
 //     groups of 4 waves when they divide evenly (two waves per SIMD
 //     overlap their phases).
 template <int FMT>
-hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s)
+hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m, int64_t n, int64_t k, hipStream_t s,
+                              void* split)
 {
     auto wgs = [&](int mt, int nt) { return ((n + nt - 1) / nt) * ((m + mt - 1) / mt); };
     const int64_t big = wgs(256, 64);
     const int64_t steps = (k / 32 + 1) / 2;
     if (big > NUM_CUS)
         return launch_prefill_ws<FMT, 64, 4>(w, x, y, m, n, k, s);
+    // split K: the 256 x 128 warp-specialised tiles over about one workgroup
+    // per CU, at least 16 steps a split, for grids whose alternatives leave
+    // CUs idle (the 256 x 64 tiles at 128..256 workgroups) or whose K is
+    // long (the partial sums cost M x N x 4 bytes per split twice)
+    const int64_t tiles = wgs(256, 128);
+    const int sp = prefill_splits(tiles, steps, NUM_CUS, 16);
+    if (split && sp > 1 && (big >= NUM_CUS / 2 || k >= 4096) &&
+        tiles * sp * prefill_tile_bytes<64, 4>() <= PREFILL_SPLIT_BYTES)
+        return launch_prefill_ws<FMT, 64, 4>(w, x, y, m, n, k, s, sp, static_cast<float4*>(split));
     if (big >= NUM_CUS / 2)
         return steps % 2 == 0 ? launch_prefill_shape<FMT, 64, 2, 2, true>(w, x, y, m, n, k, s)
                               : launch_prefill_shape<FMT, 64, 2, 1, false>(w, x, y, m, n, k, s);
@@ -987,15 +1094,15 @@ hipError_t launch_prefill_fmt(const void* w, const void* x, float* y, int64_t m,
 }  // namespace
 
 hipError_t launch_prefill(int fmt, const void* w, const void* x_bf16, float* y, int64_t m, int64_t rows, int64_t cols,
-                          hipStream_t stream)
+                          hipStream_t stream, void* split)
 {
     switch (fmt) {
-    case FMT_Q8_0: return launch_prefill_fmt<FMT_Q8_0>(w, x_bf16, y, m, rows, cols, stream);
-    case FMT_Q4_0: return launch_prefill_fmt<FMT_Q4_0>(w, x_bf16, y, m, rows, cols, stream);
-    case FMT_Q4_K: return launch_prefill_fmt<FMT_Q4_K>(w, x_bf16, y, m, rows, cols, stream);
-    case FMT_F16: return cols % 32 == 0 ? launch_prefill_fmt<FMT_F16>(w, x_bf16, y, m, rows, cols, stream)
+    case FMT_Q8_0: return launch_prefill_fmt<FMT_Q8_0>(w, x_bf16, y, m, rows, cols, stream, split);
+    case FMT_Q4_0: return launch_prefill_fmt<FMT_Q4_0>(w, x_bf16, y, m, rows, cols, stream, split);
+    case FMT_Q4_K: return launch_prefill_fmt<FMT_Q4_K>(w, x_bf16, y, m, rows, cols, stream, split);
+    case FMT_F16: return cols % 32 == 0 ? launch_prefill_fmt<FMT_F16>(w, x_bf16, y, m, rows, cols, stream, split)
                                         : hipErrorInvalidValue;
-    case FMT_F32: return cols % 32 == 0 ? launch_prefill_fmt<FMT_F32>(w, x_bf16, y, m, rows, cols, stream)
+    case FMT_F32: return cols % 32 == 0 ? launch_prefill_fmt<FMT_F32>(w, x_bf16, y, m, rows, cols, stream, split)
                                         : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }

@@ -62,6 +62,13 @@ CASES += [(f, m, n, k) for f in (native.Q8_0, native.Q4_0)
 CASES += [(f, 256, 3000, 256) for f in FORMATS]
 CASES += [(f, m, n, k) for f in (native.Q8_0, native.Q4_0)
           for (m, n, k) in [(512, 3072, 256), (500, 3000, 512), (200, 6000, 768)]]
+# K split over the 256 x 128 warp-specialised tiles with a reduction launch:
+# K >= 4096 with a partial last step (129 blocks) and token / row tails; a
+# 3072-column grid of 128..256 workgroups of 256 x 64 (3 splits) with tails;
+# Q4_K at 17 super-blocks a row
+SPLIT = [(native.Q8_0, 300, 5000, 4128), (native.Q4_0, 300, 5000, 4128), (native.Q4_0, 500, 5000, 3072),
+         (native.Q4_K, 100, 1000, 4352)]
+CASES += SPLIT
 
 
 @pytest.mark.parametrize("fmt,m,rows,cols", CASES, ids=[f"{NAMES[f]}-m{m}-{n}x{k}" for f, m, n, k in CASES])
@@ -97,6 +104,23 @@ def test_prefill_512_tokens_at_layer_shapes(hip, name, rows, cols):
     sample = np.linspace(0, m - 1, 24).astype(int)
     xs = np.ascontiguousarray(x.reshape(m, cols)[sample])
     check(y[sample], orc.gemm_prefill_f64(native.Q4_0, w, xs, len(sample), rows, cols), 2e-2, name + " oracle rows")
+
+
+@pytest.mark.parametrize("rows,cols", [(5120, 3072), (3072, 8192)], ids=["qkv", "down"])
+def test_split_k_prefill_is_reproducible(hip, rows, cols):
+    """The split-K grids (qkv: 3 splits, down: 5) add their partial sums in
+    a fixed split order: two launches give bitwise the same Y."""
+    m = 512
+    dw = hip.to_device(orc.gen_quant(native.Q4_0, 11 + rows, rows, cols))
+    dx = hip.to_device(orc.gen_normal_bf16(12 + cols, m * cols))
+    dy = hip.alloc(m * rows * 4)
+    outs = []
+    for _ in range(2):
+        hip.gemm_prefill(native.Q4_0, dw.ptr, dx.ptr, dy.ptr, m, rows, cols)
+        outs.append(dy.readback(np.uint32, m * rows))
+    assert np.array_equal(outs[0], outs[1])
+    for b in (dw, dx, dy):
+        b.free()
 
 
 def test_prefill_rejects_bad_requests(hip):
