@@ -445,12 +445,14 @@ def bench_prefill(hip, rng, m: int = 512):
     MFMA_BF16_PEAK_TFLOPS = 2500.0
     out = {"tokens": m, "shapes": {}}
     total_flops, total_us = 0.0, 0.0
+    bufs = []
     for name, rows, cols in LAYER_Q4_0:
         w = hip.to_device(synth_weights(native.Q4_0, rows, cols, rng))
         xb = rng.standard_normal(m * cols).astype(np.float32).view(np.uint32)
         xb = ((xb + 0x7FFF + ((xb >> 16) & 1)) >> 16).astype(np.uint16)
         x = hip.to_device(xb)
         y = hip.alloc(m * rows * 4)
+        bufs.append((w, x, y, rows, cols))
         plan = hip.record(lambda: hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols))
         plan.measure_us(2)
         us = sorted(plan.measure_us(8) for _ in range(5))[2]
@@ -460,11 +462,25 @@ def bench_prefill(hip, rng, m: int = 512):
         out["shapes"][name] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1)}
         log(f"  prefill {name:8s} m={m} {rows}x{cols}: {us:.1f} us, {flops / us / 1e6:.1f} TFLOP/s")
         plan.destroy()
-        for b in (w, x, y):
-            b.free()
     tflops = total_flops / total_us / 1e6
     out.update({"us_total": round(total_us, 1), "TFLOPs": round(tflops, 1),
                 "mfma_bf16_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)})
+
+    # the same four products recorded as one plan, a layer's submission
+    # (no gap between separate plan launches inside it)
+    def layer():
+        for w, x, y, rows, cols in bufs:
+            hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols)
+    plan = hip.record(layer)
+    plan.measure_us(2)
+    layer_us = sorted(plan.measure_us(8) for _ in range(5))[2]
+    plan.destroy()
+    for w, x, y, _, _ in bufs:
+        for b in (w, x, y):
+            b.free()
+    out["layer_plan"] = {"us": round(layer_us, 1), "TFLOPs": round(total_flops / layer_us / 1e6, 1),
+                         "form": "the four products in one recorded plan, replayed 8 times back to back"}
+    log(f"  prefill layer plan m={m}: {layer_us:.1f} us, {total_flops / layer_us / 1e6:.1f} TFLOP/s")
     return out
 
 
