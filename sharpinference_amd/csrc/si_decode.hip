@@ -15,6 +15,7 @@
 // rounded values back.
 #include "si_internal.hpp"
 #include "si_decode.hpp"
+#include "si_rows.hpp"
 #include "si_lanes.hpp"
 
 #include <hip/hip_fp16.h>
@@ -56,43 +57,8 @@ __global__ __launch_bounds__(256) void gather_row_kernel(const uint8_t* __restri
     const int row = *index;
     const bool valid = row >= 0 && row < rows;
     const uint8_t* rp = table + static_cast<int64_t>(valid ? row : 0) * row_bytes;
-    constexpr int BE = block_elems(FMT), BB = block_bytes(FMT);
-    for (int c = blockIdx.x * 256 + threadIdx.x; c < cols; c += gridDim.x * 256) {
-        float v;
-        if (!valid) {
-            v = __int_as_float(0x7fc00000);
-        } else {
-            const uint8_t* b = rp + (c / BE) * BB;
-            const int e = c % BE;
-            if constexpr (FMT == FMT_F16) {
-                v = ld_half_u(b);
-            } else if constexpr (FMT == FMT_F32) {
-                v = __uint_as_float(static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8) |
-                                    (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24));
-            } else if constexpr (FMT == FMT_Q8_0) {
-                v = __fmul_rn(ld_half_u(b), static_cast<float>(static_cast<int8_t>(b[2 + e])));
-            } else if constexpr (FMT == FMT_Q4_0) {
-                const int q = e < 16 ? (b[2 + e] & 15) : (b[2 + e - 16] >> 4);
-                v = __fmul_rn(ld_half_u(b), static_cast<float>(q - 8));
-            } else {
-                const int j = e / 32, l = e % 32;
-                const uint8_t* s = b + 4;
-                int sc, m;
-                if (j < 4) {
-                    sc = s[j] & 63;
-                    m = s[j + 4] & 63;
-                } else {
-                    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
-                    m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-                }
-                const float d1 = __fmul_rn(ld_half_u(b), static_cast<float>(sc));
-                const float m1 = __fmul_rn(ld_half_u(b + 2), static_cast<float>(m));
-                const int q = (b[16 + 32 * (j >> 1) + l] >> (4 * (j & 1))) & 15;
-                v = __fsub_rn(__fmul_rn(d1, static_cast<float>(q)), m1);
-            }
-        }
-        out[c] = v;
-    }
+    for (int c = blockIdx.x * 256 + threadIdx.x; c < cols; c += gridDim.x * 256)
+        out[c] = valid ? row_value<FMT>(rp, c) : __int_as_float(0x7fc00000);
 }
 
 // ---- attention ------------------------------------------------------------------

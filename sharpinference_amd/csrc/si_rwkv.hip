@@ -12,6 +12,7 @@
 #include "si_rwkv.hpp"
 #include "si_internal.hpp"
 #include "si_planes.hpp"
+#include "si_rows.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -387,17 +388,33 @@ __device__ __forceinline__ float block_sum(float v, float* red)
     return s;
 }
 
+// LayerNorm of x, or (FMT >= 0) of row *index of a GGUF table (the
+// embedding gather of the same step; an index outside the table gives a
+// row of NaN, as the gather does).
+template <int FMT>
 __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(const float* __restrict__ x, const float* w,
-                                                                 const float* b, int n, float eps, float* out)
+                                                                 const float* b, int n, float eps, float* out,
+                                                                 const uint8_t* __restrict__ table, int rows,
+                                                                 int64_t row_bytes, const int32_t* __restrict__ index)
 {
     constexpr int PER = LN_MAX / LN_THREADS;
     __shared__ float red1[LN_THREADS / 64], red2[LN_THREADS / 64];
     float v[PER];
     float s1 = 0.0f;
+    const uint8_t* rp = nullptr;
+    bool valid = true;
+    if constexpr (FMT >= 0) {
+        const int row = *index;
+        valid = row >= 0 && row < rows;
+        rp = table + static_cast<int64_t>(valid ? row : 0) * row_bytes;
+    }
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int e = threadIdx.x + k * LN_THREADS;
-        v[k] = e < n ? x[e] : 0.0f;
+        if constexpr (FMT >= 0)
+            v[k] = e < n ? (valid ? row_value<FMT>(rp, e) : __int_as_float(0x7fc00000)) : 0.0f;
+        else
+            v[k] = e < n ? x[e] : 0.0f;
         s1 += v[k];
     }
     const float mean = block_sum(s1, red1) / static_cast<float>(n);
@@ -475,7 +492,27 @@ hipError_t launch_layernorm(const float* x, const float* w, const float* b, int 
 {
     if (n <= 0 || n > LN_MAX)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(layernorm_kernel, dim3(1), dim3(LN_THREADS), 0, s, x, w, b, n, eps, out);
+    hipLaunchKernelGGL((layernorm_kernel<-1>), dim3(1), dim3(LN_THREADS), 0, s, x, w, b, n, eps, out, nullptr, 0,
+                       int64_t{0}, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_layernorm(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index,
+                                   const float* w, const float* b, float eps, float* out, hipStream_t s)
+{
+    const int64_t rb = row_bytes(fmt, cols);
+    if (cols <= 0 || cols > LN_MAX || rb < 0 || rows <= 0 || rows > INT32_MAX)
+        return hipErrorInvalidValue;
+    const uint8_t* t = static_cast<const uint8_t*>(table);
+    const int n = static_cast<int>(cols), r = static_cast<int>(rows);
+    switch (fmt) {
+    case FMT_Q8_0: hipLaunchKernelGGL((layernorm_kernel<FMT_Q8_0>), dim3(1), dim3(LN_THREADS), 0, s, nullptr, w, b, n, eps, out, t, r, rb, index); break;
+    case FMT_Q4_0: hipLaunchKernelGGL((layernorm_kernel<FMT_Q4_0>), dim3(1), dim3(LN_THREADS), 0, s, nullptr, w, b, n, eps, out, t, r, rb, index); break;
+    case FMT_Q4_K: hipLaunchKernelGGL((layernorm_kernel<FMT_Q4_K>), dim3(1), dim3(LN_THREADS), 0, s, nullptr, w, b, n, eps, out, t, r, rb, index); break;
+    case FMT_F16: hipLaunchKernelGGL((layernorm_kernel<FMT_F16>), dim3(1), dim3(LN_THREADS), 0, s, nullptr, w, b, n, eps, out, t, r, rb, index); break;
+    case FMT_F32: hipLaunchKernelGGL((layernorm_kernel<FMT_F32>), dim3(1), dim3(LN_THREADS), 0, s, nullptr, w, b, n, eps, out, t, r, rb, index); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -65,6 +65,10 @@ hipError_t launch_rwkv_wkv(const WkvArgs& a, hipStream_t s);
 // one workgroup.
 hipError_t launch_layernorm(const float* x, const float* w, const float* b, int n, float eps, float* out,
                             hipStream_t s);
+// The same LayerNorm over row *index of a GGUF table [rows, cols] (the
+// embedding gather fused in; an index outside the table gives NaN).
+hipError_t launch_gather_layernorm(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index,
+                                   const float* w, const float* b, float eps, float* out, hipStream_t s);
 // out[b][r] = sum_c m[b][r][c] * v[b][c] in FP32 (core.tensor.batched-mat-vec).
 hipError_t launch_batched_matvec(const float* m, const float* v, float* out, int batch, int rows, int cols,
                                  hipStream_t s);

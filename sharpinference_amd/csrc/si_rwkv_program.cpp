@@ -129,10 +129,9 @@ hipError_t rwkv7_step(si_hip_context* ctx, const si_hip_rwkv7_model* m)
     const RwkvScratch o = rwkv_scratch(m);
     float* ws = static_cast<float*>(m->workspace);
     float* x = m->hidden_state;
-    // x = ln0(emb[token]) (:191-193)
-    hipError_t e = si::launch_gather_row(m->embed_format, m->embed, m->vocab, D, m->control, ws + o.emb, s);
-    if (e == hipSuccess)
-        e = si::launch_layernorm(ws + o.emb, m->ln0_weight, m->ln0_bias, D, LN_EPS, x, s);
+    // x = ln0(emb[token]) (:191-193), the gather inside the LayerNorm launch
+    hipError_t e = si::launch_gather_layernorm(m->embed_format, m->embed, m->vocab, D, m->control, m->ln0_weight,
+                                               m->ln0_bias, LN_EPS, x, s);
     for (int l = 0; e == hipSuccess && l < m->layers; l++) {
         const si_hip_rwkv7_layer& L = m->layer[l];
         // 1. time-mix projections on mix(LayerNorm(x), att_prev, x_rwkvag row t)
