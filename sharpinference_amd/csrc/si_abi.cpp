@@ -60,10 +60,14 @@ int check_matrix(si_hip_context* ctx, const char* op, int fmt, const void* w, in
     if (rows <= 0 || rows > INT32_MAX)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: rows %lld out of range 1..%d", op, static_cast<long long>(rows),
                     INT32_MAX);
+    if (cols > INT32_MAX)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: columns %lld out of range 1..%d", op, static_cast<long long>(cols),
+                    INT32_MAX);
     const int64_t rb = si::row_bytes(fmt, cols);
     if (rb < 0)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: %lld columns is not a whole number of %d-element %s blocks", op,
                     static_cast<long long>(cols), si::block_elems(fmt), fmt_name(fmt));
+    // (rows and columns below 2^31 keep the byte count below 2^64)
     if (!w)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "%s: null weight pointer", op);
     *wbytes = static_cast<uint64_t>(rb) * static_cast<uint64_t>(rows);

@@ -14,6 +14,10 @@ namespace {
 
 bool misaligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) != 0; }
 
+// Largest element count of one operand (2^40 FP32 values = 4 TiB): byte
+// counts and the kernels' 64-bit indices stay far from overflow.
+constexpr int64_t MAX_ELEMENTS = int64_t{1} << 40;
+
 // Dimensions of a rank 1..4 tensor, each >= 1; element count into *count.
 bool dims_ok(int rank, const int64_t* dims, int64_t* count)
 {
@@ -21,7 +25,7 @@ bool dims_ok(int rank, const int64_t* dims, int64_t* count)
         return false;
     int64_t n = 1;
     for (int a = 0; a < rank; a++) {
-        if (dims[a] < 1 || dims[a] > (int64_t{1} << 40) / n)
+        if (dims[a] < 1 || dims[a] > MAX_ELEMENTS / n)
             return false;
         n *= dims[a];
     }
@@ -44,8 +48,8 @@ int si_hip_t0_elementwise(si_hip_context* ctx, int op, const float* left, const 
     if (op < 0 || op >= si::T0_OP_COUNT)
         return fail(ctx, SI_HIP_ERR_UNSUPPORTED, "t0_elementwise: unknown operator %d", op);
     const bool binary = si::t0_binary(op);
-    if (!left || !output || (binary && !right) || count < 1)
-        return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_elementwise: null operand or empty tensor");
+    if (!left || !output || (binary && !right) || count < 1 || count > MAX_ELEMENTS)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_elementwise: null operand, empty tensor or more than 2^40 elements");
     if (misaligned4(left) || misaligned4(output) || (binary && misaligned4(right)))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_elementwise: FP32 operands must be 4-byte aligned");
     const uint64_t bytes = static_cast<uint64_t>(count) * 4;
@@ -62,8 +66,8 @@ int si_hip_t0_cast_f16_f32(si_hip_context* ctx, const void* input, float* output
     Enter g(ctx);
     if (g.err != hipSuccess)
         return hip_fail(ctx, g.err, "hipSetDevice");
-    if (!input || !output || count < 1)
-        return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_cast: null operand or empty tensor");
+    if (!input || !output || count < 1 || count > MAX_ELEMENTS)
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_cast: null operand, empty tensor or more than 2^40 elements");
     if ((reinterpret_cast<uintptr_t>(input) & 1u) || misaligned4(output))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_cast: misaligned operand");
     if (overlaps(output, static_cast<uint64_t>(count) * 4, input, static_cast<uint64_t>(count) * 2))
@@ -79,8 +83,8 @@ int si_hip_t0_fill(si_hip_context* ctx, float value, float* output, int64_t coun
     Enter g(ctx);
     if (g.err != hipSuccess)
         return hip_fail(ctx, g.err, "hipSetDevice");
-    if (!output || count < 1 || misaligned4(output))
-        return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_fill: null, empty or misaligned output");
+    if (!output || count < 1 || count > MAX_ELEMENTS || misaligned4(output))
+        return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_fill: null, empty, misaligned or larger than 2^40 elements output");
     // TensorFillValue: non-finite values are not supported (PortableTensorOperationContracts.cs:16-20)
     if (!std::isfinite(value))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_fill: the value must be finite");
@@ -96,7 +100,8 @@ int si_hip_t0_reduce_last(si_hip_context* ctx, int mean, const float* input, flo
     Enter g(ctx);
     if (g.err != hipSuccess)
         return hip_fail(ctx, g.err, "hipSetDevice");
-    if (!input || !output || rows < 1 || cols < 1 || rows > INT32_MAX || cols > INT32_MAX)
+    if (!input || !output || rows < 1 || cols < 1 || rows > INT32_MAX || cols > INT32_MAX ||
+        rows > MAX_ELEMENTS / cols)
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_reduce: null operand or shape out of range");
     if (misaligned4(input) || misaligned4(output))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_reduce: FP32 operands must be 4-byte aligned");
@@ -188,7 +193,7 @@ int si_hip_t0_head_outer(si_hip_context* ctx, const float* left, const float* ri
     if (g.err != hipSuccess)
         return hip_fail(ctx, g.err, "hipSetDevice");
     if (!left || !right || !output || heads < 1 || rows < 1 || cols < 1 || heads > INT32_MAX ||
-        rows > INT32_MAX || cols > INT32_MAX)
+        rows > INT32_MAX || cols > INT32_MAX || rows > MAX_ELEMENTS / cols || heads > MAX_ELEMENTS / (rows * cols))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_head_outer: null operand or shape out of range");
     if (misaligned4(left) || misaligned4(right) || misaligned4(output))
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "t0_head_outer: FP32 operands must be 4-byte aligned");

@@ -384,6 +384,9 @@ def test_invalid_requests_are_rejected_without_fallback(hip):
     assert status(lambda: hip.gemv(native.Q8_0, w.ptr, x.ptr + 2, y.ptr, 4, 32)) == native.ERR_ARGUMENT  # misaligned x
     assert status(lambda: hip.dequant(native.Q4_0, w.ptr, w.ptr, 2, 32)) == native.ERR_ARGUMENT
     assert "overlaps" in native.lib().si_hip_last_error(hip.handle).decode()
+    # column counts of 2^31 and more are rejected before any launch (byte counts stay below 2^64)
+    assert status(lambda: hip.gemv(native.F32, w.ptr, x.ptr, y.ptr, 4, 2 ** 40)) == native.ERR_ARGUMENT
+    assert status(lambda: hip.dequant(native.Q8_0, w.ptr, y.ptr, 4, 2 ** 36)) == native.ERR_ARGUMENT
     for b in (w, x, y):
         b.free()
 

@@ -176,6 +176,12 @@ def test_operators_reject_bad_arguments(hip):
     assert status(lambda: hip.t0_slice(p, [4, 5], 2, 0, 1, p + 2048)) == native.ERR_ARGUMENT
     assert status(lambda: hip.t0_reduce_last(True, p, p + 4, 4, 4)) == native.ERR_ARGUMENT
     assert status(lambda: hip.t0_head_outer(p, p + 256, p + 16, 2, 4, 4)) == native.ERR_ARGUMENT
+    # element counts past 2^40 (byte counts would wrap 64 bits for the largest) are rejected before any launch
+    big = 2 ** 31 - 1
+    assert status(lambda: hip.t0_head_outer(p, p + 256, p + 2048, big, big, big)) == native.ERR_ARGUMENT
+    assert status(lambda: hip.t0_elementwise("exp", p, 0, p + 2048, 2 ** 41)) == native.ERR_ARGUMENT
+    assert status(lambda: hip.t0_fill(1.0, p, 2 ** 41)) == native.ERR_ARGUMENT
+    assert status(lambda: hip.t0_reduce_last(False, p, p + 2048, big, big)) == native.ERR_ARGUMENT
     with pytest.raises(native.HipError) as e:
         lib = native.lib()
         hip._call(lib.si_hip_t0_elementwise, 99, native._p(p), native._p(p), native._p(p + 2048), 4)
