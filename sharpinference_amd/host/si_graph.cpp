@@ -1165,17 +1165,29 @@ HipVmOptimizationResult OptimizeWithReport(const LogicalGraph& graph, const HipV
     return result;
 }
 
-std::string OptimizationReportJson(const HipVmOptimizationResult& r)
+std::string JsonString(const std::string& s)
 {
-    const auto str = [](const std::string& s) {
-        std::string o = "\"";
-        for (char c : s) {
-            if (c == '"' || c == '\\')
-                o += '\\';
+    std::string o = "\"";
+    for (char c : s) {
+        const unsigned char u = static_cast<unsigned char>(c);
+        if (c == '"' || c == '\\') {
+            o += '\\';
+            o += c;
+        } else if (u < 0x20) {
+            static const char hex[] = "0123456789abcdef";
+            o += "\\u00";
+            o += hex[u >> 4];
+            o += hex[u & 15];
+        } else {
             o += c;
         }
-        return o + "\"";
-    };
+    }
+    return o + "\"";
+}
+
+std::string OptimizationReportJson(const HipVmOptimizationResult& r)
+{
+    const auto str = [](const std::string& s) { return JsonString(s); };
     std::ostringstream j;
     j << "{\"matvec\":{\"calls\":" << r.matvec.calls << ",\"cooperativeCalls\":" << r.matvec.cooperative_calls
       << ",\"diagnostics\":[";

@@ -233,5 +233,7 @@ HipVmOptimizationResult OptimizeWithReport(const LogicalGraph& graph, const HipV
 // removedNodes, localSlots, definitions and per node {node, operation,
 // definition, implementation, threads, groups, cooperative, diagnostic}.
 std::string OptimizationReportJson(const HipVmOptimizationResult& result);
+// A JSON string literal of `s` (quotes, backslashes and control characters escaped).
+std::string JsonString(const std::string& s);
 
 }  // namespace sharpinference

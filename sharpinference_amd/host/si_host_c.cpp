@@ -102,7 +102,7 @@ void CopyOut(const std::string& text, char* buffer, uint64_t capacity, uint64_t*
 
 std::string GraphJson(const LogicalGraph& g)
 {
-    const auto str = [](const std::string& s) { return "\"" + s + "\""; };
+    const auto str = [](const std::string& s) { return JsonString(s); };
     const auto list = [&](const std::vector<std::string>& v) {
         std::string o = "[";
         for (size_t i = 0; i < v.size(); i++)

@@ -1,5 +1,6 @@
 // VmProgram XML (VmProgramXml.cs) and the HIP program artifact
 // (D3D12VmArtifact.cs:90-148) for HipVmProgram.
+#include "si_graph.hpp"
 #include "si_host.hpp"
 
 #include <algorithm>
@@ -999,24 +1000,6 @@ std::map<std::string, std::string> ReadZip(const std::vector<uint8_t>& b)
 }
 
 // ---- the manifest's JSON: one flat object of string and integer members --------------------
-
-std::string JsonString(const std::string& v)
-{
-    std::string o = "\"";
-    for (const char c : v) {
-        if (c == '"' || c == '\\') {
-            o += '\\';
-            o += c;
-        } else if (static_cast<unsigned char>(c) < 0x20) {
-            char u[8];
-            std::snprintf(u, sizeof u, "\\u%04x", c);
-            o += u;
-        } else {
-            o += c;
-        }
-    }
-    return o + "\"";
-}
 
 std::map<std::string, std::string> JsonObject(const std::string& s)
 {
