@@ -744,8 +744,9 @@ int si_hip_plan_launch_sequence(si_hip_plan* const* plans, int nplans, int64_t s
 
 /* GPU microseconds per replay over `repetitions` back-to-back replays,
  * measured with events on the context stream; repetitions outside 1..1024
- * is ARGUMENT.  Replaces: D3D12VmExecutor.MeasureGpuMicroseconds
- * (D3D12VmExecutor.cs:452-478). */
+ * is ARGUMENT, and a call while the context's timer_begin is open is STATE
+ * (both use the same event pair).  Replaces:
+ * D3D12VmExecutor.MeasureGpuMicroseconds (D3D12VmExecutor.cs:452-478). */
 int si_hip_plan_measure_us(si_hip_plan* plan, int repetitions, double* microseconds);
 
 /* Event pair on the context stream: begin records the start event, end

@@ -485,6 +485,10 @@ int si_hip_plan_measure_us(si_hip_plan* plan, int repetitions, double* microseco
         return fail(ctx, SI_HIP_ERR_ARGUMENT, "plan_measure: repetitions %d outside 1..1024", repetitions);
     if (ctx->recording)
         return fail(ctx, SI_HIP_ERR_STATE, "plan_measure: not allowed while recording a plan");
+    // the measurement records the context's timer events: an open
+    // timer_begin would lose its start
+    if (ctx->timer_open)
+        return fail(ctx, SI_HIP_ERR_STATE, "plan_measure: not allowed while a timer_begin is open");
     hipError_t e = hipEventRecord(ctx->t0, ctx->stream);
     for (int i = 0; e == hipSuccess && i < repetitions; i++)
         e = hipGraphLaunch(plan->exec, ctx->stream);

@@ -346,6 +346,13 @@ def test_plan_measure_executes_exactly_the_requested_repetitions(hip):
     hip.launch_sequence([plan, plan], 5)
     hip.sync()
     assert np.all(y.readback(np.float32) == 14 * cols)
+    # the measurement and an open timer share the context's events: refused, and the timer still ends
+    hip.timer_begin()
+    with pytest.raises(native.HipError) as e:
+        plan.measure_us(2)
+    assert e.value.status == native.ERR_STATE
+    assert hip.timer_end() >= 0.0
+    assert np.all(y.readback(np.float32) == 14 * cols)
     plan.destroy()
     for b in (w, x, y):
         b.free()
