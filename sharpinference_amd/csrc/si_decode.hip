@@ -671,8 +671,8 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i)
 template <int CTRL>
 __device__ __forceinline__ void better_dpp(float& bv, int& bi)
 {
-    const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), CTRL, 0xF, 0xF, false));
-    const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xF, 0xF, false);
+    const float ov = dpp_row<CTRL>(bv);
+    const int oi = dpp_row<CTRL>(bi);
     better(bv, bi, ov, oi);
 }
 

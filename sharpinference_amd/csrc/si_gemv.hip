@@ -21,6 +21,7 @@
 // from LDS once and reused for RL rows.  All weight loads of a lane are
 // issued before x is staged into LDS, so HBM latency overlaps the staging.
 #include "si_internal.hpp"
+#include "si_lanes.hpp"
 #include "si_planes.hpp"
 
 #include <hip/hip_fp16.h>
@@ -80,13 +81,13 @@ template <int N>
 __device__ __forceinline__ float group_sum(float v)
 {
     if constexpr (N >= 2)
-        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+        v += dpp_row<0xB1>(v);   // quad_perm 1,0,3,2
     if constexpr (N >= 4)
-        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+        v += dpp_row<0x4E>(v);   // quad_perm 2,3,0,1
     if constexpr (N >= 8)
-        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+        v += dpp_row<0x141>(v);  // row_half_mirror
     if constexpr (N >= 16)
-        v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+        v += dpp_row<0x140>(v);  // row_mirror
     static_assert(N <= 16, "groups wider than a DPP row use shuffles");
     return v;
 }

@@ -5,14 +5,33 @@
 
 namespace si {
 
+// The value that DPP control CTRL reads for this lane.  Every control used
+// by these kernels (quad_perm, row_half_mirror, row_mirror) reads a lane of
+// the reading lane's own 16-lane row, so no lane is out of range and
+// bound_ctrl changes no result; it lets the compiler fold the move into the
+// consumer as a DPP source operand (one v_add_f32_dpp / v_max_f32_dpp
+// instead of a v_mov_b32_dpp and the operation).
+template <int CTRL>
+__device__ __forceinline__ int dpp_row(int v)
+{
+    static_assert(CTRL == 0xB1 || CTRL == 0x4E || CTRL == 0x141 || CTRL == 0x140,
+                  "controls whose source lane is always inside the row");
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v)
+{
+    return __int_as_float(dpp_row<CTRL>(__float_as_int(v)));
+}
+
 // Sum over aligned groups of N (<= 16) lanes with DPP.
 template <int N>
 __device__ __forceinline__ float row_sum(float v)
 {
-    if constexpr (N >= 2) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-    if constexpr (N >= 4) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-    if constexpr (N >= 8) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
-    if constexpr (N >= 16) v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+    if constexpr (N >= 2) v += dpp_row<0xB1>(v);
+    if constexpr (N >= 4) v += dpp_row<0x4E>(v);
+    if constexpr (N >= 8) v += dpp_row<0x141>(v);
+    if constexpr (N >= 16) v += dpp_row<0x140>(v);
     return v;
 }
 
@@ -20,10 +39,10 @@ __device__ __forceinline__ float row_sum(float v)
 template <int N>
 __device__ __forceinline__ float row_max(float v)
 {
-    if constexpr (N >= 2) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
-    if constexpr (N >= 4) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
-    if constexpr (N >= 8) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
-    if constexpr (N >= 16) v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
+    if constexpr (N >= 2) v = fmaxf(v, dpp_row<0xB1>(v));
+    if constexpr (N >= 4) v = fmaxf(v, dpp_row<0x4E>(v));
+    if constexpr (N >= 8) v = fmaxf(v, dpp_row<0x141>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_row<0x140>(v));
     return v;
 }
 

@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "si_lanes.hpp"
+
 namespace si {
 
 constexpr uint32_t PLANE_BIG_BITS = 0x71800000u;    // 2^100
@@ -26,15 +28,15 @@ constexpr uint32_t PLANE_TINY_BITS = 0x0D800000u;   // 2^-100
 // swaps inside quads, then the mirror of each 8-lane half row).
 __device__ __forceinline__ uint32_t group8_max_u32(uint32_t v)
 {
-    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, false)));
-    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, false)));
-    return max(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x141, 0xF, 0xF, false)));
+    v = max(v, static_cast<uint32_t>(dpp_row<0xB1>(static_cast<int>(v))));
+    v = max(v, static_cast<uint32_t>(dpp_row<0x4E>(static_cast<int>(v))));
+    return max(v, static_cast<uint32_t>(dpp_row<0x141>(static_cast<int>(v))));
 }
 __device__ __forceinline__ int group8_sum_i32(int v)
 {
-    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
-    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
-    return v + __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
+    v += dpp_row<0xB1>(v);
+    v += dpp_row<0x4E>(v);
+    return v + dpp_row<0x141>(v);
 }
 
 // The planes of 4 consecutive values of a block whose 32 values are held

@@ -10,6 +10,7 @@
 // its 64x64 FP32 state (16 KB) is read once and written once, and every
 // per-head vector lives in LDS.
 #include "si_rwkv.hpp"
+#include "si_lanes.hpp"
 #include "si_internal.hpp"
 #include "si_planes.hpp"
 #include "si_rows.hpp"
@@ -29,16 +30,16 @@ __device__ __forceinline__ float sigm(float v) { return 1.0f / (1.0f + expf(-v))
 // no step waits for an LDS round trip.
 __device__ __forceinline__ float quad_sum(float v)
 {
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v += dpp_row<0xB1>(v);   // quad_perm 1,0,3,2
+    v += dpp_row<0x4E>(v);   // quad_perm 2,3,0,1
     return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v)
 {
     v = quad_sum(v);
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    v += dpp_row<0x141>(v);  // row_half_mirror
+    v += dpp_row<0x140>(v);  // row_mirror
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
     const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

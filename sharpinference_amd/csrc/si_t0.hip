@@ -12,6 +12,7 @@
 // launch latency, so the kernels are plain grid-stride loops with 16-byte
 // accesses where the operands allow, and one wave per reduced row.
 #include "si_t0.hpp"
+#include "si_lanes.hpp"
 
 #include <hip/hip_fp16.h>
 
@@ -91,10 +92,10 @@ __global__ __launch_bounds__(T0_THREADS) void fill_kernel(float* __restrict__ o,
 // inside quads and 16-lane rows, then swaps between row pairs and halves.
 __device__ __forceinline__ float wave_sum(float v)
 {
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    v += dpp_row<0xB1>(v);   // quad_perm 1,0,3,2
+    v += dpp_row<0x4E>(v);   // quad_perm 2,3,0,1
+    v += dpp_row<0x141>(v);  // row_half_mirror
+    v += dpp_row<0x140>(v);  // row_mirror
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
     const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
