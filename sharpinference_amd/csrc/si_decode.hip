@@ -22,6 +22,7 @@
 
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 namespace si {
 namespace {
@@ -79,6 +80,22 @@ __device__ __forceinline__ void rotate_pair(float* h, int i, int rotary, const f
     const float left = h[i], right = h[i + rotary / 2];
     h[i] = left * c - right * s;
     h[i + rotary / 2] = right * c + left * s;
+}
+
+// 8 values already rounded to fp16 precision, as the cache words hold them.
+__device__ __forceinline__ uint4 pack8(const float* f)
+{
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        w[i] = static_cast<uint32_t>(__half_as_ushort(__float2half_rn(f[2 * i]))) |
+               (static_cast<uint32_t>(__half_as_ushort(__float2half_rn(f[2 * i + 1]))) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ uint4 select4(bool c, const uint4& a, const uint4& b)
+{
+    return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
 }
 
 __device__ __forceinline__ void unpack8(const uint4& r, float* f)
@@ -533,69 +550,76 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
     // scores q.k / sqrt(head_dim) as q.k * (1 / sqrt(head_dim)), and
     // exponentials with the hardware exp2 (__expf): both within a few ulp
     // of the exact forms, far inside the attention tolerance
+    // 5. the wave's maximum and exponentials per head; weighted values
+    //
+    // A chunk that ends at or before the new position (every chunk but the
+    // last) has all its positions cached and does not hold the new one: it
+    // takes the form without masks.  The last chunk puts the new row's fp16
+    // words in place of the loaded cache words at its position and zeroes
+    // the words past the count with selects (no divergent branches), then
+    // runs the same arithmetic, so both forms give the same values.
     const float rscale = 1.0f / sqrtf(static_cast<float>(HEAD_DIM));
     float sc[GROUP][FPPL];
+    float m[GROUP], l[GROUP], acc[GROUP][8];
+    auto attend = [&](auto whole_chunk) {
+        constexpr bool WHOLE = decltype(whole_chunk)::value;
+        uint4 knw = make_uint4(0, 0, 0, 0), vnw = knw;
+        if constexpr (!WHOLE) {
+            knw = pack8(kn);
+            vnw = pack8(vn);
+        }
 #pragma unroll
-    for (int j = 0; j < FPPL; j++) {
-        const int p = wave * (FCHUNK / 4) + row + 4 * j;
-        float k8[8];
-        if (p == newp) {
+        for (int j = 0; j < FPPL; j++) {
+            const int p = wave * (FCHUNK / 4) + row + 4 * j;
+            float k8[8];
+            unpack8(WHOLE ? kr[j] : select4(p == newp, knw, kr[j]), k8);
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                k8[e] = kn[e];
-        } else {
-            unpack8(kr[j], k8);
+            for (int h = 0; h < GROUP; h++) {
+                float sdot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    sdot = fmaf(q[h][e], k8[e], sdot);
+                sdot = row_sum<16>(sdot);
+                sc[h][j] = WHOLE || p < count ? sdot * rscale : -INFINITY;
+            }
         }
 #pragma unroll
         for (int h = 0; h < GROUP; h++) {
-            float sdot = 0.0f;
+            float mh = sc[h][0];
+#pragma unroll
+            for (int j = 1; j < FPPL; j++)
+                mh = fmaxf(mh, sc[h][j]);
+            mh = rows_max(mh);
+            m[h] = mh;
+            float lh = 0.0f;
+#pragma unroll
+            for (int j = 0; j < FPPL; j++) {
+                const float e = !WHOLE && sc[h][j] == -INFINITY ? 0.0f : __expf(sc[h][j] - mh);
+                sc[h][j] = e;
+                lh += e;
+            }
+            l[h] = lh;
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                sdot = fmaf(q[h][e], k8[e], sdot);
-            sdot = row_sum<16>(sdot);
-            sc[h][j] = p < count ? sdot * rscale : -INFINITY;
+                acc[h][e] = 0.0f;
         }
-    }
-
-    // 5. the wave's maximum and exponentials per head; weighted values
-    float m[GROUP], l[GROUP], acc[GROUP][8];
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) {
-        float mh = sc[h][0];
-#pragma unroll
-        for (int j = 1; j < FPPL; j++)
-            mh = fmaxf(mh, sc[h][j]);
-        mh = rows_max(mh);
-        m[h] = mh;
-        float lh = 0.0f;
 #pragma unroll
         for (int j = 0; j < FPPL; j++) {
-            const float e = sc[h][j] == -INFINITY ? 0.0f : __expf(sc[h][j] - mh);
-            sc[h][j] = e;
-            lh += e;
+            const int p = wave * (FCHUNK / 4) + row + 4 * j;
+            float v8[8];
+            // rows past the count may hold anything
+            unpack8(WHOLE ? vr[j] : select4(p == newp, vnw, select4(p < count, vr[j], make_uint4(0, 0, 0, 0))), v8);
+#pragma unroll
+            for (int h = 0; h < GROUP; h++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    acc[h][e] = fmaf(sc[h][j], v8[e], acc[h][e]);
         }
-        l[h] = lh;
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            acc[h][e] = 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < FPPL; j++) {
-        const int p = wave * (FCHUNK / 4) + row + 4 * j;
-        float v8[8];
-        if (p == newp) {
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                v8[e] = vn[e];
-        } else {
-            unpack8(p < count ? vr[j] : make_uint4(0, 0, 0, 0), v8);   // rows past the count may hold anything
-        }
-#pragma unroll
-        for (int h = 0; h < GROUP; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                acc[h][e] = fmaf(sc[h][j], v8[e], acc[h][e]);
-    }
+    };
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(valid && start + FCHUNK <= P)))
+        attend(std::true_type{});
+    else
+        attend(std::false_type{});
 
     // the owner's 16 lanes append the new row (positions of a lane are
     // wave * 32 + row + 4 j, so the new one is in row newp % 4 of wave newp / 32)
