@@ -634,32 +634,29 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
         *reinterpret_cast<uint4*>(vc + static_cast<int64_t>(P) * HEAD_DIM + 8 * dg) = *reinterpret_cast<const uint4*>(vh);
     }
 
-    // 6. sums over the wave's four rows, then the four waves through LDS
-    __shared__ float red[4][GROUP][HEAD_DIM];
-    __shared__ float wm[4][GROUP], wl[4][GROUP];
+    // 6. every 16-lane row's sums into LDS, then the rows and the four
+    //    waves merged there: (r0 + r2) + (r1 + r3) per wave, the order of a
+    //    swap of the wave's halves followed by a swap of row pairs, so the
+    //    cross-lane swaps (and their register copies) are left out
+    __shared__ float4 red4[4][4][GROUP][HEAD_DIM / 4];
+    __shared__ float wm[4][GROUP], wl[4][4][GROUP];
 #pragma unroll
     for (int h = 0; h < GROUP; h++) {
-        l[h] = rows_sum(l[h]);
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            acc[h][e] = rows_sum(acc[h][e]);
+        red4[wave][row][h][2 * dg] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        red4[wave][row][h][2 * dg + 1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
     }
-    if (row == 0) {
+    if (dg == 0)
 #pragma unroll
-        for (int h = 0; h < GROUP; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                red[wave][h][8 * dg + e] = acc[h][e];
-        if (dg == 0)
-#pragma unroll
-            for (int h = 0; h < GROUP; h++) {
+        for (int h = 0; h < GROUP; h++) {
+            wl[wave][row][h] = l[h];
+            if (row == 0)
                 wm[wave][h] = m[h];
-                wl[wave][h] = l[h];
-            }
-    }
+        }
     __syncthreads();
     if (!valid)
         return;
+    const float* red = reinterpret_cast<const float*>(red4);
+    auto part = [&](int w, int r, int h, int d) { return red[((w * 4 + r) * GROUP + h) * HEAD_DIM + d]; };
     for (int i = t; i < GROUP * HEAD_DIM; i += ATT_THREADS) {
         const int h = i / HEAD_DIM, d = i % HEAD_DIM;
         const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
@@ -667,8 +664,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_chunk_kernel(const floa
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const float f = wm[w][h] == -INFINITY ? 0.0f : __expf(wm[w][h] - M);   // a wave without valid positions adds nothing
-            o = fmaf(red[w][h][d], f, o);
-            lsum = fmaf(wl[w][h], f, lsum);
+            const float ow = (part(w, 0, h, d) + part(w, 2, h, d)) + (part(w, 1, h, d) + part(w, 3, h, d));
+            const float lw = (wl[w][0][h] + wl[w][2][h]) + (wl[w][1][h] + wl[w][3][h]);
+            o = fmaf(ow, f, o);
+            lsum = fmaf(lw, f, lsum);
         }
         float* dst = workspace + (static_cast<int64_t>(g * GROUP + h) * max_chunks + chunk) * PART;
         dst[2 + d] = o;
