@@ -426,6 +426,7 @@ def bench_decode_dense(hip, context: int = 2048):
     sess.set_control(1, context)
     sess.plan.launch()
     hip.sync()
+    settle(lambda: sess.plan.measure_us(4))
     us = sorted(sess.plan.measure_us(16) for _ in range(5))[2]
     sess.close()
     del weights
@@ -439,9 +440,24 @@ def bench_decode_dense(hip, context: int = 2048):
             "layer_weights": "4 distinct layers uploaded as 32 separate device copies"}
 
 
+SETTLE_S = 0.04
+
+
+def settle(replay, seconds: float = SETTLE_S) -> None:
+    """Calls `replay` (untimed replays of what is measured next) for at least
+    `seconds`: after the host-side uploads between measurements the GPU's
+    clocks start low and reach their loaded state only after tens of
+    milliseconds of work (a prefill product timed right after an upload
+    measured 36.8 us, the same product 30 ms of replays later 33.7 us)."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        replay()
+
+
 def bench_prefill(hip, rng, m: int = 512):
     """Batched prefill product at the same layer shapes: M = 512 tokens of
-    bf16 activations against the Q4_0 projections (MFMA), FP32 out."""
+    bf16 activations against the Q4_0 projections (MFMA), FP32 out.  Every
+    plan is replayed untimed for 40 ms before it is timed (steady clocks)."""
     from sharpinference_amd import native
     MFMA_BF16_PEAK_TFLOPS = 2500.0
     out = {"tokens": m, "shapes": {}}
@@ -460,13 +476,13 @@ def bench_prefill(hip, rng, m: int = 512):
         # layer set's plan holds a round of steps); replayed, warmed first
         plan = hip.record(lambda: [hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols)
                                    for _ in range(reps)])
-        plan.measure_us(2)
+        settle(lambda: plan.measure_us(4))
         us = sorted(plan.measure_us(4) for _ in range(5))[2] / reps
         plan.destroy()
         # the same product as a one-launch plan replayed `reps` times: each
         # launch then also carries a plan-launch gap
         plan = hip.record(lambda: hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols))
-        plan.measure_us(2)
+        settle(lambda: plan.measure_us(4))
         us_single = sorted(plan.measure_us(reps) for _ in range(5))[2]
         plan.destroy()
         total_flops += flops
@@ -479,7 +495,8 @@ def bench_prefill(hip, rng, m: int = 512):
     tflops = total_flops / total_us / 1e6
     out.update({"us_total": round(total_us, 1), "TFLOPs": round(tflops, 1),
                 "mfma_bf16_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                "form": f"each product's {reps} launches recorded in one plan, per-launch average",
+                "form": f"each product's {reps} launches recorded in one plan, per-launch average, "
+                        f"after {SETTLE_S * 1e3:.0f} ms of untimed replays",
                 "one_launch_plans": {"us_total": round(total_us_single, 1),
                                      "TFLOPs": round(total_flops / total_us_single / 1e6, 1)}})
 
@@ -489,7 +506,7 @@ def bench_prefill(hip, rng, m: int = 512):
         for w, x, y, rows, cols in bufs:
             hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols)
     plan = hip.record(layer)
-    plan.measure_us(2)
+    settle(lambda: plan.measure_us(4))
     layer_us = sorted(plan.measure_us(8) for _ in range(5))[2]
     plan.destroy()
     for w, x, y, _, _ in bufs:
@@ -649,6 +666,8 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
     else:
         sess.plan.launch()
     hip.sync()
+    if replay_timing:
+        settle(lambda: sess.plan.measure_us(4))
     us = sorted(sess.plan.measure_us(16) for _ in range(5))[2] if replay_timing else float("nan")
     step_bytes = cfg.weight_bytes_per_token() + cfg.kv_bytes(context + 1)
     gbs = step_bytes / us / 1e3
@@ -674,6 +693,7 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
         for l in range(cfg.layers):
             prog.load_kv(l, *kv)
         prog.forward_token(1, context)
+        settle(lambda: prog.measure_us(4))
         op_us = sorted(prog.measure_us(8) for _ in range(5))[2]
         # prefill_fused_16: one batch of 16 prompt rows; attention cost grows
         # linearly with the batch's start, so the batch starting halfway
@@ -683,6 +703,7 @@ def bench_decode(hip, context: int = 2048, tokens: int = 64, cpu: bool = True, r
         prefill = {}
         for start in (0, context // 2 - 8, context - 16):
             prog.upload("control", np.array([start, 16], np.int32))
+            settle(lambda: prog.measure_us(2, "prefill_fused_16"))
             prefill[start] = sorted(prog.measure_us(4, "prefill_fused_16") for _ in range(3))[1]
         mid = prefill[context // 2 - 8]
         op_program = {"us_per_token": r1(op_us), "tok_s": r1(1e6 / op_us), "dispatches": prog.dispatch_count(),
@@ -754,6 +775,8 @@ def bench_rwkv_decode(hip, tokens: int = 64, cpu: bool = True, replay_timing: bo
     else:
         sess.plan.launch()
     hip.sync()
+    if replay_timing:
+        settle(lambda: sess.plan.measure_us(4))
     us = sorted(sess.plan.measure_us(16) for _ in range(5))[2] if replay_timing else float("nan")
     step_bytes = cfg.weight_bytes_per_token()
     gbs = step_bytes / us / 1e3
@@ -777,6 +800,7 @@ def bench_rwkv_decode(hip, tokens: int = 64, cpu: bool = True, replay_timing: bo
         from sharpinference_amd import host_program
         prog = host_program.Rwkv7GraphProgram(cfg, weights, state)
         prog.forward_token(1)
+        settle(lambda: prog.measure_us(1))
         g_us = sorted(prog.measure_us(4) for _ in range(3))[1]
         rep = prog.report()
         graph = {"us_per_token": r1(g_us), "tok_s": r1(1e6 / g_us), "dispatches": prog.dispatch_count(),
