@@ -106,7 +106,13 @@ def main() -> int:
                     help="only the Phi-4 and RWKV-7 token loops (one token at a time, no back-to-back "
                          "replays, no CPU leg); prints their JSON; for kernel-trace profiles")
     ap.add_argument("--eager", action="store_true",
-                    help="with --decode-only: launch each step kernel by kernel instead of replaying its graph")
+                    help="with --decode-only: launch each step kernel by kernel instead of replaying its graph; "
+                         "with --prefill-only: launch the four products --rounds times back to back, no graph")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the batched prefill leg (M = 512, Q4_0 layer shapes); prints its JSON")
+    ap.add_argument("--rounds", type=int, default=400,
+                    help="with --prefill-only --eager: rounds of the four products (the first ~30 ms of work "
+                         "run at lower clocks; a kernel trace takes the later launches)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before timing, copy this many MiB device-to-device once (a plain copy of "
                          "known size that scales the HBM byte counters of a profiler run)")
@@ -134,6 +140,14 @@ def main() -> int:
         return 0
 
     from sharpinference_amd import native
+
+    if args.prefill_only:
+        hip = native.HipContext(0)
+        rng = np.random.default_rng(20250101)
+        res = prefill_eager(hip, rng, args.rounds) if args.eager else bench_prefill(hip, rng)
+        hip.close()
+        print(json.dumps({"prefill": res}), flush=True)
+        return 0
 
     if args.batch_ops:
         hip = native.HipContext(0)
@@ -516,6 +530,34 @@ def bench_prefill(hip, rng, m: int = 512):
                          "form": "the four products in one recorded plan, replayed 8 times back to back"}
     log(f"  prefill layer plan m={m}: {layer_us:.1f} us, {total_flops / layer_us / 1e6:.1f} TFLOP/s")
     return out
+
+
+def prefill_eager(hip, rng, rounds: int, m: int = 512):
+    """The prefill leg's four products launched one by one, `rounds` times
+    back to back with no plan (for kernel traces and counters, which then
+    see every launch); wall time per round after a final synchronize."""
+    from sharpinference_amd import native
+    bufs = []
+    for name, rows, cols in LAYER_Q4_0:
+        w = hip.to_device(synth_weights(native.Q4_0, rows, cols, rng))
+        xb = rng.standard_normal(m * cols).astype(np.float32).view(np.uint32)
+        xb = ((xb + 0x7FFF + ((xb >> 16) & 1)) >> 16).astype(np.uint16)
+        bufs.append((w, hip.to_device(xb), hip.alloc(m * rows * 4), rows, cols))
+    hip.sync()
+    t0 = time.perf_counter()
+    for r in range(rounds):
+        for w, x, y, rows, cols in bufs:
+            hip.gemm_prefill(native.Q4_0, w.ptr, x.ptr, y.ptr, m, rows, cols)
+        if r % 100 == 99:
+            hip.sync()
+            log(f"prefill eager: {r + 1} rounds, {(time.perf_counter() - t0) * 1e3:.0f} ms")
+    hip.sync()
+    ms = (time.perf_counter() - t0) * 1e3
+    for bb in bufs:
+        for b in bb[:3]:
+            b.free()
+    return {"tokens": m, "rounds": rounds, "ms": round(ms, 2), "us_per_round": round(ms * 1e3 / max(rounds, 1), 1),
+            "form": "the four products launched eagerly, no plan"}
 
 
 def bench_batch_ops(hip, rows: int = 16, context: int = 4096):
