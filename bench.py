@@ -630,7 +630,8 @@ def bench_vendor_dense(m: int = 512):
     """The vendor library's dense bf16 product at the prefill shapes:
     torch.nn.functional.linear (hipBLASLt) of bf16 X [m, K] by bf16 W [N, K]
     (four weight copies rotated), bf16 out, timed with events on torch's
-    stream (median of 5 samples of 20 launches).  W here is already dense
+    stream (median of 5 samples of 20 launches, after 40 ms of untimed
+    launches).  W here is already dense
     bf16 (3.6x the bytes of Q4_0 and no decode), so this is a reference
     for what a plain GEMM reaches at these shapes, not a product path."""
     import torch
@@ -641,9 +642,11 @@ def bench_vendor_dense(m: int = 512):
     for name, rows, cols in LAYER_Q4_0:
         x = torch.randn(m, cols, device=dev, dtype=torch.bfloat16, generator=gen)
         ws = [torch.randn(rows, cols, device=dev, dtype=torch.bfloat16, generator=gen) for _ in range(4)]
-        for i in range(8):
-            torch.nn.functional.linear(x, ws[i % 4])
-        torch.cuda.synchronize()
+        def replay():
+            for i in range(8):
+                torch.nn.functional.linear(x, ws[i % 4])
+            torch.cuda.synchronize()
+        settle(replay)
         samples = []
         for _ in range(5):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
