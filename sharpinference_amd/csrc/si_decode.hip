@@ -42,12 +42,6 @@ constexpr int FPPL = FCHUNK / 16;  // positions per lane of the chunk kernel
 constexpr int ATT_THREADS = 256;
 constexpr int PART = HEAD_DIM + 2; // per head and chunk: max, sum, 128 weighted values
 
-__device__ __forceinline__ float ld_half_u(const uint8_t* p)
-{
-    const unsigned short h = static_cast<unsigned short>(p[0] | (p[1] << 8));
-    return __half2float(__ushort_as_half(h));
-}
-
 // ---- embedding gather -------------------------------------------------------
 
 template <int FMT>

@@ -394,7 +394,7 @@ struct HipVmSlot {
     TensorDescriptor tensor;
     VmAccess access = VmAccess::ReadWrite;
     VmSlotScope scope = VmSlotScope::Global;
-    std::string binding_key;   // empty: none
+    std::string binding_key = {};   // empty: none
 };
 
 // A lowered program's dispatch (VmDispatch, VmProgram.cs): the kernel
