@@ -458,14 +458,16 @@ SETTLE_S = 0.04
 
 
 def settle(replay, seconds: float = SETTLE_S) -> None:
-    """Calls `replay` (untimed replays of what is measured next) for at least
-    `seconds`: after the host-side uploads between measurements the GPU's
+    """Calls `replay` (untimed replays of what is measured next) at least
+    once and until `seconds` have passed: after the host-side uploads between measurements the GPU's
     clocks start low and reach their loaded state only after tens of
     milliseconds of work (a prefill product timed right after an upload
     measured 36.8 us, the same product 30 ms of replays later 33.7 us)."""
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    while True:
         replay()
+        if time.perf_counter() - t0 >= seconds:
+            break
 
 
 def bench_prefill(hip, rng, m: int = 512):

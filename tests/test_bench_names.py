@@ -66,3 +66,18 @@ def test_every_timed_plan_is_warmed(steps, warmup, copies):
     # the warm-up holds at least the requested warm-up steps
     w = sum(copies if k == ("round",) else k[1] for k in b.plan_schedule(max(warmup, 1), copies))
     assert w == max(warmup, 1)
+
+
+def test_settle_replays_until_its_time_has_passed():
+    """bench.settle (the untimed replays before a leg samples a plan) calls
+    its replay at least once and keeps calling it until the time budget has
+    passed, then stops."""
+    import time
+    b = _bench_module()
+    calls = []
+    t0 = time.perf_counter()
+    b.settle(lambda: calls.append(time.perf_counter()), seconds=0.02)
+    assert len(calls) > 1 and calls[-2] - calls[0] < 0.02 <= time.perf_counter() - t0
+    calls.clear()
+    b.settle(lambda: calls.append(1), seconds=0.0)
+    assert calls == [1]
