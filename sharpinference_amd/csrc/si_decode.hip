@@ -44,16 +44,27 @@ constexpr int PART = HEAD_DIM + 2; // per head and chunk: max, sum, 128 weighted
 
 // ---- embedding gather -------------------------------------------------------
 
+// Row `*index` of the table into out (columns strided over `blocks`
+// workgroups of 256 threads, this one `block`); an index outside the table
+// yields NaN.
+template <int FMT>
+__device__ __forceinline__ void gather_row(const uint8_t* __restrict__ table, int rows, int cols, int64_t row_bytes,
+                                           const int32_t* __restrict__ index, float* __restrict__ out, int block,
+                                           int blocks)
+{
+    const int row = *index;
+    const bool valid = row >= 0 && row < rows;
+    const uint8_t* rp = table + static_cast<int64_t>(valid ? row : 0) * row_bytes;
+    for (int c = block * 256 + threadIdx.x; c < cols; c += blocks * 256)
+        out[c] = valid ? row_value<FMT>(rp, c) : __int_as_float(0x7fc00000);
+}
+
 template <int FMT>
 __global__ __launch_bounds__(256) void gather_row_kernel(const uint8_t* __restrict__ table, int rows, int cols,
                                                          int64_t row_bytes, const int32_t* __restrict__ index,
                                                          float* __restrict__ out)
 {
-    const int row = *index;
-    const bool valid = row >= 0 && row < rows;
-    const uint8_t* rp = table + static_cast<int64_t>(valid ? row : 0) * row_bytes;
-    for (int c = blockIdx.x * 256 + threadIdx.x; c < cols; c += gridDim.x * 256)
-        out[c] = valid ? row_value<FMT>(rp, c) : __int_as_float(0x7fc00000);
+    gather_row<FMT>(table, rows, cols, row_bytes, index, out, blockIdx.x, gridDim.x);
 }
 
 // ---- attention ------------------------------------------------------------------
@@ -106,9 +117,8 @@ __device__ __forceinline__ void unpack8(const uint4& r, float* f)
 // Once per step: the rotary table of the new position (frequency
 // 1 / base^(2i / R), cos / sin scaled by rope_scale), shared by every layer
 // that attends at that position.
-__global__ __launch_bounds__(64) void attention_prep_kernel(AttentionArgs a)
+__device__ __forceinline__ void rope_table(const AttentionArgs& a, int t)
 {
-    const int t = threadIdx.x;
     const int P = *a.position;
     float* rope = a.workspace + att_rope(a.heads, a.max_chunks);
     if (t < a.rotary_dim / 2) {
@@ -117,6 +127,25 @@ __global__ __launch_bounds__(64) void attention_prep_kernel(AttentionArgs a)
         rope[t] = cosf(angle) * a.rope_scale;
         rope[64 + t] = sinf(angle) * a.rope_scale;
     }
+}
+
+__global__ __launch_bounds__(64) void attention_prep_kernel(AttentionArgs a) { rope_table(a, threadIdx.x); }
+
+// The decode step's first launch: the embedding row of the token (every
+// workgroup but the last) and the step's rotary table (the last
+// workgroup); both read only the step's control values.
+template <int FMT>
+__global__ __launch_bounds__(256) void step_start_kernel(const uint8_t* __restrict__ table, int rows, int cols,
+                                                         int64_t row_bytes, const int32_t* __restrict__ index,
+                                                         float* __restrict__ out, AttentionArgs a)
+{
+    const int gather_blocks = static_cast<int>(gridDim.x) - 1;
+    if (static_cast<int>(blockIdx.x) == gather_blocks) {
+        if (threadIdx.x < 64)
+            rope_table(a, threadIdx.x);
+        return;
+    }
+    gather_row<FMT>(table, rows, cols, row_bytes, index, out, blockIdx.x, gather_blocks);
 }
 
 constexpr int MAX_CHUNKS = 256;
@@ -813,6 +842,25 @@ hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t c
     case FMT_Q4_K: hipLaunchKernelGGL((gather_row_kernel<FMT_Q4_K>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
     case FMT_F16: hipLaunchKernelGGL((gather_row_kernel<FMT_F16>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
     case FMT_F32: hipLaunchKernelGGL((gather_row_kernel<FMT_F32>), grid, dim3(256), 0, s, t, static_cast<int>(rows), static_cast<int>(cols), rb, index, out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_step_start(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index, float* out,
+                             const AttentionArgs& a, hipStream_t s)
+{
+    const int64_t rb = row_bytes(fmt, cols);
+    const int64_t nblk = (cols + 255) / 256;
+    const dim3 grid(static_cast<unsigned>((nblk < 64 ? nblk : 64) + 1));
+    const uint8_t* t = static_cast<const uint8_t*>(table);
+    const int r = static_cast<int>(rows), c = static_cast<int>(cols);
+    switch (fmt) {
+    case FMT_Q8_0: hipLaunchKernelGGL((step_start_kernel<FMT_Q8_0>), grid, dim3(256), 0, s, t, r, c, rb, index, out, a); break;
+    case FMT_Q4_0: hipLaunchKernelGGL((step_start_kernel<FMT_Q4_0>), grid, dim3(256), 0, s, t, r, c, rb, index, out, a); break;
+    case FMT_Q4_K: hipLaunchKernelGGL((step_start_kernel<FMT_Q4_K>), grid, dim3(256), 0, s, t, r, c, rb, index, out, a); break;
+    case FMT_F16: hipLaunchKernelGGL((step_start_kernel<FMT_F16>), grid, dim3(256), 0, s, t, r, c, rb, index, out, a); break;
+    case FMT_F32: hipLaunchKernelGGL((step_start_kernel<FMT_F32>), grid, dim3(256), 0, s, t, r, c, rb, index, out, a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -50,6 +50,10 @@ hipError_t launch_gather_row(int fmt, const void* table, int64_t rows, int64_t c
 // `prep`; a program that attends several layers at one position prepares
 // once and passes prep = false afterwards.
 hipError_t launch_attention_prep(const AttentionArgs& a, hipStream_t s);
+// One launch of the decode step's start: launch_gather_row's embedding row
+// and launch_attention_prep's rotary table.
+hipError_t launch_step_start(int fmt, const void* table, int64_t rows, int64_t cols, const int32_t* index, float* out,
+                             const AttentionArgs& a, hipStream_t s);
 hipError_t launch_attention(const AttentionArgs& a, hipStream_t s, bool prep = true);
 hipError_t launch_argmax(const float* values, int64_t n, void* workspace, int32_t* out, hipStream_t s);
 

@@ -130,8 +130,8 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m, int chunk_
     const uint64_t att_bytes = (static_cast<uint64_t>(si::attention_workspace_floats(m->heads, m->capacity)) * 4 + 255) &
                                ~uint64_t(255);
     void* am_ws = static_cast<uint8_t*>(m->workspace) + att_bytes;
-    hipError_t e = si::launch_gather_row(m->embed_format, m->embed, m->vocab, H, m->control, m->hidden_state, s);
-    // every layer attends at the same position: one rotary table per step
+    // the embedding row, and (every layer attends at the same position)
+    // one rotary table per step, in one launch
     si_hip_attention a{};
     a.qkv = m->qkv;
     a.position = m->control + 1;
@@ -144,8 +144,8 @@ hipError_t phi4_step(si_hip_context* ctx, const si_hip_phi4_model* m, int chunk_
     a.capacity = m->capacity;
     a.rope_base = m->rope_base;
     a.rope_scale = m->rope_scale;
-    if (e == hipSuccess)
-        e = si::launch_attention_prep(attention_args(&a), s);
+    hipError_t e =
+        si::launch_step_start(m->embed_format, m->embed, m->vocab, H, m->control, m->hidden_state, attention_args(&a), s);
     for (int l = 0; e == hipSuccess && l < m->layers; l++) {
         const si_hip_phi4_layer& L = m->layer[l];
         si::GemvOp qkv;
