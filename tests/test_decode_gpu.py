@@ -297,6 +297,35 @@ def test_position_range_plans_across_chunk_edges(hip):
             assert np.allclose(a, b, rtol=2e-3, atol=2e-3), (l, which)
 
 
+def test_step_with_a_token_outside_the_vocabulary_yields_nan_logits(hip):
+    """The step's first launch gathers the token's embedding row (NaN for an
+    index outside the table, as the gather-row operator gives) and writes the
+    rotary table: a token past the vocabulary gives NaN logits and next
+    token 0 (the argmax rule on all-NaN values), where the oracle refuses the
+    token; a valid token at another position then matches the oracle."""
+    cfg = phi4.Phi4Config(layers=2, hidden=1024, heads=8, kv_heads=2, ffn=2048, vocab=2000, capacity=128)
+    weights = phi4.synth_weights(cfg, seed=29)
+    kv = phi4.synth_kv(cfg, length=50, seed=30)
+    sess = phi4.Phi4DecodeSession(hip, cfg, weights)
+    ref = orc.Phi4Oracle(cfg, weights)
+    try:
+        for l, (k, v) in enumerate(kv):
+            sess.load_kv(l, k, v)
+            ref.k[l][...] = k
+            ref.v[l][...] = v
+        for bad in (cfg.vocab, -1):
+            g = sess.forward_token(bad, 60)
+            logits = sess.read_logits()
+            assert np.all(np.isnan(logits)) and g == 0 == orc.argmax(logits), bad
+            with pytest.raises(ValueError):
+                ref.step(bad, 60)
+        g = sess.forward_token(17, 50)
+        o, ol = ref.step(17, 50)
+        _check_logits(g, sess.read_logits(), o, ol, "valid token after the refused ones")
+    finally:
+        sess.close()
+
+
 def test_bounded_step_rejects_positions_past_its_range(hip):
     """A step recorded for positions 0..127 replayed at position 200: NaN
     logits and no cache append at 200; the session's own plan for that
